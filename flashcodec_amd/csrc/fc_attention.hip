@@ -1,0 +1,743 @@
+// Materialisation-free decode attention over a codec archive (gfx950).
+//
+// For one query token per sequence and an archive whose blocks store s rows
+// S (s x D) with synthesis matrix A (r x s) — jpeg: A = M^T, png:
+// A = tril(1) over (anchor, deltas) — the r tokens of a block are A S, so
+//   logit[p] = scale * sum_j A[p][j] * (q . S_j)
+//   out     += sum_j (sum_p prob[p] A[p][j]) * S_j
+// (flashcodec/attention.py:1-22, 101-140).
+//
+// Kernel 1 (split): grid (split, batch*kv_head, query-head group).  A
+// workgroup owns a contiguous range of blocks of one kv head and up to GM
+// query heads of its group, so every archived row is read from HBM once per
+// group of GM query heads (the reference's Triton kernel reads it once per
+// query head).  The range is walked in passes of up to kPassRows rows:
+//   A. scores: row tasks are spread over the workgroup, LPR lanes per row
+//      with VEC features each; partial dots are reduced across the LPR
+//      lanes (DPP inside 16-lane rows, shuffles beyond) and the per-row
+//      int8 scale is applied once to the reduced dot;
+//   B. softmax: every (block, head) pair turns its s scores into r logits
+//      (base-2 domain, scale*log2(e) folded in), the pass maximum updates
+//      the running maximum, and the pair writes its s output weights
+//      w_j = sum_p 2^(logit_p - m) A[p][j] (times the V row scale) back in
+//      place of its scores;
+//   C. values: the same row tasks accumulate acc[g][d] += w_j * S_j[d].
+// The partial (m, l, acc[D]) of each (query head, split) goes to the
+// workspace.
+// Kernel 2 (merge): one workgroup per (batch, kv head) combines the split
+// partials of each query head with the raw tail tokens (attended at full
+// precision) and writes out = acc / l in the query dtype.
+#include <hip/hip_runtime.h>
+
+#include "fc_common.h"
+
+namespace fc {
+
+int check_launch();
+int esize_of(int dt);
+
+constexpr int kAttnThreads = 256;
+constexpr int kPassRows = 512;
+constexpr int kMaxSplits = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+  const void* q;
+  int q_dtype;
+  int64_t q_sb, q_sh;
+  const void* krows;
+  const float* kscales;
+  const void* kanch;
+  int64_t kcap;
+  const void* vrows;
+  const float* vscales;
+  const void* vanch;
+  int64_t vcap;
+  const float* A;  // r x s
+  int64_t Hkv, G, D, nb;
+  int r, s;
+  float scale_log2;  // attention scale * log2(e)
+  int lpr_log2;
+  int64_t blocks_per_split;
+  int n_splits;
+  float* pm;
+  float* pl;
+  float* pacc;
+};
+
+// v + (v from the lane selected by a DPP pattern); patterns stay inside a
+// 16-lane row.
+#define FC_DPP_ADD(v, CTRL)                                                          \
+  ((v) + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (CTRL), 0xf, \
+                                                    0xf, false)))
+
+// Sum over aligned groups of `lpr` lanes (power of two <= 64); every lane of
+// the group receives the group sum.
+__device__ __forceinline__ float row_sum(float v, int lpr) {
+  if (lpr >= 2) v = FC_DPP_ADD(v, 0xB1);   // quad_perm [1,0,3,2]
+  if (lpr >= 4) v = FC_DPP_ADD(v, 0x4E);   // quad_perm [2,3,0,1]
+  if (lpr >= 8) v = FC_DPP_ADD(v, 0x141);  // row_half_mirror
+  if (lpr >= 16) v = FC_DPP_ADD(v, 0x140); // row_mirror
+  if (lpr >= 32) v += __shfl_xor(v, 16, 64);
+  if (lpr >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ __forceinline__ float load_q(const void* q, int dt, int64_t idx) {
+  switch (dt) {
+    case FC_F16: return to_f32(static_cast<const f16_t*>(q)[idx]);
+    case FC_BF16: return to_f32(static_cast<const bf16_t*>(q)[idx]);
+    default: return static_cast<const float*>(q)[idx];
+  }
+}
+
+// Row `j` of block `n` of sequence `bh`, VEC features from d0, as fp32.
+// Returns the row's scale (int8 stores) or 1.
+template <typename TS, int KIND, int VEC>
+__device__ __forceinline__ float load_row(const void* rows, const float* scales,
+                                          const void* anch, int64_t cap, int64_t bh,
+                                          int64_t n, int j, int s, int r, int64_t D,
+                                          int64_t d0, bool dact, float (&x)[VEC]) {
+  if (!dact) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v] = 0.f;
+    return 1.f;
+  }
+  if constexpr (KIND == FC_STORE_JPEG_I8) {
+    const int64_t row = (bh * cap + n) * s + j;
+    load_f32<int8_t, VEC>(static_cast<const int8_t*>(rows) + row * D + d0, x);
+    return scales[row];
+  } else if constexpr (KIND == FC_STORE_JPEG_FP) {
+    const int64_t row = (bh * cap + n) * s + j;
+    load_f32<TS, VEC>(static_cast<const TS*>(rows) + row * D + d0, x);
+    return 1.f;
+  } else {
+    if (j == 0) {
+      load_f32<TS, VEC>(static_cast<const TS*>(anch) + (bh * cap + n) * D + d0, x);
+    } else {
+      const int64_t row = (bh * cap + n) * (r - 1) + (j - 1);
+      load_f32<float, VEC>(static_cast<const float*>(rows) + row * D + d0, x);
+    }
+    return 1.f;
+  }
+}
+
+template <int GM>
+__device__ __forceinline__ void wg_reduce(float (&v)[GM], float* red, bool is_max) {
+  // v[g] is this thread's partial for head g; threads of a wavefront first
+  // combine lane-wise, then the four wavefronts through LDS.  Every thread
+  // ends with the workgroup result.
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int g = 0; g < GM; ++g) {
+    float x = v[g];
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      const float y = __shfl_xor(x, m, 64);
+      x = is_max ? fmaxf(x, y) : x + y;
+    }
+    if (lane == 0) red[wave * GM + g] = x;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < GM; ++g) {
+    float x = red[g];
+#pragma unroll
+    for (int w = 1; w < kAttnThreads / 64; ++w)
+      x = is_max ? fmaxf(x, red[w * GM + g]) : x + red[w * GM + g];
+    v[g] = x;
+  }
+  __syncthreads();
+}
+
+
+// ---- per-(block, head) softmax pieces.  `sc` points at the pair's s
+// scores in LDS (stride `st`); logits live in the base-2 domain.
+// SREG: s <= 8, scores and weights held in registers.
+
+template <int KIND, bool SREG>
+__device__ __forceinline__ float pair_max(const float* sc, int st, const float* A, int r, int s,
+                                          float sl2) {
+  float mx = -INFINITY;
+  if constexpr (KIND == FC_STORE_PNG) {
+    // A = tril(1): logit_t = prefix sum of the scores
+    float run = 0.f;
+    for (int t = 0; t < r; ++t) {
+      run += sc[t * st];
+      mx = fmaxf(mx, run * sl2);
+    }
+  } else if constexpr (SREG) {
+    float sv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sv[j] = j < s ? sc[j * st] : 0.f;
+    for (int t = 0; t < r; ++t) {
+      float lg = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < s) lg = __builtin_fmaf(A[t * s + j], sv[j], lg);
+      mx = fmaxf(mx, lg * sl2);
+    }
+  } else {
+    for (int t = 0; t < r; ++t) {
+      float lg = 0.f;
+      for (int j = 0; j < s; ++j) lg = __builtin_fmaf(A[t * s + j], sc[j * st], lg);
+      mx = fmaxf(mx, lg * sl2);
+    }
+  }
+  return mx;
+}
+
+// Writes the pair's output weights w_j (times the V row scale when `vsc` is
+// given) over its scores (png, SREG) or to `wo` (generic s), and returns
+// sum_t 2^(logit_t - m).
+template <int KIND, bool SREG>
+__device__ __forceinline__ float pair_weights(float* sc, float* wo, int st, const float* A, int r,
+                                              int s, float sl2, float m, const float* vsc) {
+  float es = 0.f;
+  if constexpr (KIND == FC_STORE_PNG) {
+    float run = 0.f;
+    for (int t = 0; t < r; ++t) {
+      run += sc[t * st];
+      const float e = __builtin_amdgcn_exp2f(run * sl2 - m);
+      es += e;
+      sc[t * st] = e;
+    }
+    // w_j = sum_{t >= j} e_t
+    float suf = 0.f;
+    for (int j = r - 1; j >= 0; --j) {
+      suf += sc[j * st];
+      sc[j * st] = suf;
+    }
+  } else if constexpr (SREG) {
+    float sv[8], w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sv[j] = j < s ? sc[j * st] : 0.f;
+      w[j] = 0.f;
+    }
+    for (int t = 0; t < r; ++t) {
+      float lg = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < s) lg = __builtin_fmaf(A[t * s + j], sv[j], lg);
+      const float e = __builtin_amdgcn_exp2f(lg * sl2 - m);
+      es += e;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < s) w[j] = __builtin_fmaf(e, A[t * s + j], w[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < s) sc[j * st] = vsc ? w[j] * vsc[j] : w[j];
+  } else {
+    // generic s: weights go to a separate LDS region `wo`; token weights are
+    // recomputed for every stored row
+    for (int t = 0; t < r; ++t) {
+      float lg = 0.f;
+      for (int i = 0; i < s; ++i) lg = __builtin_fmaf(A[t * s + i], sc[i * st], lg);
+      es += __builtin_amdgcn_exp2f(lg * sl2 - m);
+    }
+    for (int j = 0; j < s; ++j) {
+      float wj = 0.f;
+      for (int t = 0; t < r; ++t) {
+        float lg = 0.f;
+        for (int i = 0; i < s; ++i) lg = __builtin_fmaf(A[t * s + i], sc[i * st], lg);
+        wj = __builtin_fmaf(__builtin_amdgcn_exp2f(lg * sl2 - m), A[t * s + j], wj);
+      }
+      wo[j * st] = vsc ? wj * vsc[j] : wj;
+    }
+  }
+  return es;
+}
+
+template <typename TS, int KIND, bool SREG, int VEC, int GM>
+__global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs p) {
+  // scores, then weights, per (row, head); the generic-s variant keeps the
+  // weights in a second region
+  constexpr int kSwRegions = (KIND != FC_STORE_PNG && !SREG) ? 2 : 1;
+  __shared__ float sw[kPassRows * GM * kSwRegions];
+  float* const wts = sw + (kSwRegions - 1) * kPassRows * GM;
+  __shared__ float red[(kAttnThreads / 64) * GM];
+
+  const int split = blockIdx.x;
+  const int64_t bh = blockIdx.y;  // b * Hkv + hkv
+  const int64_t g0 = (int64_t)blockIdx.z * GM;
+  const int64_t b = bh / p.Hkv, hkv = bh - b * p.Hkv;
+  const int tid = threadIdx.x;
+  const int lpr = 1 << p.lpr_log2;
+  const int nslot = kAttnThreads >> p.lpr_log2;
+  const int slot = tid >> p.lpr_log2;
+  const int lir = tid & (lpr - 1);
+  const int64_t d0 = (int64_t)lir * VEC;
+  const bool dact = d0 < p.D;
+  const int s = p.s, r = p.r;
+
+  // query heads of this group, as fp32, for this lane's features
+  float qv[GM][VEC];
+#pragma unroll
+  for (int g = 0; g < GM; ++g) {
+    const int64_t hq = hkv * p.G + g0 + g;
+    const bool ok = dact && (g0 + g) < p.G;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      qv[g][v] = ok ? load_q(p.q, p.q_dtype, b * p.q_sb + hq * p.q_sh + d0 + v) : 0.f;
+  }
+
+  float acc[GM][VEC];
+#pragma unroll
+  for (int g = 0; g < GM; ++g)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[g][v] = 0.f;
+  float m_run[GM], l_run[GM];
+#pragma unroll
+  for (int g = 0; g < GM; ++g) {
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.f;
+  }
+
+  const int64_t nb_begin = (int64_t)split * p.blocks_per_split;
+  const int64_t nb_end = min(p.nb, nb_begin + p.blocks_per_split);
+  const int cb_max = max(1, kPassRows / s);
+
+  for (int64_t nb0 = nb_begin; nb0 < nb_end; nb0 += cb_max) {
+    const int cb = (int)min((int64_t)cb_max, nb_end - nb0);
+    const int nrows = cb * s;
+
+    // ---- A: scores q . S_j for every row of the pass
+    for (int rho = slot; rho < nrows; rho += nslot) {
+      const int nl = rho / s, j = rho - nl * s;
+      float x[VEC];
+      const float rs = load_row<TS, KIND, VEC>(p.krows, p.kscales, p.kanch, p.kcap, bh,
+                                               nb0 + nl, j, s, r, p.D, d0, dact, x);
+      float pd[GM];
+#pragma unroll
+      for (int g = 0; g < GM; ++g) {
+        float a = 0.f;
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) a = __builtin_fmaf(qv[g][v], x[v], a);
+        pd[g] = row_sum(a, lpr);
+      }
+      if (lir == 0) {
+#pragma unroll
+        for (int g = 0; g < GM; ++g) sw[rho * GM + g] = pd[g] * rs;
+      }
+    }
+    __syncthreads();
+
+    // ---- B: logits, running max, weights (in place of the scores)
+    const int npairs = cb * GM;
+    const int gsel = tid % GM;  // every pair this thread handles has this head
+    float pmax[GM];
+#pragma unroll
+    for (int g = 0; g < GM; ++g) pmax[g] = -INFINITY;
+    for (int u = tid; u < npairs; u += kAttnThreads) {
+      const float mx = pair_max<KIND, SREG>(sw + (u / GM) * s * GM + gsel, GM, p.A, r, s,
+                                            p.scale_log2);
+#pragma unroll
+      for (int g = 0; g < GM; ++g)
+        if (g == gsel) pmax[g] = fmaxf(pmax[g], mx);
+    }
+    wg_reduce<GM>(pmax, red, true);
+    float alpha[GM];
+    float mg = 0.f;
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+      const float mn = fmaxf(m_run[g], pmax[g]);
+      alpha[g] = __builtin_amdgcn_exp2f(m_run[g] - mn);
+      m_run[g] = mn;
+      if (g == gsel) mg = mn;
+    }
+    float psum[GM];
+#pragma unroll
+    for (int g = 0; g < GM; ++g) psum[g] = 0.f;
+    for (int u = tid; u < npairs; u += kAttnThreads) {
+      const int nl = u / GM;
+      const float* vsc = KIND == FC_STORE_JPEG_I8 ? p.vscales + (bh * p.vcap + nb0 + nl) * s
+                                                  : nullptr;
+      const float es = pair_weights<KIND, SREG>(sw + nl * s * GM + gsel, wts + nl * s * GM + gsel,
+                                                GM, p.A, r, s, p.scale_log2, mg, vsc);
+#pragma unroll
+      for (int g = 0; g < GM; ++g)
+        if (g == gsel) psum[g] += es;
+    }
+    wg_reduce<GM>(psum, red, false);
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+      l_run[g] = l_run[g] * alpha[g] + psum[g];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[g][v] *= alpha[g];
+    }
+    // (wg_reduce ended with a barrier, so the weights are visible)
+
+    // ---- C: values
+    for (int rho = slot; rho < nrows; rho += nslot) {
+      const int nl = rho / s, j = rho - nl * s;
+      float x[VEC];
+      load_row<TS, KIND, VEC>(p.vrows, nullptr, p.vanch, p.vcap, bh, nb0 + nl, j, s, r, p.D,
+                              d0, dact, x);
+#pragma unroll
+      for (int g = 0; g < GM; ++g) {
+        const float w = wts[rho * GM + g];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[g][v] = __builtin_fmaf(w, x[v], acc[g][v]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- combine the row slots: lanes of a wavefront with equal `lir`, then
+  // the wavefronts through LDS (reusing sw), one head at a time.
+#pragma unroll
+  for (int g = 0; g < GM; ++g)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      float x = acc[g][v];
+      for (int m = lpr; m < 64; m <<= 1) x += __shfl_xor(x, m, 64);
+      acc[g][v] = x;
+    }
+  const int lane = tid & 63, wave = tid >> 6;
+  const int nwave = kAttnThreads / 64;
+#pragma unroll
+  for (int g = 0; g < GM; ++g) {
+    if (g0 + g >= p.G) break;  // uniform
+    for (int64_t c = 0; c < p.D; c += kPassRows * GM / nwave) {
+      const int64_t span = min((int64_t)(kPassRows * GM / nwave), p.D - c);
+      // wavefront `wave` writes features [c, c+span) it owns
+      if (lane < lpr && dact) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          const int64_t d = d0 + v - c;
+          if (d >= 0 && d < span) sw[wave * span + d] = acc[g][v];
+        }
+      }
+      __syncthreads();
+      const int64_t bq = b * (p.Hkv * p.G) + hkv * p.G + g0 + g;
+      const int64_t slot_out = bq * p.n_splits + split;
+      for (int64_t d = tid; d < span; d += kAttnThreads) {
+        float x = 0.f;
+        for (int w = 0; w < nwave; ++w) x += sw[w * span + d];
+        p.pacc[slot_out * p.D + c + d] = x;
+      }
+      __syncthreads();
+    }
+    if (tid == 0) {
+      const int64_t bq = b * (p.Hkv * p.G) + hkv * p.G + g0 + g;
+      p.pm[bq * p.n_splits + split] = m_run[g];
+      p.pl[bq * p.n_splits + split] = l_run[g];
+    }
+  }
+}
+
+struct MergeArgs {
+  const void* q;
+  int q_dtype;
+  int64_t q_sb, q_sh;
+  const void* kraw;
+  const void* vraw;
+  int raw_dtype;
+  int64_t kr_sb, kr_sh, kr_st, vr_sb, vr_sh, vr_st;
+  int64_t n_raw;
+  void* out;
+  int64_t o_sb, o_sh;
+  int64_t Hkv, G, D;
+  float scale_log2;
+  int n_splits;
+  const float* pm;
+  const float* pl;
+  const float* pacc;
+};
+
+__device__ __forceinline__ void store_any(void* p, int dt, int64_t idx, float v) {
+  switch (dt) {
+    case FC_F16: static_cast<f16_t*>(p)[idx] = from_f32<f16_t>(v); break;
+    case FC_BF16: static_cast<bf16_t*>(p)[idx] = from_f32<bf16_t>(v); break;
+    default: static_cast<float*>(p)[idx] = v; break;
+  }
+}
+
+constexpr int kMergeMaxD = FC_MAX_HEAD_DIM / 64;
+
+__global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(MergeArgs p) {
+  __shared__ float wsplit[kAttnThreads / 64][kMaxSplits];
+  __shared__ float wtail[kAttnThreads / 64][FC_MAX_BLOCK];
+  const int64_t bh = blockIdx.x;
+  const int64_t b = bh / p.Hkv, hkv = bh - b * p.Hkv;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int nwave = kAttnThreads / 64;
+  const int nd = (int)((p.D + 63) / 64);
+
+  // wavefront `wave` handles query head gbase + wave of the kv group; the
+  // loop trip count is uniform so the barriers are reached by everyone
+  for (int64_t gbase = 0; gbase < p.G; gbase += nwave) {
+    const int64_t g = gbase + wave;
+    const bool act = g < p.G;
+    const int64_t hq = hkv * p.G + (act ? g : 0);
+    const int64_t bq = b * (p.Hkv * p.G) + hq;
+    float qv[kMergeMaxD];
+#pragma unroll
+    for (int i = 0; i < kMergeMaxD; ++i) {
+      const int64_t d = lane + 64 * i;
+      qv[i] = (i < nd && d < p.D) ? load_q(p.q, p.q_dtype, b * p.q_sb + hq * p.q_sh + d) : 0.f;
+    }
+    // raw-tail logits (base-2 domain)
+    float mx = -INFINITY;
+    for (int64_t t = 0; t < p.n_raw; ++t) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < kMergeMaxD; ++i) {
+        const int64_t d = lane + 64 * i;
+        if (i < nd && d < p.D)
+          a = __builtin_fmaf(
+              qv[i], load_q(p.kraw, p.raw_dtype, b * p.kr_sb + hkv * p.kr_sh + t * p.kr_st + d),
+              a);
+      }
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) a += __shfl_xor(a, m, 64);
+      const float lg = a * p.scale_log2;
+      if (lane == 0) wtail[wave][t] = lg;
+      mx = fmaxf(mx, lg);
+    }
+    // split maxima
+    for (int sp = lane; sp < p.n_splits; sp += 64) mx = fmaxf(mx, p.pm[bq * p.n_splits + sp]);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    float l = 0.f;
+    for (int sp = lane; sp < p.n_splits; sp += 64) {
+      const float w = __builtin_amdgcn_exp2f(p.pm[bq * p.n_splits + sp] - mx);
+      wsplit[wave][sp] = w;
+      l = __builtin_fmaf(w, p.pl[bq * p.n_splits + sp], l);
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
+    __syncthreads();
+    for (int64_t t = 0; t < p.n_raw; ++t) l += __builtin_amdgcn_exp2f(wtail[wave][t] - mx);
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int i = 0; i < kMergeMaxD; ++i) {
+      const int64_t d = lane + 64 * i;
+      if (!act || i >= nd || d >= p.D) continue;
+      float o = 0.f;
+      for (int sp = 0; sp < p.n_splits; ++sp)
+        o = __builtin_fmaf(wsplit[wave][sp], p.pacc[(bq * p.n_splits + sp) * p.D + d], o);
+      for (int64_t t = 0; t < p.n_raw; ++t) {
+        const float e = __builtin_amdgcn_exp2f(wtail[wave][t] - mx);
+        o = __builtin_fmaf(
+            e, load_q(p.vraw, p.raw_dtype, b * p.vr_sb + hkv * p.vr_sh + t * p.vr_st + d), o);
+      }
+      store_any(p.out, p.q_dtype, b * p.o_sb + hq * p.o_sh + d, o * inv);
+    }
+    __syncthreads();
+  }
+}
+
+template <int... Vs, typename F>
+int attn_with_int(int v, F&& f) {
+  int rc = FC_ERR_UNSUPPORTED;
+  bool hit = false;
+  ((v == Vs ? (rc = f(std::integral_constant<int, Vs>{}), hit = true) : false), ...);
+  return hit ? rc : FC_ERR_UNSUPPORTED;
+}
+
+}  // namespace fc
+
+using namespace fc;
+
+extern "C" {
+
+int64_t fc_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int n_splits) {
+  if (B <= 0 || Hq <= 0 || D <= 0 || n_splits <= 0) return 0;
+  const int64_t slots = B * Hq * (int64_t)n_splits;
+  const int64_t bytes = slots * (2 + D) * (int64_t)sizeof(float);
+  return (bytes + 255) / 256 * 256;
+}
+
+int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G, int n_cu) {
+  if (nb <= 0) return 0;
+  if (n_cu <= 0) n_cu = 256;
+  const int64_t groups = (G + 7) / 8;
+  const int64_t cols = std::max<int64_t>(1, B * Hkv * groups);
+  int64_t want = (8 * (int64_t)n_cu + cols - 1) / cols;
+  // at least ~16 blocks per split, at most kMaxSplits splits
+  want = std::min<int64_t>(want, (nb + 15) / 16);
+  want = std::max<int64_t>(1, std::min<int64_t>(want, kMaxSplits));
+  // splits that are actually non-empty
+  const int64_t bps = (nb + want - 1) / want;
+  return (int)((nb + bps - 1) / bps);
+}
+
+}  // extern "C"
+
+namespace fc {
+
+constexpr int kPartSplit = 1, kPartMerge = 2;
+
+// Validates the arguments and enqueues the requested parts: the split pass
+// over the archived blocks and/or the merge pass (split partials + raw tail).
+static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                                  int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int store_kind,
+                                  int stream_dtype, int r, int s, int64_t nb,
+                                  const fc_stream_view* key, const fc_stream_view* value,
+                                  int64_t n_raw, const float* A, float scale, void* out,
+                                  int64_t o_sb, int64_t o_sh, void* workspace, int n_splits,
+                                  void* stream, int parts) {
+  if (!q || !out || !key || !value || B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0) return FC_ERR_ARG;
+  if (Hq % Hkv) return FC_ERR_ARG;
+  if (nb < 0 || n_raw < 0 || (nb == 0 && n_raw == 0)) return FC_ERR_ARG;
+  if (esize_of(q_dtype) == 0 || q_dtype == FC_I8) return FC_ERR_ARG;
+  if (esize_of(stream_dtype) == 0 || stream_dtype == FC_I8) return FC_ERR_ARG;
+  if (D > FC_MAX_HEAD_DIM || r > FC_MAX_BLOCK || n_raw > FC_MAX_BLOCK) return FC_ERR_UNSUPPORTED;
+  if (r < 1 || s < 1 || s > FC_MAX_BLOCK) return FC_ERR_ARG;
+  if (store_kind == FC_STORE_PNG && s != r) return FC_ERR_ARG;
+  if (nb > 0) {
+    if (!A || !key->rows || !value->rows || !workspace) return FC_ERR_ARG;
+    if (n_splits < 1 || n_splits > kMaxSplits) return FC_ERR_ARG;
+    if (store_kind == FC_STORE_JPEG_I8 && (!key->scales || !value->scales)) return FC_ERR_ARG;
+    if (store_kind == FC_STORE_PNG && (!key->anchors || !value->anchors)) return FC_ERR_ARG;
+    if (nb > key->cap || nb > value->cap) return FC_ERR_ARG;
+  } else {
+    n_splits = 0;
+  }
+  if (n_raw > 0 && (!key->raw || !value->raw)) return FC_ERR_ARG;
+  const int64_t G = Hq / Hkv;
+  const float scale_log2 = scale * kLog2e;
+  hipStream_t st = (hipStream_t)stream;
+  float* pm = static_cast<float*>(workspace);
+  float* pl = pm + B * Hq * (int64_t)n_splits;
+  float* pacc = pl + B * Hq * (int64_t)n_splits;
+
+  if (nb > 0 && (parts & kPartSplit)) {
+    // VEC = 8 features per lane; LPR = lanes per row
+    if (D % 8) return FC_ERR_UNSUPPORTED;
+    const int64_t chunks = D / 8;
+    int lg = 0;
+    while ((int64_t(1) << lg) < chunks) ++lg;
+    const int gm = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
+    AttnArgs a;
+    a.q = q;
+    a.q_dtype = q_dtype;
+    a.q_sb = q_sb;
+    a.q_sh = q_sh;
+    a.krows = key->rows;
+    a.kscales = key->scales;
+    a.kanch = key->anchors;
+    a.kcap = key->cap;
+    a.vrows = value->rows;
+    a.vscales = value->scales;
+    a.vanch = value->anchors;
+    a.vcap = value->cap;
+    a.A = A;
+    a.Hkv = Hkv;
+    a.G = G;
+    a.D = D;
+    a.nb = nb;
+    a.r = r;
+    a.s = s;
+    a.scale_log2 = scale_log2;
+    a.lpr_log2 = lg;
+    a.blocks_per_split = (nb + n_splits - 1) / n_splits;
+    a.n_splits = n_splits;
+    a.pm = pm;
+    a.pl = pl;
+    a.pacc = pacc;
+    if ((a.blocks_per_split * (n_splits - 1)) >= nb) return FC_ERR_ARG;  // empty split
+    const dim3 grid((unsigned)n_splits, (unsigned)(B * Hkv), (unsigned)((G + gm - 1) / gm));
+    const bool sreg = s <= 8;
+    auto go = [&](auto ts, auto kc, auto sc) {
+      using TS = decltype(ts);
+      constexpr int KIND = decltype(kc)::value;
+      constexpr bool SREG = decltype(sc)::value;
+      return attn_with_int<1, 2, 4, 8>(gm, [&](auto gc) {
+        constexpr int GM = decltype(gc)::value;
+        attn_split_kernel<TS, KIND, SREG, 8, GM><<<grid, kAttnThreads, 0, st>>>(a);
+        return FC_OK;
+      });
+    };
+    using KI8 = std::integral_constant<int, FC_STORE_JPEG_I8>;
+    using KFP = std::integral_constant<int, FC_STORE_JPEG_FP>;
+    using KPNG = std::integral_constant<int, FC_STORE_PNG>;
+    using ST = std::true_type;
+    using SF = std::false_type;
+    int rc = FC_ERR_ARG;
+    if (store_kind == FC_STORE_JPEG_I8) {
+      // int8 rows do not depend on the stream dtype (the raw tail is merged
+      // separately)
+      rc = sreg ? go(float{}, KI8{}, ST{}) : go(float{}, KI8{}, SF{});
+    } else if (store_kind == FC_STORE_JPEG_FP || store_kind == FC_STORE_PNG) {
+      const bool png = store_kind == FC_STORE_PNG;
+      auto pick = [&](auto ts) {
+        if (png) return go(ts, KPNG{}, ST{});
+        return sreg ? go(ts, KFP{}, ST{}) : go(ts, KFP{}, SF{});
+      };
+      switch (stream_dtype) {
+        case FC_F32: rc = pick(float{}); break;
+        case FC_F16: rc = pick(f16_t{}); break;
+        case FC_BF16: rc = pick(bf16_t{}); break;
+        default: return FC_ERR_ARG;
+      }
+    }
+    if (rc != FC_OK) return rc;
+    rc = check_launch();
+    if (rc != FC_OK) return rc;
+  } else if (nb > 0) {
+    // merge only: the split geometry must still be consistent
+    if (D % 8) return FC_ERR_UNSUPPORTED;
+  }
+  if (!(parts & kPartMerge)) return FC_OK;
+
+  MergeArgs mg;
+  mg.q = q;
+  mg.q_dtype = q_dtype;
+  mg.q_sb = q_sb;
+  mg.q_sh = q_sh;
+  mg.kraw = key->raw;
+  mg.vraw = value->raw;
+  mg.raw_dtype = stream_dtype;
+  mg.kr_sb = key->raw_sb;
+  mg.kr_sh = key->raw_sh;
+  mg.kr_st = key->raw_st;
+  mg.vr_sb = value->raw_sb;
+  mg.vr_sh = value->raw_sh;
+  mg.vr_st = value->raw_st;
+  mg.n_raw = n_raw;
+  mg.out = out;
+  mg.o_sb = o_sb;
+  mg.o_sh = o_sh;
+  mg.Hkv = Hkv;
+  mg.G = G;
+  mg.D = D;
+  mg.scale_log2 = scale_log2;
+  mg.n_splits = n_splits;
+  mg.pm = pm;
+  mg.pl = pl;
+  mg.pacc = pacc;
+  attn_merge_kernel<<<dim3((unsigned)(B * Hkv)), kAttnThreads, 0, st>>>(mg);
+  return check_launch();
+}
+
+}  // namespace fc
+
+extern "C" {
+
+#define FC_ATTN_PARAMS                                                                        \
+  const void *q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B, int64_t Hq, int64_t Hkv, \
+      int64_t D, int store_kind, int stream_dtype, int r, int s, int64_t nb,                  \
+      const fc_stream_view *key, const fc_stream_view *value, int64_t n_raw, const float *A,  \
+      float scale, void *out, int64_t o_sb, int64_t o_sh, void *workspace, int n_splits,      \
+      void *stream
+#define FC_ATTN_ARGS                                                                         \
+  q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, store_kind, stream_dtype, r, s, nb, key, value, n_raw, \
+      A, scale, out, o_sb, o_sh, workspace, n_splits, stream
+
+int fc_decode_attention(FC_ATTN_PARAMS) {
+  return decode_attention_parts(FC_ATTN_ARGS, kPartSplit | kPartMerge);
+}
+
+int fc_decode_attention_split(FC_ATTN_PARAMS) {
+  return decode_attention_parts(FC_ATTN_ARGS, kPartSplit);
+}
+
+int fc_decode_attention_merge(FC_ATTN_PARAMS) {
+  return decode_attention_parts(FC_ATTN_ARGS, kPartMerge);
+}
+
+}  // extern "C"

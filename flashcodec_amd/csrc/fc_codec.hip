@@ -1,0 +1,720 @@
+// Block-archive and reconstruction kernels of the KV codec (gfx950).
+//
+// Work decomposition shared by every kernel here: one "item" is one block
+// of r tokens of one (batch, head) sequence.  An item is handled by LPI
+// consecutive lanes of a wavefront (LPI = power of two <= 64); lane i of the
+// item owns features [i*VEC, i*VEC + VEC) and walks the r tokens of the
+// block, so the token-axis transform (DCT, deltas, running sums) is
+// lane-local and every global access is a coalesced VEC-wide vector of a
+// token row.  Per-row reductions over the feature axis (int8 absmax) are
+// butterfly shuffles inside the item's lane group.
+//
+// Bit-exactness against the reference's CPU arithmetic:
+//   * DCT encode: coefficient = fma chain over the r taps starting from 0,
+//     rounded once to the stream dtype (the CPU GEMM's accumulation order).
+//   * DCT decode: same chain over the k coefficients.
+//   * int8: scale = dtype(absmax / 127) in fp32, 1 when not > 0, codes =
+//     round-half-even(c / scale) clamped to [-127, 127].
+//   * png cumsum: fp64 running sum rounded to fp32 per step (CPU cumsum
+//     accumulates float in double), anchor + sum in fp32, then the anchor
+//     dtype.
+// The file is compiled with -ffp-contract=off so no other multiply-add is
+// fused behind our back.
+#include <initializer_list>
+#include <utility>
+
+#include "fc_common.h"
+#include "fc_topm.h"
+
+namespace fc {
+
+constexpr int kThreads = 256;
+
+struct ItemMap {
+  int64_t item;
+  int lane;  // lane index inside the item group
+};
+
+// lpi_log2: log2 of the lanes per item.
+__device__ __forceinline__ ItemMap item_of_thread(int lpi_log2) {
+  ItemMap m;
+  m.item = (int64_t)blockIdx.x * (kThreads >> lpi_log2) + (threadIdx.x >> lpi_log2);
+  m.lane = threadIdx.x & ((1 << lpi_log2) - 1);
+  return m;
+}
+
+// ---------------------------------------------------------------- jpeg encode
+
+template <typename T, int VEC, int RMAX, bool QUANT>
+__global__ __launch_bounds__(kThreads) void jpeg_encode_kernel(
+    const T* __restrict__ x, int64_t sb, int64_t sh, int64_t ss, int64_t H, int64_t m,
+    int64_t D, int64_t s_valid, int r, int k, const float* __restrict__ basis,
+    void* __restrict__ out, float* __restrict__ scales, int64_t cap, int64_t n0,
+    int64_t items, int lpi_log2) {
+  const ItemMap im = item_of_thread(lpi_log2);
+  // Dead lanes still take part in the group shuffles below; they work on
+  // item 0 and store nothing.
+  const bool live = im.item < items;
+  const int64_t item = live ? im.item : 0;
+  const int64_t bh = item / m, blk = item - bh * m;
+  const int64_t b = bh / H, h = bh - b * H;
+  const int64_t d0 = (int64_t)im.lane * VEC;
+  const bool active = live && d0 < D;
+  const T* src = x + b * sb + h * sh + (active ? d0 : 0);
+  const int64_t tok0 = blk * r;
+
+  float xr[RMAX > 0 ? RMAX : 1][VEC];
+  if constexpr (RMAX > 0) {
+#pragma unroll
+    for (int t = 0; t < RMAX; ++t) {
+      if (t < r && active && tok0 + t < s_valid) {
+        load_f32<T, VEC>(src + (tok0 + t) * ss, xr[t]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) xr[t][v] = 0.f;
+      }
+    }
+  }
+
+  const int64_t out_row0 = (bh * cap + n0 + blk) * k;
+  for (int j = 0; j < k; ++j) {
+    const float* mj = basis + (int64_t)j * r;
+    float acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = 0.f;
+    if constexpr (RMAX > 0) {
+#pragma unroll
+      for (int t = 0; t < RMAX; ++t) {
+        if (t < r) {
+          const float w = mj[t];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[v] = __builtin_fmaf(xr[t][v], w, acc[v]);
+        }
+      }
+    } else {
+      for (int t = 0; t < r; ++t) {
+        float xv[VEC];
+        if (active && tok0 + t < s_valid) {
+          load_f32<T, VEC>(src + (tok0 + t) * ss, xv);
+        } else {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) xv[v] = 0.f;
+        }
+        const float w = mj[t];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = __builtin_fmaf(xv[v], w, acc[v]);
+      }
+    }
+    // round once to the stream dtype (dct_compress returns x.dtype)
+    float c[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) c[v] = to_f32(from_f32<T>(acc[v]));
+
+    if constexpr (!QUANT) {
+      if (active) store_from_f32<T, VEC>(static_cast<T*>(out) + (out_row0 + j) * D + d0, c);
+    } else {
+      float amax = 0.f;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) amax = fmaxf(amax, fabsf(c[v]));
+      amax = group_max_rt(amax, 1 << lpi_log2);
+      float s = to_f32(from_f32<T>(amax / 127.0f));
+      if (!(s > 0.f)) s = 1.0f;
+      if (active) {
+        vec_t<int8_t, VEC> qv;
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          float qf = __builtin_rintf(c[v] / s);
+          qf = fminf(fmaxf(qf, -127.f), 127.f);
+          qv.v[v] = (int8_t)(int)qf;
+        }
+        *reinterpret_cast<vec_t<int8_t, VEC>*>(static_cast<int8_t*>(out) + (out_row0 + j) * D +
+                                               d0) = qv;
+        if (im.lane == 0) scales[out_row0 + j] = s;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- jpeg decode
+
+template <typename TI, typename TO, int VEC, int RMAX, bool QUANT>
+__global__ __launch_bounds__(kThreads) void jpeg_decode_kernel(
+    const TI* __restrict__ store, const float* __restrict__ scales, int64_t H, int64_t cap,
+    int64_t a, int64_t nblk, int64_t D, int r, int k, const float* __restrict__ basis,
+    TO* __restrict__ out, int64_t osb, int64_t osh, int64_t oss, int64_t out_len,
+    int64_t items, int lpi_log2) {
+  const ItemMap im = item_of_thread(lpi_log2);
+  if (im.item >= items) return;
+  const int64_t bh = im.item / nblk, blk = a + (im.item - bh * nblk);
+  const int64_t b = bh / H, h = bh - b * H;
+  const int64_t d0 = (int64_t)im.lane * VEC;
+  if (d0 >= D) return;
+  const int64_t row0 = (bh * cap + blk) * k;
+  TO* dst = out + b * osb + h * osh + d0;
+  const int64_t tok0 = blk * r;
+
+  if constexpr (RMAX > 0) {
+    float acc[RMAX][VEC];
+#pragma unroll
+    for (int t = 0; t < RMAX; ++t)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[t][v] = 0.f;
+    for (int j = 0; j < k; ++j) {
+      float c[VEC];
+      load_f32<TI, VEC>(store + (row0 + j) * D + d0, c);
+      if constexpr (QUANT) {
+        const float s = scales[row0 + j];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) c[v] = c[v] * s;
+      }
+      const float* mj = basis + (int64_t)j * r;
+#pragma unroll
+      for (int t = 0; t < RMAX; ++t) {
+        if (t < r) {
+          const float w = mj[t];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[t][v] = __builtin_fmaf(c[v], w, acc[t][v]);
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < RMAX; ++t)
+      if (t < r && tok0 + t < out_len) store_from_f32<TO, VEC>(dst + (tok0 + t) * oss, acc[t]);
+  } else {
+    for (int t = 0; t < r; ++t) {
+      if (tok0 + t >= out_len) break;
+      float acc[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = 0.f;
+      for (int j = 0; j < k; ++j) {
+        float c[VEC];
+        load_f32<TI, VEC>(store + (row0 + j) * D + d0, c);
+        if constexpr (QUANT) {
+          const float s = scales[row0 + j];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) c[v] = c[v] * s;
+        }
+        const float w = basis[(int64_t)j * r + t];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = __builtin_fmaf(c[v], w, acc[v]);
+      }
+      store_from_f32<TO, VEC>(dst + (tok0 + t) * oss, acc);
+    }
+  }
+}
+
+// ------------------------------------------------------------ quantize rows
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kThreads) void quantize_rows_kernel(
+    const T* __restrict__ c, int64_t n_rows, int64_t rs, int64_t D, int8_t* __restrict__ codes,
+    float* __restrict__ scales, int lpi_log2) {
+  const ItemMap im = item_of_thread(lpi_log2);
+  const bool live = im.item < n_rows;
+  const int64_t row = live ? im.item : 0;
+  const int64_t d0 = (int64_t)im.lane * VEC;
+  const bool active = live && d0 < D;
+  float v[VEC];
+  if (active) {
+    load_f32<T, VEC>(c + row * rs + d0, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) v[i] = 0.f;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = group_max_rt(amax, 1 << lpi_log2);
+  float s = to_f32(from_f32<T>(amax / 127.0f));
+  if (!(s > 0.f)) s = 1.0f;
+  if (!active) return;
+  vec_t<int8_t, VEC> q;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    float qf = __builtin_rintf(v[i] / s);
+    qf = fminf(fmaxf(qf, -127.f), 127.f);
+    q.v[i] = (int8_t)(int)qf;
+  }
+  *reinterpret_cast<vec_t<int8_t, VEC>*>(codes + row * D + d0) = q;
+  if (im.lane == 0) scales[row] = s;
+}
+
+template <typename TO>
+__global__ __launch_bounds__(kThreads) void dequantize_rows_kernel(
+    const int8_t* __restrict__ codes, const float* __restrict__ scales, int64_t n, int64_t D,
+    TO* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  // q.to(dtype) * scale.to(dtype): both operands rounded to the output
+  // dtype first, product rounded once.
+  const float qv = to_f32(from_f32<TO>((float)(int)codes[i]));
+  const float sv = to_f32(from_f32<TO>(scales[i / D]));
+  out[i] = from_f32<TO>(qv * sv);
+}
+
+// ----------------------------------------------------------------- png encode
+
+// Descending bitonic sort of N (power of two) keys held in registers.
+template <int N>
+__device__ __forceinline__ void bitonic_sort_desc(uint32_t (&k)[N]) {
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool desc = (i & size) == 0;
+          const uint32_t a = k[i], c = k[j];
+          const uint32_t hi = a > c ? a : c, lo = a > c ? c : a;
+          k[i] = desc ? hi : lo;
+          k[j] = desc ? lo : hi;
+        }
+      }
+    }
+  }
+}
+
+// Keep mask of the `m` largest of `n` keys (n < RMAX).  The common case —
+// the m-th and (m+1)-th largest keys differ, or the cut falls on zero,
+// where keeping or zeroing a +-0 delta stores the same bits — is decided
+// from a sorting network; a nonzero tie across the cut takes the exact
+// introselect restatement.
+template <int RMAX>
+__device__ __forceinline__ uint64_t topm_mask(const uint32_t (&key)[RMAX], int n, int m) {
+  uint32_t s[RMAX];
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i) s[i] = i < n ? key[i] : 0u;
+  bitonic_sort_desc<RMAX>(s);
+  uint32_t vm = 0, vm1 = 0;
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i) {
+    if (i == m - 1) vm = s[i];
+    if (i == m) vm1 = s[i];
+  }
+  if (vm == 0u || vm != vm1) {
+    uint64_t mask = 0;
+#pragma unroll
+    for (int i = 0; i < RMAX; ++i)
+      if (i < n && key[i] >= vm) mask |= (uint64_t)1 << i;
+    return mask;
+  }
+  uint32_t kk[64];
+  for (int i = 0; i < n; ++i) kk[i] = key[i];
+  return topm_mask_exact(kk, n, m);
+}
+
+template <typename T, int VEC, int RMAX>
+__global__ __launch_bounds__(kThreads) void png_encode_kernel(
+    const T* __restrict__ x, int64_t sb, int64_t sh, int64_t ss, int64_t H, int64_t m,
+    int64_t D, int64_t s_valid, int r, int keep_m, float* __restrict__ deltas,
+    T* __restrict__ anchors, int64_t cap, int64_t n0, int64_t items, int lpi_log2) {
+  const ItemMap im = item_of_thread(lpi_log2);
+  if (im.item >= items) return;
+  const int64_t bh = im.item / m, blk = im.item - bh * m;
+  const int64_t b = bh / H, h = bh - b * H;
+  const int64_t d0 = (int64_t)im.lane * VEC;
+  if (d0 >= D) return;
+  const T* src = x + b * sb + h * sh + d0;
+  const int64_t tok0 = blk * r;
+  const int64_t slot = bh * cap + n0 + blk;
+
+  // anchor: token 0 of the block, copied in the stream dtype
+  {
+    vec_t<T, VEC> av;
+    if (tok0 < s_valid) {
+      av = *reinterpret_cast<const vec_t<T, VEC>*>(src + tok0 * ss);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) av.v[v] = from_f32<T>(0.f);
+    }
+    *reinterpret_cast<vec_t<T, VEC>*>(anchors + slot * D + d0) = av;
+  }
+
+  float xd[RMAX][VEC];
+#pragma unroll
+  for (int t = 0; t < RMAX; ++t) {
+    if (t < r && tok0 + t < s_valid) {
+      load_f32<T, VEC>(src + (tok0 + t) * ss, xd[t]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) xd[t][v] = 0.f;
+    }
+  }
+  // deltas in fp32, in place: xd[i] <- x_{i+1} - x_i
+#pragma unroll
+  for (int i = 0; i + 1 < RMAX; ++i)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) xd[i][v] = xd[i + 1][v] - xd[i][v];
+
+  const int n = r - 1;
+  if (keep_m > 0 && keep_m < n) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      uint32_t key[RMAX];
+#pragma unroll
+      for (int i = 0; i < RMAX; ++i) key[i] = i < n ? topm_key(__float_as_uint(xd[i][v])) : 0u;
+      const uint64_t mask = topm_mask<RMAX>(key, n, keep_m);
+#pragma unroll
+      for (int i = 0; i + 1 < RMAX; ++i)
+        if (!((mask >> i) & 1)) xd[i][v] = xd[i][v] * 0.0f;
+    }
+  }
+  float* dst = deltas + slot * (int64_t)n * D + d0;
+#pragma unroll
+  for (int i = 0; i + 1 < RMAX; ++i)
+    if (i < n) store_from_f32<float, VEC>(dst + i * D, xd[i]);
+}
+
+// ----------------------------------------------------------------- png decode
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kThreads) void png_decode_kernel(
+    const float* __restrict__ deltas, const T* __restrict__ anchors, int64_t H, int64_t cap,
+    int64_t a, int64_t nblk, int64_t D, int r, T* __restrict__ out, int64_t osb, int64_t osh,
+    int64_t oss, int64_t out_len, int64_t items, int lpi_log2) {
+  const ItemMap im = item_of_thread(lpi_log2);
+  if (im.item >= items) return;
+  const int64_t bh = im.item / nblk, blk = a + (im.item - bh * nblk);
+  const int64_t b = bh / H, h = bh - b * H;
+  const int64_t d0 = (int64_t)im.lane * VEC;
+  if (d0 >= D) return;
+  const int64_t slot = bh * cap + blk;
+  T* dst = out + b * osb + h * osh + d0;
+  const int64_t tok0 = blk * r;
+  float base[VEC];
+  load_f32<T, VEC>(anchors + slot * D + d0, base);
+  if (tok0 < out_len) store_from_f32<T, VEC>(dst + tok0 * oss, base);
+  double run[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) run[v] = 0.0;
+  const float* src = deltas + slot * (int64_t)(r - 1) * D + d0;
+  for (int i = 1; i < r; ++i) {
+    if (tok0 + i >= out_len) break;
+    float dv[VEC], o[VEC];
+    load_f32<float, VEC>(src + (int64_t)(i - 1) * D, dv);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      run[v] += (double)dv[v];
+      o[v] = base[v] + (float)run[v];
+    }
+    store_from_f32<T, VEC>(dst + (tok0 + i) * oss, o);
+  }
+}
+
+// ------------------------------------------------------------ host helpers
+
+thread_local int g_last_hip_error = 0;
+
+int check_launch() {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    g_last_hip_error = (int)e;
+    return FC_ERR_HIP;
+  }
+  return FC_OK;
+}
+
+static bool aligned(const void* p, int64_t bytes) {
+  return p == nullptr || ((uintptr_t)p % (uintptr_t)bytes) == 0;
+}
+
+int esize_of(int dt) {
+  switch (dt) {
+    case FC_F32: return 4;
+    case FC_F16: return 2;
+    case FC_BF16: return 2;
+    case FC_I8: return 1;
+    default: return 0;
+  }
+}
+
+// Elements per lane: the widest of {8, 4, 1} (<= max_vec) that divides D
+// and every stride, keeps every pointer aligned and needs <= 64 lanes.
+// 0 if none fits.
+static int pick_vec(int64_t D, int max_vec, std::initializer_list<int64_t> strides,
+                    std::initializer_list<std::pair<const void*, int>> ptrs) {
+  for (int vec : {8, 4, 1}) {
+    if (vec > max_vec || D % vec || (D + vec - 1) / vec > 64) continue;
+    bool ok = true;
+    for (int64_t s : strides) ok = ok && (s % vec == 0);
+    for (const auto& pp : ptrs) ok = ok && aligned(pp.first, (int64_t)vec * pp.second);
+    if (ok) return vec;
+  }
+  return 0;
+}
+
+static int log2_lanes(int64_t D, int vec) {
+  const int64_t need = (D + vec - 1) / vec;
+  int l = 0;
+  while ((int64_t(1) << l) < need) ++l;
+  return l;
+}
+
+static dim3 grid_for(int64_t items, int lpi_log2) {
+  const int64_t per = kThreads >> lpi_log2;
+  return dim3((unsigned)((items + per - 1) / per));
+}
+
+// Register-resident block size bucket for r, or 0 for the streaming path.
+// rmax*vec is kept <= 64 floats per lane.
+static int rmax_for(int r) { return r <= 8 ? 8 : (r <= 16 ? 16 : 0); }
+static int max_vec_for(int rmax) { return rmax == 8 ? 8 : (rmax == 16 ? 4 : 8); }
+
+template <typename F>
+int with_float_type(int dt, F&& f) {
+  switch (dt) {
+    case FC_F32: return f(float{});
+    case FC_F16: return f(f16_t{});
+    case FC_BF16: return f(bf16_t{});
+    default: return FC_ERR_ARG;
+  }
+}
+
+template <int... Vs, typename F>
+int with_int(int v, F&& f) {
+  int rc = FC_ERR_UNSUPPORTED;
+  bool hit = false;
+  ((v == Vs ? (rc = f(std::integral_constant<int, Vs>{}), hit = true) : false), ...);
+  return hit ? rc : FC_ERR_UNSUPPORTED;
+}
+
+}  // namespace fc
+
+using namespace fc;
+
+extern "C" {
+
+int fc_version(void) { return 100; }
+
+const char* fc_status_string(int status) {
+  switch (status) {
+    case FC_OK: return "ok";
+    case FC_ERR_ARG: return "invalid argument";
+    case FC_ERR_UNSUPPORTED: return "unsupported by this build's kernels";
+    case FC_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+int fc_last_hip_error(void) { return g_last_hip_error; }
+
+int fc_jpeg_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb, int64_t x_sh,
+                   int64_t x_ss, int64_t s_valid, int64_t m, int64_t D, int r, int k,
+                   const float* basis, void* coeffs, float* scales, int64_t cap, int64_t n0,
+                   int quant_bits, void* stream) {
+  if (B < 0 || H < 0 || m < 0 || D <= 0 || r < 1 || k < 1 || k > r) return FC_ERR_ARG;
+  if (quant_bits != 0 && quant_bits != 8) return FC_ERR_ARG;
+  if (n0 < 0 || n0 + m > cap) return FC_ERR_ARG;
+  const int64_t items = B * H * m;
+  if (items == 0) return FC_OK;
+  if (!x || !basis || !coeffs || (quant_bits && !scales)) return FC_ERR_ARG;
+  if (r > FC_MAX_BLOCK || D > FC_MAX_HEAD_DIM) return FC_ERR_UNSUPPORTED;
+  const int es = esize_of(x_dtype);
+  if (es == 0 || x_dtype == FC_I8) return FC_ERR_ARG;
+  const int rmax = rmax_for(r);
+  const int vec = pick_vec(D, max_vec_for(rmax), {x_sb, x_sh, x_ss},
+                           {{x, es}, {coeffs, quant_bits ? 1 : es}});
+  if (!vec) return FC_ERR_UNSUPPORTED;
+  const int lg = log2_lanes(D, vec);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = grid_for(items, lg);
+  const int rc = with_float_type(x_dtype, [&](auto tv) {
+    using T = decltype(tv);
+    return with_int<1, 4, 8>(vec, [&](auto vc) {
+      constexpr int VEC = decltype(vc)::value;
+      return with_int<8, 16, 0>(rmax, [&](auto rc_) {
+        constexpr int RMAX = decltype(rc_)::value;
+        if (quant_bits)
+          jpeg_encode_kernel<T, VEC, RMAX, true><<<grid, kThreads, 0, st>>>(
+              (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, k, basis, coeffs, scales, cap,
+              n0, items, lg);
+        else
+          jpeg_encode_kernel<T, VEC, RMAX, false><<<grid, kThreads, 0, st>>>(
+              (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, k, basis, coeffs, scales, cap,
+              n0, items, lg);
+        return FC_OK;
+      });
+    });
+  });
+  return rc != FC_OK ? rc : check_launch();
+}
+
+int fc_jpeg_decode(const void* store, int store_dtype, const float* scales, int64_t B,
+                   int64_t H, int64_t cap, int64_t a, int64_t nblk, int64_t D, int r, int k,
+                   const float* basis, void* out, int out_dtype, int64_t o_sb, int64_t o_sh,
+                   int64_t o_ss, int64_t out_len, void* stream) {
+  if (B < 0 || H < 0 || a < 0 || nblk < 0 || a + nblk > cap || D <= 0 || r < 1 || k < 1 ||
+      k > r)
+    return FC_ERR_ARG;
+  const int64_t items = B * H * nblk;
+  if (items == 0) return FC_OK;
+  if (!store || !basis || !out) return FC_ERR_ARG;
+  const bool quant = store_dtype == FC_I8;
+  if (quant && !scales) return FC_ERR_ARG;
+  if (r > FC_MAX_BLOCK || D > FC_MAX_HEAD_DIM) return FC_ERR_UNSUPPORTED;
+  const int es_in = esize_of(store_dtype), es_out = esize_of(out_dtype);
+  if (!es_in || !es_out || out_dtype == FC_I8) return FC_ERR_ARG;
+  const int rmax = rmax_for(r);
+  const int vec =
+      pick_vec(D, max_vec_for(rmax), {o_sb, o_sh, o_ss}, {{store, es_in}, {out, es_out}});
+  if (!vec) return FC_ERR_UNSUPPORTED;
+  const int lg = log2_lanes(D, vec);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = grid_for(items, lg);
+  auto launch = [&](auto ti, auto to) {
+    using TI = decltype(ti);
+    using TO = decltype(to);
+    return with_int<1, 4, 8>(vec, [&](auto vc) {
+      constexpr int VEC = decltype(vc)::value;
+      return with_int<8, 16, 0>(rmax, [&](auto rc_) {
+        constexpr int RMAX = decltype(rc_)::value;
+        jpeg_decode_kernel<TI, TO, VEC, RMAX, std::is_same<TI, int8_t>::value>
+            <<<grid, kThreads, 0, st>>>((const TI*)store, scales, H, cap, a, nblk, D, r, k,
+                                        basis, (TO*)out, o_sb, o_sh, o_ss, out_len, items, lg);
+        return FC_OK;
+      });
+    });
+  };
+  int rc;
+  if (quant) {
+    rc = with_float_type(out_dtype, [&](auto to) { return launch(int8_t{}, to); });
+  } else if (out_dtype == FC_F32) {
+    rc = with_float_type(store_dtype, [&](auto ti) { return launch(ti, float{}); });
+  } else if (out_dtype == store_dtype) {
+    rc = with_float_type(store_dtype, [&](auto ti) { return launch(ti, ti); });
+  } else {
+    return FC_ERR_UNSUPPORTED;
+  }
+  return rc != FC_OK ? rc : check_launch();
+}
+
+int fc_quantize_rows(const void* c, int c_dtype, int64_t n_rows, int64_t c_rs, int64_t D,
+                     int8_t* codes, float* scales, void* stream) {
+  if (n_rows < 0 || D <= 0) return FC_ERR_ARG;
+  if (n_rows == 0) return FC_OK;
+  if (!c || !codes || !scales) return FC_ERR_ARG;
+  const int es = esize_of(c_dtype);
+  if (!es || c_dtype == FC_I8) return FC_ERR_ARG;
+  if (D > FC_MAX_HEAD_DIM) return FC_ERR_UNSUPPORTED;
+  const int vec = pick_vec(D, 8, {c_rs}, {{c, es}, {codes, 1}});
+  if (!vec) return FC_ERR_UNSUPPORTED;
+  const int lg = log2_lanes(D, vec);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = grid_for(n_rows, lg);
+  const int rc = with_float_type(c_dtype, [&](auto tv) {
+    using T = decltype(tv);
+    return with_int<1, 4, 8>(vec, [&](auto vc) {
+      constexpr int VEC = decltype(vc)::value;
+      quantize_rows_kernel<T, VEC>
+          <<<grid, kThreads, 0, st>>>((const T*)c, n_rows, c_rs, D, codes, scales, lg);
+      return FC_OK;
+    });
+  });
+  return rc != FC_OK ? rc : check_launch();
+}
+
+int fc_dequantize_rows(const int8_t* codes, const float* scales, int64_t n_rows, int64_t D,
+                       void* out, int out_dtype, void* stream) {
+  if (n_rows < 0 || D <= 0) return FC_ERR_ARG;
+  const int64_t n = n_rows * D;
+  if (n == 0) return FC_OK;
+  if (!codes || !scales || !out) return FC_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)((n + kThreads - 1) / kThreads));
+  const int rc = with_float_type(out_dtype, [&](auto to) {
+    using TO = decltype(to);
+    dequantize_rows_kernel<TO><<<grid, kThreads, 0, st>>>(codes, scales, n, D, (TO*)out);
+    return FC_OK;
+  });
+  return rc != FC_OK ? rc : check_launch();
+}
+
+int fc_png_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb, int64_t x_sh,
+                  int64_t x_ss, int64_t s_valid, int64_t m, int64_t D, int r, int keep_m,
+                  float* deltas, void* anchors, int64_t cap, int64_t n0, void* stream) {
+  if (B < 0 || H < 0 || m < 0 || D <= 0 || r < 2 || keep_m < 0) return FC_ERR_ARG;
+  if (n0 < 0 || n0 + m > cap) return FC_ERR_ARG;
+  const int64_t items = B * H * m;
+  if (items == 0) return FC_OK;
+  if (!x || !deltas || !anchors) return FC_ERR_ARG;
+  if (r > FC_MAX_BLOCK || D > FC_MAX_HEAD_DIM) return FC_ERR_UNSUPPORTED;
+  const int es = esize_of(x_dtype);
+  if (!es || x_dtype == FC_I8) return FC_ERR_ARG;
+  // register-resident block bucket; rmax*vec <= 64 floats per lane
+  const int rmax = r <= 8 ? 8 : (r <= 16 ? 16 : (r <= 32 ? 32 : 64));
+  const int max_vec = rmax == 8 ? 8 : (rmax == 16 ? 4 : 1);
+  const int vec =
+      pick_vec(D, max_vec, {x_sb, x_sh, x_ss}, {{x, es}, {anchors, es}, {deltas, 4}});
+  if (!vec) return FC_ERR_UNSUPPORTED;
+  const int lg = log2_lanes(D, vec);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = grid_for(items, lg);
+  const int rc = with_float_type(x_dtype, [&](auto tv) {
+    using T = decltype(tv);
+    return with_int<1, 4, 8>(vec, [&](auto vc) {
+      constexpr int VEC = decltype(vc)::value;
+      return with_int<8, 16, 32, 64>(rmax, [&](auto rc_) {
+        constexpr int RMAX = decltype(rc_)::value;
+        if constexpr (RMAX * VEC <= 64) {
+          png_encode_kernel<T, VEC, RMAX><<<grid, kThreads, 0, st>>>(
+              (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, keep_m, deltas, (T*)anchors,
+              cap, n0, items, lg);
+          return FC_OK;
+        } else {
+          return FC_ERR_UNSUPPORTED;
+        }
+      });
+    });
+  });
+  return rc != FC_OK ? rc : check_launch();
+}
+
+int fc_png_decode(const float* deltas, const void* anchors, int anchor_dtype, int64_t B,
+                  int64_t H, int64_t cap, int64_t a, int64_t nblk, int64_t D, int r, void* out,
+                  int64_t o_sb, int64_t o_sh, int64_t o_ss, int64_t out_len, void* stream) {
+  if (B < 0 || H < 0 || a < 0 || nblk < 0 || a + nblk > cap || D <= 0 || r < 2)
+    return FC_ERR_ARG;
+  const int64_t items = B * H * nblk;
+  if (items == 0) return FC_OK;
+  if (!deltas || !anchors || !out) return FC_ERR_ARG;
+  if (r > FC_MAX_BLOCK || D > FC_MAX_HEAD_DIM) return FC_ERR_UNSUPPORTED;
+  const int es = esize_of(anchor_dtype);
+  if (!es || anchor_dtype == FC_I8) return FC_ERR_ARG;
+  const int vec =
+      pick_vec(D, 8, {o_sb, o_sh, o_ss}, {{anchors, es}, {out, es}, {deltas, 4}});
+  if (!vec) return FC_ERR_UNSUPPORTED;
+  const int lg = log2_lanes(D, vec);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = grid_for(items, lg);
+  const int rc = with_float_type(anchor_dtype, [&](auto tv) {
+    using T = decltype(tv);
+    return with_int<1, 4, 8>(vec, [&](auto vc) {
+      constexpr int VEC = decltype(vc)::value;
+      png_decode_kernel<T, VEC><<<grid, kThreads, 0, st>>>(
+          deltas, (const T*)anchors, H, cap, a, nblk, D, r, (T*)out, o_sb, o_sh, o_ss, out_len,
+          items, lg);
+      return FC_OK;
+    });
+  });
+  return rc != FC_OK ? rc : check_launch();
+}
+
+// Host restatement hook: the Top-M keep mask the png kernel computes for
+// one column of n <= 63 deltas (same source as the device path).  Lets the
+// CPU tests check the selection without a GPU.
+uint64_t fc_png_topm_mask_host(const float* delta, int n, int keep_m) {
+  const int m = keep_m;
+  if (n <= 0 || n > 63 || m <= 0) return 0;
+  if (m >= n) return n == 64 ? ~0ull : ((uint64_t)1 << n) - 1;
+  uint32_t keys[64];
+  for (int i = 0; i < n; ++i) {
+    uint32_t bits;
+    __builtin_memcpy(&bits, &delta[i], 4);
+    keys[i] = topm_key(bits);
+  }
+  return topm_mask_exact(keys, n, m);
+}
+
+}  // extern "C"

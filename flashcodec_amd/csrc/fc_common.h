@@ -1,0 +1,99 @@
+// Shared device helpers for the flashcodec_amd kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "flashcodec_amd.h"
+
+namespace fc {
+
+// bf16 storage word. Arithmetic always happens in fp32.
+struct bf16_t {
+  uint16_t bits;
+};
+typedef _Float16 f16_t;
+
+template <typename T>
+struct dtype_code;
+template <>
+struct dtype_code<float> {
+  static constexpr int value = FC_F32;
+};
+template <>
+struct dtype_code<f16_t> {
+  static constexpr int value = FC_F16;
+};
+template <>
+struct dtype_code<bf16_t> {
+  static constexpr int value = FC_BF16;
+};
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16_t x) {
+  return __uint_as_float((uint32_t)x.bits << 16);
+}
+__device__ __forceinline__ float to_f32(int8_t x) { return (float)(int)x; }
+
+// Round-to-nearest-even conversions from fp32 (the rounding torch's CPU
+// casts perform; bf16 NaN becomes the canonical 0x7FC0 like c10::BFloat16).
+template <typename T>
+__device__ __forceinline__ T from_f32(float f);
+template <>
+__device__ __forceinline__ float from_f32<float>(float f) {
+  return f;
+}
+template <>
+__device__ __forceinline__ f16_t from_f32<f16_t>(float f) {
+  return (f16_t)f;
+}
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t{0x7fc0};
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bf16_t{(uint16_t)(u >> 16)};
+}
+
+// Vector of N elements of T moved as one aligned memory operation.
+template <typename T, int N>
+struct alignas(sizeof(T) * N) vec_t {
+  T v[N];
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&out)[N]) {
+  vec_t<T, N> t = *reinterpret_cast<const vec_t<T, N>*>(p);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = to_f32(t.v[i]);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float (&in)[N]) {
+  vec_t<T, N> t;
+#pragma unroll
+  for (int i = 0; i < N; ++i) t.v[i] = from_f32<T>(in[i]);
+  *reinterpret_cast<vec_t<T, N>*>(p) = t;
+}
+
+// Butterfly reductions over aligned groups of `width` lanes (power of two,
+// <= 64) inside a wavefront.
+template <int WIDTH>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int m = 1; m < WIDTH; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < WIDTH; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float group_max_rt(float v, int width) {
+  for (int m = 1; m < width; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+}  // namespace fc

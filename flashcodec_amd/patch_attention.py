@@ -1,0 +1,146 @@
+"""Route decode steps of Llama/Qwen-style attention through the
+coefficient-domain kernels (flashcodec/patch_attention.py:1-151).
+
+``apply_flash_codec`` swaps the cache, but transformers still attends on the
+reconstructed view.  This patch replaces the forward of standard attention
+modules (q_proj / k_proj / v_proj / o_proj, optional q_norm / k_norm, plain
+or gated query projection) so that a single-token decode step on a codec
+layer runs projection + norm + RoPE as usual, appends K/V to the codec
+streams and attends with ``codec_decode_attention`` — no (S, D) view.
+
+Guards (anything else calls the original forward): codec cache layer, eval
+mode, one query token, ``position_embeddings`` given, no sliding window, a
+RoPE function in the model's module, and either batch 1 or no attention mask
+(transformers passes no mask to SDPA-style attention when nothing is padded,
+so unpadded batched decoding takes the codec path too; the reference stops
+at batch 1, patch_attention.py:52).
+"""
+
+import importlib
+
+import torch
+
+from .attention import codec_decode_attention
+from .cache import FlashCodecLayer
+
+_ROPE_CACHE = {}
+
+
+def _rope_fn(module):
+    """``apply_rotary_pos_emb`` of the modeling file that defines the module."""
+    name = type(module).__module__
+    if name not in _ROPE_CACHE:
+        _ROPE_CACHE[name] = getattr(importlib.import_module(name), "apply_rotary_pos_emb", None)
+    return _ROPE_CACHE[name]
+
+
+def _codec_layer(module, past_key_values):
+    layers = getattr(past_key_values, "layers", None)
+    if layers is None:
+        return None
+    try:
+        layer = layers[module.layer_idx]
+    except (IndexError, TypeError):
+        return None
+    return layer if isinstance(layer, FlashCodecLayer) else None
+
+
+def _attention_forward(module, orig, hidden_states, position_embeddings=None,
+                       attention_mask=None, past_key_values=None, **kwargs):
+    layer = _codec_layer(module, past_key_values)
+    usable = (layer is not None
+              and not module.training
+              and hidden_states.shape[-2] == 1
+              and (hidden_states.shape[0] == 1 or attention_mask is None)
+              and position_embeddings is not None
+              and getattr(module, "sliding_window", None) is None
+              and _rope_fn(module) is not None)
+    if not usable:
+        return orig(hidden_states, position_embeddings=position_embeddings,
+                    attention_mask=attention_mask, past_key_values=past_key_values, **kwargs)
+
+    lead = hidden_states.shape[:-1]
+    hd = module.head_dim
+    width = module.o_proj.in_features
+    gated = module.q_proj.out_features == 2 * width      # Qwen3.5-style output gate
+    qp = module.q_proj(hidden_states)
+    gate = None
+    if gated:
+        q, gate = torch.chunk(qp.view(*lead, -1, 2 * hd), 2, dim=-1)
+        gate = gate.reshape(*lead, -1)
+    else:
+        q = qp
+    q = q.view(*lead, -1, hd)
+    k = module.k_proj(hidden_states).view(*lead, -1, hd)
+    v = module.v_proj(hidden_states).view(*lead, -1, hd).transpose(1, 2)
+    if hasattr(module, "q_norm"):
+        q = module.q_norm(q)
+    if hasattr(module, "k_norm"):
+        k = module.k_norm(k)
+    q, k = q.transpose(1, 2), k.transpose(1, 2)
+    cos, sin = position_embeddings
+    q, k = _rope_fn(module)(q, k, cos, sin)
+
+    if not layer.is_initialized:
+        layer.lazy_initialization(k, v)
+    # the prefill view is dead weight once decoding attends on the archive
+    for st in (layer._key_stream, layer._value_stream):
+        if st._rec is not None:
+            st.discard_view()
+    layer.keys = layer.values = None
+    layer._key_stream.append(k)
+    layer._value_stream.append(v)
+    out = codec_decode_attention(q, layer._key_stream, layer._value_stream,
+                                 scale=module.scaling)
+    out = out.transpose(1, 2).reshape(*lead, -1).contiguous()
+    if gated:
+        out = out * torch.sigmoid(gate)
+    module._flashcodec_codec_steps = getattr(module, "_flashcodec_codec_steps", 0) + 1
+    return module.o_proj(out), None
+
+
+def _supported(module):
+    if not all(hasattr(module, a) for a in
+               ("q_proj", "k_proj", "v_proj", "o_proj", "layer_idx", "head_dim")):
+        return False
+    width = module.o_proj.in_features
+    if module.head_dim <= 0 or width % module.head_dim:
+        return False
+    return module.q_proj.out_features in (width, 2 * width)
+
+
+def apply_codec_attention(model):
+    """Patch every supported attention module; idempotent.  Returns the
+    number of wrapped modules."""
+    wrapped = 0
+    for module in model.modules():
+        if not _supported(module):
+            continue
+        if getattr(module, "_flashcodec_orig_forward", None) is None:
+            orig = module.forward
+
+            def forward(*args, _module=module, _orig=orig, **kw):
+                return _attention_forward(_module, _orig, *args, **kw)
+
+            module._flashcodec_orig_forward = orig
+            module.forward = forward
+        wrapped += 1
+    return wrapped
+
+
+def remove_codec_attention(model):
+    """Restore the original forwards; returns how many were restored."""
+    restored = 0
+    for module in model.modules():
+        orig = getattr(module, "_flashcodec_orig_forward", None)
+        if orig is not None:
+            module.forward = orig
+            del module._flashcodec_orig_forward
+            restored += 1
+    return restored
+
+
+def codec_attention_stats(model):
+    """Number of attention modules currently wrapped."""
+    return sum(1 for m in model.modules()
+               if getattr(m, "_flashcodec_orig_forward", None) is not None)

@@ -1,0 +1,238 @@
+/*
+ * flashcodec_amd — C ABI of the MI355X (gfx950) KV-codec hot path.
+ *
+ * Every entry point is stateless apart from the basis/launch configuration
+ * the caller passes in, takes raw device pointers, element strides and
+ * sizes, enqueues its kernels on the given HIP stream (`stream` is a
+ * hipStream_t; NULL = the default stream) and returns an int status:
+ * FC_OK (0) or one of the negative FC_ERR_* codes below.  Nothing here
+ * allocates device memory, synchronises the stream or throws.
+ *
+ * Layout conventions (all element strides, innermost dimension D is
+ * contiguous, i.e. stride 1):
+ *   sequence input  x[b][h][t][d]      at x + b*x_sb + h*x_sh + t*x_ss + d
+ *   coefficient store   (B*H, cap, k, D)   contiguous (jpeg)
+ *   scale store         (B*H, cap, k)      contiguous fp32 (jpeg int8)
+ *   delta store         (B*H, cap, r-1, D) contiguous fp32 (png)
+ *   anchor store        (B*H, cap, D)      contiguous, stream dtype (png)
+ * which are exactly the reference buffers `_coeffs`, `_scales`, `_deltas`,
+ * `_anchors` of flashcodec/cache.py:94-104 (the trailing size-1 axis of
+ * `_scales` is dropped because it has no extent).
+ *
+ * dtype codes: FC_F32, FC_F16, FC_BF16 for floating tensors, FC_I8 for int8.
+ */
+#ifndef FLASHCODEC_AMD_H
+#define FLASHCODEC_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FC_F32 = 0,
+  FC_F16 = 1,
+  FC_BF16 = 2,
+  FC_I8 = 3
+};
+
+enum {
+  FC_OK = 0,
+  FC_ERR_ARG = -1,         /* invalid argument (shape, dtype, pointer)       */
+  FC_ERR_UNSUPPORTED = -2, /* valid but outside this build's kernel limits   */
+  FC_ERR_HIP = -3          /* a HIP runtime call failed (see fc_last_hip_error) */
+};
+
+/* Limits of the kernels in this library. */
+#define FC_MAX_BLOCK 64    /* block size r (tokens per archived block)    */
+#define FC_MAX_HEAD_DIM 512
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int fc_version(void);
+
+/* Human-readable text for a status code. */
+const char* fc_status_string(int status);
+
+/* hipError_t of the last failing HIP call in this thread (0 if none). */
+int fc_last_hip_error(void);
+
+/*
+ * JPEG-mode archive: blockwise orthonormal DCT-II along the token axis, keep
+ * the lowest k frequencies, optionally quantise them to int8 with one fp32
+ * scale per (block, frequency).
+ *
+ * Encodes m blocks of r tokens for each of the B*H sequences of x (tokens
+ * t >= s_valid are treated as zeros, which is the reference's zero padding)
+ * and writes them at block offset n0 of a store with capacity `cap` blocks.
+ * quant_bits == 0: `coeffs` has x's dtype.  quant_bits == 8: `coeffs` is
+ * int8 and `scales` receives the fp32 scales.  `basis` is the k x r fp32
+ * DCT-II matrix (row-major, device memory).
+ *
+ * Replaces dct_compress + quantize_coeffs + the in-place slice copies of
+ * _CodecStream._archive (flashcodec/codecs/jpeg.py:55-67, 85-100;
+ * flashcodec/cache.py:123-136), and dct_compress alone when quant_bits == 0.
+ */
+int fc_jpeg_encode(const void* x, int x_dtype, int64_t B, int64_t H,
+                   int64_t x_sb, int64_t x_sh, int64_t x_ss, int64_t s_valid,
+                   int64_t m, int64_t D, int r, int k, const float* basis,
+                   void* coeffs, float* scales, int64_t cap, int64_t n0,
+                   int quant_bits, void* stream);
+
+/*
+ * JPEG-mode reconstruction of blocks [a, a+nblk) of every sequence of a
+ * store (dtype store_dtype: FC_I8 with `scales`, or a float dtype with
+ * scales == NULL) into out[b][h][t][d] (dtype out_dtype, element strides
+ * o_sb, o_sh, o_ss), token t = block*r + row.  Tokens t >= out_len are not
+ * written (the reference's out_len trim).
+ *
+ * Replaces dequantize_coeffs + dct_decompress and the copy into the
+ * memoised view of _CodecStream._decode_pending
+ * (flashcodec/codecs/jpeg.py:70-82, 103-105; flashcodec/cache.py:182-192).
+ */
+int fc_jpeg_decode(const void* store, int store_dtype, const float* scales,
+                   int64_t B, int64_t H, int64_t cap, int64_t a, int64_t nblk,
+                   int64_t D, int r, int k, const float* basis, void* out,
+                   int out_dtype, int64_t o_sb, int64_t o_sh, int64_t o_ss,
+                   int64_t out_len, void* stream);
+
+/*
+ * Symmetric int8 quantisation of coefficient rows: n_rows rows of D values
+ * (dtype c_dtype, row stride c_rs elements) -> int8 codes (contiguous
+ * rows of D) and one fp32 scale per row.
+ * Replaces quantize_coeffs (flashcodec/codecs/jpeg.py:85-100).
+ */
+int fc_quantize_rows(const void* c, int c_dtype, int64_t n_rows, int64_t c_rs,
+                     int64_t D, int8_t* codes, float* scales, void* stream);
+
+/*
+ * Dequantisation q.to(dtype) * scale.to(dtype): n_rows rows of D int8
+ * codes with one fp32 scale per row -> out (dtype out_dtype, contiguous).
+ * Replaces dequantize_coeffs (flashcodec/codecs/jpeg.py:103-105).
+ */
+int fc_dequantize_rows(const int8_t* codes, const float* scales, int64_t n_rows,
+                       int64_t D, void* out, int out_dtype, void* stream);
+
+/*
+ * PNG-mode archive: per block an anchor (token 0, stored in x's dtype) and
+ * r-1 fp32 first-order deltas; when 0 < keep_m < r-1 only the keep_m
+ * largest |delta| per (block, feature) survive, the others are multiplied
+ * by 0 (sign kept).  Ties at the cut are resolved exactly as the
+ * reference's CPU topk resolves them.
+ * Replaces png_filter + the slice copies of _CodecStream._archive
+ * (flashcodec/codecs/png.py:36-60; flashcodec/cache.py:137-140).
+ */
+int fc_png_encode(const void* x, int x_dtype, int64_t B, int64_t H,
+                  int64_t x_sb, int64_t x_sh, int64_t x_ss, int64_t s_valid,
+                  int64_t m, int64_t D, int r, int keep_m, float* deltas,
+                  void* anchors, int64_t cap, int64_t n0, void* stream);
+
+/*
+ * PNG-mode reconstruction (anchor + running sum of deltas) of blocks
+ * [a, a+nblk) into out (anchor dtype), as fc_jpeg_decode.
+ * Replaces png_reconstruct + the view copy (flashcodec/codecs/png.py:63-74;
+ * flashcodec/cache.py:189-192).
+ */
+int fc_png_decode(const float* deltas, const void* anchors, int anchor_dtype,
+                  int64_t B, int64_t H, int64_t cap, int64_t a, int64_t nblk,
+                  int64_t D, int r, void* out, int64_t o_sb, int64_t o_sh,
+                  int64_t o_ss, int64_t out_len, void* stream);
+
+/*
+ * Host-side (CPU) evaluation of the exact tie-aware Top-M rule the png
+ * kernel applies to one (block, feature) column: bit i of the result is set
+ * when step i of the n (<= 63) deltas survives keep_m.  Same source as the
+ * kernel's tie path; exported so the selection can be checked without a
+ * GPU.  Restates the topk selection of flashcodec/codecs/png.py:54-58.
+ */
+uint64_t fc_png_topm_mask_host(const float* delta, int n, int keep_m);
+
+/* Archive kind of a stream for fc_decode_attention. */
+enum {
+  FC_STORE_JPEG_I8 = 0,  /* rows: int8 coeffs x fp32 scale, s = k      */
+  FC_STORE_JPEG_FP = 1,  /* rows: coeffs in the stream dtype, s = k    */
+  FC_STORE_PNG = 2       /* rows: anchor (stream dtype) + r-1 fp32 deltas, s = r */
+};
+
+/* One KV stream as seen by the decode attention. */
+typedef struct fc_stream_view {
+  const void* rows;      /* jpeg: coeffs (B*H, cap, k, D); png: deltas (B*H, cap, r-1, D) */
+  const float* scales;   /* jpeg int8: (B*H, cap, k); else NULL */
+  const void* anchors;   /* png: (B*H, cap, D); else NULL */
+  int64_t cap;           /* capacity of the store in blocks */
+  const void* raw;       /* raw tail (B, H, n_raw, D) in the stream dtype, or NULL */
+  int64_t raw_sb, raw_sh, raw_st; /* element strides of the raw tail */
+} fc_stream_view;
+
+/*
+ * Bytes of device workspace fc_decode_attention needs for B*Hq query heads,
+ * head size D and n_splits splits (0 when n_splits == 0).
+ */
+int64_t fc_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t D,
+                                     int n_splits);
+
+/*
+ * Split count the library would choose for nb archived blocks spread over
+ * B*Hkv kv heads with G query heads each on a device with n_cu compute
+ * units (>= 1 whenever nb > 0; 0 when nb == 0).
+ */
+int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G,
+                                 int n_cu);
+
+/*
+ * Materialisation-free decode attention of one query token per sequence:
+ *   q (B, Hq, 1, D) in q_dtype with element strides q_sb, q_sh
+ *   K/V archives of nb blocks with s stored rows each, synthesis matrix
+ *   A (r x s, fp32 row-major, device) and raw tails of n_raw tokens,
+ *   out (B, Hq, 1, D) in q_dtype with element strides o_sb, o_sh.
+ * Query head hq reads kv head hq / G (G = Hq / Hkv).  Scores are
+ * scale * q . (A S)[p]; softmax in fp32; output (p A) S + p_raw V_raw.
+ * Every query head reads its kv head's rows once per group of up to eight
+ * query heads.  `workspace` must hold fc_attention_workspace_bytes(...).
+ *
+ * Replaces codec_decode_attention's jpeg Triton path and its png / torch
+ * path (flashcodec/attention.py:64-140;
+ * flashcodec/triton_attention.py:34-222).
+ */
+int fc_decode_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                        int store_kind, int stream_dtype, int r, int s,
+                        int64_t nb, const fc_stream_view* key,
+                        const fc_stream_view* value, int64_t n_raw,
+                        const float* A, float scale, void* out, int64_t o_sb,
+                        int64_t o_sh, void* workspace, int n_splits,
+                        void* stream);
+
+/*
+ * The two passes of fc_decode_attention as separate entry points (same
+ * arguments): _split enqueues the pass over the archived blocks that fills
+ * the workspace partials, _merge the pass that combines them with the raw
+ * tail into `out`.  Calling _split then _merge on one stream equals
+ * fc_decode_attention; callers use them to time or overlap the passes.
+ * No reference counterpart (the Triton path launches its split and combine
+ * kernels back to back, flashcodec/triton_attention.py:199-221).
+ */
+int fc_decode_attention_split(const void* q, int q_dtype, int64_t q_sb,
+                              int64_t q_sh, int64_t B, int64_t Hq, int64_t Hkv,
+                              int64_t D, int store_kind, int stream_dtype,
+                              int r, int s, int64_t nb,
+                              const fc_stream_view* key,
+                              const fc_stream_view* value, int64_t n_raw,
+                              const float* A, float scale, void* out,
+                              int64_t o_sb, int64_t o_sh, void* workspace,
+                              int n_splits, void* stream);
+int fc_decode_attention_merge(const void* q, int q_dtype, int64_t q_sb,
+                              int64_t q_sh, int64_t B, int64_t Hq, int64_t Hkv,
+                              int64_t D, int store_kind, int stream_dtype,
+                              int r, int s, int64_t nb,
+                              const fc_stream_view* key,
+                              const fc_stream_view* value, int64_t n_raw,
+                              const float* A, float scale, void* out,
+                              int64_t o_sb, int64_t o_sh, void* workspace,
+                              int n_splits, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHCODEC_AMD_H */

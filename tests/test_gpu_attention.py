@@ -1,0 +1,214 @@
+"""GPU: materialisation-free decode attention against the fp64 oracle, the
+reference's torch-path outputs (golden) and dense attention on the
+reconstructed view.
+
+Tolerances (the contract's): fp32 outputs within 1e-5 absolute; fp16 / bf16
+outputs within 2e-3 * max|ref| plus half an ulp of the output dtype at each
+element (the final rounding the output dtype forces).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import flashcodec_amd as fc
+from flashcodec_amd.cache import _CodecStream
+from tests.conftest import Golden, seed_of, to_torch, to_values, torch_dtype
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+HALF_ULP = {"f16": 2.0 ** -11, "bf16": 2.0 ** -8}
+
+
+def assert_close(out, ref, dt):
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(out - ref)
+    if dt == "f32":
+        assert err.max() <= 1e-5, f"max abs err {err.max():.3e}"
+    else:
+        tol = 2e-3 * np.abs(ref).max() + HALF_ULP[dt] * np.abs(ref)
+        bad = err > tol
+        assert not bad.any(), f"{bad.sum()} elements out of tolerance; max err {err.max():.3e}"
+
+
+def stream_rows(oracle, st):
+    """fp64 stored rows of a stream, read from its device buffers."""
+    n = st.n_blocks
+    if st.codec.name == "jpeg":
+        c = st._coeffs[:, :, :n].float().cpu().numpy()
+        if st.codec.quantized:
+            return oracle.stored_rows_jpeg(c, st._scales[:, :, :n, :, 0].cpu().numpy())
+        return oracle.stored_rows_jpeg(c)
+    return oracle.stored_rows_png(st._deltas[:, :, :n].cpu().numpy(),
+                                  st._anchors[:, :, :n].float().cpu().numpy())
+
+
+def oracle_out(oracle, q, ks, vs, scale):
+    c = ks.codec
+    r = ks.block_size
+    if c.name == "jpeg":
+        A = oracle.synthesis_matrix("jpeg", r, fc.dct_basis(r, c.keep_freqs).numpy())
+    else:
+        A = oracle.synthesis_matrix("png", r)
+    if ks.n_blocks:
+        rk, rv = stream_rows(oracle, ks), stream_rows(oracle, vs)
+    else:
+        Bq, Hk, D = q.shape[0], (ks.raw.shape[1]), q.shape[-1]
+        s = c.keep_freqs if c.name == "jpeg" else r
+        rk = rv = np.zeros((Bq, Hk, 0, s, D))
+    zk = None if ks.raw is None else to_values(ks.raw)
+    zv = None if vs.raw is None else to_values(vs.raw)
+    return oracle.attention(to_values(q)[:, :, 0], rk, rv, zk, zv, A, scale, n_threads=8)
+
+
+def build_streams(cfg, dt, B, Hk, S, D, seed, oracle, feed="bulk"):
+    rng = np.random.default_rng(seed)
+    sc = np.exp(rng.uniform(-1, 1, (B, Hk, 1, D))).astype(np.float32)
+    k = torch.from_numpy(oracle.ar1((B, Hk, S, D), 0.95, seed) * sc).to(torch_dtype(dt)).to(DEV)
+    v = torch.from_numpy(oracle.ar1((B, Hk, S, D), 0.95, seed + 1)).to(torch_dtype(dt)).to(DEV)
+    ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
+    if feed == "bulk":
+        ks.append(k)
+        vs.append(v)
+    else:
+        for t in range(0, S, feed):
+            ks.append(k[..., t:t + feed, :])
+            vs.append(v[..., t:t + feed, :])
+    return ks, vs
+
+
+CASES = [
+    # name, cfg, dtype, B, Hk, G, S, D
+    ("jpeg-i8-f16-g4", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16", 2, 4, 4, 8 * 200 + 5, 128),
+    ("jpeg-i8-bf16-g8", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "bf16", 1, 2, 8, 8 * 100 + 7, 64),
+    ("jpeg-i8-f32-g1", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8), "f32", 2, 3, 1, 8 * 50 + 3, 32),
+    ("jpeg-fp-f32-k8-g2", dict(mode="jpeg", block_size=8, keep_freqs=8), "f32", 1, 2, 2, 8 * 64, 128),
+    ("jpeg-fp-f16-k16-g3", dict(mode="jpeg", block_size=16, keep_freqs=16), "f16", 1, 2, 3, 16 * 20 + 9, 64),
+    ("jpeg-fp-bf16-g16", dict(mode="jpeg", block_size=8, keep_freqs=2), "bf16", 1, 1, 16, 8 * 40 + 1, 128),
+    ("png-f32-k1-g4", dict(mode="png", block_size=8, keep_ratio=1.0), "f32", 2, 2, 4, 8 * 30 + 6, 128),
+    ("png-bf16-k05-g2", dict(mode="png", block_size=16, keep_ratio=0.5), "bf16", 1, 2, 2, 16 * 25 + 11, 64),
+    ("png-f16-r4-g5", dict(mode="png", block_size=4, keep_ratio=1.0), "f16", 2, 1, 5, 4 * 40 + 2, 16),
+    ("jpeg-i8-f16-d256", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16", 1, 2, 4, 8 * 64 + 4, 256),
+    ("jpeg-i8-bf16-d512", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8), "bf16", 1, 1, 2, 8 * 16 + 2, 512),
+    ("jpeg-i8-f16-tail-only", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16", 2, 2, 4, 5, 128),
+    ("jpeg-i8-f32-no-tail", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f32", 1, 2, 4, 8 * 33, 64),
+    ("jpeg-i8-f16-32k", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16", 1, 2, 4, 8 * 4096 + 5, 128),
+    ("jpeg-i8-f32-r16-d40", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8), "f32", 1, 2, 2, 16 * 9 + 4, 40),
+]
+
+
+@pytest.mark.parametrize("name,cfg,dt,B,Hk,G,S,D", CASES, ids=[c[0] for c in CASES])
+def test_decode_attention_matches_oracle(name, cfg, dt, B, Hk, G, S, D, oracle):
+    print(f"case attention/{name}", flush=True)
+    seed = seed_of(name)
+    ks, vs = build_streams(cfg, dt, B, Hk, S, D, seed % 10000, oracle)
+    rng = np.random.default_rng(seed)
+    q = torch.from_numpy((rng.standard_normal((B, Hk * G, 1, D)) / math.sqrt(D))
+                         .astype(np.float32)).to(torch_dtype(dt)).to(DEV)
+    out = fc.codec_decode_attention(q, ks, vs)
+    assert out.shape == q.shape and out.dtype == q.dtype
+    assert ks._rec is None and vs._rec is None
+    ref = oracle_out(oracle, q, ks, vs, D ** -0.5)
+    assert_close(to_values(out)[:, :, 0], ref, dt)
+
+
+@pytest.mark.parametrize("name", Golden("attention").names())
+def test_decode_attention_matches_reference_torch_path(name, oracle):
+    G = Golden("attention")
+    c, m = G.case(name), G.meta[name]
+    dt = m["dtype"]
+    print(f"case attention-golden/{name}", flush=True)
+    k, v, q = to_torch(c["k"], dt), to_torch(c["v"], dt), to_torch(c["q"], dt)
+    ks, vs = _CodecStream(fc.make_codec(**m["cfg"])), _CodecStream(fc.make_codec(**m["cfg"]))
+    ks.append(k)
+    vs.append(v)
+    out = to_values(fc.codec_decode_attention(q, ks, vs))[:, :, 0]
+    ref_torch = oracle.values_of(c["out"], dt)[:, :, 0]
+    ref = oracle_out(oracle, q, ks, vs, m["D"] ** -0.5)
+    assert_close(out, ref, dt)
+    # and the reference's own path, whose half-precision einsums carry more error
+    tol = 1e-5 if dt == "f32" else 4e-3 * np.abs(ref_torch).max()
+    assert np.abs(out - ref_torch).max() <= tol
+
+
+MODES = [("jpeg", dict(keep_freqs=2)), ("jpeg", dict(keep_freqs=8)),
+         ("jpeg", dict(keep_freqs=2, quant_bits=8)), ("png", dict(keep_ratio=1.0)),
+         ("png", dict(keep_ratio=0.5))]
+
+
+def test_matches_materialized_attention():
+    """Coefficient path == softmax(q K^T) V on the reconstructed view (fp32),
+    the reference's tests/test_attention.py:43-53."""
+    torch.manual_seed(0)
+    B, Hk, S, D = 2, 4, 96, 32
+    k_seq = torch.cumsum(torch.randn(B, Hk, S, D, device=DEV) * 0.1, dim=-2)
+    v_seq = torch.cumsum(torch.randn(B, Hk, S, D, device=DEV) * 0.1, dim=-2)
+    for g in (1, 2):
+        q = torch.randn(B, Hk * g, 1, D, device=DEV)
+        for mode, kw in MODES:
+            cache = fc.CodecKVCache(mode=mode, block_size=8, **kw)
+            cache.forward(k_seq, v_seq)
+            out = fc.codec_decode_attention(q, cache._keys[0], cache._values[0])
+            kr = cache.key_cache[0].repeat_interleave(g, dim=1)
+            vr = cache.value_cache[0].repeat_interleave(g, dim=1)
+            p = torch.softmax(q @ kr.transpose(-2, -1) / math.sqrt(D), dim=-1)
+            ref = p @ vr
+            assert (out - ref).abs().max().item() < 1e-5, (mode, kw, g)
+
+
+def test_no_materialization_and_stream_untouched():
+    torch.manual_seed(0)
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8)
+    ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
+    ks.append(torch.randn(2, 4, 99, 32, device=DEV))
+    vs.append(torch.randn(2, 4, 99, 32, device=DEV))
+    before = [t.clone() for t in ks._archive_tensors()]
+    n, L = ks.n_blocks, ks.seq_len
+    out = fc.codec_decode_attention(torch.randn(2, 4, 1, 32, device=DEV), ks, vs)
+    assert ks._rec is None and vs._rec is None
+    assert ks.n_blocks == n and ks.seq_len == L
+    assert all(torch.equal(a, b) for a, b in zip(ks._archive_tensors(), before))
+    assert torch.isfinite(out).all()
+
+
+def test_empty_cache_prefill_guard_and_layouts(oracle):
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=2)
+    ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
+    q = torch.randn(2, 4, 1, 32, device=DEV)
+    assert torch.equal(fc.codec_decode_attention(q, ks, vs), torch.zeros_like(q))
+    ks.append(torch.randn(2, 4, 40, 32, device=DEV))
+    vs.append(torch.randn(2, 4, 40, 32, device=DEV))
+    with pytest.raises(ValueError):
+        fc.codec_decode_attention(torch.randn(2, 4, 4, 32, device=DEV), ks, vs)
+    # a query that is a strided view (heads innermost-but-one, like HF's
+    # transpose of (B, 1, Hq, D)) and a query dtype other than the stream's
+    qt = torch.randn(2, 1, 8, 32, device=DEV).transpose(1, 2)
+    assert not qt.is_contiguous()
+    ref = fc.codec_decode_attention(qt.contiguous(), ks, vs)
+    assert torch.equal(fc.codec_decode_attention(qt, ks, vs), ref)
+    q16 = qt.to(torch.float16)
+    o16 = fc.codec_decode_attention(q16, ks, vs)
+    assert o16.dtype == torch.float16
+    ref16 = oracle_out(oracle, q16, ks, vs, 32 ** -0.5)
+    assert_close(to_values(o16)[:, :, 0], ref16, "f16")
+
+
+def test_incremental_decode_tracks_oracle(oracle):
+    """Token-by-token appends with an attention call after each step (raw tail
+    lengths 0..7 and every archive boundary)."""
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+    B, Hk, G, D, S = 1, 2, 4, 64, 8 * 5
+    ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
+    k = torch.from_numpy(oracle.ar1((B, Hk, S, D), 0.9, 5)).half().to(DEV)
+    v = torch.from_numpy(oracle.ar1((B, Hk, S, D), 0.9, 6)).half().to(DEV)
+    rng = np.random.default_rng(9)
+    for t in range(S):
+        ks.append(k[..., t:t + 1, :])
+        vs.append(v[..., t:t + 1, :])
+        q = torch.from_numpy(rng.standard_normal((B, Hk * G, 1, D)).astype(np.float32)
+                             / 8).half().to(DEV)
+        out = fc.codec_decode_attention(q, ks, vs)
+        assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "f16")

@@ -1,0 +1,171 @@
+"""GPU: archive / reconstruction kernels bit-exact against the reference's
+golden vectors and against the oracle on seeded inputs (dtypes, block sizes,
+feature widths, strides, padding, zero blocks, Top-M ties)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import flashcodec_amd as fc
+from tests.conftest import Golden, bits, seed_of, to_torch, to_values, torch_dtype
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("name", Golden("jpeg").names())
+def test_jpeg_kernels_match_reference_bits(name, oracle):
+    G = Golden("jpeg")
+    c, m = G.case(name), G.meta[name]
+    dt, r, k, S = m["dtype"], m["r"], m["k"], m["shape"][-2]
+    print(f"case jpeg/{name}", flush=True)
+    x = to_torch(c["x"], dt)
+    coef = fc.dct_compress(x, r, k)
+    assert coef.dtype == x.dtype
+    assert np.array_equal(bits(to_values(coef)), bits(oracle.values_of(c["coef"], dt)))
+    q, s = fc.quantize_coeffs(coef)
+    assert q.dtype == torch.int8 and s.shape == coef.shape[:-1] + (1,)
+    assert np.array_equal(q.cpu().numpy(), c["codes"])
+    assert np.array_equal(bits(s[..., 0].cpu().numpy()), bits(c["scales"]))
+    deq = fc.dequantize_coeffs(q, s)
+    assert np.array_equal(bits(deq.cpu().numpy()), bits(c["deq_f32"]))
+    deq_t = fc.dequantize_coeffs(q, s, torch_dtype(dt))
+    assert np.array_equal(bits(to_values(deq_t)), bits(oracle.values_of(c["deq_T"], dt)))
+    rec = fc.dct_decompress(coef, r, out_len=S)
+    assert rec.dtype == torch.float32 and rec.shape == x.shape
+    assert np.array_equal(bits(rec.cpu().numpy()), bits(c["rec"]))
+    codec = fc.JPEGCodec(block_size=r, keep_freqs=k, quant_bits=8)
+    rec_q = codec.decompress(q, out_len=S, scales=s)
+    assert np.array_equal(bits(rec_q.cpu().numpy()), bits(c["rec_q"]))
+
+
+@pytest.mark.parametrize("name", Golden("png").names())
+def test_png_kernels_match_reference_bits(name, oracle):
+    G = Golden("png")
+    c, m = G.case(name), G.meta[name]
+    dt, r, keep = m["dtype"], m["r"], m["keep"]
+    print(f"case png/{name}", flush=True)
+    x = to_torch(c["x"], dt)
+    d, a = fc.png_filter(x, r, keep)
+    assert d.dtype == torch.float32 and a.dtype == x.dtype
+    assert np.array_equal(bits(d.cpu().numpy()), bits(c["deltas"]))
+    assert np.array_equal(bits(to_values(a)), bits(oracle.values_of(c["anchors"], dt)))
+    rec = fc.png_reconstruct(d, a)
+    assert np.array_equal(bits(to_values(rec)), bits(oracle.values_of(c["rec"], dt)))
+
+
+JPEG_RANDOM = [
+    # dtype, r, k, (B, H, S, D)
+    ("f16", 8, 4, (4, 8, 256, 128)),
+    ("bf16", 8, 2, (2, 8, 203, 128)),
+    ("f32", 8, 8, (2, 4, 64, 256)),
+    ("f16", 16, 4, (1, 4, 160, 64)),
+    ("f32", 4, 3, (2, 2, 40, 36)),      # D % 8 != 0: 4-wide lanes
+    ("bf16", 8, 4, (1, 2, 64, 7)),      # odd D: scalar lanes
+    ("f16", 24, 5, (1, 2, 96, 48)),     # streaming path (r > 16)
+    ("f32", 64, 8, (1, 1, 130, 32)),    # largest block
+    ("bf16", 2, 1, (3, 1, 9, 512)),     # widest head
+]
+
+
+def _oracle_jpeg(oracle, x_vals, r, k, dt):
+    basis = fc.dct_basis(r, k).numpy()
+    return oracle.jpeg_encode(x_vals, r, k, basis, dt, quant=True), basis
+
+
+@pytest.mark.parametrize("dt,r,k,shape", JPEG_RANDOM)
+def test_jpeg_kernels_match_oracle(dt, r, k, shape, oracle):
+    print(f"case jpeg-random {dt} r={r} k={k} shape={shape}", flush=True)
+    rng = np.random.default_rng(seed_of(dt, r, k, shape))
+    xv = oracle.round_to(oracle.ar1(shape, 0.9, 1) * np.exp(rng.uniform(-3, 3, shape[:-2] + (1, shape[-1]))).astype(np.float32), dt)
+    x = torch.from_numpy(xv).to(torch_dtype(dt)).to(DEV)
+    (coef, codes, scales), basis = _oracle_jpeg(oracle, xv, r, k, dt)
+    got = fc.dct_compress(x, r, k)
+    assert np.array_equal(bits(to_values(got)), bits(coef))
+    q, s = fc.quantize_coeffs(got)
+    assert np.array_equal(q.cpu().numpy(), codes)
+    assert np.array_equal(bits(s[..., 0].cpu().numpy()), bits(scales))
+    S = shape[-2]
+    rec = fc.dct_decompress(got, r, out_len=S)
+    assert np.array_equal(bits(rec.cpu().numpy()), bits(oracle.jpeg_decode(coef, r, basis)[..., :S, :]))
+    # strided input: a transposed (B, S, H, D) buffer viewed as (B, H, S, D)
+    xt = x.transpose(1, 2).contiguous().transpose(1, 2)
+    assert not xt.is_contiguous()
+    assert torch.equal(fc.dct_compress(xt, r, k), got)
+
+
+PNG_RANDOM = [
+    ("f32", 16, 0.25, (2, 8, 512, 128), "ar1"),
+    ("f32", 16, 1.0, (2, 4, 256, 128), "ar1"),
+    ("bf16", 8, 0.5, (2, 4, 200, 64), "ties"),
+    ("f16", 16, 0.25, (1, 4, 256, 32), "ties"),
+    ("f32", 12, 0.3, (1, 2, 100, 40), "ties"),
+    ("f32", 32, 0.2, (1, 2, 128, 16), "ties"),
+    ("bf16", 64, 0.1, (1, 1, 192, 8), "ties"),
+    ("f32", 2, 0.5, (2, 2, 33, 24), "ar1"),
+    ("f16", 8, 0.25, (1, 2, 64, 5), "ties"),
+]
+
+
+@pytest.mark.parametrize("dt,r,keep,shape,kind", PNG_RANDOM)
+def test_png_kernels_match_oracle(dt, r, keep, shape, kind, oracle):
+    print(f"case png-random {dt} r={r} keep={keep} shape={shape} {kind}", flush=True)
+    rng = np.random.default_rng(seed_of(dt, r, keep, shape))
+    if kind == "ties":
+        xv = (rng.integers(-6, 7, shape) / 8.0).astype(np.float32)
+    else:
+        xv = oracle.ar1(shape, 0.98, 3)
+    xv = oracle.round_to(xv, dt)
+    x = torch.from_numpy(xv).to(torch_dtype(dt)).to(DEV)
+    d_ref, a_ref = oracle.png_encode(xv, r, keep)
+    d, a = fc.png_filter(x, r, keep)
+    assert np.array_equal(bits(d.cpu().numpy()), bits(d_ref))
+    assert np.array_equal(bits(to_values(a)), bits(a_ref))
+    rec = fc.png_reconstruct(d, a)
+    assert np.array_equal(bits(to_values(rec)), bits(oracle.png_decode(d_ref, a_ref, dt)))
+
+
+def test_png_bf16_lossless_and_pruning_counts():
+    torch.manual_seed(0)
+    x = torch.randn(2, 4, 64, 32, device=DEV).to(torch.bfloat16)
+    d, a = fc.png_filter(x, 8, 1.0)
+    assert torch.equal(fc.png_reconstruct(d, a)[..., :64, :], x)
+    xs = torch.cumsum(torch.randn(2, 4, 64, 32, device=DEV) * 0.1, dim=-2)
+    d, a = fc.png_filter(xs, 16, 0.25)
+    assert int((d != 0).sum(-2).max()) <= math.ceil(15 * 0.25)
+    err1 = (fc.png_reconstruct(*fc.png_filter(xs, 8, 1.0)) - xs).abs().mean()
+    err05 = (fc.png_reconstruct(*fc.png_filter(xs, 8, 0.5)) - xs).abs().mean()
+    assert err05 > err1
+
+
+def test_dct_autograd_and_shapes():
+    x = torch.randn(2, 3, 50, 16, device=DEV, requires_grad=True)
+    rec = fc.dct_decompress(fc.dct_compress(x, 8, 2), 8, out_len=50)
+    assert rec.shape == x.shape
+    rec.pow(2).mean().backward()
+    assert x.grad is not None and torch.isfinite(x.grad).all()
+    # gradient of the orthogonal projection P = M^T M (per block): dL/dx = P dL/drec
+    g = 2 * rec.detach() / rec.numel()
+    xp = torch.nn.functional.pad(g, (0, 0, 0, 6)).reshape(2, 3, 7, 8, 16)
+    M = fc.dct_basis(8, 2).to(DEV).double()
+    P = M.t() @ M
+    want = torch.einsum("ts,bhnsd->bhntd", P, xp.double()).reshape(2, 3, 56, 16)[..., :50, :]
+    assert torch.allclose(x.grad.double(), want, atol=1e-6)
+    flat = torch.randn(100, 16, device=DEV)
+    assert fc.dct_decompress(fc.dct_compress(flat, 8, 2), 8, 100).shape == flat.shape
+
+
+def test_jpeg_quality_properties():
+    torch.manual_seed(0)
+    B, H, S, D, R = 2, 4, 64, 32, 8
+    x = torch.randn(B, H, S, D, device=DEV)
+    assert (fc.dct_decompress(fc.dct_compress(x, R, R), R, S) - x).abs().max() < 1e-5
+    smooth = torch.cumsum(torch.randn(B, H, S, D, device=DEV) * 0.1, dim=-2)
+    rec = fc.dct_decompress(fc.dct_compress(smooth, R, 2), R, S)
+    cos = torch.nn.functional.cosine_similarity(rec.flatten(), smooth.flatten(), dim=0)
+    assert cos > 0.99
+    e2 = (fc.dct_decompress(fc.dct_compress(smooth, R, 2), R, S) - smooth).abs().mean()
+    e4 = (fc.dct_decompress(fc.dct_compress(smooth, R, 4), R, S) - smooth).abs().mean()
+    assert e4 < e2

@@ -1,0 +1,318 @@
+"""CPU: pin the oracle against the reference's golden vectors, the
+mathematics, and the library routines the reference runs on.
+
+Pinning map of oracle/oracle.py:
+  round_to / orc_round   -> torch's CPU casts (library routine)
+  dct basis bits         -> golden basis (reference dct_basis); closed form
+                            within 2 ulp; orthonormality
+  jpeg_encode (+quant)   -> golden dct_compress / quantize_coeffs bits;
+                            k = r lossless; |q| <= 127, error <= scale/2;
+                            zero block -> scale 1
+  jpeg_decode/dequantize -> golden dct_decompress / dequantize_coeffs bits
+  topk_keep              -> torch.topk on tie-heavy columns; golden png
+  png_encode/png_decode  -> golden png_filter / png_reconstruct bits;
+                            bf16 / f32 keep=1 lossless; kept count == m
+  stream (append/read)   -> golden _CodecStream archives, read() and crop
+  attention              -> golden torch-path outputs; dense attention on
+                            the golden reconstructed view
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+TORCH_DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+def _torch_values(storage, dtype):
+    if dtype == "bf16":
+        return torch.from_numpy(storage.view(np.int16).copy()).view(torch.bfloat16).float()
+    return torch.from_numpy(np.asarray(storage).copy()).float()
+
+
+# ---------------------------------------------------------------- rounding
+
+def test_rounding_matches_torch_casts(oracle):
+    rng = np.random.default_rng(0)
+    v = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10 ** rng.uniform(-9, 5, 20000),
+        np.float32([0.0, -0.0, 65504, 65519.9, 65520, 1e-8, 6e-8, 5.96e-8, 3e-8, 2.98e-8,
+                    1 + 2 ** -11, 1 + 3 * 2 ** -11, 1 + 2 ** -8, 1 + 3 * 2 ** -8, -1e30]),
+    ]).astype(np.float32)
+    t = torch.from_numpy(v)
+    for dt in ("f16", "bf16"):
+        ref = t.to(TORCH_DT[dt]).float().numpy()
+        with np.errstate(over="ignore"):
+            got = oracle.round_to(v, dt)
+        assert np.array_equal(_bits(got), _bits(ref)), dt
+        sample = v[::97]
+        c = np.float32([oracle.round_scalar_c(dt, f) for f in sample])
+        assert np.array_equal(_bits(c), _bits(ref[::97])), dt
+
+
+# ---------------------------------------------------------------- basis
+
+@pytest.mark.parametrize("r", [2, 4, 8, 12, 16, 32, 64])
+def test_basis_bits_match_reference(golden, r):
+    from flashcodec_amd import dct_basis
+    g = golden("basis").data[f"r{r}"]
+    mine = dct_basis(r, r).numpy()
+    assert np.array_equal(_bits(mine), _bits(g))
+    for k in (1, max(1, r // 2), r):
+        assert np.array_equal(_bits(dct_basis(r, k).numpy()), _bits(g[:k]))
+
+
+@pytest.mark.parametrize("r", [2, 4, 8, 12, 16, 32, 64])
+def test_basis_closed_form_and_orthonormal(golden, oracle, r):
+    g = golden("basis").data[f"r{r}"]
+    # same fp32 angle, correctly rounded cos: torch's cos is within an ulp
+    f32 = oracle.dct_basis_fp32_angle(r, r)
+    ulp = np.spacing(np.abs(f32)).astype(np.float64)
+    assert np.all(np.abs(g.astype(np.float64) - f32) <= 2 * ulp)
+    # and the table is the orthonormal DCT-II up to the fp32 angle error
+    # (which grows with r: the angle reaches ~pi * r)
+    exact = oracle.dct_basis_closed_form(r, r)
+    assert np.abs(g - exact).max() < 1e-7 * r
+    assert np.allclose(g.astype(np.float64) @ g.T, np.eye(r), atol=max(1e-6, 2e-7 * r))
+
+
+# ---------------------------------------------------------------- jpeg
+
+def _jpeg_cases():
+    from tests.conftest import Golden
+    return Golden("jpeg").names()
+
+
+@pytest.mark.parametrize("name", _jpeg_cases())
+def test_jpeg_oracle_matches_reference(golden, oracle, name):
+    G = golden("jpeg")
+    c, m = G.case(name), G.meta[name]
+    dt, r, k = m["dtype"], m["r"], m["k"]
+    basis = golden("basis").data[f"r{r}"][:k]
+    x = oracle.values_of(c["x"], dt)
+    coef, codes, scales = oracle.jpeg_encode(x, r, k, basis, dt, quant=True)
+    assert np.array_equal(_bits(coef), _bits(oracle.values_of(c["coef"], dt)))
+    assert np.array_equal(codes, c["codes"])
+    assert np.array_equal(_bits(scales), _bits(c["scales"]))
+    deq = oracle.dequantize(codes, scales, "f32")
+    assert np.array_equal(_bits(deq), _bits(c["deq_f32"]))
+    deq_t = oracle.dequantize(codes, scales, dt)
+    assert np.array_equal(_bits(deq_t), _bits(oracle.values_of(c["deq_T"], dt)))
+    S = m["shape"][-2]
+    rec = oracle.jpeg_decode(coef, r, basis, "f32")[..., :S, :]
+    assert np.array_equal(_bits(rec), _bits(c["rec"]))
+    rec_q = oracle.jpeg_decode(None, r, basis, "f32", codes=codes, scales=scales)[..., :S, :]
+    assert np.array_equal(_bits(rec_q), _bits(c["rec_q"]))
+
+
+def test_jpeg_closed_form_properties(golden, oracle):
+    rng = np.random.default_rng(3)
+    r = 8
+    basis = golden("basis").data["r8"]
+    x = rng.standard_normal((2, 3, 64, 32)).astype(np.float32)
+    # k == r is an orthonormal change of basis: lossless up to fp32 rounding
+    rec = oracle.jpeg_decode(oracle.jpeg_encode(x, r, r, basis, "f32"), r, basis, "f32")
+    assert np.abs(rec - x).max() < 1e-5
+    # quantiser bounds
+    coef, codes, scales = oracle.jpeg_encode(x, r, 2, basis[:2], "f32", quant=True)
+    assert np.abs(codes.astype(np.int32)).max() <= 127
+    err = np.abs(codes * scales[..., None] - coef)
+    assert np.all(err <= scales[..., None] / 2 * (1 + 1e-6))
+    # the largest |coefficient| of a row maps to +-127
+    assert np.all(np.abs(codes).max(-1) == 127)
+    # all-zero block: scale 1, codes 0
+    z = np.zeros((1, 1, 8, 16), np.float32)
+    _, zc, zs = oracle.jpeg_encode(z, r, 4, basis[:4], "f16", quant=True)
+    assert np.all(zs == 1.0) and np.all(zc == 0)
+    # a planted mistake (reversed tap order) is caught by the golden bits
+    G = golden("jpeg")
+    c, m = G.case("f32_r8k2"), G.meta["f32_r8k2"]
+    xg = oracle.values_of(c["x"], "f32")
+    flipped = oracle.jpeg_encode(xg[..., ::-1, :].copy(), 8, 2, basis[:2, ::-1].copy(), "f32")
+    assert not np.array_equal(_bits(flipped), _bits(c["coef"]))
+
+
+# ---------------------------------------------------------------- png
+
+def test_topk_keep_matches_torch_topk(oracle):
+    rng = np.random.default_rng(5)
+    for n in (3, 7, 15, 31, 63):
+        for m in sorted({1, 2, max(1, n // 4), n // 2, n - 1}):
+            for trial in range(60):
+                kind = trial % 3
+                if kind == 0:
+                    v = rng.integers(0, 3, n).astype(np.float32)
+                elif kind == 1:
+                    v = (rng.integers(0, 6, n) * 0.5).astype(np.float32)
+                else:
+                    v = np.abs(rng.standard_normal(n)).astype(np.float32)
+                col = torch.from_numpy(v).reshape(1, n, 1).repeat(1, 1, 2)
+                idx = col.topk(m, dim=-2).indices[0, :, 0].numpy()
+                ref = np.zeros(n, bool)
+                ref[idx] = True
+                assert np.array_equal(oracle.topk_keep(v, m), ref), (n, m, v)
+
+
+def _png_cases():
+    from tests.conftest import Golden
+    return Golden("png").names()
+
+
+@pytest.mark.parametrize("name", _png_cases())
+def test_png_oracle_matches_reference(golden, oracle, name):
+    G = golden("png")
+    c, m = G.case(name), G.meta[name]
+    dt, r, keep = m["dtype"], m["r"], m["keep"]
+    x = oracle.values_of(c["x"], dt)
+    d, a = oracle.png_encode(x, r, keep)
+    assert np.array_equal(_bits(d), _bits(c["deltas"]))          # includes -0.0 signs
+    assert np.array_equal(_bits(a), _bits(oracle.values_of(c["anchors"], dt)))
+    rec = oracle.png_decode(d, a, dt)
+    assert np.array_equal(_bits(rec), _bits(oracle.values_of(c["rec"], dt)))
+
+
+def test_png_closed_form_properties(oracle):
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((2, 2, 64, 32)).astype(np.float32)
+    # keep=1: bf16 round trip is bitwise (bf16 deltas are exact in fp32);
+    # fp32 is lossless up to the fp32 rounding of anchor + prefix sum
+    xb = oracle.round_to(x, "bf16")
+    d, a = oracle.png_encode(xb, 8, 1.0)
+    assert np.array_equal(_bits(oracle.png_decode(d, a, "bf16")), _bits(xb))
+    d, a = oracle.png_encode(x, 8, 1.0)
+    assert np.abs(oracle.png_decode(d, a, "f32") - x).max() < 1e-6
+    # Top-M on tie-free data keeps exactly the m largest |delta| per column
+    d, a = oracle.png_encode(x, 16, 0.25)
+    full, _ = oracle.png_encode(x, 16, 1.0)
+    m = math.ceil(15 * 0.25)
+    kept = d != 0
+    assert np.all(kept.sum(-2) == m)
+    order = np.argsort(-np.abs(full), axis=-2, kind="stable")[..., :m, :]
+    want = np.zeros_like(kept)
+    np.put_along_axis(want, order, True, axis=-2)
+    assert np.array_equal(kept, want)
+    assert np.array_equal(d[kept], full[kept])
+
+
+# ---------------------------------------------------------------- stream
+
+def _stream_cases():
+    from tests.conftest import Golden
+    return Golden("stream").names()
+
+
+@pytest.mark.parametrize("name", _stream_cases())
+def test_stream_archive_is_blockwise_encode(golden, oracle, name):
+    """_CodecStream.append (token by token, in chunks or in bulk) archives
+    exactly the blockwise encode of the complete blocks; read() is their
+    decode followed by the raw tail; crop(-5) is an exact truncation."""
+    G = golden("stream")
+    c, m = G.case(name), G.meta[name]
+    cfg, dt = m["cfg"], m["dtype"]
+    r = cfg["block_size"]
+    x = oracle.values_of(c["x"], dt)
+    S = x.shape[-2]
+    n = S // r
+    head = x[..., :n * r, :]
+    if cfg["mode"] == "jpeg":
+        k = cfg["keep_freqs"]
+        basis = golden("basis").data[f"r{r}"][:k]
+        if cfg.get("quant_bits"):
+            _, codes, scales = oracle.jpeg_encode(head, r, k, basis, dt, quant=True)
+            assert np.array_equal(codes, c["coeffs"])
+            assert np.array_equal(_bits(scales), _bits(c["scales"]))
+            rec = oracle.jpeg_decode(None, r, basis, dt, codes=codes, scales=scales)
+        else:
+            coef = oracle.jpeg_encode(head, r, k, basis, dt)
+            assert np.array_equal(_bits(coef), _bits(oracle.values_of(c["coeffs"], dt)))
+            rec = oracle.jpeg_decode(coef, r, basis, dt)
+    else:
+        d, a = oracle.png_encode(head, r, cfg["keep_ratio"])
+        assert np.array_equal(_bits(d), _bits(c["deltas"]))
+        assert np.array_equal(_bits(a), _bits(oracle.values_of(c["anchors"], dt)))
+        rec = oracle.png_decode(d, a, dt)
+    read = oracle.values_of(c["read"], dt)
+    assert np.array_equal(_bits(read[..., :n * r, :]), _bits(rec))
+    assert np.array_equal(_bits(read[..., n * r:, :]), _bits(x[..., n * r:, :]))
+    assert np.array_equal(_bits(oracle.values_of(c["read_crop5"], dt)), _bits(read[..., :-5, :]))
+
+
+# ---------------------------------------------------------------- attention
+
+def _attn_cases():
+    from tests.conftest import Golden
+    return Golden("attention").names()
+
+
+def oracle_attention_inputs(oracle, golden, c, m):
+    """Oracle archive rows + raw tails of a golden attention case."""
+    cfg, dt = m["cfg"], m["dtype"]
+    r = cfg["block_size"]
+    k = oracle.values_of(c["k"], dt)
+    v = oracle.values_of(c["v"], dt)
+    S = k.shape[-2]
+    n = S // r
+    rows = []
+    for x in (k, v):
+        head = x[..., :n * r, :]
+        if cfg["mode"] == "jpeg":
+            kk = cfg["keep_freqs"]
+            basis = golden("basis").data[f"r{r}"][:kk]
+            if cfg.get("quant_bits"):
+                _, codes, scales = oracle.jpeg_encode(head, r, kk, basis, dt, quant=True)
+                rows.append(oracle.stored_rows_jpeg(codes, scales))
+            else:
+                rows.append(oracle.stored_rows_jpeg(oracle.jpeg_encode(head, r, kk, basis, dt)))
+            A = oracle.synthesis_matrix("jpeg", r, basis)
+        else:
+            d, a = oracle.png_encode(head, r, cfg["keep_ratio"])
+            rows.append(oracle.stored_rows_png(d, a))
+            A = oracle.synthesis_matrix("png", r)
+    q = oracle.values_of(c["q"], dt)[:, :, 0]
+    raw_k = k[..., n * r:, :] if S > n * r else None
+    raw_v = v[..., n * r:, :] if S > n * r else None
+    return q, rows[0], rows[1], raw_k, raw_v, A
+
+
+@pytest.mark.parametrize("name", _attn_cases())
+def test_attention_oracle_matches_reference_torch_path(golden, oracle, name):
+    G = golden("attention")
+    c, m = G.case(name), G.meta[name]
+    q, rk, rv, zk, zv, A = oracle_attention_inputs(oracle, golden, c, m)
+    D = m["D"]
+    ref = oracle.values_of(c["out"], m["dtype"])[:, :, 0]
+    got = oracle.attention(q, rk, rv, zk, zv, A, D ** -0.5)
+    if m["dtype"] == "f32":
+        assert np.abs(got - ref).max() < 1e-5
+    else:
+        # the reference's torch path runs its einsums in the query dtype
+        assert np.abs(got - ref).max() <= 2e-3 * max(np.abs(ref).max(), 1e-3)
+
+
+def test_attention_oracle_matches_dense_softmax_on_reconstruction(golden, oracle):
+    """The coefficient-domain definition equals softmax(q K^T) V on the
+    reconstructed tokens (jpeg int8, G=2, 3-token tail)."""
+    G = golden("attention")
+    name = "jpeg_i8_f32_g2_t3"
+    c, m = G.case(name), G.meta[name]
+    q, rk, rv, zk, zv, A = oracle_attention_inputs(oracle, golden, c, m)
+    D, g = m["D"], m["G"]
+    toks_k = np.concatenate([np.einsum("ps,bhnsd->bhnpd", A, rk).reshape(
+        rk.shape[0], rk.shape[1], -1, D), zk], axis=2)
+    toks_v = np.concatenate([np.einsum("ps,bhnsd->bhnpd", A, rv).reshape(
+        rv.shape[0], rv.shape[1], -1, D), zv], axis=2)
+    kk = np.repeat(toks_k, g, axis=1)
+    vv = np.repeat(toks_v, g, axis=1)
+    logits = np.einsum("bhd,bhtd->bht", q.astype(np.float64), kk) / math.sqrt(D)
+    p = np.exp(logits - logits.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    dense = np.einsum("bht,bhtd->bhd", p, vv)
+    got = oracle.attention(q, rk, rv, zk, zv, A, D ** -0.5)
+    assert np.abs(got - dense).max() < 1e-10
