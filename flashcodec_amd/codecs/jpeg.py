@@ -129,7 +129,8 @@ def _compress(x, r, k):
 def _decompress(coeffs, r, out_len=None):
     N.require_gpu(coeffs)
     lead, (n, k, D) = coeffs.shape[:-3], coeffs.shape[-3:]
-    T = n * r if out_len is None else int(out_len)
+    # out_len trims the padding; it never extends past the n*r decoded tokens
+    T = n * r if out_len is None else max(0, min(int(out_len), n * r))
     c4 = coeffs.reshape(-1, 1, n, k, D) if coeffs.dim() >= 3 else coeffs
     c4 = c4.contiguous()
     BH = c4.shape[0]
