@@ -183,10 +183,10 @@ def test_empty_cache_prefill_guard_and_layouts(oracle):
     vs.append(torch.randn(2, 4, 40, 32, device=DEV))
     with pytest.raises(ValueError):
         fc.codec_decode_attention(torch.randn(2, 4, 4, 32, device=DEV), ks, vs)
-    # a query that is a strided view (heads innermost-but-one, like HF's
-    # transpose of (B, 1, Hq, D)) and a query dtype other than the stream's
-    qt = torch.randn(2, 1, 8, 32, device=DEV).transpose(1, 2)
-    assert not qt.is_contiguous()
+    # a strided query view (every other head of a wider buffer) and a query
+    # dtype other than the stream's
+    qt = torch.randn(2, 16, 1, 32, device=DEV)[:, ::2]
+    assert not qt.is_contiguous() and qt.stride(-1) == 1
     ref = fc.codec_decode_attention(qt.contiguous(), ks, vs)
     assert torch.equal(fc.codec_decode_attention(qt, ks, vs), ref)
     q16 = qt.to(torch.float16)
