@@ -495,8 +495,12 @@ class FlashCodecCache(_HFCache):
             layer_types, layer_kwargs = get_layer_types_and_kwargs(decoder)
         except Exception:
             n = getattr(decoder, "num_hidden_layers", 1)
-            layer_types = list(getattr(decoder, "layer_types", ["full_attention"] * n))
-            layer_kwargs = [{} for _ in layer_types]
+            layer_types = list(getattr(decoder, "layer_types", None) or ["full_attention"] * n)
+            layer_kwargs = {}
+        # transformers returns one kwargs dict shared by every layer (5.15) or
+        # one dict per layer (later releases)
+        if isinstance(layer_kwargs, dict):
+            layer_kwargs = [layer_kwargs] * len(layer_types)
         per_layer = per_layer or {}
         base = dict(mode=mode, block_size=block_size, keep_freqs=keep_freqs,
                     keep_ratio=keep_ratio, quant_bits=quant_bits)

@@ -90,9 +90,11 @@ def test_jpeg_kernels_match_oracle(dt, r, k, shape, oracle):
     S = shape[-2]
     rec = fc.dct_decompress(got, r, out_len=S)
     assert np.array_equal(bits(rec.cpu().numpy()), bits(oracle.jpeg_decode(coef, r, basis)[..., :S, :]))
-    # strided input: a transposed (B, S, H, D) buffer viewed as (B, H, S, D)
-    xt = x.transpose(1, 2).contiguous().transpose(1, 2)
-    assert not xt.is_contiguous()
+    # strided input: rows of a wider buffer (token stride D + 8)
+    wide = torch.zeros(shape[:-1] + (shape[-1] + 8,), dtype=x.dtype, device=DEV)
+    wide[..., :shape[-1]] = x
+    xt = wide[..., :shape[-1]]
+    assert not xt.is_contiguous() and xt.stride(-1) == 1
     assert torch.equal(fc.dct_compress(xt, r, k), got)
 
 

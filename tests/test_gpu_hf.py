@@ -49,7 +49,8 @@ def test_explicit_cache():
     assert cache.get_seq_length() == PROMPT_LEN + NEW - 1
     assert cache._seen_tokens == PROMPT_LEN + NEW - 1
     assert len(cache.layers) == model.config.num_hidden_layers
-    raw = (PROMPT_LEN + NEW) * 1 * 2 * 16 * 4 * 2
+    # raw KV bytes: tokens x 2 layers x 2 heads x head_dim 16 x fp32 x (K, V)
+    raw = (PROMPT_LEN + NEW) * 2 * 2 * 16 * 4 * 2
     assert cache.storage_bytes() < 0.5 * raw
 
 
@@ -84,7 +85,7 @@ def test_long_generation_stability_and_storage():
         layer0 = cache.layers[0]
         assert layer0._key_stream.n_archived > 0
         assert total - 1 - layer0._key_stream.n_archived < 8
-        raw = (total - 1) * 1 * 2 * 16 * 4 * 2
+        raw = (total - 1) * 2 * 2 * 16 * 4 * 2
         assert cache.storage_bytes() < expect * raw
 
 
