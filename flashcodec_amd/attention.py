@@ -59,7 +59,8 @@ def _view(stream, keep):
     return v
 
 
-def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="auto"):
+def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="auto",
+                           _n_splits=None):
     """Attention of one new query token against a codec archive without
     materialising the reconstructed KV.
 
@@ -74,6 +75,7 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
 
     GQA: query head hq attends kv head hq // (Hq / Hkv).  Raises ValueError
     for more than one query token (prefill attends the materialised view).
+    ``_n_splits`` overrides the split-K count (testing and tuning only).
     """
     B, Hq, Sq, D = query.shape
     if Sq != 1:
@@ -113,6 +115,10 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
     dev = q.device
     L = N.lib()
     n_splits = L.fc_attention_default_splits(nb, B, Hkv, Hq // Hkv, N.num_cus(dev))
+    if _n_splits is not None and nb:
+        # split count override (tests / tuning); trimmed to non-empty splits
+        per = -(-nb // max(1, int(_n_splits)))
+        n_splits = -(-nb // per)
     ws = None
     if n_splits:
         nbytes = L.fc_attention_workspace_bytes(B, Hq, D, n_splits)

@@ -29,12 +29,26 @@
 // precision) and writes out = acc / l in the query dtype.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+
 #include "fc_common.h"
 
 namespace fc {
 
 int check_launch();
 int esize_of(int dt);
+bool split_i8_mfma_supported(int q_dtype, int64_t D, int s);
+int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
+                         int64_t Hq, int64_t Hkv, int64_t D, int r, int s, int64_t nb,
+                         const fc_stream_view* key, const fc_stream_view* value, const float* A,
+                         float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
+                         hipStream_t st);
+
+// FLASHCODEC_AMD_ATTN=valu forces the vector-ALU split pass (A/B testing).
+static bool mfma_split_allowed() {
+  const char* v = getenv("FLASHCODEC_AMD_ATTN");
+  return !(v && v[0] == 'v');
+}
 
 constexpr int kAttnThreads = 256;
 constexpr int kPassRows = 512;
@@ -605,7 +619,13 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
   float* pl = pm + B * Hq * (int64_t)n_splits;
   float* pacc = pl + B * Hq * (int64_t)n_splits;
 
-  if (nb > 0 && (parts & kPartSplit)) {
+  if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_JPEG_I8 &&
+      split_i8_mfma_supported(q_dtype, D, s) && mfma_split_allowed()) {
+    if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
+    const int rc = launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb, key,
+                                        value, A, scale_log2, pm, pl, pacc, n_splits, st);
+    if (rc != FC_OK) return rc;
+  } else if (nb > 0 && (parts & kPartSplit)) {
     // VEC = 8 features per lane; LPR = lanes per row
     if (D % 8) return FC_ERR_UNSUPPORTED;
     const int64_t chunks = D / 8;

@@ -100,9 +100,35 @@ CASES = [
 ]
 
 
+I8 = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+CASES += [
+    # matrix-core split pass shapes: head groups, rows per block, widths
+    ("i8-f16-g16", I8, "f16", 1, 2, 16, 8 * 300 + 3, 128),
+    ("i8-bf16-g32", I8, "bf16", 1, 1, 32, 8 * 90 + 6, 128),
+    ("i8-f16-g3", I8, "f16", 2, 2, 3, 8 * 77 + 1, 128),
+    ("i8-f16-s1", dict(mode="jpeg", block_size=8, keep_freqs=1, quant_bits=8), "f16", 1, 2, 4, 8 * 150 + 2, 128),
+    ("i8-bf16-s2-r16", dict(mode="jpeg", block_size=16, keep_freqs=2, quant_bits=8), "bf16", 1, 2, 8, 16 * 70 + 9, 64),
+    ("i8-f16-d256-g2", I8, "f16", 1, 2, 2, 8 * 128 + 7, 256),
+    ("i8-f16-d64-g4", I8, "f16", 2, 4, 4, 8 * 123 + 4, 64),
+]
+
+
+@pytest.fixture(params=["auto", "valu"])
+def split_variant(request, monkeypatch):
+    """Run int8 cases on the matrix-core split pass (auto) and on the
+    vector-ALU one."""
+    if request.param == "valu":
+        monkeypatch.setenv("FLASHCODEC_AMD_ATTN", "valu")
+    else:
+        monkeypatch.delenv("FLASHCODEC_AMD_ATTN", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("name,cfg,dt,B,Hk,G,S,D", CASES, ids=[c[0] for c in CASES])
-def test_decode_attention_matches_oracle(name, cfg, dt, B, Hk, G, S, D, oracle):
-    print(f"case attention/{name}", flush=True)
+def test_decode_attention_matches_oracle(name, cfg, dt, B, Hk, G, S, D, oracle, split_variant):
+    if split_variant == "valu" and not cfg.get("quant_bits"):
+        pytest.skip("one split pass only for non-int8 stores")
+    print(f"case attention/{name} [{split_variant}]", flush=True)
     seed = seed_of(name)
     ks, vs = build_streams(cfg, dt, B, Hk, S, D, seed % 10000, oracle)
     rng = np.random.default_rng(seed)
@@ -212,3 +238,18 @@ def test_incremental_decode_tracks_oracle(oracle):
                              / 8).half().to(DEV)
         out = fc.codec_decode_attention(q, ks, vs)
         assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "f16")
+
+
+@pytest.mark.parametrize("n_splits", [1, 2, 3, 7, 64, 256])
+def test_split_counts_agree(n_splits, oracle, split_variant):
+    """Any split count (1 = one workgroup walks 1024 blocks, several passes
+    per wavefront; 256 = a few blocks per split) gives the same attention."""
+    print(f"case attention/splits={n_splits} [{split_variant}]", flush=True)
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+    B, Hk, G, D, S = 2, 2, 4, 128, 8 * 1024 + 3
+    ks, vs = build_streams(cfg, "f16", B, Hk, S, D, 77, oracle)
+    rng = np.random.default_rng(78)
+    q = torch.from_numpy((rng.standard_normal((B, Hk * G, 1, D)) / math.sqrt(D))
+                         .astype(np.float32)).half().to(DEV)
+    out = fc.codec_decode_attention(q, ks, vs, _n_splits=n_splits)
+    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "f16")
