@@ -37,7 +37,8 @@ namespace fc {
 
 int check_launch();
 int esize_of(int dt);
-bool split_i8_mfma_supported(int q_dtype, int64_t D, int s);
+bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
+                             int s, const fc_stream_view* key, const fc_stream_view* value);
 int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
                          int64_t Hq, int64_t Hkv, int64_t D, int r, int s, int64_t nb,
                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
@@ -544,6 +545,133 @@ __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(MergeArgs p) {
   }
 }
 
+// Merge pass, one workgroup per query head (D % 4 == 0): split maxima and
+// raw-tail logits first, then every thread owns 4 features of one split
+// group and keeps all of that group's partial loads in flight at once.
+constexpr int kMerge2Threads = 128;
+
+__global__ __launch_bounds__(kMerge2Threads) void attn_merge_head_kernel(MergeArgs p) {
+  __shared__ float wsp[kMaxSplits];
+  __shared__ float wtl[FC_MAX_BLOCK];
+  __shared__ float red[kMerge2Threads / 64];
+  __shared__ float4 part[kMerge2Threads];
+  const int64_t bq = blockIdx.x;                 // b * Hq + hq
+  const int64_t Hq = p.Hkv * p.G;
+  const int64_t b = bq / Hq, hq = bq - b * Hq, hkv = hq / p.G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int nwave = kMerge2Threads / 64;
+  const int ns = p.n_splits;
+
+  // raw-tail logits: wavefront w takes tokens w, w + nwave, ...
+  float qv[kMergeMaxD];
+#pragma unroll
+  for (int i = 0; i < kMergeMaxD; ++i) {
+    const int64_t d = lane + 64 * i;
+    qv[i] = (p.n_raw > 0 && d < p.D) ? load_q(p.q, p.q_dtype, b * p.q_sb + hq * p.q_sh + d) : 0.f;
+  }
+  float mx = -INFINITY;
+  for (int64_t t = wave; t < p.n_raw; t += nwave) {
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMergeMaxD; ++i) {
+      const int64_t d = lane + 64 * i;
+      if (d < p.D)
+        a = __builtin_fmaf(
+            qv[i], load_q(p.kraw, p.raw_dtype, b * p.kr_sb + hkv * p.kr_sh + t * p.kr_st + d), a);
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) a += __shfl_xor(a, m, 64);
+    a *= p.scale_log2;
+    if (lane == 0) wtl[t] = a;
+    mx = fmaxf(mx, a);
+  }
+  for (int sp = tid; sp < ns; sp += kMerge2Threads) mx = fmaxf(mx, p.pm[bq * ns + sp]);
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < nwave; ++w) mx = fmaxf(mx, red[w]);
+  __syncthreads();
+  float l = 0.f;
+  for (int sp = tid; sp < ns; sp += kMerge2Threads) {
+    const float w = __builtin_amdgcn_exp2f(p.pm[bq * ns + sp] - mx);
+    wsp[sp] = w;
+    l = __builtin_fmaf(w, p.pl[bq * ns + sp], l);
+  }
+  for (int64_t t = tid; t < p.n_raw; t += kMerge2Threads) {
+    const float e = __builtin_amdgcn_exp2f(wtl[t] - mx);
+    wtl[t] = e;
+    l += e;
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
+  __syncthreads();  // weights visible; red reusable
+  if (lane == 0) red[wave] = l;
+  __syncthreads();
+  l = red[0];
+#pragma unroll
+  for (int w = 1; w < nwave; ++w) l += red[w];
+  const float inv = 1.0f / l;
+
+  // features: thread -> (group g, 4 features c*4..c*4+3); groups stride splits
+  const int chunks = (int)(p.D / 4);
+  const int ngroup = kMerge2Threads / chunks;    // >= 1 since D <= 512
+  const int grp = tid / chunks, c = tid - grp * chunks;
+  float4 o = {0.f, 0.f, 0.f, 0.f};
+  if (grp < ngroup) {
+    const float4* src = reinterpret_cast<const float4*>(p.pacc + bq * ns * p.D) + c;
+    const int64_t stride = p.D / 4;
+    int sp = grp;
+    for (; sp + 3 * ngroup < ns; sp += 4 * ngroup) {
+      const float4 a0 = src[(int64_t)sp * stride];
+      const float4 a1 = src[(int64_t)(sp + ngroup) * stride];
+      const float4 a2 = src[(int64_t)(sp + 2 * ngroup) * stride];
+      const float4 a3 = src[(int64_t)(sp + 3 * ngroup) * stride];
+      const float w0 = wsp[sp], w1 = wsp[sp + ngroup], w2 = wsp[sp + 2 * ngroup],
+                  w3 = wsp[sp + 3 * ngroup];
+      o.x = __builtin_fmaf(w0, a0.x, o.x); o.y = __builtin_fmaf(w0, a0.y, o.y);
+      o.z = __builtin_fmaf(w0, a0.z, o.z); o.w = __builtin_fmaf(w0, a0.w, o.w);
+      o.x = __builtin_fmaf(w1, a1.x, o.x); o.y = __builtin_fmaf(w1, a1.y, o.y);
+      o.z = __builtin_fmaf(w1, a1.z, o.z); o.w = __builtin_fmaf(w1, a1.w, o.w);
+      o.x = __builtin_fmaf(w2, a2.x, o.x); o.y = __builtin_fmaf(w2, a2.y, o.y);
+      o.z = __builtin_fmaf(w2, a2.z, o.z); o.w = __builtin_fmaf(w2, a2.w, o.w);
+      o.x = __builtin_fmaf(w3, a3.x, o.x); o.y = __builtin_fmaf(w3, a3.y, o.y);
+      o.z = __builtin_fmaf(w3, a3.z, o.z); o.w = __builtin_fmaf(w3, a3.w, o.w);
+    }
+    for (; sp < ns; sp += ngroup) {
+      const float4 a0 = src[(int64_t)sp * stride];
+      const float w0 = wsp[sp];
+      o.x = __builtin_fmaf(w0, a0.x, o.x); o.y = __builtin_fmaf(w0, a0.y, o.y);
+      o.z = __builtin_fmaf(w0, a0.z, o.z); o.w = __builtin_fmaf(w0, a0.w, o.w);
+    }
+    // raw-tail values: group g takes tokens g, g + ngroup, ...
+    for (int64_t t = grp; t < p.n_raw; t += ngroup) {
+      const float e = wtl[t];
+      const int64_t base = b * p.vr_sb + hkv * p.vr_sh + t * p.vr_st + 4 * c;
+      o.x = __builtin_fmaf(e, load_q(p.vraw, p.raw_dtype, base + 0), o.x);
+      o.y = __builtin_fmaf(e, load_q(p.vraw, p.raw_dtype, base + 1), o.y);
+      o.z = __builtin_fmaf(e, load_q(p.vraw, p.raw_dtype, base + 2), o.z);
+      o.w = __builtin_fmaf(e, load_q(p.vraw, p.raw_dtype, base + 3), o.w);
+    }
+  }
+  part[tid] = o;
+  __syncthreads();
+  if (tid < chunks) {
+    float4 s4 = part[tid];
+    for (int g = 1; g < ngroup; ++g) {
+      const float4 x = part[g * chunks + tid];
+      s4.x += x.x; s4.y += x.y; s4.z += x.z; s4.w += x.w;
+    }
+    const int64_t ob = b * p.o_sb + hq * p.o_sh + 4 * tid;
+    store_any(p.out, p.q_dtype, ob + 0, s4.x * inv);
+    store_any(p.out, p.q_dtype, ob + 1, s4.y * inv);
+    store_any(p.out, p.q_dtype, ob + 2, s4.z * inv);
+    store_any(p.out, p.q_dtype, ob + 3, s4.w * inv);
+  }
+}
+
 template <int... Vs, typename F>
 int attn_with_int(int v, F&& f) {
   int rc = FC_ERR_UNSUPPORTED;
@@ -561,7 +689,8 @@ extern "C" {
 int64_t fc_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int n_splits) {
   if (B <= 0 || Hq <= 0 || D <= 0 || n_splits <= 0) return 0;
   const int64_t slots = B * Hq * (int64_t)n_splits;
-  const int64_t bytes = slots * (2 + D) * (int64_t)sizeof(float);
+  const int64_t head = (slots + 3) / 4 * 4;  // pm and pl sections, 16-byte aligned
+  const int64_t bytes = (2 * head + slots * D) * (int64_t)sizeof(float);
   return (bytes + 255) / 256 * 256;
 }
 
@@ -615,12 +744,14 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
   const int64_t G = Hq / Hkv;
   const float scale_log2 = scale * kLog2e;
   hipStream_t st = (hipStream_t)stream;
+  // workspace: pm | pl | pacc, sections 16-byte aligned
+  const int64_t ws_head = (B * Hq * (int64_t)n_splits + 3) / 4 * 4;
   float* pm = static_cast<float*>(workspace);
-  float* pl = pm + B * Hq * (int64_t)n_splits;
-  float* pacc = pl + B * Hq * (int64_t)n_splits;
+  float* pl = pm + ws_head;
+  float* pacc = pl + ws_head;
 
   if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_JPEG_I8 &&
-      split_i8_mfma_supported(q_dtype, D, s) && mfma_split_allowed()) {
+      split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) && mfma_split_allowed()) {
     if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
     const int rc = launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb, key,
                                         value, A, scale_log2, pm, pl, pacc, n_splits, st);
@@ -730,7 +861,11 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
   mg.pm = pm;
   mg.pl = pl;
   mg.pacc = pacc;
-  attn_merge_kernel<<<dim3((unsigned)(B * Hkv)), kAttnThreads, 0, st>>>(mg);
+  if (D % 4 == 0 && D / 4 <= kMerge2Threads) {
+    attn_merge_head_kernel<<<dim3((unsigned)(B * Hq)), kMerge2Threads, 0, st>>>(mg);
+  } else {
+    attn_merge_kernel<<<dim3((unsigned)(B * Hkv)), kAttnThreads, 0, st>>>(mg);
+  }
   return check_launch();
 }
 

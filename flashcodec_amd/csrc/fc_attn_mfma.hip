@@ -112,10 +112,16 @@ template <int SROWS, int DK, int GP>
 __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   constexpr int D = 32 * DK;
   constexpr int DV = (D + 127) / 128;  // 128-feature groups of the value product
+  // rows per wavefront pass: its K codes (NT tiles) and V codes (NS slabs)
+  // are in flight while the previous stage computes
+  constexpr int PR = D == 256 ? 32 : 64;
+  constexpr int NT = PR / 16;
+  constexpr int NS = PR / 32;
+  constexpr int KDW = 2 * DK;  // K dwords per lane per tile
   __shared__ float s_lds[kWaves][16][kSPad];
   __shared__ _Float16 w_lds[kWaves][16][kWPad];
-  __shared__ float comb[kWaves][16][2];
-  __shared__ float red[kWaves];
+  __shared__ float sc_lds[kWaves][2][PR];  // K and V row scales of the pass
+  __shared__ float comb[kWaves][16][3];
 
   const int split = blockIdx.x;
   const int64_t bh = blockIdx.y;
@@ -133,38 +139,45 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   const int64_t spw = (nslab + kWaves - 1) / kWaves;
   const int64_t wrow0 = min(row_end, row_begin + (int64_t)wave * spw * 32);
   const int64_t wrow1 = min(row_end, wrow0 + spw * 32);
+  const int64_t last_row = row_end - 1;  // every load address is clamped to <= last_row
 
   const int8_t* kbase = p.kcodes + bh * p.kcap * SROWS * D;
   const int8_t* vbase = p.vcodes + bh * p.vcap * SROWS * D;
   const float* ksc = p.kscales + bh * p.kcap * SROWS;
   const float* vsc = p.vscales + bh * p.vcap * SROWS;
 
-  // ---- workgroup-wide weight normaliser: 2^-sig * max(V row scale) in [1, 2)
-  float smax = 0.f;
-  for (int64_t i = row_begin + tid; i < row_end; i += kMThreads) smax = fmaxf(smax, vsc[i]);
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) smax = fmaxf(smax, __shfl_xor(smax, m, 64));
-  if (lane == 0) red[wave] = smax;
-
   // ---- queries: B operand of the score product.  Lane (q, c): head c,
-  // features q*D/4 + 8*kc + i of product kc; per-head power-of-two scale.
+  // features q*D/4 + 8*kc + i of product kc, scaled per head by a power of two
   const bool hq_ok = lc < G;
   const int64_t hq = hkv * p.G + g0 + (hq_ok ? lc : 0);
+  const uint16_t* qrow =
+      static_cast<const uint16_t*>(p.q) + b * p.q_sb + hq * p.q_sh + lq * (D / 4);
+  const bool q_f16 = p.q_dtype == FC_F16;
   float qf[DK][8];
   float qmax = 0.f;
+  // dtype branch outside the loops; fp16 lanes are read through a half8 view
+  // (hipcc 7.2 reused dword 0's conversion for all dwords when each dword was
+  // bit-cast to half2 inside an unrolled loop)
 #pragma unroll
-  for (int kc = 0; kc < DK; ++kc)
+  for (int kc = 0; kc < DK; ++kc) {
+    const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + 8 * kc);
+    if (q_f16) {
+      const half8_t h = __builtin_bit_cast(half8_t, raw);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[kc][i] = (float)h[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qf[kc][2 * i] = __uint_as_float(raw[i] << 16);
+        qf[kc][2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float v = 0.f;
-      if (hq_ok) {
-        const int64_t idx = b * p.q_sb + hq * p.q_sh + lq * (D / 4) + 8 * kc + i;
-        v = p.q_dtype == FC_F16 ? to_f32(static_cast<const f16_t*>(p.q)[idx])
-                                : to_f32(static_cast<const bf16_t*>(p.q)[idx]);
-      }
-      qf[kc][i] = v;
-      qmax = fmaxf(qmax, fabsf(v));
+      qf[kc][i] = hq_ok ? qf[kc][i] : 0.f;
+      qmax = fmaxf(qmax, fabsf(qf[kc][i]));
     }
+  }
   qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
   qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
   const int qe = pow2_exp_for(qmax, 14);
@@ -173,58 +186,76 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   for (int kc = 0; kc < DK; ++kc)
 #pragma unroll
     for (int i = 0; i < 8; ++i) qop[kc][i] = (_Float16)ldexpf(qf[kc][i], -qe);
-  // raw score of head c -> base-2 logit before the K row scale
-  const float head_mul = ldexpf(p.scale_log2, qe);
-
-  __syncthreads();
-  smax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const int sig = pow2_exp_for(smax, 1);
-  const float wmul = ldexpf(1.0f, -sig);
-
-  // weight rows of absent heads stay zero
-  for (int i = lane; i < 16 * kWPad; i += 64)
-    if (i / kWPad >= G) w_lds[wave][i / kWPad][i % kWPad] = (_Float16)0.f;
+  const float head_mul = ldexpf(p.scale_log2, qe);  // raw score -> base-2 logit / K scale
 
   float4_t acc[DV][8];
 #pragma unroll
   for (int dv = 0; dv < DV; ++dv)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[dv][e] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  // running max / sum of head (lane % GP), identical in all lanes of a head
+  // running max / sum of head (lane % GP), identical in all lanes of a head;
+  // the accumulators hold acc * 2^-sig_run
   const int myh = lane % GP;
   float m_run = -INFINITY, l_run = 0.f;
+  int sig_run = -1000;
 
-  for (int64_t pr0 = wrow0; pr0 < wrow1; pr0 += kPassRowsW) {
-    const int prow = (int)min<int64_t>(kPassRowsW, wrow1 - pr0);  // multiple of SROWS
-    const int ntile = (prow + 15) / 16;
-    const int rend = ((prow + 31) / 32) * 32;
-    // ------------------------------------------------------------ scores
-    for (int t = 0; t < ntile; ++t) {
-      const int64_t row = pr0 + 16 * t + lc;
-      uint32_t raw[2 * DK];
+  // ---- loads of one pass (addresses clamped in range; values masked later)
+  uint32_t kr[NT][KDW];
+  float ks_r, vs_r;
+  auto load_k = [&](int64_t pr0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int64_t row = min(pr0 + 16 * t + lc, last_row);
       const int8_t* src = kbase + row * D + lq * (D / 4);
-      if (row < pr0 + prow) {
 #pragma unroll
-        for (int h = 0; h < DK / 2; ++h) {
-          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(src + 16 * h);
+      for (int h = 0; h < DK / 2; ++h) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(src + 16 * h);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) raw[4 * h + i] = v[i] ^ 0x80808080u;
-        }
-        if constexpr (DK & 1) {
-          const u32x2_t v = *reinterpret_cast<const u32x2_t*>(src + 16 * (DK / 2));
-          raw[2 * DK - 2] = v[0] ^ 0x80808080u;
-          raw[2 * DK - 1] = v[1] ^ 0x80808080u;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 2 * DK; ++i) raw[i] = 0x80808080u;  // code 0
+        for (int i = 0; i < 4; ++i) kr[t][4 * h + i] = v[i];
       }
+      if constexpr (DK & 1) {
+        const u32x2_t v = *reinterpret_cast<const u32x2_t*>(src + 16 * (DK / 2));
+        kr[t][KDW - 2] = v[0];
+        kr[t][KDW - 1] = v[1];
+      }
+    }
+    const int64_t srow = min(pr0 + (lane % PR), last_row);
+    ks_r = ksc[srow];
+    vs_r = vsc[srow];
+  };
+  uint32_t vr[NS][DV][16];
+  auto load_v = [&](int64_t pr0) {
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl)
+#pragma unroll
+      for (int dv = 0; dv < DV; ++dv) {
+        const int dcol = min(128 * dv + 8 * lc, D - 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int64_t row = min(pr0 + 32 * sl + 8 * lq + i, last_row);
+          const u32x2_t v = *reinterpret_cast<const u32x2_t*>(vbase + row * D + dcol);
+          vr[sl][dv][2 * i] = v[0];
+          vr[sl][dv][2 * i + 1] = v[1];
+        }
+      }
+  };
+
+  if (wrow0 < wrow1) load_k(wrow0);
+  for (int64_t pr0 = wrow0; pr0 < wrow1; pr0 += PR) {
+    const int prow = (int)min<int64_t>(PR, wrow1 - pr0);  // multiple of SROWS
+    const int rend = ((prow + 31) / 32) * 32;
+    load_v(pr0);
+
+    // ------------------------------------------------------------ scores
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const bool ok = 16 * t + lc < prow;
       float4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < DK; ++kc) {
         uint32_t a0, a1, a2, a3;
-        biased_to_f16(raw[2 * kc], a0, a1);
-        biased_to_f16(raw[2 * kc + 1], a2, a3);
+        biased_to_f16((ok ? kr[t][2 * kc] : 0u) ^ 0x80808080u, a0, a1);
+        biased_to_f16((ok ? kr[t][2 * kc + 1] : 0u) ^ 0x80808080u, a2, a3);
         sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a0, a1, a2, a3), qop[kc], sacc,
                                                       0, 0, 0);
       }
@@ -233,6 +264,18 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
         *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = sv;
       }
     }
+    if (lane < PR) {
+      sc_lds[wave][0][lane] = ks_r;
+      sc_lds[wave][1][lane] = vs_r;
+    }
+    // V row scale exponent of this pass
+    float smax = lane < prow ? vs_r : 0.f;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) smax = fmaxf(smax, __shfl_xor(smax, m, 64));
+    const int sig_new = max(sig_run, pow2_exp_for(smax, 1));
+    const float wmul = ldexpf(1.0f, -sig_new);
+    // next pass's K codes and scales fly during the softmax and value stages
+    if (pr0 + PR < wrow1) load_k(pr0 + PR);
     wave_lds_sync();
 
     // ------------------------------------------------------------ softmax
@@ -242,10 +285,10 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
     for (int u = lane; u < npair; u += 64) {
       const int bl = u / GP;
       if (myh >= G) continue;
-      const int64_t grow = pr0 + (int64_t)bl * SROWS;
       float sv[SROWS];
 #pragma unroll
-      for (int j = 0; j < SROWS; ++j) sv[j] = s_lds[wave][myh][bl * SROWS + j] * ksc[grow + j];
+      for (int j = 0; j < SROWS; ++j)
+        sv[j] = s_lds[wave][myh][bl * SROWS + j] * sc_lds[wave][0][bl * SROWS + j];
       for (int t = 0; t < r; ++t) {
         float lg = 0.f;
 #pragma unroll
@@ -262,11 +305,10 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
     for (int u = lane; u < npair; u += 64) {
       const int bl = u / GP;
       if (myh >= G) continue;
-      const int64_t grow = pr0 + (int64_t)bl * SROWS;
       float sv[SROWS], w[SROWS];
 #pragma unroll
       for (int j = 0; j < SROWS; ++j) {
-        sv[j] = s_lds[wave][myh][bl * SROWS + j] * ksc[grow + j];
+        sv[j] = s_lds[wave][myh][bl * SROWS + j] * sc_lds[wave][0][bl * SROWS + j];
         w[j] = 0.f;
       }
       for (int t = 0; t < r; ++t) {
@@ -280,18 +322,22 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
       }
 #pragma unroll
       for (int j = 0; j < SROWS; ++j)
-        w_lds[wave][myh][bl * SROWS + j] = (_Float16)(w[j] * (vsc[grow + j] * wmul));
+        w_lds[wave][myh][bl * SROWS + j] =
+            (_Float16)(w[j] * (sc_lds[wave][1][bl * SROWS + j] * wmul));
     }
     // rows past the pass end inside the last slab carry zero weight
-    for (int i = prow + lane; i < rend; i += 64)
-      for (int h = 0; h < G; ++h) w_lds[wave][h][i] = (_Float16)0.f;
+    if (prow < rend)
+      for (int i = prow + lane; i < rend; i += 64)
+        for (int h = 0; h < G; ++h) w_lds[wave][h][i] = (_Float16)0.f;
 #pragma unroll
     for (int m = GP; m < 64; m <<= 1) lsum += __shfl_xor(lsum, m, 64);
     l_run = l_run * alpha + lsum;
     // rescale the accumulators: lane (q, c) register i holds head 4q + i
+    const float sfix = ldexpf(1.0f, max(sig_run - sig_new, -126));
+    sig_run = sig_new;
     float al[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lq + i, 64);
+    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lq + i, 64) * sfix;
 #pragma unroll
     for (int dv = 0; dv < DV; ++dv)
 #pragma unroll
@@ -301,32 +347,27 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
     wave_lds_sync();
 
     // ------------------------------------------------------------ values
-    const int nslab_p = rend / 32;
-    for (int sl = 0; sl < nslab_p; ++sl) {
-      const u32x4_t wa = *reinterpret_cast<const u32x4_t*>(&w_lds[wave][lc][32 * sl + 8 * lq]);
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) {
+      if (32 * sl >= rend) continue;
+      u32x4_t wa = *reinterpret_cast<const u32x4_t*>(&w_lds[wave][lc][32 * sl + 8 * lq]);
+      if (lc >= G) wa = (u32x4_t){0u, 0u, 0u, 0u};
       const half8_t wop = __builtin_bit_cast(half8_t, wa);
 #pragma unroll
       for (int dv = 0; dv < DV; ++dv) {
-        const int dcol = 128 * dv + 8 * lc;
-        const bool dok = dcol < D;
-        uint32_t w0[8], w1[8];  // rows 8q+i: bytes [dcol, dcol+4), [dcol+4, dcol+8)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int rr = 32 * sl + 8 * lq + i;
-          u32x2_t v = {0u, 0u};
-          if (dok && rr < prow) v = *reinterpret_cast<const u32x2_t*>(vbase + (pr0 + rr) * D + dcol);
-          w0[i] = v[0] ^ 0x80808080u;
-          w1[i] = v[1] ^ 0x80808080u;
-        }
+        const bool dok = 128 * dv + 8 * lc < D;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          const uint32_t* wv = hh ? w1 : w0;
           // row pair (a, b) = (2pp, 2pp+1): t0 = [a0 b0 a1 b1], t1 = [a2 b2 a3 b3]
           uint32_t t0[4], t1[4];
 #pragma unroll
           for (int pp = 0; pp < 4; ++pp) {
-            t0[pp] = __builtin_amdgcn_perm(wv[2 * pp + 1], wv[2 * pp], 0x05010400u);
-            t1[pp] = __builtin_amdgcn_perm(wv[2 * pp + 1], wv[2 * pp], 0x07030602u);
+            const bool oka = dok && 32 * sl + 8 * lq + 2 * pp < prow;
+            const bool okb = dok && 32 * sl + 8 * lq + 2 * pp + 1 < prow;
+            const uint32_t ra = (oka ? vr[sl][dv][2 * (2 * pp) + hh] : 0u) ^ 0x80808080u;
+            const uint32_t rb = (okb ? vr[sl][dv][2 * (2 * pp + 1) + hh] : 0u) ^ 0x80808080u;
+            t0[pp] = __builtin_amdgcn_perm(rb, ra, 0x05010400u);
+            t1[pp] = __builtin_amdgcn_perm(rb, ra, 0x07030602u);
           }
 #pragma unroll
           for (int ee = 0; ee < 4; ++ee) {
@@ -347,10 +388,12 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
     wave_lds_sync();
   }
 
-  // ---- combine the wavefronts.  Lane c < GP carries head c's (max, sum).
+  // ---- combine the wavefronts.  Lane c < GP carries head c's (max, sum);
+  // each wave's accumulators carry a factor 2^-sig_run.
   if (lane < GP) {
     comb[wave][lane][0] = m_run;
     comb[wave][lane][1] = l_run;
+    comb[wave][lane][2] = ldexpf(1.0f, max(sig_run, -126));
   }
   float* obuf = &s_lds[0][0][0];  // [wave*4 + i][D] for the 4 heads of a lane group
   for (int h0 = 0; h0 < G; h0 += 4) {
@@ -379,12 +422,12 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
       for (int w = 0; w < kWaves; ++w) {
         const float mw = comb[w][h][0];
         const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-        o = __builtin_fmaf(f, obuf[(w * 4 + i) * D + d], o);
+        o = __builtin_fmaf(f * comb[w][h][2], obuf[(w * 4 + i) * D + d], o);
         l = __builtin_fmaf(f, comb[w][h][1], l);
       }
       const int64_t bq = b * (p.Hkv * p.G) + hkv * p.G + g0 + h;
       const int64_t slot = bq * p.n_splits + split;
-      p.pacc[slot * D + d] = o * ldexpf(1.0f, sig);
+      p.pacc[slot * D + d] = o;
       if (d == 0) {
         p.pm[slot] = M;
         p.pl[slot] = l;
@@ -402,9 +445,14 @@ int mfma_with_int(int v, F&& f) {
 }
 
 // Whether the matrix-core split pass handles this configuration.
-bool split_i8_mfma_supported(int q_dtype, int64_t D, int s) {
+// The pass reads 16 query bytes and 16 code bytes per load: the query rows
+// and both code stores must be 16-byte aligned.
+bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
+                             int s, const fc_stream_view* key, const fc_stream_view* value) {
+  const auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   return (q_dtype == FC_F16 || q_dtype == FC_BF16) && (D == 64 || D == 128 || D == 256) &&
-         (s == 1 || s == 2 || s == 4);
+         (s == 1 || s == 2 || s == 4) && al16(q) && q_sb % 8 == 0 && q_sh % 8 == 0 &&
+         al16(key->rows) && al16(value->rows);
 }
 
 int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
