@@ -7,14 +7,15 @@ sequence (r=8, k=4, int8 K and V coefficients + fp32 scales) plus a raw tail
 of 5 fp16 tokens; queries fp16 N(0,1)/sqrt(D); K/V synthetic AR(1) rho=0.95
 fp16, archived by this package's own kernels before timing.
 
-One step = one `codec_decode_attention` call (split pass + merge pass) on
-inputs resident in HBM.  `value` is algorithmic GB/s of the call:
+One step = one `codec_decode_attention` call on inputs resident in HBM: one
+launch of the matrix-core split pass, whose last workgroup per head group
+merges the split partials with the raw tail.  `value` is algorithmic GB/s of
+the call:
   K+V int8 codes 2*134,217,728 + fp32 scales 2*4,194,304 + raw tails
   163,840 + q 65,536 + out 65,536 = 277,118,976 bytes per call.
-The roofline object covers the dominant kernel (the split pass, timed alone
-with HIP events on the launching stream): it reads the codes, scales and q,
-276,889,600 bytes per launch.  `cpu_baseline` times the fp64 CPU oracle on
-sequence 0 of 8 (1/8 of the call).
+The roofline object covers that kernel, each launch timed with HIP events on
+the stream it is launched on.  `cpu_baseline` times the fp64 CPU oracle on
+the same workload's sequences for at least 10 s (one whole call or more).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
   python bench.py --mode copy     # plain copy, for PMC byte calibration
@@ -38,7 +39,6 @@ CODE_BYTES = B * HKV * NB * K * D              # per stream
 SCALE_BYTES = B * HKV * NB * K * 4
 Q_BYTES = B * HQ * D * 2
 ALG_BYTES_CALL = 2 * CODE_BYTES + 2 * SCALE_BYTES + 2 * B * HKV * TAIL * D * 2 + 2 * Q_BYTES
-ALG_BYTES_SPLIT = 2 * CODE_BYTES + 2 * SCALE_BYTES + Q_BYTES
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "attn_split_c3_pmc.md")
 
 
@@ -85,6 +85,15 @@ def copy_mode(args):
                       "read_plus_write_GBs": 2 * n / ms / 1e6}))
 
 
+def split_kernel_name():
+    """Kernel of this workload's call (int8 codes, fp16 q, D=128, 4 rows per
+    block, groups of 4 q heads): the matrix-core split pass with its merge
+    fused in (one launch)."""
+    if os.environ.get("FLASHCODEC_AMD_ATTN", "").startswith("v"):
+        return "attn_split_kernel + attn_merge_head_kernel"
+    return "attn_split_i8_mfma<4,4,4> (merge fused)"
+
+
 def read_pmc_traffic():
     """HBM bytes per split launch from the committed PMC summary, if any."""
     if not os.path.exists(PMC_SUMMARY):
@@ -95,32 +104,44 @@ def read_pmc_traffic():
     return None
 
 
-def cpu_baseline(q, ks, vs):
-    """fp64 CPU oracle on sequence 0 of the workload (1/8 of one call)."""
+def cpu_baseline(q, ks, vs, min_seconds=10.0):
+    """The CPU restatement of the path (oracle/) on the same workload: per
+    sequence, dequantise the int8 K/V codes to rows and run fp64 decode
+    attention over 32 q heads.  Sequences are taken in turn until at least
+    `min_seconds` have passed and every sequence has run once (one whole
+    call); host copies of the codes are made before the clock starts.
+    Returns (sequence-0 output, baseline record)."""
     import numpy as np
     from oracle import oracle as O
     import flashcodec_amd as fc
     threads = min(len(os.sched_getaffinity(0)), 16)
-    rows = []
-    for st in (ks, vs):
-        c = st._coeffs[:1, :, :NB].float().cpu().numpy()
-        s = st._scales[:1, :, :NB, :, 0].cpu().numpy()
-        rows.append(O.stored_rows_jpeg(c, s))
-    zk = ks.raw[:1].float().cpu().numpy()
-    zv = vs.raw[:1].float().cpu().numpy()
+    codes = [st._coeffs[:, :, :NB].cpu().numpy() for st in (ks, vs)]
+    scales = [st._scales[:, :, :NB, :, 0].cpu().numpy() for st in (ks, vs)]
+    raws = [st.raw.float().cpu().numpy() for st in (ks, vs)]
     A = O.synthesis_matrix("jpeg", R, fc.dct_basis(R, K).numpy())
-    qn = q[:1, :, 0].float().cpu().numpy()
-    O.attention(qn[:, :2], rows[0][:, :1], rows[1][:, :1], zk[:, :1], zv[:, :1], A,
-                D ** -0.5, n_threads=threads)                     # warm-up
+    qn = q[:, :, 0].float().cpu().numpy()
+
+    def one(b):
+        rk = O.stored_rows_jpeg(codes[0][b:b + 1], scales[0][b:b + 1])
+        rv = O.stored_rows_jpeg(codes[1][b:b + 1], scales[1][b:b + 1])
+        return O.attention(qn[b:b + 1], rk, rv, raws[0][b:b + 1], raws[1][b:b + 1], A,
+                           D ** -0.5, n_threads=threads)
+
+    ref0, done = None, 0
     t0 = time.perf_counter()
-    ref = O.attention(qn, rows[0], rows[1], zk, zv, A, D ** -0.5, n_threads=threads)
+    while done < B or time.perf_counter() - t0 < min_seconds:
+        o = one(done % B)
+        if done == 0:
+            ref0 = o
+        done += 1
     dt = time.perf_counter() - t0
-    sample_bytes = ALG_BYTES_CALL / B
-    return ref, {"value": round(sample_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
-                 "kind": "port",
-                 "sample": "fp64 C++ oracle (OpenMP) on sequence 0 of 8: 32 q heads x "
-                           "(32768 archived + 5 raw tokens), 1/8 of one call",
-                 "seconds": round(dt, 3)}
+    seq_bytes = ALG_BYTES_CALL / B
+    return ref0, {"value": round(done * seq_bytes / dt / 1e9, 3), "unit": "GB/s",
+                  "cores": threads, "kind": "port",
+                  "sample": f"{done} sequences of the workload ({done / B:.2f} calls): int8 "
+                            "codes -> fp64 rows (numpy) -> fp64 decode attention over 32 q "
+                            "heads x (32768 archived + 5 raw tokens) (C++ oracle, OpenMP)",
+                  "seconds": round(dt, 3)}
 
 
 def main():
@@ -168,27 +189,24 @@ def main():
 
     L = N.lib()
     n_splits = args.splits or L.fc_attention_default_splits(NB, B, HKV, HQ // HKV, N.num_cus(dev))
-
-    def call():
-        return fc.codec_decode_attention(q, ks, vs)
+    keep = []
+    kv, vv = _view(ks, keep), _view(vs, keep)
+    A = _device_A(ks.codec, R, dev)
+    out_c = torch.empty_like(q)
+    # zero-filled once: its arrival counters return to zero after every call
+    ws = torch.zeros(L.fc_attention_workspace_bytes(B, HQ, D, n_splits), dtype=torch.uint8,
+                     device=dev)
+    abi_args = (q.data_ptr(), N.F16, q.stride(0), q.stride(1), B, HQ, HKV, D, N.STORE_JPEG_I8,
+                N.F16, R, K, NB, kv, vv, TAIL, A.data_ptr(), D ** -0.5, out_c.data_ptr(),
+                out_c.stride(0), out_c.stride(1), ws.data_ptr(), n_splits, N.stream_ptr(dev))
 
     if args.splits:
-        # same call with an explicit split count
-        ws = torch.empty(L.fc_attention_workspace_bytes(B, HQ, D, n_splits), dtype=torch.uint8,
-                         device=dev)
-        keep = []
-        kv, vv = _view(ks, keep), _view(vs, keep)
-        A = _device_A(ks.codec, R, dev)
-        out_t = torch.empty_like(q)
-
-        def call():  # noqa: F811
-            rc = L.fc_decode_attention(
-                q.data_ptr(), N.F16, q.stride(0), q.stride(1), B, HQ, HKV, D, N.STORE_JPEG_I8,
-                N.F16, R, K, NB, kv, vv, TAIL, A.data_ptr(), D ** -0.5, out_t.data_ptr(),
-                out_t.stride(0), out_t.stride(1), ws.data_ptr(), n_splits,
-                N.stream_ptr(dev))
-            N.check(rc, "fc_decode_attention")
-            return out_t
+        def call():
+            N.check(L.fc_decode_attention(*abi_args), "fc_decode_attention")
+            return out_c
+    else:
+        def call():
+            return fc.codec_decode_attention(q, ks, vs)
 
     log(f"bench: warmup {args.warmup}, steps {args.steps}, splits {n_splits}")
     for _ in range(args.warmup):
@@ -203,30 +221,22 @@ def main():
     ms = e0.elapsed_time(e1) / args.steps
     log(f"bench: {ms * 1e3:.1f} us per call")
 
-    # dominant kernel alone: the split pass, bracketed by events on the same
-    # stream it is launched on
-    ws = torch.empty(L.fc_attention_workspace_bytes(B, HQ, D, n_splits), dtype=torch.uint8,
-                     device=dev)
-    keep = []
-    kv, vv = _view(ks, keep), _view(vs, keep)
-    A = _device_A(ks.codec, R, dev)
-    out_s = torch.empty_like(q)
-    split_args = (q.data_ptr(), N.F16, q.stride(0), q.stride(1), B, HQ, HKV, D, N.STORE_JPEG_I8,
-                  N.F16, R, K, NB, kv, vv, TAIL, A.data_ptr(), D ** -0.5, out_s.data_ptr(),
-                  out_s.stride(0), out_s.stride(1), ws.data_ptr(), n_splits, N.stream_ptr(dev))
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    for a, b in evs[:3]:
-        N.check(L.fc_decode_attention_split(*split_args), "split")
+    # dominant kernel: the call is one launch of the split kernel (its last
+    # workgroup per head group merges); K back-to-back launches through the
+    # C ABI between two events on the stream they are launched on
+    for _ in range(3):
+        N.check(L.fc_decode_attention(*abi_args), "fc_decode_attention")
     torch.cuda.synchronize()
-    for a, b in evs:
-        a.record()
-        N.check(L.fc_decode_attention_split(*split_args), "split")
-        b.record()
+    stream = torch.cuda.current_stream(dev)   # the stream N.stream_ptr hands the library
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record(stream)
+    for _ in range(args.steps):
+        N.check(L.fc_decode_attention(*abi_args), "fc_decode_attention")
+    k1.record(stream)
     torch.cuda.synchronize()
-    split_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
-    achieved = ALG_BYTES_SPLIT / (split_ms * 1e-3) / 1e9
-    log(f"bench: split pass {split_ms * 1e3:.1f} us, {achieved:.0f} GB/s")
+    launch_ms = k0.elapsed_time(k1) / args.steps
+    achieved = ALG_BYTES_CALL / (launch_ms * 1e-3) / 1e9
+    log(f"bench: kernel {launch_ms * 1e3:.1f} us per launch, {achieved:.0f} GB/s")
 
     result = {
         "metric": METRIC,
@@ -239,7 +249,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16",
+        "accumulate": "f32",
         "data": "synthetic AR(1) rho=0.95 K/V (fp16, archived int8 by the kernels), "
                 "q fp16 N(0,1)/sqrt(D)",
         "config": {"workload": "C3 coefficient-domain split-K decode attention",
@@ -249,16 +260,16 @@ def main():
                    "algorithmic_bytes_per_call": ALG_BYTES_CALL},
         "hbm_frac": round(ALG_BYTES_CALL / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(B / (ms * 1e-3), 1),
-        "launches_per_call": 2,
-        "roofline": {"bound": "hbm", "kernel": "attn_split_kernel",
+        "launches_per_call": 1,
+        "roofline": {"bound": "hbm", "kernel": split_kernel_name(),
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": read_pmc_traffic(),
-                     "algorithmic_bytes_per_launch": ALG_BYTES_SPLIT,
-                     "avg_launch_us": round(split_ms * 1e3, 2)},
+                     "algorithmic_bytes_per_launch": ALG_BYTES_CALL,
+                     "avg_launch_us": round(launch_ms * 1e3, 2)},
     }
     if not args.no_cpu_baseline:
-        log("bench: cpu baseline (fp64 oracle, sequence 0)")
+        log("bench: cpu baseline (fp64 oracle, >= 10 s of the workload)")
         ref, cpu = cpu_baseline(q, ks, vs)
         got = out[:1, :, 0].float().cpu().numpy()
         err = float(np.abs(got - ref).max() / np.abs(ref).max())

@@ -11,6 +11,9 @@ file, so the library travels with the source tree.  Flags:
   instructions are generated.
 * ``-mcode-object-version=5``: loadable by the ROCm runtime bundled with
   PyTorch as well as the system one.
+* ``-mllvm -amdgpu-mfma-vgpr-form`` (matrix-core sources only): matrix-core
+  results in ordinary VGPRs, so the softmax rescale of the accumulators needs
+  no copies through the accumulation registers.
 """
 
 import os
@@ -51,9 +54,15 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
+FILE_FLAGS = {
+    "fc_attn_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj]
+    extra = FILE_FLAGS.get(os.path.basename(src), [])
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{res.stdout}\n{res.stderr}")

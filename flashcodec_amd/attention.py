@@ -19,6 +19,7 @@ from . import _native as N
 from .codecs import dct_basis
 
 _A_CACHE = {}
+_WORKSPACES = {}
 
 
 def block_basis(codec, block_size, device=None, dtype=torch.float32):
@@ -37,6 +38,22 @@ def _device_A(codec, r, device):
         A = block_basis(codec, r, dtype=torch.float32).contiguous().to(device)
         _A_CACHE[key] = A
     return A
+
+
+def workspace(device, nbytes):
+    """Workspace of the decode attention for the current stream of `device`,
+    at least `nbytes` long.  Zero-filled when created: its arrival counters
+    must start at zero, and every call returns them to zero, so the calls of
+    one stream (which run in order) share it.  Calls on other streams get
+    their own."""
+    device = torch.device(device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
 
 
 def _view(stream, keep):
@@ -121,8 +138,7 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
         n_splits = -(-nb // per)
     ws = None
     if n_splits:
-        nbytes = L.fc_attention_workspace_bytes(B, Hq, D, n_splits)
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        ws = workspace(dev, L.fc_attention_workspace_bytes(B, Hq, D, n_splits))
     A = _device_A(c, r, dev) if nb else None
     keep = []
     kv, vv = _view(ks, keep), _view(vs, keep)

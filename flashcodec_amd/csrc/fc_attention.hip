@@ -31,19 +31,10 @@
 
 #include <cstdlib>
 
+#include "fc_attn_internal.h"
 #include "fc_common.h"
 
 namespace fc {
-
-int check_launch();
-int esize_of(int dt);
-bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
-                             int s, const fc_stream_view* key, const fc_stream_view* value);
-int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
-                         int64_t Hq, int64_t Hkv, int64_t D, int r, int s, int64_t nb,
-                         const fc_stream_view* key, const fc_stream_view* value, const float* A,
-                         float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
-                         hipStream_t st);
 
 // FLASHCODEC_AMD_ATTN=valu forces the vector-ALU split pass (A/B testing).
 static bool mfma_split_allowed() {
@@ -96,14 +87,6 @@ __device__ __forceinline__ float row_sum(float v, int lpr) {
   if (lpr >= 32) v += __shfl_xor(v, 16, 64);
   if (lpr >= 64) v += __shfl_xor(v, 32, 64);
   return v;
-}
-
-__device__ __forceinline__ float load_q(const void* q, int dt, int64_t idx) {
-  switch (dt) {
-    case FC_F16: return to_f32(static_cast<const f16_t*>(q)[idx]);
-    case FC_BF16: return to_f32(static_cast<const bf16_t*>(q)[idx]);
-    default: return static_cast<const float*>(q)[idx];
-  }
 }
 
 // Row `j` of block `n` of sequence `bh`, VEC features from d0, as fp32.
@@ -462,14 +445,6 @@ struct MergeArgs {
   const float* pacc;
 };
 
-__device__ __forceinline__ void store_any(void* p, int dt, int64_t idx, float v) {
-  switch (dt) {
-    case FC_F16: static_cast<f16_t*>(p)[idx] = from_f32<f16_t>(v); break;
-    case FC_BF16: static_cast<bf16_t*>(p)[idx] = from_f32<bf16_t>(v); break;
-    default: static_cast<float*>(p)[idx] = v; break;
-  }
-}
-
 constexpr int kMergeMaxD = FC_MAX_HEAD_DIM / 64;
 
 __global__ __launch_bounds__(kAttnThreads) void attn_merge_kernel(MergeArgs p) {
@@ -684,22 +659,39 @@ int attn_with_int(int v, F&& f) {
 
 using namespace fc;
 
+namespace fc {
+
+// Workspace of one call: kCounterWords 32-bit arrival counters of the fused
+// merge (a fixed region, so calls of any shape find their counters at the same
+// place), then pm | pl | pacc (fp32, sections 16-byte aligned, 256-byte
+// rounded).  The counters must be zero before a workspace's first use; every
+// call leaves them zero.
+constexpr int64_t kCounterWords = 16384;
+constexpr int64_t kCounterBytes = kCounterWords * 4;
+static int64_t ws_partial_bytes(int64_t B, int64_t Hq, int64_t D, int n_splits) {
+  const int64_t slots = B * Hq * (int64_t)n_splits;
+  const int64_t head = (slots + 3) / 4 * 4;
+  const int64_t bytes = (2 * head + slots * D) * (int64_t)sizeof(float);
+  return (bytes + 255) / 256 * 256;
+}
+
+}  // namespace fc
+
 extern "C" {
 
 int64_t fc_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t D, int n_splits) {
   if (B <= 0 || Hq <= 0 || D <= 0 || n_splits <= 0) return 0;
-  const int64_t slots = B * Hq * (int64_t)n_splits;
-  const int64_t head = (slots + 3) / 4 * 4;  // pm and pl sections, 16-byte aligned
-  const int64_t bytes = (2 * head + slots * D) * (int64_t)sizeof(float);
-  return (bytes + 255) / 256 * 256;
+  return fc::kCounterBytes + fc::ws_partial_bytes(B, Hq, D, n_splits);
 }
 
 int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G, int n_cu) {
   if (nb <= 0) return 0;
   if (n_cu <= 0) n_cu = 256;
-  const int64_t groups = (G + 7) / 8;
+  // one round of workgroups: two per compute unit, one per (split, batch,
+  // kv head, group of up to 16 query heads)
+  const int64_t groups = (G + 15) / 16;
   const int64_t cols = std::max<int64_t>(1, B * Hkv * groups);
-  int64_t want = (8 * (int64_t)n_cu + cols - 1) / cols;
+  int64_t want = (2 * (int64_t)n_cu + cols - 1) / cols;
   // at least ~16 blocks per split, at most kMaxSplits splits
   want = std::min<int64_t>(want, (nb + 15) / 16);
   want = std::max<int64_t>(1, std::min<int64_t>(want, kMaxSplits));
@@ -744,18 +736,33 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
   const int64_t G = Hq / Hkv;
   const float scale_log2 = scale * kLog2e;
   hipStream_t st = (hipStream_t)stream;
-  // workspace: pm | pl | pacc, sections 16-byte aligned
+  // workspace: counters | pm | pl | pacc, sections 16-byte aligned
   const int64_t ws_head = (B * Hq * (int64_t)n_splits + 3) / 4 * 4;
-  float* pm = static_cast<float*>(workspace);
+  unsigned int* counters = static_cast<unsigned int*>(workspace);
+  float* pm = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   float* pl = pm + ws_head;
   float* pacc = pl + ws_head;
 
   if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_JPEG_I8 &&
       split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) && mfma_split_allowed()) {
     if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
+    // one launch per call when the merge is requested too: the split pass's
+    // last workgroup per head group merges
+    const bool fuse = (parts & kPartMerge) && split_i8_mfma_fusable(n_splits) &&
+                      B * Hkv * ((G + 15) / 16) <= kCounterWords;
+    MfmaFuse fz{};
+    if (fuse) {
+      fz.raw_dtype = stream_dtype;
+      fz.n_raw = n_raw;
+      fz.out = out;
+      fz.o_sb = o_sb;
+      fz.o_sh = o_sh;
+      fz.counters = counters;
+    }
     const int rc = launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb, key,
-                                        value, A, scale_log2, pm, pl, pacc, n_splits, st);
-    if (rc != FC_OK) return rc;
+                                        value, A, scale_log2, pm, pl, pacc, n_splits,
+                                        fuse ? &fz : nullptr, st);
+    if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit)) {
     // VEC = 8 features per lane; LPR = lanes per row
     if (D % 8) return FC_ERR_UNSUPPORTED;

@@ -1,0 +1,37 @@
+// Declarations shared by the decode-attention sources (fc_attention.hip:
+// argument checks, vector-ALU split pass, merge pass; fc_attn_mfma.hip:
+// matrix-core split pass for int8 jpeg archives).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "flashcodec_amd.h"
+
+namespace fc {
+
+int check_launch();
+int esize_of(int dt);
+
+// Fused merge of the matrix-core split pass: the last workgroup of each
+// (batch, kv head, head group) combines the split partials with the raw
+// tail and writes the output.
+struct MfmaFuse {
+  int raw_dtype;
+  int64_t n_raw;
+  void* out;
+  int64_t o_sb, o_sh;
+  unsigned int* counters;  // one word per (batch, kv head, head group); zero on entry and exit
+};
+
+bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
+                             int s, const fc_stream_view* key, const fc_stream_view* value);
+bool split_i8_mfma_fusable(int n_splits);
+// fuse == nullptr: write the split partials only (pm, pl, pacc)
+int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
+                         int64_t Hq, int64_t Hkv, int64_t D, int r, int s, int64_t nb,
+                         const fc_stream_view* key, const fc_stream_view* value, const float* A,
+                         float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
+                         const MfmaFuse* fuse, hipStream_t st);
+
+}  // namespace fc

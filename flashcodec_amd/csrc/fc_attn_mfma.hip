@@ -35,11 +35,12 @@
 // partial per (query head, split) for the merge kernel.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
+#include "fc_attn_internal.h"
 #include "fc_common.h"
 
 namespace fc {
-
-int check_launch();
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -65,13 +66,29 @@ struct MfmaArgs {
   float* pm;
   float* pl;
   float* pacc;
+  // fused merge (fused != 0): raw tail, output and arrival counters
+  int fused;
+  const void* kraw;
+  const void* vraw;
+  int raw_dtype;
+  int64_t kr_sb, kr_sh, kr_st, vr_sb, vr_sh, vr_st;
+  int64_t n_raw;
+  void* out;
+  int64_t o_sb, o_sh;
+  unsigned int* counters;  // one per (batch, kv head, head group), zero between calls
 };
 
 constexpr int kMThreads = 256;
+constexpr int kFuseMaxSplits = 64;  // split count limit of the fused merge
 constexpr int kWaves = kMThreads / 64;
-constexpr int kPassRowsW = 128;        // rows per wavefront pass
+constexpr int kPassRowsW = 64;         // max rows per wavefront pass
 constexpr int kSPad = kPassRowsW + 4;  // float stride of a score row in LDS
 constexpr int kWPad = kPassRowsW + 8;  // half stride of a weight row in LDS
+constexpr float kLazyMax = 8.f;        // exponentials may reach 2^8 before a rescale
+constexpr int kTapsUnrolled = 16;      // softmax taps unrolled (block sizes up to 16)
+constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor: 32-bit data format
+constexpr int kCachePolicySc1 = 16;    // buffer load cache policy: device scope (sc1)
+constexpr int kWaitVmcnt0 = 0x0F70;    // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
 
 // Orders this wavefront's LDS writes before its later LDS reads (lanes of a
 // wavefront exchange data through its private LDS region).
@@ -108,6 +125,172 @@ __device__ __forceinline__ int pow2_exp_for(float x, int target) {
   return e - target;
 }
 
+// buffer descriptor over `bytes` bytes at `base`: loads at offsets past the
+// end return zero (rows past the end of a pass read as code 0 / scale 0)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kBufWord3);
+}
+
+// Element load / store with the dtype fixed at compile time (T = f16_t,
+// bf16_t) or read at run time (T = void).
+template <typename T>
+__device__ __forceinline__ float ld_elem(const void* ptr, int dt, int64_t i) {
+  if constexpr (std::is_void_v<T>) {
+    return load_q(ptr, dt, i);
+  } else {
+    return to_f32(static_cast<const T*>(ptr)[i]);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st_elem(void* ptr, int dt, int64_t i, float v) {
+  if constexpr (std::is_void_v<T>) {
+    store_any(ptr, dt, i, v);
+  } else {
+    static_cast<T*>(ptr)[i] = from_f32<T>(v);
+  }
+}
+
+// Merge of one (batch, kv head, head group) by the workgroup that arrived
+// last: the n_splits partials of its G query heads (read with device-scope
+// loads) and the raw-tail tokens, out = (sum_s w_s acc_s + sum_t e_t v_t) / l.
+// TQ: query / output element type, TR: raw-tail element type (void: dtypes
+// read at run time).  `lds` holds >= 16 * (2 * kFuseMaxSplits + FC_MAX_BLOCK)
+// + 16 floats.
+template <int D, typename TQ, typename TR>
+__device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
+                            int tid, float* lds) {
+  constexpr int C4 = D / 4;      // float4 chunks of a head's output
+  constexpr int kPre = 16;       // partials prefetched per thread
+  const int lane = tid & 63, wave = tid >> 6;
+  const int ns = p.n_splits;
+  const int nr = (int)p.n_raw;
+  const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;  // slot of head 0 of the group
+  float* wsp = lds;                            // [16][kFuseMaxSplits] split maxima -> weights
+  float* plv = wsp + 16 * kFuseMaxSplits;      // [16][kFuseMaxSplits] split sums
+  float* etl = plv + 16 * kFuseMaxSplits;      // [16][FC_MAX_BLOCK] tail logits -> exps
+  float* inv = etl + 16 * FC_MAX_BLOCK;        // [16] 1 / softmax denominator
+
+  // device-scope (L2-missing) loads of the group's partials
+  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, G * ns * D * 4);
+  auto part = [&](int h, int sp, int c) {
+    return __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(rp, ((h * ns + sp) * C4 + c) * 16, 0,
+                                                      kCachePolicySc1));
+  };
+  // one output task (head, 4 features) per thread when they fit: its
+  // partials are requested now, with the statistics and the tail logits
+  const bool one_task = G * C4 <= kMThreads && ns <= kPre;
+  float4 pre[kPre];
+  if (one_task && tid < G * C4) {
+    const int h = tid / C4, c = tid - h * C4;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j)
+      if (j < ns) pre[j] = part(h, j, c);
+  }
+  for (int u = tid; u < G * ns; u += kMThreads) {
+    const int h = u / ns, sp = u - h * ns;
+    const int64_t slot = (bq0 + h) * ns + sp;
+    wsp[h * kFuseMaxSplits + sp] =
+        __hip_atomic_load(p.pm + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    plv[h * kFuseMaxSplits + sp] =
+        __hip_atomic_load(p.pl + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  {
+    // raw-tail logits: 16 lanes per (head, token), features strided by 16
+    const int grp = tid >> 4, gl = tid & 15;
+    for (int u = grp; u < G * nr; u += kMThreads / 16) {
+      const int h = u / nr, t = u - h * nr;
+      const int64_t hq_t = hkv * p.G + g0 + h;
+      float qv[D / 16], kv[D / 16];
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        qv[i] = ld_elem<TQ>(p.q, p.q_dtype, b * p.q_sb + hq_t * p.q_sh + gl + 16 * i);
+        kv[i] = ld_elem<TR>(p.kraw, p.raw_dtype,
+                            b * p.kr_sb + hkv * p.kr_sh + t * p.kr_st + gl + 16 * i);
+      }
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) a = __builtin_fmaf(qv[i], kv[i], a);
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) a += __shfl_xor(a, m, 16);
+      if (gl == 0) etl[h * FC_MAX_BLOCK + t] = a * p.scale_log2;
+    }
+  }
+  __syncthreads();
+  for (int h = wave; h < G; h += kWaves) {
+    float mx = -INFINITY;
+    for (int sp = lane; sp < ns; sp += 64) mx = fmaxf(mx, wsp[h * kFuseMaxSplits + sp]);
+    for (int t = lane; t < nr; t += 64) mx = fmaxf(mx, etl[h * FC_MAX_BLOCK + t]);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    float l = 0.f;
+    for (int sp = lane; sp < ns; sp += 64) {
+      const float pmv = wsp[h * kFuseMaxSplits + sp];
+      const float w = pmv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pmv - mx);
+      wsp[h * kFuseMaxSplits + sp] = w;
+      l = __builtin_fmaf(w, plv[h * kFuseMaxSplits + sp], l);
+    }
+    for (int t = lane; t < nr; t += 64) {
+      const float e = __builtin_amdgcn_exp2f(etl[h * FC_MAX_BLOCK + t] - mx);
+      etl[h * FC_MAX_BLOCK + t] = e;
+      l += e;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
+    if (lane == 0) inv[h] = 1.0f / l;
+  }
+  __syncthreads();
+
+  auto finish = [&](int h, int c, float4 o) {
+    for (int t = 0; t < nr; ++t) {
+      const float e = etl[h * FC_MAX_BLOCK + t];
+      const int64_t base = b * p.vr_sb + hkv * p.vr_sh + t * p.vr_st + 4 * c;
+      o.x = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 0), o.x);
+      o.y = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 1), o.y);
+      o.z = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 2), o.z);
+      o.w = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 3), o.w);
+    }
+    const float iv = inv[h];
+    const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
+    st_elem<TQ>(p.out, p.q_dtype, ob + 0, o.x * iv);
+    st_elem<TQ>(p.out, p.q_dtype, ob + 1, o.y * iv);
+    st_elem<TQ>(p.out, p.q_dtype, ob + 2, o.z * iv);
+    st_elem<TQ>(p.out, p.q_dtype, ob + 3, o.w * iv);
+  };
+  auto fma4 = [](float w, const float4& v, float4& o) {
+    o.x = __builtin_fmaf(w, v.x, o.x);
+    o.y = __builtin_fmaf(w, v.y, o.y);
+    o.z = __builtin_fmaf(w, v.z, o.z);
+    o.w = __builtin_fmaf(w, v.w, o.w);
+  };
+  if (one_task) {
+    if (tid < G * C4) {
+      const int h = tid / C4, c = tid - h * C4;
+      float4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < kPre; ++j)
+        if (j < ns) fma4(wsp[h * kFuseMaxSplits + j], pre[j], o);
+      finish(h, c, o);
+    }
+    return;
+  }
+  for (int task = tid; task < G * C4; task += kMThreads) {
+    const int h = task / C4, c = task - h * C4;
+    const float* wh = wsp + h * kFuseMaxSplits;
+    float4 o = {0.f, 0.f, 0.f, 0.f};
+    int sp = 0;
+    for (; sp + 8 <= ns; sp += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = part(h, sp + j, c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) fma4(wh[sp + j], v[j], o);
+    }
+    for (; sp < ns; ++sp) fma4(wh[sp], part(h, sp, c), o);
+    finish(h, c, o);
+  }
+}
+
 template <int SROWS, int DK, int GP>
 __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   constexpr int D = 32 * DK;
@@ -118,19 +301,25 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   constexpr int NT = PR / 16;
   constexpr int NS = PR / 32;
   constexpr int KDW = 2 * DK;  // K dwords per lane per tile
+  static_assert(DK % 2 == 0 && PR <= kPassRowsW, "feature width");
   __shared__ float s_lds[kWaves][16][kSPad];
   __shared__ _Float16 w_lds[kWaves][16][kWPad];
   __shared__ float sc_lds[kWaves][2][PR];  // K and V row scales of the pass
+  __shared__ float a_lds[FC_MAX_BLOCK * 4];
   __shared__ float comb[kWaves][16][3];
+  __shared__ int s_last;
 
   const int split = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const int64_t g0 = (int64_t)blockIdx.z * 16;
   const int64_t b = bh / p.Hkv, hkv = bh - b * p.Hkv;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, lc = lane & 15;
   const int G = (int)min<int64_t>(16, p.G - g0);  // heads of this group (<= GP)
   const int r = p.r;
+
+  for (int i = tid; i < r * SROWS; i += kMThreads) a_lds[i] = p.A[i];
 
   const int64_t nb_begin = (int64_t)split * p.blocks_per_split;
   const int64_t nb_end = min(p.nb, nb_begin + p.blocks_per_split);
@@ -139,7 +328,6 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   const int64_t spw = (nslab + kWaves - 1) / kWaves;
   const int64_t wrow0 = min(row_end, row_begin + (int64_t)wave * spw * 32);
   const int64_t wrow1 = min(row_end, wrow0 + spw * 32);
-  const int64_t last_row = row_end - 1;  // every load address is clamped to <= last_row
 
   const int8_t* kbase = p.kcodes + bh * p.kcap * SROWS * D;
   const int8_t* vbase = p.vcodes + bh * p.vcap * SROWS * D;
@@ -193,53 +381,98 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   for (int dv = 0; dv < DV; ++dv)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[dv][e] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  // running max / sum of head (lane % GP), identical in all lanes of a head;
-  // the accumulators hold acc * 2^-sig_run
+  // Head (lane % GP): reference max m_run (identical in all lanes of a head)
+  // and this lane's share of the exponential sum, both relative to m_run.
+  // The accumulators hold acc * 2^-sig_run.  Both references move only when
+  // a logit exceeds m_run + kLazyMax or a V row scale reaches 2^(sig_run+1).
   const int myh = lane % GP;
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_run = -INFINITY, l_lane = 0.f;
   int sig_run = -1000;
+  float wmul_run = INFINITY;  // 2^-sig_run
 
-  // ---- loads of one pass (addresses clamped in range; values masked later)
+  // loop-invariant lane offsets (bytes) of the pass loads
+  const int k_off = lc * D + lq * (D / 4);
+  int v_off[DV];
+#pragma unroll
+  for (int dv = 0; dv < DV; ++dv) v_off[dv] = 8 * lq * D + min(128 * dv + 8 * lc, D - 8);
+  const int sc_off = (lane % PR) * 4;
+
   uint32_t kr[NT][KDW];
   float ks_r, vs_r;
   auto load_k = [&](int64_t pr0) {
+    const int prow = (int)min<int64_t>(PR, wrow1 - pr0);
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kbase + pr0 * D, prow * D);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int64_t row = min(pr0 + 16 * t + lc, last_row);
-      const int8_t* src = kbase + row * D + lq * (D / 4);
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int h = 0; h < DK / 2; ++h) {
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(src + 16 * h);
+        const u32x4_t v = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, k_off + 16 * t * D + 16 * h, 0, 0));
 #pragma unroll
         for (int i = 0; i < 4; ++i) kr[t][4 * h + i] = v[i];
       }
-      if constexpr (DK & 1) {
-        const u32x2_t v = *reinterpret_cast<const u32x2_t*>(src + 16 * (DK / 2));
-        kr[t][KDW - 2] = v[0];
-        kr[t][KDW - 1] = v[1];
-      }
-    }
-    const int64_t srow = min(pr0 + (lane % PR), last_row);
-    ks_r = ksc[srow];
-    vs_r = vsc[srow];
+    ks_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         buf_rsrc(ksc + pr0, prow * 4), sc_off, 0, 0));
+    vs_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         buf_rsrc(vsc + pr0, prow * 4), sc_off, 0, 0));
   };
   uint32_t vr[NS][DV][16];
   auto load_v = [&](int64_t pr0) {
+    const int prow = (int)min<int64_t>(PR, wrow1 - pr0);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vbase + pr0 * D, prow * D);
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl)
 #pragma unroll
-      for (int dv = 0; dv < DV; ++dv) {
-        const int dcol = min(128 * dv + 8 * lc, D - 8);
+      for (int dv = 0; dv < DV; ++dv)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const int64_t row = min(pr0 + 32 * sl + 8 * lq + i, last_row);
-          const u32x2_t v = *reinterpret_cast<const u32x2_t*>(vbase + row * D + dcol);
+          const u32x2_t v = __builtin_bit_cast(
+              u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rv, v_off[dv] + (32 * sl + i) * D, 0, 0));
           vr[sl][dv][2 * i] = v[0];
           vr[sl][dv][2 * i + 1] = v[1];
         }
-      }
   };
 
+  // Output weights of the pass's (block, head) pairs, exponentials relative
+  // to mref, scaled by the V row scale * wm, into w_lds; returns this lane's
+  // largest logit and exponential sum.
+  auto weights = [&](int prow, float mref, float wm, float& pmax, float& lsum) {
+    pmax = -INFINITY;
+    lsum = 0.f;
+    if (myh >= G) return;
+    const int npair = (prow / SROWS) * GP;
+    for (int u = lane; u < npair; u += 64) {
+      const int row0 = (u / GP) * SROWS;
+      float sv[SROWS], w[SROWS];
+#pragma unroll
+      for (int j = 0; j < SROWS; ++j) {
+        sv[j] = s_lds[wave][myh][row0 + j] * sc_lds[wave][0][row0 + j];
+        w[j] = 0.f;
+      }
+      auto tap = [&](int t) {
+        float lg = 0.f;
+#pragma unroll
+        for (int j = 0; j < SROWS; ++j) lg = __builtin_fmaf(a_lds[t * SROWS + j], sv[j], lg);
+        pmax = fmaxf(pmax, lg);
+        const float e = __builtin_amdgcn_exp2f(lg - mref);
+        lsum += e;
+#pragma unroll
+        for (int j = 0; j < SROWS; ++j) w[j] = __builtin_fmaf(e, a_lds[t * SROWS + j], w[j]);
+      };
+      if (r <= kTapsUnrolled) {
+#pragma unroll
+        for (int t = 0; t < kTapsUnrolled; ++t)
+          if (t < r) tap(t);
+      } else {
+        for (int t = 0; t < r; ++t) tap(t);
+      }
+#pragma unroll
+      for (int j = 0; j < SROWS; ++j)
+        w_lds[wave][myh][row0 + j] = (_Float16)(w[j] * (sc_lds[wave][1][row0 + j] * wm));
+    }
+  };
+
+  __syncthreads();  // a_lds
   if (wrow0 < wrow1) load_k(wrow0);
   for (int64_t pr0 = wrow0; pr0 < wrow1; pr0 += PR) {
     const int prow = (int)min<int64_t>(PR, wrow1 - pr0);  // multiple of SROWS
@@ -249,13 +482,12 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
     // ------------------------------------------------------------ scores
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const bool ok = 16 * t + lc < prow;
       float4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < DK; ++kc) {
         uint32_t a0, a1, a2, a3;
-        biased_to_f16((ok ? kr[t][2 * kc] : 0u) ^ 0x80808080u, a0, a1);
-        biased_to_f16((ok ? kr[t][2 * kc + 1] : 0u) ^ 0x80808080u, a2, a3);
+        biased_to_f16(kr[t][2 * kc] ^ 0x80808080u, a0, a1);
+        biased_to_f16(kr[t][2 * kc + 1] ^ 0x80808080u, a2, a3);
         sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a0, a1, a2, a3), qop[kc], sacc,
                                                       0, 0, 0);
       }
@@ -268,82 +500,53 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
       sc_lds[wave][0][lane] = ks_r;
       sc_lds[wave][1][lane] = vs_r;
     }
-    // V row scale exponent of this pass
-    float smax = lane < prow ? vs_r : 0.f;
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) smax = fmaxf(smax, __shfl_xor(smax, m, 64));
-    const int sig_new = max(sig_run, pow2_exp_for(smax, 1));
-    const float wmul = ldexpf(1.0f, -sig_new);
+    // a V row scale past the headroom of the current exponent forces a rescale
+    const bool sig_need = vs_r * wmul_run >= 2.0f;
+    const float vs_pass = vs_r;
     // next pass's K codes and scales fly during the softmax and value stages
     if (pr0 + PR < wrow1) load_k(pr0 + PR);
     wave_lds_sync();
 
     // ------------------------------------------------------------ softmax
-    const int nblk = prow / SROWS;
-    const int npair = nblk * GP;
-    float pmax = -INFINITY;
-    for (int u = lane; u < npair; u += 64) {
-      const int bl = u / GP;
-      if (myh >= G) continue;
-      float sv[SROWS];
+    float pmax, lsum;
+    weights(prow, m_run, wmul_run, pmax, lsum);
+    const bool m_need = pmax > m_run + kLazyMax;
+    if (__builtin_amdgcn_ballot_w64(sig_need || m_need) != 0) {
+      // move the references: V exponent from the pass's largest row scale,
+      // head maxima from the pass's logits; recompute the weights
+      float smax = vs_pass;
 #pragma unroll
-      for (int j = 0; j < SROWS; ++j)
-        sv[j] = s_lds[wave][myh][bl * SROWS + j] * sc_lds[wave][0][bl * SROWS + j];
-      for (int t = 0; t < r; ++t) {
-        float lg = 0.f;
+      for (int m = 1; m < 64; m <<= 1) smax = fmaxf(smax, __shfl_xor(smax, m, 64));
+      const int sig_new = max(sig_run, pow2_exp_for(smax, 1));
 #pragma unroll
-        for (int j = 0; j < SROWS; ++j) lg = __builtin_fmaf(p.A[t * SROWS + j], sv[j], lg);
-        pmax = fmaxf(pmax, lg);
-      }
-    }
+      for (int m = GP; m < 64; m <<= 1) pmax = fmaxf(pmax, __shfl_xor(pmax, m, 64));
+      const float m_new = fmaxf(m_run, pmax);
+      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float wm = ldexpf(1.0f, -sig_new);
+      float pdummy;
+      weights(prow, m_new, wm, pdummy, lsum);
+      l_lane = l_lane * alpha + lsum;
+      // lane (q, c) register i holds head 4q + i
+      const float sfix = ldexpf(1.0f, sig_run - sig_new);
+      float al[4];
 #pragma unroll
-    for (int m = GP; m < 64; m <<= 1) pmax = fmaxf(pmax, __shfl_xor(pmax, m, 64));
-    const float m_new = fmaxf(m_run, pmax);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first pass
-    m_run = m_new;
-    float lsum = 0.f;
-    for (int u = lane; u < npair; u += 64) {
-      const int bl = u / GP;
-      if (myh >= G) continue;
-      float sv[SROWS], w[SROWS];
+      for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lq + i, 64) * sfix;
 #pragma unroll
-      for (int j = 0; j < SROWS; ++j) {
-        sv[j] = s_lds[wave][myh][bl * SROWS + j] * sc_lds[wave][0][bl * SROWS + j];
-        w[j] = 0.f;
-      }
-      for (int t = 0; t < r; ++t) {
-        float lg = 0.f;
+      for (int dv = 0; dv < DV; ++dv)
 #pragma unroll
-        for (int j = 0; j < SROWS; ++j) lg = __builtin_fmaf(p.A[t * SROWS + j], sv[j], lg);
-        const float e = __builtin_amdgcn_exp2f(lg - m_new);
-        lsum += e;
+        for (int e = 0; e < 8; ++e)
 #pragma unroll
-        for (int j = 0; j < SROWS; ++j) w[j] = __builtin_fmaf(e, p.A[t * SROWS + j], w[j]);
-      }
-#pragma unroll
-      for (int j = 0; j < SROWS; ++j)
-        w_lds[wave][myh][bl * SROWS + j] =
-            (_Float16)(w[j] * (sc_lds[wave][1][bl * SROWS + j] * wmul));
+          for (int i = 0; i < 4; ++i) acc[dv][e][i] *= al[i];
+      m_run = m_new;
+      sig_run = sig_new;
+      wmul_run = wm;
+    } else {
+      l_lane += lsum;
     }
     // rows past the pass end inside the last slab carry zero weight
     if (prow < rend)
       for (int i = prow + lane; i < rend; i += 64)
         for (int h = 0; h < G; ++h) w_lds[wave][h][i] = (_Float16)0.f;
-#pragma unroll
-    for (int m = GP; m < 64; m <<= 1) lsum += __shfl_xor(lsum, m, 64);
-    l_run = l_run * alpha + lsum;
-    // rescale the accumulators: lane (q, c) register i holds head 4q + i
-    const float sfix = ldexpf(1.0f, max(sig_run - sig_new, -126));
-    sig_run = sig_new;
-    float al[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lq + i, 64) * sfix;
-#pragma unroll
-    for (int dv = 0; dv < DV; ++dv)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[dv][e][i] *= al[i];
     wave_lds_sync();
 
     // ------------------------------------------------------------ values
@@ -355,17 +558,14 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
       const half8_t wop = __builtin_bit_cast(half8_t, wa);
 #pragma unroll
       for (int dv = 0; dv < DV; ++dv) {
-        const bool dok = 128 * dv + 8 * lc < D;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           // row pair (a, b) = (2pp, 2pp+1): t0 = [a0 b0 a1 b1], t1 = [a2 b2 a3 b3]
           uint32_t t0[4], t1[4];
 #pragma unroll
           for (int pp = 0; pp < 4; ++pp) {
-            const bool oka = dok && 32 * sl + 8 * lq + 2 * pp < prow;
-            const bool okb = dok && 32 * sl + 8 * lq + 2 * pp + 1 < prow;
-            const uint32_t ra = (oka ? vr[sl][dv][2 * (2 * pp) + hh] : 0u) ^ 0x80808080u;
-            const uint32_t rb = (okb ? vr[sl][dv][2 * (2 * pp + 1) + hh] : 0u) ^ 0x80808080u;
+            const uint32_t ra = vr[sl][dv][2 * (2 * pp) + hh] ^ 0x80808080u;
+            const uint32_t rb = vr[sl][dv][2 * (2 * pp + 1) + hh] ^ 0x80808080u;
             t0[pp] = __builtin_amdgcn_perm(rb, ra, 0x05010400u);
             t1[pp] = __builtin_amdgcn_perm(rb, ra, 0x07030602u);
           }
@@ -390,10 +590,12 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
 
   // ---- combine the wavefronts.  Lane c < GP carries head c's (max, sum);
   // each wave's accumulators carry a factor 2^-sig_run.
+#pragma unroll
+  for (int m = GP; m < 64; m <<= 1) l_lane += __shfl_xor(l_lane, m, 64);
   if (lane < GP) {
     comb[wave][lane][0] = m_run;
-    comb[wave][lane][1] = l_run;
-    comb[wave][lane][2] = ldexpf(1.0f, max(sig_run, -126));
+    comb[wave][lane][1] = l_lane;
+    comb[wave][lane][2] = ldexpf(1.0f, sig_run);
   }
   float* obuf = &s_lds[0][0][0];  // [wave*4 + i][D] for the 4 heads of a lane group
   for (int h0 = 0; h0 < G; h0 += 4) {
@@ -427,12 +629,46 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
       }
       const int64_t bq = b * (p.Hkv * p.G) + hkv * p.G + g0 + h;
       const int64_t slot = bq * p.n_splits + split;
-      p.pacc[slot * D + d] = o;
+      // agent-coherent stores: another workgroup may merge them
+      __hip_atomic_store(p.pacc + slot * D + d, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (d == 0) {
-        p.pm[slot] = M;
-        p.pl[slot] = l;
+        __hip_atomic_store(p.pm + slot, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.pl + slot, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+  }
+  if (!p.fused) return;
+
+  // ---- fused merge.  Each workgroup publishes its partials and counts its
+  // arrival; the last of the n_splits workgroups of this (batch, kv head,
+  // head group) combines them with the raw tail and returns the counter to
+  // zero for the next call.
+  // Publication without cache-wide writeback/invalidate (each costs ~0.1 us
+  // and they serialize per XCD): partials are device-scope stores, complete
+  // (vmcnt 0) before the arrival is counted, and are read back with
+  // device-scope loads.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (tid == 0) {
+    unsigned int* ctr = p.counters + ((int64_t)blockIdx.y * gridDim.z + blockIdx.z);
+    const unsigned int old = atomicAdd(ctr, 1u);
+    const bool last = old + 1 == (unsigned int)p.n_splits;
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  const bool q16 = p.q_dtype == FC_F16;
+  if (p.raw_dtype == p.q_dtype) {
+    if (q16)
+      fused_merge<D, f16_t, f16_t>(p, b, hkv, g0, G, tid, &s_lds[0][0][0]);
+    else
+      fused_merge<D, bf16_t, bf16_t>(p, b, hkv, g0, G, tid, &s_lds[0][0][0]);
+  } else {
+    fused_merge<D, void, void>(p, b, hkv, g0, G, tid, &s_lds[0][0][0]);
   }
 }
 
@@ -455,12 +691,14 @@ bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q
          al16(key->rows) && al16(value->rows);
 }
 
+bool split_i8_mfma_fusable(int n_splits) { return n_splits <= kFuseMaxSplits; }
+
 int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
                          int64_t Hq, int64_t Hkv, int64_t D, int r, int s, int64_t nb,
                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
-                         hipStream_t st) {
-  MfmaArgs a;
+                         const MfmaFuse* fuse, hipStream_t st) {
+  MfmaArgs a{};
   a.q = q;
   a.q_dtype = q_dtype;
   a.q_sb = q_sb;
@@ -482,6 +720,24 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   a.pm = pm;
   a.pl = pl;
   a.pacc = pacc;
+  if (fuse) {
+    if (n_splits > kFuseMaxSplits || !fuse->counters) return FC_ERR_ARG;
+    a.fused = 1;
+    a.kraw = key->raw;
+    a.vraw = value->raw;
+    a.raw_dtype = fuse->raw_dtype;
+    a.kr_sb = key->raw_sb;
+    a.kr_sh = key->raw_sh;
+    a.kr_st = key->raw_st;
+    a.vr_sb = value->raw_sb;
+    a.vr_sh = value->raw_sh;
+    a.vr_st = value->raw_st;
+    a.n_raw = fuse->n_raw;
+    a.out = fuse->out;
+    a.o_sb = fuse->o_sb;
+    a.o_sh = fuse->o_sh;
+    a.counters = fuse->counters;
+  }
   const int64_t G = Hq / Hkv;
   const int gg = (int)std::min<int64_t>(G, 16);
   const int gp = gg <= 1 ? 1 : gg <= 2 ? 2 : gg <= 4 ? 4 : gg <= 8 ? 8 : 16;

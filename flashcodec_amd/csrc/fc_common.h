@@ -96,4 +96,22 @@ __device__ __forceinline__ float group_max_rt(float v, int width) {
   return v;
 }
 
+// element `idx` of a float tensor of dtype `dt` (FC_F32 / FC_F16 / FC_BF16)
+__device__ __forceinline__ float load_q(const void* q, int dt, int64_t idx) {
+  switch (dt) {
+    case FC_F16: return to_f32(static_cast<const f16_t*>(q)[idx]);
+    case FC_BF16: return to_f32(static_cast<const bf16_t*>(q)[idx]);
+    default: return static_cast<const float*>(q)[idx];
+  }
+}
+
+// store v (round to nearest even) as element `idx` of a tensor of dtype `dt`
+__device__ __forceinline__ void store_any(void* p, int dt, int64_t idx, float v) {
+  switch (dt) {
+    case FC_F16: static_cast<f16_t*>(p)[idx] = from_f32<f16_t>(v); break;
+    case FC_BF16: static_cast<bf16_t*>(p)[idx] = from_f32<bf16_t>(v); break;
+    default: static_cast<float*>(p)[idx] = v; break;
+  }
+}
+
 }  // namespace fc

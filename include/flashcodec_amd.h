@@ -166,7 +166,11 @@ typedef struct fc_stream_view {
 
 /*
  * Bytes of device workspace fc_decode_attention needs for B*Hq query heads,
- * head size D and n_splits splits (0 when n_splits == 0).
+ * head size D and n_splits splits (0 when n_splits == 0).  The workspace
+ * must be zero-filled before its first use: it starts with arrival counters
+ * that every call returns to zero, so one workspace (of the largest size
+ * needed) serves any number of calls ordered on one stream.  Calls that may
+ * run concurrently need separate workspaces.
  */
 int64_t fc_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t D,
                                      int n_splits);
@@ -187,8 +191,11 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G,
  *   out (B, Hq, 1, D) in q_dtype with element strides o_sb, o_sh.
  * Query head hq reads kv head hq / G (G = Hq / Hkv).  Scores are
  * scale * q . (A S)[p]; softmax in fp32; output (p A) S + p_raw V_raw.
- * Every query head reads its kv head's rows once per group of up to eight
- * query heads.  `workspace` must hold fc_attention_workspace_bytes(...).
+ * Every query head reads its kv head's rows once per group of up to 16
+ * query heads.  `workspace` must hold fc_attention_workspace_bytes(...) and
+ * follow its zero-fill rule.  int8 jpeg archives with fp16/bf16 queries and
+ * D in {64, 128, 256} run as one launch (the split pass merges its own
+ * partials); other cases launch the split and merge passes.
  *
  * Replaces codec_decode_attention's jpeg Triton path and its png / torch
  * path (flashcodec/attention.py:64-140;
