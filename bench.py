@@ -95,8 +95,9 @@ def split_kernel_name():
 
 
 def read_pmc_traffic():
-    """HBM bytes per split launch from the committed PMC summary, if any."""
-    if not os.path.exists(PMC_SUMMARY):
+    """HBM bytes per launch of the matrix-core kernel from the committed PMC
+    summary, if any (None for the vector-ALU variant, which it does not cover)."""
+    if os.environ.get("FLASHCODEC_AMD_ATTN", "").startswith("v") or not os.path.exists(PMC_SUMMARY):
         return None
     for line in open(PMC_SUMMARY):
         if line.startswith("traffic_bytes_per_launch:"):
