@@ -661,13 +661,14 @@ using namespace fc;
 
 namespace fc {
 
-// Workspace of one call: kCounterWords 32-bit arrival counters of the fused
-// merge (a fixed region, so calls of any shape find their counters at the same
-// place), then pm | pl | pacc (fp32, sections 16-byte aligned, 256-byte
-// rounded).  The counters must be zero before a workspace's first use; every
-// call leaves them zero.
-constexpr int64_t kCounterWords = 16384;
+// Workspace of one call: kCounterWords 32-bit counters of the matrix-core
+// split pass (pass queues and arrival counts; a fixed region, so calls of any
+// shape find their counters at the same place), then pm | pl | pacc (fp32,
+// sections 16-byte aligned, 256-byte rounded).  The counters must be zero
+// before a workspace's first use; every call leaves them zero.
+constexpr int64_t kCounterWords = 262144;  // 1 MiB: 2 x 4096 counters, one per 128-byte line
 constexpr int64_t kCounterBytes = kCounterWords * 4;
+constexpr int64_t kCounterStride = 32;  // words between counters (no two share a line)
 static int64_t ws_partial_bytes(int64_t B, int64_t Hq, int64_t D, int n_splits) {
   const int64_t slots = B * Hq * (int64_t)n_splits;
   const int64_t head = (slots + 3) / 4 * 4;
@@ -744,12 +745,12 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
   float* pacc = pl + ws_head;
 
   if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_JPEG_I8 &&
-      split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) && mfma_split_allowed()) {
+      split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) &&
+      2 * B * Hkv * ((G + 15) / 16) * kCounterStride <= kCounterWords && mfma_split_allowed()) {
     if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
     // one launch per call when the merge is requested too: the split pass's
     // last workgroup per head group merges
-    const bool fuse = (parts & kPartMerge) && split_i8_mfma_fusable(n_splits) &&
-                      B * Hkv * ((G + 15) / 16) <= kCounterWords;
+    const bool fuse = (parts & kPartMerge) && split_i8_mfma_fusable(n_splits);
     MfmaFuse fz{};
     if (fuse) {
       fz.raw_dtype = stream_dtype;
@@ -757,11 +758,10 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
       fz.out = out;
       fz.o_sb = o_sb;
       fz.o_sh = o_sh;
-      fz.counters = counters;
     }
     const int rc = launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb, key,
-                                        value, A, scale_log2, pm, pl, pacc, n_splits,
-                                        fuse ? &fz : nullptr, st);
+                                        value, A, scale_log2, pm, pl, pacc, n_splits, counters,
+                                        kCounterWords, kCounterStride, fuse ? &fz : nullptr, st);
     if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit)) {
     // VEC = 8 features per lane; LPR = lanes per row

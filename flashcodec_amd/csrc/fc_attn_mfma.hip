@@ -1,38 +1,42 @@
 // Split pass of the decode attention for int8 jpeg archives on gfx950 matrix
-// cores.
+// cores, with the merge of the split partials fused in.
 //
 // With G query heads per kv head, a block's work is a skinny GEMM: scores
 // S = K_rows . Q^T (M = rows, N = heads, K-dim = features) and output
 // O = W . V_rows (M = heads, N = features, K-dim = rows).  On the vector ALU
-// that costs ~4 fp32 FMAs per code byte per head group — as much VALU time
-// as the HBM time of the bytes — so both products run as
-// v_mfma_f32_16x16x32_f16 and the VALU only converts codes and runs the
-// softmax.
+// that costs ~4 fp32 FMAs per code byte per head group — more VALU time than
+// the HBM time of the bytes — so both products run on the matrix cores and
+// the VALU runs the softmax and the V code conversion.
 //
-// Codes convert to f16 exactly: for a code byte b, u = b ^ 0x80 = b + 128;
-// the f16 with bits 0x6400 | u is 1024 + u, and one packed f16 add of -1152
-// (exact) leaves b.  Queries enter as f16 scaled by a per-head power of two
-// (exact for fp16 queries, and for bf16 queries in the normal f16 range);
-// output weights enter as f16 scaled by a per-workgroup power of two.
-// Products are exact in fp32 and the matrix cores accumulate in fp32.
+// Scores: v_mfma_i32_16x16x64_i8 straight on the K codes.  Each head's query
+// is scaled by a power of two to integers of at most 14 bits and split as
+// q' = 256 hi + lo (int8 hi, lo): 256 (K . hi) + (K . lo) is the exact
+// integer score.
+// Values: v_mfma_f32_16x16x32_f16.  A V code b converts to f16 exactly:
+// u = b ^ 0x80 = b + 128, the f16 with bits 0x6400 | u is 1024 + u, and one
+// packed f16 add of -1152 (exact) leaves b.  Output weights enter as f16
+// scaled by a per-wavefront power of two; products are exact in fp32 and
+// the matrix cores accumulate in fp32.
 //
 // Workgroup = 4 wavefronts = one (batch, kv head, split, group of <= 16 query
 // heads).  Each wavefront owns a contiguous run of 32-row slabs of the split
-// and walks it in passes of up to 128 rows:
-//   scores: per 16-row tile, lane (q, m) holds row m, features
-//      [q*D/4, (q+1)*D/4) (any relabelling of the feature axis shared by both
-//      operands is allowed), DK products of 32 features; lane (q, c < G) gets
-//      the scores of rows 4q..4q+3 for head c and parks them in LDS.
+// and walks it in passes of 64 rows (32 at D = 256):
+//   scores: per 16-row tile and 64-feature chunk k, lane (q, m) holds row m,
+//      features 64k + 16q .. +15 (one 64-byte run of each row per load; any
+//      relabelling of the feature axis shared by both operands is allowed);
+//      lane (q, c < G) gets the scores of rows 4q..4q+3 for head c and parks
+//      them in LDS.
 //   softmax: (block, head) pairs over all 64 lanes (head = lane % GP): r
-//      logits from the s scores, the pass maximum per head, exponentials and
-//      s output weights w_j = sum_p 2^(logit_p - m) A[p][j] times the V row
-//      scale, stored as f16 in LDS.
+//      logits from the s scores, exponentials against a running reference
+//      maximum, and s output weights w_j = sum_p 2^(logit_p - m) A[p][j] times
+//      the V row scale, stored as f16 in LDS.
 //   values: per 32-row slab, lane (q, c) loads rows 8q..8q+7, bytes
 //      [8c, 8c+8) (16 lanes cover a 128-byte row) and transposes the 8x8
 //      byte tile in registers, so matrix-core instance e of the slab sees
 //      feature 8c + e in column c.
-// The four wavefronts combine their (max, sum, acc) in LDS and write one
-// partial per (query head, split) for the merge kernel.
+// The four wavefronts combine their (max, sum, acc) in LDS into one partial
+// per (query head, split); the last workgroup of each head group to finish
+// merges the partials with the raw tail (fused_merge).
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -47,6 +51,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 
 struct MfmaArgs {
   const void* q;
@@ -63,6 +68,11 @@ struct MfmaArgs {
   float scale_log2;
   int64_t blocks_per_split;
   int n_splits;
+  int64_t ngroups;  // B * Hkv * zg (zg = groups of <= 16 query heads per kv head)
+  int zg;
+  unsigned int* arrive;  // per group: workgroups done (zero between calls)
+  unsigned int* passq;   // per group: next pass to take (zero between calls)
+  int64_t cstride;       // words between the counters of consecutive groups
   float* pm;
   float* pl;
   float* pacc;
@@ -75,11 +85,11 @@ struct MfmaArgs {
   int64_t n_raw;
   void* out;
   int64_t o_sb, o_sh;
-  unsigned int* counters;  // one per (batch, kv head, head group), zero between calls
 };
 
 constexpr int kMThreads = 256;
 constexpr int kFuseMaxSplits = 64;  // split count limit of the fused merge
+
 constexpr int kWaves = kMThreads / 64;
 constexpr int kPassRowsW = 64;         // max rows per wavefront pass
 constexpr int kSPad = kPassRowsW + 4;  // float stride of a score row in LDS
@@ -96,25 +106,6 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-__device__ __forceinline__ uint32_t f16x2_sub1152(uint32_t v) {
-  half2_t h = __builtin_bit_cast(half2_t, v);
-  const half2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-  h = h + off;
-  return __builtin_bit_cast(uint32_t, h);
-}
-
-// four int8 codes (one dword, already xor 0x80808080) -> f16 pairs
-// (codes 0, 1) and (codes 2, 3)
-__device__ __forceinline__ void biased_to_f16(uint32_t u, uint32_t& lo, uint32_t& hi) {
-  lo = f16x2_sub1152(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
-  hi = f16x2_sub1152(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
-}
-
-__device__ __forceinline__ half8_t as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  const u32x4_t v = {a, b, c, d};
-  return __builtin_bit_cast(half8_t, v);
 }
 
 // exponent e with x * 2^-e in [2^(target-1), 2^target) for x > 0; 0 for x == 0
@@ -292,7 +283,7 @@ __device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g
 }
 
 template <int SROWS, int DK, int GP>
-__global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
+__global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma(MfmaArgs p) {
   constexpr int D = 32 * DK;
   constexpr int DV = (D + 127) / 128;  // 128-feature groups of the value product
   // rows per wavefront pass: its K codes (NT tiles) and V codes (NS slabs)
@@ -309,9 +300,13 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   __shared__ float comb[kWaves][16][3];
   __shared__ int s_last;
 
-  const int split = blockIdx.x;
-  const int64_t bh = blockIdx.y;
-  const int64_t g0 = (int64_t)blockIdx.z * 16;
+  // 1-D grid, split-major: workgroup L runs split s of group g; the splits of
+  // a group are spread over the dispatch order and over the XCDs
+  const int64_t L = blockIdx.x;
+  const int split = (int)(L / p.ngroups);
+  const int64_t g = ((L % p.ngroups) - split % p.ngroups + p.ngroups) % p.ngroups;
+  const int64_t bh = g / p.zg;
+  const int64_t g0 = (g % p.zg) * 16;
   const int64_t b = bh / p.Hkv, hkv = bh - b * p.Hkv;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -321,13 +316,18 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
 
   for (int i = tid; i < r * SROWS; i += kMThreads) a_lds[i] = p.A[i];
 
-  const int64_t nb_begin = (int64_t)split * p.blocks_per_split;
-  const int64_t nb_end = min(p.nb, nb_begin + p.blocks_per_split);
-  const int64_t row_begin = nb_begin * SROWS, row_end = nb_end * SROWS;
-  const int64_t nslab = (row_end - row_begin + 31) / 32;
-  const int64_t spw = (nslab + kWaves - 1) / kWaves;
-  const int64_t wrow0 = min(row_end, row_begin + (int64_t)wave * spw * 32);
-  const int64_t wrow1 = min(row_end, wrow0 + spw * 32);
+  // The group's rows are cut into passes of PR rows; every wavefront of the
+  // group's n_splits workgroups takes the next untaken pass from the group's
+  // queue until none is left, so faster wavefronts take more passes.
+  const int64_t rows_total = p.nb * SROWS;
+  const int64_t npass = (rows_total + PR - 1) / PR;
+  unsigned int* passq = p.passq + g * p.cstride;
+  auto grab = [&]() -> unsigned int {  // result in lane 0, read when needed
+    unsigned int v = 0;
+    if (lane == 0) v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return v;
+  };
+  auto pass_of = [](unsigned int v) { return (int64_t)__builtin_amdgcn_readfirstlane((int)v); };
 
   const int8_t* kbase = p.kcodes + bh * p.kcap * SROWS * D;
   const int8_t* vbase = p.vcodes + bh * p.vcap * SROWS * D;
@@ -338,8 +338,9 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   // features q*D/4 + 8*kc + i of product kc, scaled per head by a power of two
   const bool hq_ok = lc < G;
   const int64_t hq = hkv * p.G + g0 + (hq_ok ? lc : 0);
+  // lane (q, c) holds features 64 k + 16 q + [0, 16) of chunk k
   const uint16_t* qrow =
-      static_cast<const uint16_t*>(p.q) + b * p.q_sb + hq * p.q_sh + lq * (D / 4);
+      static_cast<const uint16_t*>(p.q) + b * p.q_sb + hq * p.q_sh + 16 * lq;
   const bool q_f16 = p.q_dtype == FC_F16;
   float qf[DK][8];
   float qmax = 0.f;
@@ -348,7 +349,7 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   // bit-cast to half2 inside an unrolled loop)
 #pragma unroll
   for (int kc = 0; kc < DK; ++kc) {
-    const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + 8 * kc);
+    const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + 64 * (kc / 2) + 8 * (kc % 2));
     if (q_f16) {
       const half8_t h = __builtin_bit_cast(half8_t, raw);
 #pragma unroll
@@ -368,13 +369,30 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   }
   qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
   qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+  // 14-bit integer query per head (largest magnitude in [2^13, 2^14)), split
+  // q' = 256 * hi + lo into two int8 operands: scores are exact integers
+  // 256 * (K . hi) + (K . lo) from the int8 matrix cores
   const int qe = pow2_exp_for(qmax, 14);
-  half8_t qop[DK];
+  constexpr int NC = D / 64;  // 64-feature chunks of the score product
+  i32x4_t qhi[NC], qlo[NC];
 #pragma unroll
-  for (int kc = 0; kc < DK; ++kc)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qop[kc][i] = (_Float16)ldexpf(qf[kc][i], -qe);
-  const float head_mul = ldexpf(p.scale_log2, qe);  // raw score -> base-2 logit / K scale
+    for (int w = 0; w < 4; ++w) {
+      uint32_t hw = 0, lw = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 16 * c + 4 * w + j;  // feature 64c + 16q + 4w + j
+        const int qi = (int)rintf(ldexpf(qf[e / 8][e % 8], -qe));
+        const int lo = (int)(int8_t)(qi & 0xff);
+        const int hi = (qi - lo) >> 8;
+        lw |= (uint32_t)(lo & 0xff) << (8 * j);
+        hw |= (uint32_t)(hi & 0xff) << (8 * j);
+      }
+      qhi[c][w] = (int)hw;
+      qlo[c][w] = (int)lw;
+    }
+  const float head_mul = ldexpf(p.scale_log2, qe);  // integer score -> base-2 logit / K scale
 
   float4_t acc[DV][8];
 #pragma unroll
@@ -391,7 +409,7 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   float wmul_run = INFINITY;  // 2^-sig_run
 
   // loop-invariant lane offsets (bytes) of the pass loads
-  const int k_off = lc * D + lq * (D / 4);
+  const int k_off = lc * D + 16 * lq;
   int v_off[DV];
 #pragma unroll
   for (int dv = 0; dv < DV; ++dv) v_off[dv] = 8 * lq * D + min(128 * dv + 8 * lc, D - 8);
@@ -399,15 +417,14 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
 
   uint32_t kr[NT][KDW];
   float ks_r, vs_r;
-  auto load_k = [&](int64_t pr0) {
-    const int prow = (int)min<int64_t>(PR, wrow1 - pr0);
+  auto load_k = [&](int64_t pr0, int prow) {
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kbase + pr0 * D, prow * D);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int h = 0; h < DK / 2; ++h) {
         const u32x4_t v = __builtin_bit_cast(
-            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, k_off + 16 * t * D + 16 * h, 0, 0));
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, k_off + 16 * t * D + 64 * h, 0, 0));
 #pragma unroll
         for (int i = 0; i < 4; ++i) kr[t][4 * h + i] = v[i];
       }
@@ -417,8 +434,7 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
                                          buf_rsrc(vsc + pr0, prow * 4), sc_off, 0, 0));
   };
   uint32_t vr[NS][DV][16];
-  auto load_v = [&](int64_t pr0) {
-    const int prow = (int)min<int64_t>(PR, wrow1 - pr0);
+  auto load_v = [&](int64_t pr0, int prow) {
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vbase + pr0 * D, prow * D);
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl)
@@ -473,26 +489,32 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
   };
 
   __syncthreads();  // a_lds
-  if (wrow0 < wrow1) load_k(wrow0);
-  for (int64_t pr0 = wrow0; pr0 < wrow1; pr0 += PR) {
-    const int prow = (int)min<int64_t>(PR, wrow1 - pr0);  // multiple of SROWS
-    const int rend = ((prow + 31) / 32) * 32;
-    load_v(pr0);
+  auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
+  int64_t cur = pass_of(grab());
+  unsigned int nxt_v = grab();
+  if (cur < npass) load_k(cur * PR, rows_of(cur));
+  while (cur < npass) {
+    const int64_t pr0 = cur * PR;
+    const int prow = rows_of(cur);  // multiple of SROWS
+    load_v(pr0, prow);
+    const unsigned int nxt2_v = grab();  // the pass after next, read one pass later
 
     // ------------------------------------------------------------ scores
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      float4_t sacc = {0.f, 0.f, 0.f, 0.f};
+      i32x4_t shi = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
 #pragma unroll
-      for (int kc = 0; kc < DK; ++kc) {
-        uint32_t a0, a1, a2, a3;
-        biased_to_f16(kr[t][2 * kc] ^ 0x80808080u, a0, a1);
-        biased_to_f16(kr[t][2 * kc + 1] ^ 0x80808080u, a2, a3);
-        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(a0, a1, a2, a3), qop[kc], sacc,
-                                                      0, 0, 0);
+      for (int c = 0; c < NC; ++c) {
+        // lane (q, m): row m, features 64c + 16q .. +15, straight from the load
+        const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
+                           (int)kr[t][4 * c + 3]};
+        shi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qhi[c], shi, 0, 0, 0);
+        slo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qlo[c], slo, 0, 0, 0);
       }
       if (lc < G) {
-        const float4_t sv = sacc * head_mul;
+        float4_t sv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = (float)(shi[i] * 256 + slo[i]) * head_mul;
         *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = sv;
       }
     }
@@ -504,7 +526,8 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
     const bool sig_need = vs_r * wmul_run >= 2.0f;
     const float vs_pass = vs_r;
     // next pass's K codes and scales fly during the softmax and value stages
-    if (pr0 + PR < wrow1) load_k(pr0 + PR);
+    const int64_t nxt = pass_of(nxt_v);
+    if (nxt < npass) load_k(nxt * PR, rows_of(nxt));
     wave_lds_sync();
 
     // ------------------------------------------------------------ softmax
@@ -543,16 +566,15 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
     } else {
       l_lane += lsum;
     }
-    // rows past the pass end inside the last slab carry zero weight
-    if (prow < rend)
-      for (int i = prow + lane; i < rend; i += 64)
+    // rows past the pass end carry zero weight (their codes read as zero)
+    if (prow < PR)
+      for (int i = prow + lane; i < PR; i += 64)
         for (int h = 0; h < G; ++h) w_lds[wave][h][i] = (_Float16)0.f;
     wave_lds_sync();
 
     // ------------------------------------------------------------ values
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl) {
-      if (32 * sl >= rend) continue;
       u32x4_t wa = *reinterpret_cast<const u32x4_t*>(&w_lds[wave][lc][32 * sl + 8 * lq]);
       if (lc >= G) wa = (u32x4_t){0u, 0u, 0u, 0u};
       const half8_t wop = __builtin_bit_cast(half8_t, wa);
@@ -571,21 +593,26 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
           }
 #pragma unroll
           for (int ee = 0; ee < 4; ++ee) {
-            uint32_t o[4];
+            // the operand is built in place as one 4-dword vector (no copies)
+            half8_t ov;
 #pragma unroll
             for (int pp = 0; pp < 4; ++pp) {
               const uint32_t src = ee < 2 ? t0[pp] : t1[pp];
               const uint32_t sel = (ee & 1) ? 0x04030402u : 0x04010400u;
-              o[pp] = f16x2_sub1152(__builtin_amdgcn_perm(0x64646464u, src, sel));
+              const half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, src, sel)) +
+                                 (half2_t){(_Float16)-1152.0f, (_Float16)-1152.0f};
+              ov[2 * pp] = h2[0];
+              ov[2 * pp + 1] = h2[1];
             }
             const int e = 4 * hh + ee;
-            acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                wop, as_half8(o[0], o[1], o[2], o[3]), acc[dv][e], 0, 0, 0);
+            acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, ov, acc[dv][e], 0, 0, 0);
           }
         }
       }
     }
     wave_lds_sync();
+    cur = nxt;
+    nxt_v = nxt2_v;
   }
 
   // ---- combine the wavefronts.  Lane c < GP carries head c's (max, sum);
@@ -637,29 +664,30 @@ __global__ __launch_bounds__(kMThreads) void attn_split_i8_mfma(MfmaArgs p) {
       }
     }
   }
-  if (!p.fused) return;
-
-  // ---- fused merge.  Each workgroup publishes its partials and counts its
-  // arrival; the last of the n_splits workgroups of this (batch, kv head,
-  // head group) combines them with the raw tail and returns the counter to
-  // zero for the next call.
+  // ---- arrival.  Each workgroup publishes its partials and counts its
+  // arrival; the last of the group's n_splits workgroups returns the group's
+  // counters to zero for the next call and, in the fused form, merges the
+  // partials with the raw tail.
   // Publication without cache-wide writeback/invalidate (each costs ~0.1 us
   // and they serialize per XCD): partials are device-scope stores, complete
-  // (vmcnt 0) before the arrival is counted, and are read back with
-  // device-scope loads.
+  // (vmcnt 0, which also covers the pass-queue atomics) before the arrival is
+  // counted, and are read back with device-scope loads.
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   if (tid == 0) {
-    unsigned int* ctr = p.counters + ((int64_t)blockIdx.y * gridDim.z + blockIdx.z);
-    const unsigned int old = atomicAdd(ctr, 1u);
+    unsigned int* arrive = p.arrive + g * p.cstride;
+    const unsigned int old = atomicAdd(arrive, 1u);
     const bool last = old + 1 == (unsigned int)p.n_splits;
-    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) {
+      __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     s_last = last ? 1 : 0;
   }
   __syncthreads();
-  if (!s_last) return;
+  if (!s_last || !p.fused) return;
 
   const bool q16 = p.q_dtype == FC_F16;
   if (p.raw_dtype == p.q_dtype) {
@@ -697,6 +725,7 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          int64_t Hq, int64_t Hkv, int64_t D, int r, int s, int64_t nb,
                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
+                         unsigned int* counters, int64_t counter_words, int64_t stride,
                          const MfmaFuse* fuse, hipStream_t st) {
   MfmaArgs a{};
   a.q = q;
@@ -721,7 +750,7 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   a.pl = pl;
   a.pacc = pacc;
   if (fuse) {
-    if (n_splits > kFuseMaxSplits || !fuse->counters) return FC_ERR_ARG;
+    if (n_splits > kFuseMaxSplits) return FC_ERR_ARG;
     a.fused = 1;
     a.kraw = key->raw;
     a.vraw = value->raw;
@@ -736,12 +765,17 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
     a.out = fuse->out;
     a.o_sb = fuse->o_sb;
     a.o_sh = fuse->o_sh;
-    a.counters = fuse->counters;
   }
   const int64_t G = Hq / Hkv;
   const int gg = (int)std::min<int64_t>(G, 16);
   const int gp = gg <= 1 ? 1 : gg <= 2 ? 2 : gg <= 4 ? 4 : gg <= 8 ? 8 : 16;
-  const dim3 grid((unsigned)n_splits, (unsigned)(B * Hkv), (unsigned)((G + 15) / 16));
+  a.zg = (int)((G + 15) / 16);
+  a.ngroups = B * Hkv * a.zg;
+  if (!counters || 2 * a.ngroups * stride > counter_words) return FC_ERR_ARG;
+  a.arrive = counters;
+  a.passq = counters + counter_words / 2;
+  a.cstride = stride;
+  const dim3 grid((unsigned)(a.ngroups * n_splits));
   const int rc = mfma_with_int<1, 2, 4>(s, [&](auto sc) {
     constexpr int SR = decltype(sc)::value;
     return mfma_with_int<2, 4, 8>((int)(D / 32), [&](auto dc) {
