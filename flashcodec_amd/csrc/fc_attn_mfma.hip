@@ -232,6 +232,14 @@ __device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g
   }
   __syncthreads();
 
+  auto finish_out = [&](int h, int c, const float4& o) {
+    const float iv = inv[h];
+    const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
+    st_elem<TQ>(p.out, p.q_dtype, ob + 0, o.x * iv);
+    st_elem<TQ>(p.out, p.q_dtype, ob + 1, o.y * iv);
+    st_elem<TQ>(p.out, p.q_dtype, ob + 2, o.z * iv);
+    st_elem<TQ>(p.out, p.q_dtype, ob + 3, o.w * iv);
+  };
   auto finish = [&](int h, int c, float4 o) {
     for (int t = 0; t < nr; ++t) {
       const float e = etl[h * FC_MAX_BLOCK + t];
@@ -241,12 +249,7 @@ __device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g
       o.z = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 2), o.z);
       o.w = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 3), o.w);
     }
-    const float iv = inv[h];
-    const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
-    st_elem<TQ>(p.out, p.q_dtype, ob + 0, o.x * iv);
-    st_elem<TQ>(p.out, p.q_dtype, ob + 1, o.y * iv);
-    st_elem<TQ>(p.out, p.q_dtype, ob + 2, o.z * iv);
-    st_elem<TQ>(p.out, p.q_dtype, ob + 3, o.w * iv);
+    finish_out(h, c, o);
   };
   auto fma4 = [](float w, const float4& v, float4& o) {
     o.x = __builtin_fmaf(w, v.x, o.x);
@@ -491,13 +494,14 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   __syncthreads();  // a_lds
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
   int64_t cur = pass_of(grab());
-  unsigned int nxt_v = grab();
   if (cur < npass) load_k(cur * PR, rows_of(cur));
   while (cur < npass) {
     const int64_t pr0 = cur * PR;
     const int prow = rows_of(cur);  // multiple of SROWS
     load_v(pr0, prow);
-    const unsigned int nxt2_v = grab();  // the pass after next, read one pass later
+    // the next pass, taken now and read after the score products (a wavefront
+    // holds at most one pass beyond the current one)
+    const unsigned int nxt_v = grab();
 
     // ------------------------------------------------------------ scores
 #pragma unroll
@@ -612,7 +616,6 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
     }
     wave_lds_sync();
     cur = nxt;
-    nxt_v = nxt2_v;
   }
 
   // ---- combine the wavefronts.  Lane c < GP carries head c's (max, sum);
