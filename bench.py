@@ -94,6 +94,149 @@ def split_kernel_name():
     return "attn_split_i8_mfma<4,4,4> (merge fused)"
 
 
+def timed(fn, steps, warmup):
+    """Average ms of fn() over `steps` calls between events on the current
+    stream, after `warmup` calls."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def c2_mode(args):
+    """jpeg int8 archive + read of fp16 KV (B=4, H=32,
+    S=8192, D=128), AR(1) rho=0.95 with a per-channel scale log-uniform in
+    [0.1, 10]; r=8, k=4.  Bulk archive (fc_jpeg_encode of all 1024 blocks,
+    one launch) and bulk read (fc_jpeg_decode of all blocks into an fp16
+    view, one launch), algorithmic bytes per stream 268,435,456 (fp16 tokens)
+    + 67,108,864 (codes) + 2,097,152 (fp32 scales); then the token-by-token
+    append path of one stream."""
+    import torch
+    import flashcodec_amd as fc
+    from flashcodec_amd import _native as N
+    from flashcodec_amd.cache import _CodecStream
+    from flashcodec_amd.codecs import jpeg as J
+    dev = torch.device("cuda:0")
+    b_, h_, s_, d_, r, k = 4, 32, 8192, 128, 8, 4
+    nb = s_ // r
+    g = torch.Generator(device=dev).manual_seed(2)
+    scale = torch.exp(torch.empty((b_, h_, 1, d_), device=dev).uniform_(math.log(0.1), math.log(10.0),
+                                                                       generator=g))
+    x = (ar1_device((b_, h_, s_, d_), 0.95, 1, dev) * scale).to(torch.float16)
+    coeffs = torch.empty((b_, h_, nb, k, d_), dtype=torch.int8, device=dev)
+    scales = torch.empty((b_, h_, nb, k, 1), dtype=torch.float32, device=dev)
+    out = torch.empty_like(x)
+    alg = b_ * h_ * s_ * d_ * 2 + b_ * h_ * nb * k * d_ + b_ * h_ * nb * k * 4
+
+    def archive():
+        J.encode_into(x, r, k, 8, coeffs, scales, nb, 0, nb, s_)
+
+    def read():
+        J.decode_into(coeffs, scales, b_, h_, nb, 0, nb, d_, r, k, out, s_)
+
+    t_arch = timed(archive, args.steps, args.warmup)
+    t_read = timed(read, args.steps, args.warmup)
+    log(f"bench c2: archive {t_arch * 1e3:.1f} us, read {t_read * 1e3:.1f} us")
+
+    # token-by-token appends through the stream API (one token per call)
+    n_tok = 512
+    st = _CodecStream(fc.make_codec(mode="jpeg", block_size=r, keep_freqs=k, quant_bits=8))
+    for t in range(16):                                  # warm the allocator and kernels
+        st.append(x[:, :, t:t + 1])
+    st = _CodecStream(fc.make_codec(mode="jpeg", block_size=r, keep_freqs=k, quant_bits=8))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(n_tok):
+        st.append(x[:, :, t:t + 1])
+    torch.cuda.synchronize()
+    t_tok = (time.perf_counter() - t0) / n_tok
+    same = bool(torch.equal(st._coeffs[:, :, :n_tok // r], coeffs[:, :, :n_tok // r]) and
+                torch.equal(st._scales[:, :, :n_tok // r], scales[:, :, :n_tok // r]))
+    print(json.dumps({
+        "metric": "jpeg int8 archive / read GB/s (C2)", "unit": "GB/s", "n_gpus": 1,
+        "archive_GBs": round(alg / (t_arch * 1e-3) / 1e9, 1),
+        "read_GBs": round(alg / (t_read * 1e-3) / 1e9, 1),
+        "archive_us": round(t_arch * 1e3, 2), "read_us": round(t_read * 1e3, 2),
+        "hbm_frac_archive": round(alg / (t_arch * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "hbm_frac_read": round(alg / (t_read * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes": alg,
+        "append_us_per_token": round(t_tok * 1e6, 2),
+        "append_launches_per_token": "2 copies (raw tail concat + contiguous) + 1 archive launch per 8 tokens",
+        "token_by_token_codes_equal_bulk": same,
+        "config": {"workload": "C2 jpeg int8 archive + read", "B": b_, "H": h_, "S": s_, "D": d_,
+                   "block": r, "keep_freqs": k, "dtype": "fp16"},
+        "data": "synthetic AR(1) rho=0.95, per-channel scale log-uniform [0.1, 10]"}))
+
+
+def c4_mode(args):
+    """png mode on fp32 KV (B=2, H=8, S=16384, D=128),
+    AR(1) rho=0.98, r=16, keep_ratio 0.25 (4 of 15 deltas) and 1.0.  Bulk
+    archive and bulk read of one stream (algorithmic bytes 134,217,728 fp32
+    tokens + 125,829,120 fp32 deltas + 8,388,608 fp32 anchors), and decode
+    attention of 32 query heads (one fp32 query token per sequence) over K
+    and V archives (268,435,456 bytes of stored rows + q + out); keep_ratio
+    1.0 is checked against dense fp32 attention over the original tokens."""
+    import torch
+    import flashcodec_amd as fc
+    from flashcodec_amd.cache import _CodecStream
+    from flashcodec_amd.codecs import png as P
+    dev = torch.device("cuda:0")
+    b_, h_, s_, d_, r, hq = 2, 8, 16384, 128, 16, 32
+    nb = s_ // r
+    x = {"k": ar1_device((b_, h_, s_, d_), 0.98, 1, dev), "v": ar1_device((b_, h_, s_, d_), 0.98, 2, dev)}
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = torch.randn((b_, hq, 1, d_), generator=g, device=dev) / math.sqrt(d_)
+    alg_codec = b_ * h_ * s_ * d_ * 4 + b_ * h_ * nb * (r - 1) * d_ * 4 + b_ * h_ * nb * d_ * 4
+    alg_attn = 2 * b_ * h_ * nb * r * d_ * 4 + 2 * b_ * hq * d_ * 4
+    res = {"metric": "png archive / read / decode attention (C4)", "unit": "GB/s", "n_gpus": 1,
+           "config": {"workload": "C4 png", "B": b_, "H": h_, "S": s_, "D": d_, "block": r,
+                      "q_heads": hq, "dtype": "fp32"},
+           "data": "synthetic AR(1) rho=0.98", "algorithmic_bytes_codec": alg_codec,
+           "algorithmic_bytes_attention": alg_attn}
+    for keep in (0.25, 1.0):
+        codec = fc.make_codec(mode="png", block_size=r, keep_ratio=keep)
+        m_keep = codec.keep_m
+        deltas = torch.empty((b_, h_, nb, r - 1, d_), dtype=torch.float32, device=dev)
+        anchors = torch.empty((b_, h_, nb, d_), dtype=torch.float32, device=dev)
+        out = torch.empty_like(x["k"])
+
+        def archive():
+            P.encode_into(x["k"], r, m_keep, deltas, anchors, nb, 0, nb, s_)
+
+        def read():
+            P.decode_into(deltas, anchors, b_, h_, nb, 0, nb, d_, r, out, s_)
+
+        t_arch = timed(archive, args.steps, args.warmup)
+        t_read = timed(read, args.steps, args.warmup)
+        ks, vs = _CodecStream(codec), _CodecStream(codec)
+        ks.append(x["k"])
+        vs.append(x["v"])
+        t_attn = timed(lambda: fc.codec_decode_attention(q, ks, vs), args.steps, args.warmup)
+        tag = f"keep{keep}"
+        res[tag] = {"archive_GBs": round(alg_codec / (t_arch * 1e-3) / 1e9, 1),
+                    "read_GBs": round(alg_codec / (t_read * 1e-3) / 1e9, 1),
+                    "attention_GBs": round(alg_attn / (t_attn * 1e-3) / 1e9, 1),
+                    "archive_us": round(t_arch * 1e3, 2), "read_us": round(t_read * 1e3, 2),
+                    "attention_us": round(t_attn * 1e3, 2), "kept_deltas": m_keep}
+        if keep == 1.0:
+            o = fc.codec_decode_attention(q, ks, vs)
+            G = hq // h_
+            kk = x["k"].repeat_interleave(G, dim=1)
+            vv = x["v"].repeat_interleave(G, dim=1)
+            p_ = torch.softmax((q @ kk.transpose(-1, -2).contiguous()) * d_ ** -0.5, dim=-1)
+            ref = p_ @ vv
+            res[tag]["vs_dense_max_abs_err"] = float((o - ref).abs().max())
+        log(f"bench c4 keep {keep}: {res[tag]}")
+    print(json.dumps(res))
+
+
 def read_pmc_traffic():
     """HBM bytes per launch of the matrix-core kernel from the committed PMC
     summary, if any (None for the vector-ALU variant, which it does not cover)."""
@@ -150,7 +293,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--mode", choices=["c3", "copy"], default="c3")
+    ap.add_argument("--mode", choices=["c3", "c2", "c4", "copy"], default="c3")
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--splits", type=int, default=0, help="override the split count")
@@ -166,6 +309,10 @@ def main():
         sys.exit(2)
     if args.mode == "copy":
         return copy_mode(args)
+    if args.mode == "c2":
+        return c2_mode(args)
+    if args.mode == "c4":
+        return c4_mode(args)
 
     import numpy as np
     import flashcodec_amd as fc
