@@ -237,6 +237,67 @@ def c4_mode(args):
     print(json.dumps(res))
 
 
+def c1_mode(args):
+    """jpeg round trip of fp32 KV (B=1, H=8, S=4096,
+    D=128), each (b, h, d) channel AR(1) rho=0.97 with unit variance; r=8,
+    k=2, no quantization; encode all 512 blocks, then read(); PSNR
+    (20 log10(max|x| / rmse)) and max abs error, and the reconstruction
+    compared bit for bit with the CPU oracle."""
+    import numpy as np
+    import torch
+    import flashcodec_amd as fc
+    from flashcodec_amd.cache import _CodecStream
+    from oracle import oracle as O
+    dev = torch.device("cuda:0")
+    b_, h_, s_, d_, r, k = 1, 8, 4096, 128, 8, 2
+    x = ar1_device((b_, h_, s_, d_), 0.97, 1, dev)
+    st = _CodecStream(fc.make_codec(mode="jpeg", block_size=r, keep_freqs=k))
+    st.append(x)
+    rec = st.read()
+    err = (rec - x).float()
+    rmse = float(err.pow(2).mean().sqrt())
+    psnr = 20 * math.log10(float(x.abs().max()) / rmse)
+    basis = fc.dct_basis(r, k).numpy()
+    xn = x.cpu().numpy()
+    coef = O.jpeg_encode(xn, r, k, basis, "f32")
+    ref = O.jpeg_decode(coef, r, basis, "f32")
+    bit_exact = bool(np.array_equal(rec.cpu().numpy().view(np.uint32), np.asarray(ref, np.float32).view(np.uint32)))
+    alg = b_ * h_ * s_ * d_ * 4 + b_ * h_ * (s_ // r) * k * d_ * 4
+    t_arch = timed(lambda: _CodecStream(st.codec).append(x), args.steps, args.warmup)
+    print(json.dumps({"metric": "jpeg fp32 round trip accuracy (C1)", "psnr_db": round(psnr, 3),
+                      "max_abs_err": float(err.abs().max()), "rmse": rmse,
+                      "bit_exact_vs_oracle": bit_exact,
+                      "archive_us": round(t_arch * 1e3, 2),
+                      "archive_GBs": round(alg / (t_arch * 1e-3) / 1e9, 1),
+                      "config": {"workload": "C1 jpeg round trip", "B": b_, "H": h_, "S": s_, "D": d_,
+                                 "block": r, "keep_freqs": k, "dtype": "fp32"},
+                      "data": "synthetic AR(1) rho=0.97, unit variance"}))
+
+
+def refshapes_mode(args):
+    """The reference's published decode-attention timings (flashcodec
+    README.md:318-325: Triton split-K 0.09 ms at S=16384 and 0.16 ms at
+    S=65536; one layer, B=1, Hkv=8, Hq=16, D=128, jpeg r=8 k=2 int8, on an
+    unstated CUDA GPU) against this build on the same shapes."""
+    import torch
+    import flashcodec_amd as fc
+    from flashcodec_amd.cache import _CodecStream
+    dev = torch.device("cuda:0")
+    res = {"metric": "decode attention ms at the reference's published shapes", "unit": "ms",
+           "reference_ms": {"16384": 0.09, "65536": 0.16}, "ours": {}}
+    for s_ in (16384, 65536):
+        cfg = dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8)
+        ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
+        for st, seed in ((ks, 1), (vs, 2)):
+            st.append(ar1_device((1, 8, s_, 128), 0.95, seed, dev).to(torch.float16))
+        q = (torch.randn((1, 16, 1, 128), device=dev) / math.sqrt(128)).to(torch.float16)
+        ms = timed(lambda: fc.codec_decode_attention(q, ks, vs), args.steps, args.warmup)
+        nbytes = 2 * (1 * 8 * (s_ // 8) * 2 * 128 + 1 * 8 * (s_ // 8) * 2 * 4)
+        res["ours"][str(s_)] = {"ms": round(ms, 4), "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                "speedup_vs_reference": round(res["reference_ms"][str(s_)] / ms, 2)}
+    print(json.dumps(res))
+
+
 def read_pmc_traffic():
     """HBM bytes per launch of the matrix-core kernel from the committed PMC
     summary, if any (None for the vector-ALU variant, which it does not cover)."""
@@ -293,7 +354,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--mode", choices=["c3", "c2", "c4", "copy"], default="c3")
+    ap.add_argument("--mode", choices=["c3", "c1", "c2", "c4", "refshapes", "copy"], default="c3")
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--splits", type=int, default=0, help="override the split count")
@@ -309,8 +370,12 @@ def main():
         sys.exit(2)
     if args.mode == "copy":
         return copy_mode(args)
+    if args.mode == "c1":
+        return c1_mode(args)
     if args.mode == "c2":
         return c2_mode(args)
+    if args.mode == "refshapes":
+        return refshapes_mode(args)
     if args.mode == "c4":
         return c4_mode(args)
 
