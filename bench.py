@@ -298,6 +298,67 @@ def refshapes_mode(args):
     print(json.dumps(res))
 
 
+def c5_mode(args):
+    """end-to-end greedy decoding through the attention
+    patch on a randomly initialised Qwen3-0.6B-shaped decoder (28 layers,
+    hidden 1024, 16 q / 8 kv heads, head_dim 128, intermediate 3072, vocab
+    151936, tied embeddings, bf16): batch 16, 4096 random prompt ids, 256
+    decode steps, jpeg r=8 k=4 int8 with materialization-free attention,
+    against the same model with transformers' own KV cache.  Also batch 1,
+    4096 + 32 (the setting of flashcodec README.md:334-343: 40.3 tok/s
+    materialization-free on an unstated CUDA GPU)."""
+    import torch
+    import flashcodec_amd as fc
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    dev = torch.device("cuda:0")
+    cfg = Qwen3Config(vocab_size=151936, hidden_size=1024, intermediate_size=3072,
+                      num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8,
+                      head_dim=128, max_position_embeddings=8192, tie_word_embeddings=True)
+    torch.manual_seed(0)
+    model = Qwen3ForCausalLM(cfg).to(device=dev, dtype=torch.bfloat16).eval()
+    model.generation_config.eos_token_id = None
+
+    def run(batch, prompt, steps):
+        g = torch.Generator().manual_seed(1)
+        ids = torch.randint(1, cfg.vocab_size, (batch, prompt), generator=g).to(dev)
+        with torch.no_grad():
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = model(input_ids=ids, use_cache=True, logits_to_keep=1)
+            pkv = out.past_key_values
+            nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for _ in range(steps):
+                out = model(input_ids=nxt, past_key_values=pkv, use_cache=True, logits_to_keep=1)
+                pkv = out.past_key_values
+                nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+        return {"prefill_s": round(t1 - t0, 4), "decode_ms_per_step": round((t2 - t1) / steps * 1e3, 3),
+                "decode_tokens_per_s": round(batch * steps / (t2 - t1), 1)}
+
+    res = {"metric": "end-to-end decode tokens/s (C5)", "unit": "tokens/s", "n_gpus": 1,
+           "config": {"workload": "C5 Qwen3-0.6B-shaped greedy decoding", "layers": 28,
+                      "hidden": 1024, "q_heads": 16, "kv_heads": 8, "head_dim": 128,
+                      "dtype": "bf16", "codec": "jpeg r=8 k=4 int8, materialization-free"},
+           "data": "random-init weights, random prompt ids"}
+    run(2, 64, 4)                                              # warm-up (kernels, allocator)
+    res["raw_kv_b16"] = run(16, 4096, 256)
+    res["raw_kv_b1"] = run(1, 4096, 32)
+    fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8,
+                         materialization_free=True)
+    run(2, 64, 4)
+    res["codec_b16"] = run(16, 4096, 256)
+    res["codec_b1"] = run(1, 4096, 32)
+    steps = [getattr(m, "_flashcodec_codec_steps", 0) for m in fc.find_attention_modules(model)]
+    res["codec_attention_steps_per_layer"] = max(steps) if steps else 0
+    res["value"] = res["codec_b16"]["decode_tokens_per_s"]
+    res["reference_published_b1_tok_s"] = 40.3
+    log(f"bench c5: {res}")
+    print(json.dumps(res))
+
+
 def read_pmc_traffic():
     """HBM bytes per launch of the matrix-core kernel from the committed PMC
     summary, if any (None for the vector-ALU variant, which it does not cover)."""
@@ -354,7 +415,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--mode", choices=["c3", "c1", "c2", "c4", "refshapes", "copy"], default="c3")
+    ap.add_argument("--mode", choices=["c3", "c1", "c2", "c4", "c5", "refshapes", "copy"],
+                    default="c3")
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--splits", type=int, default=0, help="override the split count")
@@ -376,6 +438,8 @@ def main():
         return c2_mode(args)
     if args.mode == "refshapes":
         return refshapes_mode(args)
+    if args.mode == "c5":
+        return c5_mode(args)
     if args.mode == "c4":
         return c4_mode(args)
 
