@@ -43,6 +43,20 @@ __device__ __forceinline__ ItemMap item_of_thread(int lpi_log2) {
   return m;
 }
 
+// clamp(rint(fl(c / s)), -127, 127) for a quantizer row with scale s and
+// rs = fl(1 / s), where fl(c / s) is the IEEE single-precision quotient.
+// For |c / s| < 128: x = fl(c * rs) is within |c/s| 2^-23 <= 2^-16 of c / s
+// and fl(c / s) within 2^-17 of it, so they round to the same integer unless
+// a half-integer lies within 2^-15 of x; only then is the quotient computed
+// exactly.  (Scales are fl(amax / 127) rounded to the stream dtype, so
+// |c / s| <= 127 (1 + 2^-8) < 128.)
+__device__ __forceinline__ float quant_code(float c, float s, float rs) {
+  const float x = c * rs;
+  float q = __builtin_rintf(x);
+  if (!(0.5f - fabsf(x - q) > 0x1p-15f)) q = __builtin_rintf(c / s);
+  return fminf(fmaxf(q, -127.f), 127.f);
+}
+
 // ---------------------------------------------------------------- jpeg encode
 
 template <typename T, int VEC, int RMAX, bool QUANT>
@@ -119,14 +133,11 @@ __global__ __launch_bounds__(kThreads) void jpeg_encode_kernel(
       amax = group_max_rt(amax, 1 << lpi_log2);
       float s = to_f32(from_f32<T>(amax / 127.0f));
       if (!(s > 0.f)) s = 1.0f;
+      const float rs = 1.0f / s;
       if (active) {
         vec_t<int8_t, VEC> qv;
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          float qf = __builtin_rintf(c[v] / s);
-          qf = fminf(fmaxf(qf, -127.f), 127.f);
-          qv.v[v] = (int8_t)(int)qf;
-        }
+        for (int v = 0; v < VEC; ++v) qv.v[v] = (int8_t)(int)quant_code(c[v], s, rs);
         *reinterpret_cast<vec_t<int8_t, VEC>*>(static_cast<int8_t*>(out) + (out_row0 + j) * D +
                                                d0) = qv;
         if (im.lane == 0) scales[out_row0 + j] = s;
@@ -227,14 +238,11 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(
   amax = group_max_rt(amax, 1 << lpi_log2);
   float s = to_f32(from_f32<T>(amax / 127.0f));
   if (!(s > 0.f)) s = 1.0f;
+  const float inv_s = 1.0f / s;
   if (!active) return;
   vec_t<int8_t, VEC> q;
 #pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    float qf = __builtin_rintf(v[i] / s);
-    qf = fminf(fmaxf(qf, -127.f), 127.f);
-    q.v[i] = (int8_t)(int)qf;
-  }
+  for (int i = 0; i < VEC; ++i) q.v[i] = (int8_t)(int)quant_code(v[i], s, inv_s);
   *reinterpret_cast<vec_t<int8_t, VEC>*>(codes + row * D + d0) = q;
   if (im.lane == 0) scales[row] = s;
 }

@@ -171,3 +171,72 @@ def test_jpeg_quality_properties():
     e2 = (fc.dct_decompress(fc.dct_compress(smooth, R, 2), R, S) - smooth).abs().mean()
     e4 = (fc.dct_decompress(fc.dct_compress(smooth, R, 4), R, S) - smooth).abs().mean()
     assert e4 < e2
+
+
+def _near_tie_rows(dt, rng, D=64):
+    """Quantizer rows whose quotients c / s sit on or a few ulp beside the
+    half-integers where rint changes value: element 0 of each row is the row
+    maximum amax (so s = T(amax / 127)), the others are ((n + 1/2) s) nudged
+    by -3..3 ulp for f32; for f16 / bf16 every finite value of the dtype with
+    |c| <= amax.  Scales span normal, tiny and subnormal magnitudes (1 / s
+    overflows for the last)."""
+    rows = []
+    if dt == "f32":
+        amaxes = [np.float32(v) for v in np.exp2(rng.uniform(-40, 40, 96))]
+        amaxes += [np.float32(127 * 2.0 ** e * (1 + j / 16)) for e in (-20, -3, 0, 5) for j in range(16)]
+        amaxes += [np.float32(1e-37), np.float32(3e-39), np.float32(1e-44)]
+        for amax in amaxes:
+            s = np.float32(amax) / np.float32(127)
+            n = rng.integers(-127, 127, D - 1).astype(np.float64)
+            c = ((n + 0.5) * np.float64(s)).astype(np.float32)
+            ib = c.view(np.int32) + rng.integers(-3, 4, D - 1).astype(np.int32)
+            c = np.where(c == 0, c, ib.view(np.float32))
+            c = np.clip(c, -amax, amax)
+            rows.append(np.concatenate([[amax], c]).astype(np.float32))
+    else:
+        bits16 = np.arange(1 << 16, dtype=np.uint32)
+        if dt == "bf16":
+            vals = (bits16 << 16).view(np.float32)
+        else:
+            vals = bits16.astype(np.uint16).view(np.float16).astype(np.float32)
+        vals = vals[np.isfinite(vals)]
+        for amax in (1.5, 0.009765625, 300.0, 127 / 16, 127 * 8):
+            amax = np.float32(amax)
+            sel = vals[np.abs(vals) <= amax]
+            pad = (-len(sel)) % (D - 1)
+            sel = np.concatenate([sel, np.zeros(pad, np.float32)]).reshape(-1, D - 1)
+            rows.append(np.concatenate([np.full((len(sel), 1), amax, np.float32), sel], 1))
+    return np.vstack([np.atleast_2d(r) for r in rows]).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_quantizer_near_half_integer_quotients(dt, oracle):
+    """Codes and scales of quantize_coeffs and of the fused int8 archive
+    kernel stay bit-identical to the IEEE-quotient quantizer on the inputs
+    where a reciprocal-multiply shortcut would round the other way."""
+    from flashcodec_amd.codecs import jpeg as jp
+    print(f"case quant-ties {dt}", flush=True)
+    rng = np.random.default_rng(seed_of("quant-ties", dt))
+    rows = _near_tie_rows(dt, rng)
+    R, D = rows.shape
+    codes, scales = oracle.quantize(rows, dt)
+    # the rows do sit where a bare rint(c * fl(1 / s)) picks other codes (f32)
+    # or hit exact ties (all dtypes)
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        x = rows * (np.float32(1) / scales.astype(np.float32))[:, None]
+        bare = np.clip(np.rint(x), -127, 127)
+        assert (np.abs(np.abs(x - np.rint(x)) - 0.5) < 2.0 ** -15).sum() > 100
+    if dt == "f32":
+        assert (bare != codes).sum() > 100
+    assert np.array_equal(oracle.round_to(rows, dt), rows)  # representable in dt
+    t = torch.from_numpy(rows).to(torch_dtype(dt)).to(DEV)
+    q, s = fc.quantize_coeffs(t)
+    assert np.array_equal(q.cpu().numpy(), codes)
+    assert np.array_equal(bits(s[..., 0].cpu().numpy()), bits(scales))
+    # fused archive kernel, r = k = 1: the coefficient is the token itself
+    x4 = t.reshape(1, 1, R, D)
+    cq = torch.zeros((1, 1, R, 1, D), dtype=torch.int8, device=DEV)
+    cs = torch.zeros((1, 1, R, 1, 1), dtype=torch.float32, device=DEV)
+    jp.encode_into(x4, 1, 1, 8, cq, cs, R, 0, R, R)
+    assert np.array_equal(cq.reshape(R, D).cpu().numpy(), codes)
+    assert np.array_equal(bits(cs.reshape(R).cpu().numpy()), bits(scales))
