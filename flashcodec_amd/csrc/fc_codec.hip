@@ -21,6 +21,7 @@
 // The file is compiled with -ffp-contract=off so no other multiply-add is
 // fused behind our back.
 #include <initializer_list>
+#include <type_traits>
 #include <utility>
 
 #include "fc_common.h"
@@ -142,6 +143,138 @@ __global__ __launch_bounds__(kThreads) void jpeg_encode_kernel(
                                                d0) = qv;
         if (im.lane == 0) scales[out_row0 + j] = s;
       }
+    }
+  }
+}
+
+// ------------------------------------------------- jpeg int8 archive, r = 8
+
+// Max over aligned groups of `width` lanes of non-negative, non-NaN floats
+// (compared as integers, which orders them the same way): DPP row permutes
+// inside 16 lanes (quad swaps, half-row and row mirrors), shuffles beyond.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_umax(uint32_t v) {
+  return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float group_amax(float v, int width) {
+  uint32_t u = __float_as_uint(v);
+  if (width > 1) u = dpp_umax<0xB1>(u);   // quad_perm [1,0,3,2]
+  if (width > 2) u = dpp_umax<0x4E>(u);   // quad_perm [2,3,0,1]
+  if (width > 4) u = dpp_umax<0x141>(u);  // row_half_mirror
+  if (width > 8) u = dpp_umax<0x140>(u);  // row_mirror
+  if (width > 16) u = max(u, (uint32_t)__shfl_xor((int)u, 16, 64));
+  if (width > 32) u = max(u, (uint32_t)__shfl_xor((int)u, 32, 64));
+  return __uint_as_float(u);
+}
+
+// fl(a / 127) for every finite a >= 0: y0 = fl(a R) with R = fl(1/127) is
+// within an ulp of the quotient, the residual a - 127 y0 is exact in one
+// fma, and one correction step rounds correctly (checked exhaustively over
+// all 2^31 non-negative finite floats by tests/test_quant_shortcut.py).
+__device__ __forceinline__ float div127(float a) {
+  constexpr float R = 1.0f / 127.0f;
+  const float y0 = a * R;
+  const float e = __builtin_fmaf(-y0, 127.0f, a);
+  return __builtin_fmaf(e, R, y0);
+}
+
+// stream-dtype rounding of a value that is only used again as fp32 (NaN
+// stays NaN; the payload is irrelevant here)
+template <typename T>
+__device__ __forceinline__ float round_trip(float f) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    return (float)(__bf16)f;
+  } else {
+    return to_f32(from_f32<T>(f));
+  }
+}
+
+// Codes of VEC coefficients of one quantizer row with scale s: the same
+// codes as quant_code, with the hardware reciprocal (relative error
+// <= 2^-23) in place of fl(1 / s).  For |c / s| < 128, x = fl(c rs) lies
+// within 1.5 * 2^-16 of c / s and fl(c / s) within 2^-18, so both round to
+// the same integer unless x is within 2^-14 of a half-integer; those
+// elements (and every element of a row whose scale is not a normal float)
+// take the IEEE quotient.  NaN quotients clamp to -127 as in quant_code.
+template <int VEC>
+__device__ __forceinline__ void quantize_vec(const float (&c)[VEC], float s,
+                                             vec_t<int8_t, VEC>& out) {
+  const bool normal = s >= 0x1p-126f && s <= 0x1p126f;
+  const float rs = normal ? __builtin_amdgcn_rcpf(s) : __builtin_nanf("");
+  float q[VEC];
+  uint32_t redo = 0;
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    const float x = c[v] * rs;
+    q[v] = __builtin_rintf(x);
+    redo |= (uint32_t)!(fabsf(x - q[v]) < 0.5f - 0x1p-14f) << v;
+  }
+  if (redo) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (redo >> v & 1u) q[v] = fmaxf(__builtin_rintf(c[v] / s), -127.f);
+  }
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) out.v[v] = (int8_t)(int)__builtin_amdgcn_fmed3f(q[v], -127.f, 127.f);
+}
+
+// jpeg int8 archive of complete 8-token blocks, 8 features per lane: the
+// jpeg_encode_kernel<T, 8, 8, true> computation (same fma chain, dtype
+// rounding, scale and codes) with the block loads unconditional, the row
+// absmax on DPP and the divisions replaced by exact shortcuts.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void jpeg_encode_r8q_kernel(
+    const T* __restrict__ x, int64_t sb, int64_t sh, int64_t ss, int64_t H, int64_t m,
+    int64_t D, int k, const float* __restrict__ basis, int8_t* __restrict__ out,
+    float* __restrict__ scales, int64_t cap, int64_t n0, int64_t items, int lpi_log2) {
+  constexpr int R = 8, VEC = 8;
+  const ItemMap im = item_of_thread(lpi_log2);
+  const bool live = im.item < items;
+  const int64_t item = live ? im.item : 0;
+  const int64_t bh = item / m, blk = item - bh * m;
+  const int64_t b = bh / H, h = bh - b * H;
+  const int64_t d0 = (int64_t)im.lane * VEC;
+  const bool active = live && d0 < D;
+  const T* src = x + b * sb + h * sh + blk * R * ss + (active ? d0 : 0);
+
+  float xr[R][VEC];
+  if (active) {
+#pragma unroll
+    for (int t = 0; t < R; ++t) load_f32<T, VEC>(src + t * ss, xr[t]);
+  } else {
+#pragma unroll
+    for (int t = 0; t < R; ++t)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) xr[t][v] = 0.f;
+  }
+
+  const int64_t out_row0 = (bh * cap + n0 + blk) * k;
+  const int width = 1 << lpi_log2;
+  for (int j = 0; j < k; ++j) {
+    const float* mj = basis + j * R;
+    float c[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) c[v] = 0.f;
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+      const float w = mj[t];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) c[v] = __builtin_fmaf(xr[t][v], w, c[v]);
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      c[v] = round_trip<T>(c[v]);
+      amax = fmaxf(amax, fabsf(c[v]));
+    }
+    amax = group_amax(amax, width);
+    float s = round_trip<T>(amax <= 0x1.fffffep127f ? div127(amax) : amax / 127.0f);
+    if (!(s > 0.f)) s = 1.0f;
+    vec_t<int8_t, VEC> qv;
+    quantize_vec<VEC>(c, s, qv);
+    if (active) {
+      *reinterpret_cast<vec_t<int8_t, VEC>*>(out + (out_row0 + j) * D + d0) = qv;
+      if (im.lane == 0) scales[out_row0 + j] = s;
     }
   }
 }
@@ -528,6 +661,16 @@ int fc_jpeg_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_s
   const int lg = log2_lanes(D, vec);
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid = grid_for(items, lg);
+  if (quant_bits && r == 8 && vec == 8 && s_valid >= m * r) {
+    const int rc = with_float_type(x_dtype, [&](auto tv) {
+      using T = decltype(tv);
+      jpeg_encode_r8q_kernel<T><<<grid, kThreads, 0, st>>>(
+          (const T*)x, x_sb, x_sh, x_ss, H, m, D, k, basis, (int8_t*)coeffs, scales, cap, n0,
+          items, lg);
+      return FC_OK;
+    });
+    return rc != FC_OK ? rc : check_launch();
+  }
   const int rc = with_float_type(x_dtype, [&](auto tv) {
     using T = decltype(tv);
     return with_int<1, 4, 8>(vec, [&](auto vc) {

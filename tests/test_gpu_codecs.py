@@ -173,6 +173,14 @@ def test_jpeg_quality_properties():
     assert e4 < e2
 
 
+def _dtype_values(dt):
+    """Every finite value of f16 / bf16, as float32."""
+    b = np.arange(1 << 16, dtype=np.uint32)
+    vals = (b << 16).view(np.float32) if dt == "bf16" else \
+        b.astype(np.uint16).view(np.float16).astype(np.float32)
+    return vals[np.isfinite(vals)]
+
+
 def _near_tie_rows(dt, rng, D=64):
     """Quantizer rows whose quotients c / s sit on or a few ulp beside the
     half-integers where rint changes value: element 0 of each row is the row
@@ -194,12 +202,7 @@ def _near_tie_rows(dt, rng, D=64):
             c = np.clip(c, -amax, amax)
             rows.append(np.concatenate([[amax], c]).astype(np.float32))
     else:
-        bits16 = np.arange(1 << 16, dtype=np.uint32)
-        if dt == "bf16":
-            vals = (bits16 << 16).view(np.float32)
-        else:
-            vals = bits16.astype(np.uint16).view(np.float16).astype(np.float32)
-        vals = vals[np.isfinite(vals)]
+        vals = _dtype_values(dt)
         for amax in (1.5, 0.009765625, 300.0, 127 / 16, 127 * 8):
             amax = np.float32(amax)
             sel = vals[np.abs(vals) <= amax]
@@ -240,3 +243,73 @@ def test_quantizer_near_half_integer_quotients(dt, oracle):
     jp.encode_into(x4, 1, 1, 8, cq, cs, R, 0, R, R)
     assert np.array_equal(cq.reshape(R, D).cpu().numpy(), codes)
     assert np.array_equal(bits(cs.reshape(R).cpu().numpy()), bits(scales))
+
+
+def _near_tie_blocks(dt, rng, D=64):
+    """8-token blocks whose only nonzero token is the first, so the freq-0
+    DCT coefficient is fl(v w0) (w0 = basis[0][0]); v is picked per element
+    so that these coefficients sit on or a few ulp beside half-integer
+    multiples of the row's scale (f32), or runs over every finite dtype
+    value in a range (f16 / bf16)."""
+    w0 = np.float32(fc.dct_basis(8, 4).numpy()[0, 0])
+    rows = []
+    if dt == "f32":
+        for vmax in np.exp2(rng.uniform(-30, 30, 160)).astype(np.float32):
+            amax = np.float32(vmax * w0)
+            s = amax / np.float32(127)
+            n = rng.integers(-127, 127, D - 1).astype(np.float64)
+            v = ((n + 0.5) * np.float64(s) / np.float64(w0)).astype(np.float32)
+            vb = v.view(np.int32) + rng.integers(-3, 4, D - 1).astype(np.int32)
+            v = np.clip(np.where(v == 0, v, vb.view(np.float32)), -vmax, vmax)
+            rows.append(np.concatenate([[vmax], v]).astype(np.float32))
+        rows = np.vstack(rows)
+    else:
+        # row maxima whose scale has at most 3 significant bits, so every
+        # coefficient that is an odd multiple of a small power of two is an
+        # exact tie
+        from oracle import oracle as O
+        allv = _dtype_values(dt)
+        for e in (-4, 3, -10):
+            target = np.float32(127 * 2.0 ** e / w0)
+            cand = allv[(allv >= target / 2) & (allv <= target * 2)]
+            sc = O.round_to(O.round_to(cand * w0, dt) / np.float32(127), dt)
+            frac, _ = np.frexp(sc)
+            vmax = cand[(frac * 8) == np.round(frac * 8)][0]
+            sel = allv[np.abs(allv) <= vmax]
+            pad = (-len(sel)) % (D - 1)
+            sel = np.concatenate([sel, np.zeros(pad, np.float32)]).reshape(-1, D - 1)
+            rows.append(np.concatenate([np.full((len(sel), 1), vmax, np.float32), sel], 1))
+        rows = np.vstack(rows)
+    R = rows.shape[0]
+    x = np.zeros((1, 1, R * 8, D), np.float32)
+    x[0, 0, ::8] = rows
+    return x
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_archive_r8_near_half_integer_quotients(dt, oracle):
+    """The r = 8 int8 archive kernel (reciprocal codes, DPP row max, fma
+    division for the scale) stays bit-identical to the IEEE-quotient
+    quantizer on coefficients at and around rounding ties."""
+    from flashcodec_amd.codecs import jpeg as jp
+    print(f"case archive-r8-ties {dt}", flush=True)
+    rng = np.random.default_rng(seed_of("archive-r8-ties", dt))
+    xv = _near_tie_blocks(dt, rng)
+    assert np.array_equal(oracle.round_to(xv, dt), xv)
+    _, S, D = xv.shape[1:]
+    m = S // 8
+    basis = fc.dct_basis(8, 4).numpy()
+    _, codes, scales = oracle.jpeg_encode(xv, 8, 4, basis, dt, quant=True)
+    coef = oracle.jpeg_encode(xv, 8, 4, basis, dt)
+    c0, s0 = coef[0, 0, :, 0], scales[0, 0, :, 0]
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        xq = c0 * (np.float32(1) / s0)[:, None]
+        assert (np.abs(np.abs(xq - np.rint(xq)) - 0.5) < 2.0 ** -15).sum() > 100
+        if dt == "f32":
+            assert (np.clip(np.rint(xq), -127, 127) != codes[0, 0, :, 0]).sum() > 100
+    x = torch.from_numpy(xv).to(torch_dtype(dt)).to(DEV)
+    cq = torch.zeros((1, 1, m, 4, D), dtype=torch.int8, device=DEV)
+    cs = torch.zeros((1, 1, m, 4, 1), dtype=torch.float32, device=DEV)
+    jp.encode_into(x, 8, 4, 8, cq, cs, m, 0, m, S)
+    assert np.array_equal(cq.cpu().numpy(), codes)
+    assert np.array_equal(bits(cs[..., 0].cpu().numpy()), bits(scales))
