@@ -44,8 +44,14 @@ template <>
 __device__ __forceinline__ float from_f32<float>(float f) {
   return f;
 }
+// The empty asm pins f as an fp32 value: without it the backend may fold
+// the fma / multiply that produced f and this conversion into one
+// mixed-precision instruction (v_fma_mixlo_f16), which rounds the exact
+// result to f16 once instead of fp32-then-f16, and the two differ when the
+// fp32 value lands on an f16 halfway point.
 template <>
 __device__ __forceinline__ f16_t from_f32<f16_t>(float f) {
+  __asm__("" : "+v"(f));
   return (f16_t)f;
 }
 template <>

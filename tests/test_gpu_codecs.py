@@ -313,3 +313,88 @@ def test_archive_r8_near_half_integer_quotients(dt, oracle):
     jp.encode_into(x, 8, 4, 8, cq, cs, m, 0, m, S)
     assert np.array_equal(cq.cpu().numpy(), codes)
     assert np.array_equal(bits(cs[..., 0].cpu().numpy()), bits(scales))
+
+
+def _double_rounding_blocks(rng, n_blocks=1 << 20):
+    """f16 8-token blocks whose DCT coefficient (r = 8, k = 4), an fma chain
+    in fp32, lands exactly on an f16 halfway point while the exact value of
+    the last fma does not: fp32-then-f16 rounding (the reference's) and a
+    single rounding to f16 then give neighbouring f16 values.  Returns
+    (blocks (n, 8) f32 values, freq, correct f16 value, single-rounded)."""
+    w = fc.dct_basis(8, 4).numpy().astype(np.float64)
+    x = (rng.standard_normal((n_blocks, 8)) * rng.uniform(0.1, 10, (n_blocks, 1)))
+    x = x.astype(np.float16).astype(np.float64)
+    out = []
+    for j in range(4):
+        acc = np.zeros(n_blocks)
+        exact = np.ones(n_blocks, bool)
+        for t in range(8):
+            p = x[:, t] * w[j, t]                  # exact: 11 x 24 bits
+            e = p + acc
+            exact &= ((e - acc) == p) & ((e - p) == acc)
+            if t < 7:
+                acc = e.astype(np.float32).astype(np.float64)
+        good = e.astype(np.float32).astype(np.float16).astype(np.float64)
+        single = e.astype(np.float16).astype(np.float64)
+        for i in np.nonzero(exact & (good != single))[0]:
+            out.append((x[i].astype(np.float32), j, good[i], single[i]))
+    return out
+
+
+def test_f16_coefficients_round_through_fp32(oracle):
+    """f16 coefficients are the fp32 fma chain rounded to f16 (two
+    roundings), never a fused single rounding: checked on blocks where the
+    two differ, for dct_compress and for the r = 8 int8 archive kernel
+    (rows built so the correct coefficient sits exactly on a code tie)."""
+    from flashcodec_amd.codecs import jpeg as jp
+    print("case f16-double-rounding", flush=True)
+    rng = np.random.default_rng(seed_of("f16-double-rounding"))
+    hits = _double_rounding_blocks(rng)
+    assert len(hits) > 100
+    w = fc.dct_basis(8, 4).numpy()
+    f16 = _dtype_values("f16")
+    f16 = f16[f16 > 0]
+    blocks, expect_flip = [], 0
+    for xb, j, good, single in hits:
+        # scale s with good / s = n + 1/2 exactly (an odd divisor d of the
+        # significand M of |good|, n = (d - 1) / 2 <= 126)
+        mant, ex = np.frexp(abs(good))
+        M, e2 = int(mant * 2048), int(ex) - 11
+        while M % 2 == 0:
+            M, e2 = M // 2, e2 + 1
+        d = max([dd for dd in range(1, 254, 2) if M % dd == 0])
+        s = np.float32(2.0 * abs(good) / d)
+        if s < 2.0 ** -14 or oracle.round_to(np.array([s]), "f16")[0] != s:
+            continue
+        # a block whose only token gives freq-j coefficient A with
+        # f16(A / 127) == s: the row's absmax, so the row scale is s
+        tgt = 127 * float(s) / abs(float(w[j, 0]))
+        cand = f16[(f16 > tgt * 0.98) & (f16 < tgt * 1.02)]
+        coefs = oracle.round_to((cand * np.float32(abs(w[j, 0]))).astype(np.float32), "f16")
+        sc = oracle.round_to(coefs / np.float32(127), "f16")
+        ok = (sc == s) & (coefs >= abs(good))
+        if not ok.any():
+            continue
+        v = cand[ok][0] * np.sign(w[j, 0])
+        blk = np.zeros((8, 8), np.float32)
+        blk[:, 0] = xb
+        blk[0, 1] = v
+        blocks.append(blk)
+        q_good = np.rint(np.float32(good) / s)
+        q_single = np.rint(np.float32(single) / s)
+        expect_flip += int(q_good != q_single)
+        if len(blocks) == 64:
+            break
+    assert len(blocks) >= 32 and expect_flip >= 8
+    xv = np.concatenate(blocks)[None, None]           # (1, 1, 8n, 8)
+    x = torch.from_numpy(xv).to(torch.float16).to(DEV)
+    basis = fc.dct_basis(8, 4).numpy()
+    coef, codes, scales = oracle.jpeg_encode(xv, 8, 4, basis, "f16", quant=True)
+    got = fc.dct_compress(x, 8, 4)
+    assert np.array_equal(bits(to_values(got)), bits(coef))
+    m = len(blocks)
+    cq = torch.zeros((1, 1, m, 4, 8), dtype=torch.int8, device=DEV)
+    cs = torch.zeros((1, 1, m, 4, 1), dtype=torch.float32, device=DEV)
+    jp.encode_into(x, 8, 4, 8, cq, cs, m, 0, m, 8 * m)
+    assert np.array_equal(bits(cs[..., 0].cpu().numpy()), bits(scales))
+    assert np.array_equal(cq.cpu().numpy(), codes)
