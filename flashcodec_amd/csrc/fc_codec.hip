@@ -14,7 +14,7 @@
 //     rounded once to the stream dtype (the CPU GEMM's accumulation order).
 //   * DCT decode: same chain over the k coefficients.
 //   * int8: scale = dtype(absmax / 127) in fp32, 1 when not > 0, codes =
-//     round-half-even(c / scale) clamped to [-127, 127].
+//     round-half-even(c / scale) clamped to [-127, 127] (0 for a NaN quotient).
 //   * png cumsum: fp64 running sum rounded to fp32 per step (CPU cumsum
 //     accumulates float in double), anchor + sum in fp32, then the anchor
 //     dtype.
@@ -51,11 +51,13 @@ __device__ __forceinline__ ItemMap item_of_thread(int lpi_log2) {
 // a half-integer lies within 2^-15 of x; only then is the quotient computed
 // exactly.  (Scales are fl(amax / 127) rounded to the stream dtype, so
 // |c / s| <= 127 (1 + 2^-8) < 128.)
+// A NaN quotient gets code 0 (the reference's int8 cast of NaN is
+// undefined; 0 is what x86's truncating conversion gives).
 __device__ __forceinline__ float quant_code(float c, float s, float rs) {
   const float x = c * rs;
   float q = __builtin_rintf(x);
   if (!(0.5f - fabsf(x - q) > 0x1p-15f)) q = __builtin_rintf(c / s);
-  return fminf(fmaxf(q, -127.f), 127.f);
+  return q == q ? fminf(fmaxf(q, -127.f), 127.f) : 0.f;
 }
 
 // ---------------------------------------------------------------- jpeg encode
@@ -189,45 +191,71 @@ __device__ __forceinline__ float round_trip(float f) {
   }
 }
 
-// Codes of VEC coefficients of one quantizer row with scale s: the same
-// codes as quant_code, with the hardware reciprocal (relative error
-// <= 2^-23) in place of fl(1 / s).  For |c / s| < 128, x = fl(c rs) lies
-// within 1.5 * 2^-16 of c / s and fl(c / s) within 2^-18, so both round to
-// the same integer unless x is within 2^-14 of a half-integer; those
-// elements (and every element of a row whose scale is not a normal float)
-// take the IEEE quotient.  NaN quotients clamp to -127 as in quant_code.
-template <int VEC>
-__device__ __forceinline__ void quantize_vec(const float (&c)[VEC], float s,
-                                             vec_t<int8_t, VEC>& out) {
-  const bool normal = s >= 0x1p-126f && s <= 0x1p126f;
-  const float rs = normal ? __builtin_amdgcn_rcpf(s) : __builtin_nanf("");
-  float q[VEC];
-  uint32_t redo = 0;
+// Smallest normal scale of the stream dtype: with a normal scale the
+// row's quotients stay below 127.5 in magnitude (the scale is absmax / 127
+// rounded with relative error <= 2^-8), so their rounded values need no
+// clamp.
+template <typename T>
+__device__ __forceinline__ constexpr float min_normal_scale() {
+  return std::is_same<T, f16_t>::value ? 0x1p-14f : 0x1p-126f;
+}
+
+// Codes of 8 coefficients of one quantizer row with scale s, packed into
+// two dwords; the same codes as quant_code.  rs is the hardware reciprocal
+// (relative error <= 2^-23): for |c / s| < 128, x = fl(c rs) lies within
+// 1.5 * 2^-16 of c / s and fl(c / s) within 2^-18, so both round to the
+// same integer unless x is within 2^-14 of a half-integer.  x + 1.5 * 2^23
+// rounds x to an integer held in the low mantissa bits (two's complement
+// in the low byte), so one add gives rint(x) and the code byte.  Rows with a
+// tie candidate or a scale outside the normal range take the IEEE quotient
+// for all 8 elements (a few rows in a thousand).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ u32x2 quantize8(const float (&c)[8], float s) {
+  constexpr float kMagic = 0x1.8p23f;
+  const bool normal = s >= min_normal_scale<T>() && s <= 0x1p126f;
+  const float rs = __builtin_amdgcn_rcpf(s);
+  float y[8];
+  float dm = 0.f;
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) {
+  for (int v = 0; v < 8; ++v) {
     const float x = c[v] * rs;
-    q[v] = __builtin_rintf(x);
-    redo |= (uint32_t)!(fabsf(x - q[v]) < 0.5f - 0x1p-14f) << v;
+    y[v] = x + kMagic;
+    dm = fmaxf(dm, fabsf(x - (y[v] - kMagic)));
   }
-  if (redo) {
+  // NaN elements (dropped by the max) have NaN y and code 0, as below
+  if (!normal || !(dm < 0.5f - 0x1p-14f)) {
 #pragma unroll
-    for (int v = 0; v < VEC; ++v)
-      if (redo >> v & 1u) q[v] = fmaxf(__builtin_rintf(c[v] / s), -127.f);
+    for (int v = 0; v < 8; ++v) {
+      const float q = __builtin_rintf(c[v] / s);
+      y[v] = (q == q ? fminf(fmaxf(q, -127.f), 127.f) : 0.f) + kMagic;
+    }
   }
+  uint32_t u[8];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) out.v[v] = (int8_t)(int)__builtin_amdgcn_fmed3f(q[v], -127.f, 127.f);
+  for (int v = 0; v < 8; ++v) u[v] = __float_as_uint(y[v]);
+  const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(u[3], u[2], 0x0c0c0400u),
+                                            __builtin_amdgcn_perm(u[1], u[0], 0x0c0c0400u),
+                                            0x05040100u);
+  const uint32_t hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(u[7], u[6], 0x0c0c0400u),
+                                            __builtin_amdgcn_perm(u[5], u[4], 0x0c0c0400u),
+                                            0x05040100u);
+  return u32x2{lo, hi};
 }
 
 // jpeg int8 archive of complete 8-token blocks, 8 features per lane: the
 // jpeg_encode_kernel<T, 8, 8, true> computation (same fma chain, dtype
 // rounding, scale and codes) with the block loads unconditional, the row
-// absmax on DPP and the divisions replaced by exact shortcuts.
-template <typename T>
+// absmax on DPP, the divisions replaced by exact shortcuts and KT (the
+// kept frequencies, 0 = runtime k) unrolled.
+template <typename T, int KT>
 __global__ __launch_bounds__(kThreads) void jpeg_encode_r8q_kernel(
     const T* __restrict__ x, int64_t sb, int64_t sh, int64_t ss, int64_t H, int64_t m,
-    int64_t D, int k, const float* __restrict__ basis, int8_t* __restrict__ out,
+    int64_t D, int k_rt, const float* __restrict__ basis, int8_t* __restrict__ out,
     float* __restrict__ scales, int64_t cap, int64_t n0, int64_t items, int lpi_log2) {
   constexpr int R = 8, VEC = 8;
+  const int k = KT > 0 ? KT : k_rt;
   const ItemMap im = item_of_thread(lpi_log2);
   const bool live = im.item < items;
   const int64_t item = live ? im.item : 0;
@@ -237,19 +265,30 @@ __global__ __launch_bounds__(kThreads) void jpeg_encode_r8q_kernel(
   const bool active = live && d0 < D;
   const T* src = x + b * sb + h * sh + blk * R * ss + (active ? d0 : 0);
 
-  float xr[R][VEC];
+  // All R token loads are issued before any of them is consumed (the
+  // scheduling barrier keeps the backend from waiting on the first load to
+  // widen it while the others are still unissued).
+  vec_t<T, VEC> raw[R];
   if (active) {
 #pragma unroll
-    for (int t = 0; t < R; ++t) load_f32<T, VEC>(src + t * ss, xr[t]);
+    for (int t = 0; t < R; ++t) raw[t] = *reinterpret_cast<const vec_t<T, VEC>*>(src + t * ss);
   } else {
 #pragma unroll
     for (int t = 0; t < R; ++t)
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) xr[t][v] = 0.f;
+      for (int v = 0; v < VEC; ++v) raw[t].v[v] = from_f32<T>(0.f);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  float xr[R][VEC];
+#pragma unroll
+  for (int t = 0; t < R; ++t)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) xr[t][v] = to_f32(raw[t].v[v]);
 
-  const int64_t out_row0 = (bh * cap + n0 + blk) * k;
+  int8_t* dst = out + (bh * cap + n0 + blk) * k * D + d0;
+  float* sdst = scales + (bh * cap + n0 + blk) * k;
   const int width = 1 << lpi_log2;
+#pragma unroll
   for (int j = 0; j < k; ++j) {
     const float* mj = basis + j * R;
     float c[VEC];
@@ -270,11 +309,12 @@ __global__ __launch_bounds__(kThreads) void jpeg_encode_r8q_kernel(
     amax = group_amax(amax, width);
     float s = round_trip<T>(amax <= 0x1.fffffep127f ? div127(amax) : amax / 127.0f);
     if (!(s > 0.f)) s = 1.0f;
-    vec_t<int8_t, VEC> qv;
-    quantize_vec<VEC>(c, s, qv);
+    const u32x2 qv = quantize8<T>(c, s);
     if (active) {
-      *reinterpret_cast<vec_t<int8_t, VEC>*>(out + (out_row0 + j) * D + d0) = qv;
-      if (im.lane == 0) scales[out_row0 + j] = s;
+      // nontemporal stores: this write-once stream runs measurably faster
+      // when it does not allocate in the caches
+      __builtin_nontemporal_store(qv, reinterpret_cast<u32x2*>(dst + (int64_t)j * D));
+      if (im.lane == 0) __builtin_nontemporal_store(s, sdst + j);
     }
   }
 }
@@ -345,6 +385,89 @@ __global__ __launch_bounds__(kThreads) void jpeg_decode_kernel(
       store_from_f32<TO, VEC>(dst + (tok0 + t) * oss, acc);
     }
   }
+}
+
+// ---------------------------------------- jpeg int8 reconstruct, r = 8
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 8 consecutive outputs of one token row, rounded to TO and written with
+// nontemporal stores (16 B for f16 / bf16, 2 x 16 B for f32)
+template <typename TO>
+__device__ __forceinline__ void nt_store8(TO* p, const float (&v)[8]) {
+  vec_t<TO, 8> o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o.v[i] = from_f32<TO>(v[i]);
+  if constexpr (sizeof(TO) == 2) {
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), reinterpret_cast<u32x4*>(p));
+  } else {
+    struct Two { u32x4 a, b; };
+    const Two t = __builtin_bit_cast(Two, o);
+    __builtin_nontemporal_store(t.a, reinterpret_cast<u32x4*>(p));
+    __builtin_nontemporal_store(t.b, reinterpret_cast<u32x4*>(p) + 1);
+  }
+}
+
+// jpeg_decode_kernel<int8_t, TO, 8, 8, true> for r = 8 (same products,
+// same fma order): the k code rows and scales of an item are all requested
+// before the first is used, KT (0 = runtime k <= 8) is unrolled, and the
+// reconstructed rows go out with nontemporal stores.
+template <typename TO, int KT>
+__global__ __launch_bounds__(kThreads) void jpeg_decode_r8q_kernel(
+    const int8_t* __restrict__ store, const float* __restrict__ scales, int64_t H, int64_t cap,
+    int64_t a, int64_t nblk, int64_t D, int k_rt, const float* __restrict__ basis,
+    TO* __restrict__ out, int64_t osb, int64_t osh, int64_t oss, int64_t out_len,
+    int64_t items, int lpi_log2) {
+  constexpr int R = 8, VEC = 8, KMAX = KT > 0 ? KT : 8;
+  const int k = KT > 0 ? KT : k_rt;
+  const ItemMap im = item_of_thread(lpi_log2);
+  if (im.item >= items) return;
+  const int64_t bh = im.item / nblk, blk = a + (im.item - bh * nblk);
+  const int64_t b = bh / H, h = bh - b * H;
+  const int64_t d0 = (int64_t)im.lane * VEC;
+  if (d0 >= D) return;
+  const int64_t row0 = (bh * cap + blk) * k;
+  const int8_t* src = store + row0 * D + d0;
+
+  u32x2 q[KMAX];
+  float s[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < k) {
+      q[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src + (int64_t)j * D));
+      s[j] = scales[row0 + j];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  float acc[R][VEC];
+#pragma unroll
+  for (int t = 0; t < R; ++t)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[t][v] = 0.f;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (j < k) {
+      float c[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const int code = (int)(int8_t)(q[j][v >> 2] >> (8 * (v & 3)));
+        c[v] = (float)code * s[j];
+      }
+      const float* mj = basis + j * R;
+#pragma unroll
+      for (int t = 0; t < R; ++t) {
+        const float w = mj[t];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[t][v] = __builtin_fmaf(c[v], w, acc[t][v]);
+      }
+    }
+  }
+  TO* dst = out + b * osb + h * osh + d0 + blk * R * oss;
+  const int64_t tok0 = blk * R;
+#pragma unroll
+  for (int t = 0; t < R; ++t)
+    if (tok0 + t < out_len) nt_store8<TO>(dst + t * oss, acc[t]);
 }
 
 // ------------------------------------------------------------ quantize rows
@@ -664,10 +787,13 @@ int fc_jpeg_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_s
   if (quant_bits && r == 8 && vec == 8 && s_valid >= m * r) {
     const int rc = with_float_type(x_dtype, [&](auto tv) {
       using T = decltype(tv);
-      jpeg_encode_r8q_kernel<T><<<grid, kThreads, 0, st>>>(
-          (const T*)x, x_sb, x_sh, x_ss, H, m, D, k, basis, (int8_t*)coeffs, scales, cap, n0,
-          items, lg);
-      return FC_OK;
+      return with_int<2, 4, 8, 0>(k == 2 || k == 4 || k == 8 ? k : 0, [&](auto kc) {
+        constexpr int KT = decltype(kc)::value;
+        jpeg_encode_r8q_kernel<T, KT><<<grid, kThreads, 0, st>>>(
+            (const T*)x, x_sb, x_sh, x_ss, H, m, D, k, basis, (int8_t*)coeffs, scales, cap, n0,
+            items, lg);
+        return FC_OK;
+      });
     });
     return rc != FC_OK ? rc : check_launch();
   }
@@ -729,7 +855,18 @@ int fc_jpeg_decode(const void* store, int store_dtype, const float* scales, int6
     });
   };
   int rc;
-  if (quant) {
+  if (quant && r == 8 && vec == 8) {
+    rc = with_float_type(out_dtype, [&](auto to) {
+      using TO = decltype(to);
+      return with_int<2, 4, 8, 0>(k == 2 || k == 4 || k == 8 ? k : 0, [&](auto kc) {
+        constexpr int KT = decltype(kc)::value;
+        jpeg_decode_r8q_kernel<TO, KT><<<grid, kThreads, 0, st>>>(
+            (const int8_t*)store, scales, H, cap, a, nblk, D, k, basis, (TO*)out, o_sb, o_sh,
+            o_ss, out_len, items, lg);
+        return FC_OK;
+      });
+    });
+  } else if (quant) {
     rc = with_float_type(out_dtype, [&](auto to) { return launch(int8_t{}, to); });
   } else if (out_dtype == FC_F32) {
     rc = with_float_type(store_dtype, [&](auto ti) { return launch(ti, float{}); });

@@ -81,6 +81,15 @@ float round_to(int dtype, float f) {
   }
 }
 
+// int8 code of a rounded quotient q: clamp to [-127, 127]
+// (quantize_coeffs, flashcodec/codecs/jpeg.py:96-99).  The reference casts
+// a NaN quotient to int8, which C++ leaves undefined; x86's truncating
+// conversion gives 0 there, and 0 is the code used here.
+int8_t quant_clamp(float q) {
+  if (std::isnan(q)) return 0;
+  return (int8_t)std::min(127.0f, std::max(-127.0f, q));
+}
+
 }  // namespace
 
 extern "C" {
@@ -109,9 +118,8 @@ void orc_jpeg_encode(const float* x, long n_items, int r, int k, long D, const f
       if (!(s > 0.0f)) s = 1.0f;
       scales[it * k + j] = s;
       for (long d = 0; d < D; ++d) {
-        float q = std::nearbyint(cb[j * D + d] / s);  // default mode: ties to even
-        q = std::min(127.0f, std::max(-127.0f, q));
-        codes[(it * k + j) * D + d] = (int8_t)q;
+        const float q = std::nearbyint(cb[j * D + d] / s);  // default mode: ties to even
+        codes[(it * k + j) * D + d] = quant_clamp(q);
       }
     }
   }
@@ -135,8 +143,8 @@ void orc_quantize(const float* c, long n_rows, long D, int dtype, int8_t* codes,
     if (!(s > 0.0f)) s = 1.0f;
     scales[i] = s;
     for (long d = 0; d < D; ++d) {
-      float q = std::nearbyint(c[i * D + d] / s);
-      codes[i * D + d] = (int8_t)std::min(127.0f, std::max(-127.0f, q));
+      const float q = std::nearbyint(c[i * D + d] / s);
+      codes[i * D + d] = quant_clamp(q);
     }
   }
 }

@@ -398,3 +398,38 @@ def test_f16_coefficients_round_through_fp32(oracle):
     jp.encode_into(x, 8, 4, 8, cq, cs, m, 0, m, 8 * m)
     assert np.array_equal(bits(cs[..., 0].cpu().numpy()), bits(scales))
     assert np.array_equal(cq.cpu().numpy(), codes)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_quantizer_nan_and_inf(dt, oracle):
+    """NaN coefficients get code 0 and leave the row's absmax alone; an
+    infinite coefficient makes the scale infinite (codes 0), in the row
+    quantizer and in both int8 archive kernels (r = 1 general, r = 8)."""
+    from flashcodec_amd.codecs import jpeg as jp
+    print(f"case quant-nan-inf {dt}", flush=True)
+    rng = np.random.default_rng(seed_of("quant-nan-inf", dt))
+    D, R = 64, 48
+    rows = oracle.round_to(rng.standard_normal((R, D)).astype(np.float32) * 3, dt)
+    for i in range(0, R, 3):
+        rows[i, rng.integers(0, D, 3)] = np.nan
+    rows[5, 7] = np.inf
+    rows[11, 0] = -np.inf
+    codes, scales = oracle.quantize(rows, dt)
+    assert (codes[np.isnan(rows)] == 0).all()
+    t = torch.from_numpy(rows).to(torch_dtype(dt)).to(DEV)
+    q, s = fc.quantize_coeffs(t)
+    assert np.array_equal(q.cpu().numpy(), codes)
+    assert np.array_equal(bits(s[..., 0].cpu().numpy()), bits(scales))
+    # r = 1 (general kernel) and r = 8 (token 0 of each block carries the row)
+    for r in (1, 8):
+        xv = np.zeros((1, 1, R * r, D), np.float32)
+        xv[0, 0, ::r] = rows
+        k = 1 if r == 1 else 4
+        basis = fc.dct_basis(r, k).numpy()
+        _, codes_r, scales_r = oracle.jpeg_encode(xv, r, k, basis, dt, quant=True)
+        x = torch.from_numpy(xv).to(torch_dtype(dt)).to(DEV)
+        cq = torch.zeros((1, 1, R, k, D), dtype=torch.int8, device=DEV)
+        cs = torch.zeros((1, 1, R, k, 1), dtype=torch.float32, device=DEV)
+        jp.encode_into(x, r, k, 8, cq, cs, R, 0, R, R * r)
+        assert np.array_equal(cq.cpu().numpy(), codes_r), r
+        assert np.array_equal(bits(cs[..., 0].cpu().numpy()), bits(scales_r)), r
