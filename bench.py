@@ -413,8 +413,8 @@ def cpu_baseline(q, ks, vs, min_seconds=10.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--mode", choices=["c3", "c1", "c2", "c4", "c5", "refshapes", "copy"],
                     default="c3")
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)

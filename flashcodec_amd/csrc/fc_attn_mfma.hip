@@ -98,6 +98,7 @@ constexpr float kLazyMax = 8.f;        // exponentials may reach 2^8 before a re
 constexpr int kTapsUnrolled = 16;      // softmax taps unrolled (block sizes up to 16)
 constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor: 32-bit data format
 constexpr int kCachePolicySc1 = 16;    // buffer load cache policy: device scope (sc1)
+constexpr int kCachePolicyNt = 2;      // buffer load cache policy: nontemporal (streaming)
 constexpr int kWaitVmcnt0 = 0x0F70;    // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
 
 // Orders this wavefront's LDS writes before its later LDS reads (lanes of a
@@ -445,8 +446,12 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
       for (int dv = 0; dv < DV; ++dv)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
+          // V rows are consumed once per pass: streaming loads (measured
+          // faster than default or device-scope policy; K stays default,
+          // where streaming measured slower)
           const u32x2_t v = __builtin_bit_cast(
-              u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rv, v_off[dv] + (32 * sl + i) * D, 0, 0));
+              u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                           rv, v_off[dv] + (32 * sl + i) * D, 0, kCachePolicyNt));
           vr[sl][dv][2 * i] = v[0];
           vr[sl][dv][2 * i + 1] = v[1];
         }
