@@ -100,6 +100,8 @@ constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor: 32-bit data for
 constexpr int kCachePolicySc1 = 16;    // buffer load cache policy: device scope (sc1)
 constexpr int kCachePolicyNt = 2;      // buffer load cache policy: nontemporal (streaming)
 constexpr int kWaitVmcnt0 = 0x0F70;    // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
+constexpr int kPubWord = 1;            // publication counter: word 1 of a group's arrival line
+constexpr int kSpinCap = 1 << 24;      // polls of the publication counter before giving up
 
 // Orders this wavefront's LDS writes before its later LDS reads (lanes of a
 // wavefront exchange data through its private LDS region).
@@ -142,67 +144,29 @@ __device__ __forceinline__ void st_elem(void* ptr, int dt, int64_t i, float v) {
   }
 }
 
-// Merge of one (batch, kv head, head group) by the workgroup that arrived
-// last: the n_splits partials of its G query heads (read with device-scope
-// loads) and the raw-tail tokens, out = (sum_s w_s acc_s + sum_t e_t v_t) / l.
-// TQ: query / output element type, TR: raw-tail element type (void: dtypes
-// read at run time).  `lds` holds >= 16 * (2 * kFuseMaxSplits + FC_MAX_BLOCK)
-// + 16 floats.
-template <int D, typename TQ, typename TR>
-__device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
-                            int tid, float* lds) {
-  constexpr int C4 = D / 4;      // float4 chunks of a head's output
-  constexpr int kPre = 16;       // partials prefetched per thread
+// Raw-tail partial of one (batch, kv head, head group): for each of its G
+// query heads the base-2 logits of the n_raw tail tokens at full precision,
+// their maximum tm[h], sum tl[h] = sum_t 2^(logit_t - tm[h]) and
+// acc[h][d] = sum_t 2^(logit_t - tm[h]) v_t[d].  `etl` holds
+// 16 * FC_MAX_BLOCK floats; every thread of the workgroup takes part.
+template <int D>
+__device__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
+                                 int tid, float* etl, float* acc, float* tm, float* tl) {
   const int lane = tid & 63, wave = tid >> 6;
-  const int ns = p.n_splits;
   const int nr = (int)p.n_raw;
-  const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;  // slot of head 0 of the group
-  float* wsp = lds;                            // [16][kFuseMaxSplits] split maxima -> weights
-  float* plv = wsp + 16 * kFuseMaxSplits;      // [16][kFuseMaxSplits] split sums
-  float* etl = plv + 16 * kFuseMaxSplits;      // [16][FC_MAX_BLOCK] tail logits -> exps
-  float* inv = etl + 16 * FC_MAX_BLOCK;        // [16] 1 / softmax denominator
-
-  // device-scope (L2-missing) loads of the group's partials
-  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, G * ns * D * 4);
-  auto part = [&](int h, int sp, int c) {
-    return __builtin_bit_cast(
-        float4, __builtin_amdgcn_raw_buffer_load_b128(rp, ((h * ns + sp) * C4 + c) * 16, 0,
-                                                      kCachePolicySc1));
-  };
-  // one output task (head, 4 features) per thread when they fit: its
-  // partials are requested now, with the statistics and the tail logits
-  const bool one_task = G * C4 <= kMThreads && ns <= kPre;
-  float4 pre[kPre];
-  if (one_task && tid < G * C4) {
-    const int h = tid / C4, c = tid - h * C4;
-#pragma unroll
-    for (int j = 0; j < kPre; ++j)
-      if (j < ns) pre[j] = part(h, j, c);
-  }
-  for (int u = tid; u < G * ns; u += kMThreads) {
-    const int h = u / ns, sp = u - h * ns;
-    const int64_t slot = (bq0 + h) * ns + sp;
-    wsp[h * kFuseMaxSplits + sp] =
-        __hip_atomic_load(p.pm + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    plv[h * kFuseMaxSplits + sp] =
-        __hip_atomic_load(p.pl + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
   {
-    // raw-tail logits: 16 lanes per (head, token), features strided by 16
+    // logits: 16 lanes per (head, token), features strided by 16
     const int grp = tid >> 4, gl = tid & 15;
     for (int u = grp; u < G * nr; u += kMThreads / 16) {
       const int h = u / nr, t = u - h * nr;
-      const int64_t hq_t = hkv * p.G + g0 + h;
-      float qv[D / 16], kv[D / 16];
-#pragma unroll
-      for (int i = 0; i < D / 16; ++i) {
-        qv[i] = ld_elem<TQ>(p.q, p.q_dtype, b * p.q_sb + hq_t * p.q_sh + gl + 16 * i);
-        kv[i] = ld_elem<TR>(p.kraw, p.raw_dtype,
-                            b * p.kr_sb + hkv * p.kr_sh + t * p.kr_st + gl + 16 * i);
-      }
+      const int64_t hq = hkv * p.G + g0 + h;
       float a = 0.f;
 #pragma unroll
-      for (int i = 0; i < D / 16; ++i) a = __builtin_fmaf(qv[i], kv[i], a);
+      for (int i = 0; i < D / 16; ++i)
+        a = __builtin_fmaf(load_q(p.q, p.q_dtype, b * p.q_sb + hq * p.q_sh + gl + 16 * i),
+                           load_q(p.kraw, p.raw_dtype,
+                                  b * p.kr_sb + hkv * p.kr_sh + t * p.kr_st + gl + 16 * i),
+                           a);
 #pragma unroll
       for (int m = 8; m >= 1; m >>= 1) a += __shfl_xor(a, m, 16);
       if (gl == 0) etl[h * FC_MAX_BLOCK + t] = a * p.scale_log2;
@@ -211,17 +175,10 @@ __device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g
   __syncthreads();
   for (int h = wave; h < G; h += kWaves) {
     float mx = -INFINITY;
-    for (int sp = lane; sp < ns; sp += 64) mx = fmaxf(mx, wsp[h * kFuseMaxSplits + sp]);
     for (int t = lane; t < nr; t += 64) mx = fmaxf(mx, etl[h * FC_MAX_BLOCK + t]);
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
     float l = 0.f;
-    for (int sp = lane; sp < ns; sp += 64) {
-      const float pmv = wsp[h * kFuseMaxSplits + sp];
-      const float w = pmv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pmv - mx);
-      wsp[h * kFuseMaxSplits + sp] = w;
-      l = __builtin_fmaf(w, plv[h * kFuseMaxSplits + sp], l);
-    }
     for (int t = lane; t < nr; t += 64) {
       const float e = __builtin_amdgcn_exp2f(etl[h * FC_MAX_BLOCK + t] - mx);
       etl[h * FC_MAX_BLOCK + t] = e;
@@ -229,28 +186,52 @@ __device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g
     }
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
-    if (lane == 0) inv[h] = 1.0f / l;
+    if (lane == 0) {
+      tm[h] = mx;
+      tl[h] = l;
+    }
   }
   __syncthreads();
+  for (int x = tid; x < G * D; x += kMThreads) {
+    const int h = x / D, d = x - h * D;
+    float o = 0.f;
+    for (int t = 0; t < nr; ++t)
+      o = __builtin_fmaf(etl[h * FC_MAX_BLOCK + t],
+                         load_q(p.vraw, p.raw_dtype, b * p.vr_sb + hkv * p.vr_sh + t * p.vr_st + d),
+                         o);
+    acc[h * D + d] = o;
+  }
+}
 
-  auto finish_out = [&](int h, int c, const float4& o) {
-    const float iv = inv[h];
-    const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
-    st_elem<TQ>(p.out, p.q_dtype, ob + 0, o.x * iv);
-    st_elem<TQ>(p.out, p.q_dtype, ob + 1, o.y * iv);
-    st_elem<TQ>(p.out, p.q_dtype, ob + 2, o.z * iv);
-    st_elem<TQ>(p.out, p.q_dtype, ob + 3, o.w * iv);
+// Merge of one (batch, kv head, head group) by the workgroup that arrived
+// last, once every other workgroup of the group has published its partial:
+// out = sum_s w_s acc_s / sum_s w_s l_s over the n_splits partials of its G
+// query heads, w_s = 2^(m_s - max_s m_s).  This workgroup's own partial is
+// read from LDS (own_acc [16][D], own_m, own_l), the others with
+// device-scope loads; the raw tail is part of split 0's partial.  Each
+// thread owns an output task (head, 4 features) and reduces its head's
+// statistics itself, so the merge needs no barrier.
+template <int D>
+__device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
+                            int split, int tid, const float* own_acc, const float* own_m,
+                            const float* own_l) {
+  constexpr int C4 = D / 4;  // float4 chunks of a head's output
+  constexpr int kPre = 8;    // splits held in registers by one task
+  const int ns = p.n_splits;
+  const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;  // slot of head 0 of the group
+
+  // device-scope (L2-missing) loads of the group's partials
+  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, G * ns * D * 4);
+  auto part = [&](int h, int sp, int c) {
+    if (sp == split) return *reinterpret_cast<const float4*>(own_acc + h * D + 4 * c);
+    return __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(rp, ((h * ns + sp) * C4 + c) * 16, 0,
+                                                      kCachePolicySc1));
   };
-  auto finish = [&](int h, int c, float4 o) {
-    for (int t = 0; t < nr; ++t) {
-      const float e = etl[h * FC_MAX_BLOCK + t];
-      const int64_t base = b * p.vr_sb + hkv * p.vr_sh + t * p.vr_st + 4 * c;
-      o.x = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 0), o.x);
-      o.y = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 1), o.y);
-      o.z = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 2), o.z);
-      o.w = __builtin_fmaf(e, ld_elem<TR>(p.vraw, p.raw_dtype, base + 3), o.w);
-    }
-    finish_out(h, c, o);
+  auto stat = [&](const float* v, const float* own, int h, int sp) {
+    return sp == split ? own[h]
+                       : __hip_atomic_load(v + (bq0 + h) * ns + sp, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
   };
   auto fma4 = [](float w, const float4& v, float4& o) {
     o.x = __builtin_fmaf(w, v.x, o.x);
@@ -258,31 +239,50 @@ __device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g
     o.z = __builtin_fmaf(w, v.z, o.z);
     o.w = __builtin_fmaf(w, v.w, o.w);
   };
-  if (one_task) {
-    if (tid < G * C4) {
-      const int h = tid / C4, c = tid - h * C4;
-      float4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < kPre; ++j)
-        if (j < ns) fma4(wsp[h * kFuseMaxSplits + j], pre[j], o);
-      finish(h, c, o);
-    }
-    return;
-  }
+  auto finish_out = [&](int h, int c, const float4& o, float l) {
+    const float iv = 1.0f / l;
+    const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
+    store_any(p.out, p.q_dtype, ob + 0, o.x * iv);
+    store_any(p.out, p.q_dtype, ob + 1, o.y * iv);
+    store_any(p.out, p.q_dtype, ob + 2, o.z * iv);
+    store_any(p.out, p.q_dtype, ob + 3, o.w * iv);
+  };
   for (int task = tid; task < G * C4; task += kMThreads) {
     const int h = task / C4, c = task - h * C4;
-    const float* wh = wsp + h * kFuseMaxSplits;
+    float mx = -INFINITY, l = 0.f;
     float4 o = {0.f, 0.f, 0.f, 0.f};
-    int sp = 0;
-    for (; sp + 8 <= ns; sp += 8) {
-      float4 v[8];
+    // kPre splits at a time, every load of a chunk in flight at once
+    for (int sp0 = 0; sp0 < ns; sp0 += kPre) {
+      float4 pre[kPre];
+      float pm[kPre], pl[kPre];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = part(h, sp + j, c);
+      for (int j = 0; j < kPre; ++j)
+        if (sp0 + j < ns) {
+          pre[j] = part(h, sp0 + j, c);
+          pm[j] = stat(p.pm, own_m, h, sp0 + j);
+          pl[j] = stat(p.pl, own_l, h, sp0 + j);
+        }
+      float nm = mx;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) fma4(wh[sp + j], v[j], o);
+      for (int j = 0; j < kPre; ++j)
+        if (sp0 + j < ns) nm = fmaxf(nm, pm[j]);
+      if (nm == -INFINITY) continue;  // empty partials only so far
+      const float f = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mx - nm);
+      l *= f;
+      o.x *= f;
+      o.y *= f;
+      o.z *= f;
+      o.w *= f;
+#pragma unroll
+      for (int j = 0; j < kPre; ++j)
+        if (sp0 + j < ns) {
+          const float w = pm[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[j] - nm);
+          l = __builtin_fmaf(w, pl[j], l);
+          fma4(w, pre[j], o);
+        }
+      mx = nm;
     }
-    for (; sp < ns; ++sp) fma4(wh[sp], part(h, sp, c), o);
-    finish(h, c, o);
+    finish_out(h, c, o, l);
   }
 }
 
@@ -302,6 +302,10 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   __shared__ float sc_lds[kWaves][2][PR];  // K and V row scales of the pass
   __shared__ float a_lds[FC_MAX_BLOCK * 4];
   __shared__ float comb[kWaves][16][3];
+  __shared__ float cbuf[kWaves][GP][D];  // the wavefronts' accumulators, for the combine
+  __shared__ __attribute__((aligned(16))) float part_lds[16 * D];  // raw-tail partial, then this workgroup's partial
+  __shared__ float tail_ml[2][16];    // raw-tail (max, sum) per head
+  __shared__ float wg_ml[2][16];      // this workgroup's (max, sum) per head
   __shared__ int s_last;
 
   // 1-D grid, split-major: workgroup L runs split s of group g; the splits of
@@ -496,7 +500,14 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
     }
   };
 
-  __syncthreads();  // a_lds
+  // raw tail (fused calls): split 0 computes its partial before the passes
+  // and folds it into its own, so the final merge reads partials only
+  const bool fold_tail = p.fused && split == 0 && p.n_raw > 0;
+  if (fold_tail)
+    raw_tail_partial<D>(p, b, hkv, g0, G, tid, reinterpret_cast<float*>(&w_lds[0][0][0]),
+                        part_lds, tail_ml[0], tail_ml[1]);
+
+  __syncthreads();  // a_lds; the tail's scratch (w_lds) is free again
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
   int64_t cur = pass_of(grab());
   if (cur < npass) load_k(cur * PR, rows_of(cur));
@@ -623,8 +634,10 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
     cur = nxt;
   }
 
-  // ---- combine the wavefronts.  Lane c < GP carries head c's (max, sum);
-  // each wave's accumulators carry a factor 2^-sig_run.
+  // ---- combine the wavefronts.  Each wavefront parks its (max, sum,
+  // 2^sig_run) per head and its accumulators in its own LDS region; after one
+  // barrier thread x of the G * D outputs combines them (lane (q, c) of a
+  // wavefront carries head c's statistics; its register i holds head 4q + i).
 #pragma unroll
   for (int m = GP; m < 64; m <<= 1) l_lane += __shfl_xor(l_lane, m, 64);
   if (lane < GP) {
@@ -632,25 +645,20 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
     comb[wave][lane][1] = l_lane;
     comb[wave][lane][2] = ldexpf(1.0f, sig_run);
   }
-  float* obuf = &s_lds[0][0][0];  // [wave*4 + i][D] for the 4 heads of a lane group
-  for (int h0 = 0; h0 < G; h0 += 4) {
-    __syncthreads();
-    if (lq == h0 / 4) {
+  constexpr int NI = GP < 4 ? GP : 4;  // accumulator registers that can hold a head
 #pragma unroll
-      for (int dv = 0; dv < DV; ++dv)
+  for (int dv = 0; dv < DV; ++dv)
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
+    for (int e = 0; e < 8; ++e)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int d = 128 * dv + 8 * lc + e;
-            if (d < D) obuf[(wave * 4 + i) * D + d] = acc[dv][e][i];
-          }
-    }
-    __syncthreads();
-    for (int x = tid; x < 4 * D; x += kMThreads) {
-      const int i = x / D, d = x - i * D;
-      const int h = h0 + i;
-      if (h >= G) continue;
+      for (int i = 0; i < NI; ++i) {
+        const int h = 4 * lq + i, d = 128 * dv + 8 * lc + e;
+        if (h < G && d < D) cbuf[wave][h][d] = acc[dv][e][i];
+      }
+  __syncthreads();
+  {
+    for (int x = tid; x < G * D; x += kMThreads) {
+      const int h = x / D, d = x - h * D;
       float M = -INFINITY;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[w][h][0]);
@@ -659,53 +667,86 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
       for (int w = 0; w < kWaves; ++w) {
         const float mw = comb[w][h][0];
         const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-        o = __builtin_fmaf(f * comb[w][h][2], obuf[(w * 4 + i) * D + d], o);
+        o = __builtin_fmaf(f * comb[w][h][2], cbuf[w][h][d], o);
         l = __builtin_fmaf(f, comb[w][h][1], l);
       }
-      const int64_t bq = b * (p.Hkv * p.G) + hkv * p.G + g0 + h;
-      const int64_t slot = bq * p.n_splits + split;
-      // agent-coherent stores: another workgroup may merge them
-      __hip_atomic_store(p.pacc + slot * D + d, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (fold_tail) {
+        // rescale both sums to the common maximum max(M, mt)
+        const float mt = tail_ml[0][h];
+        const float mm = fmaxf(M, mt);
+        const float fw = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mm);
+        const float ft = __builtin_amdgcn_exp2f(mt - mm);
+        o = __builtin_fmaf(ft, part_lds[h * D + d], o * fw);
+        l = __builtin_fmaf(ft, tail_ml[1][h], l * fw);
+        M = mm;
+      }
+      part_lds[x] = o;
       if (d == 0) {
-        __hip_atomic_store(p.pm + slot, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.pl + slot, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wg_ml[0][h] = M;
+        wg_ml[1][h] = l;
       }
     }
   }
-  // ---- arrival.  Each workgroup publishes its partials and counts its
-  // arrival; the last of the group's n_splits workgroups returns the group's
-  // counters to zero for the next call and, in the fused form, merges the
-  // partials with the raw tail.
-  // Publication without cache-wide writeback/invalidate (each costs ~0.1 us
-  // and they serialize per XCD): partials are device-scope stores, complete
-  // (vmcnt 0, which also covers the pass-queue atomics) before the arrival is
-  // counted, and are read back with device-scope loads.
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __syncthreads();
+  // ---- arrival, then publication.  A workgroup counts its arrival first;
+  // all but the last of the group's n_splits workgroups then publish their
+  // partial (device-scope stores) and, once the stores are complete, count
+  // the publication.  The last one keeps its own partial in LDS, waits for
+  // the other n_splits - 1 publications (they arrived before it and need
+  // nothing more to finish), returns the group's counters to zero for the
+  // next call and merges.  No cache-wide writeback/invalidate is used (each
+  // costs ~0.1 us and they serialize per XCD); partials are read back with
+  // device-scope loads.  Without the fused merge every workgroup publishes
+  // and the merge runs as its own kernel.
+  // thread x publishes (or merges) the outputs x + 256 k it combined itself;
+  // the barrier below orders the combine before the last workgroup's merge
+  unsigned int* arrive = p.arrive + g * p.cstride;
   if (tid == 0) {
-    unsigned int* arrive = p.arrive + g * p.cstride;
     const unsigned int old = atomicAdd(arrive, 1u);
-    const bool last = old + 1 == (unsigned int)p.n_splits;
-    if (last) {
+    s_last = old + 1 == (unsigned int)p.n_splits ? 1 : 0;
+  }
+  __syncthreads();
+  const bool last = s_last != 0;
+  if (!last || !p.fused) {
+    const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;
+    for (int x = tid; x < G * D; x += kMThreads) {
+      const int h = x / D, d = x - h * D;
+      const int64_t slot = (bq0 + h) * p.n_splits + split;
+      __hip_atomic_store(p.pacc + slot * D + d, part_lds[x], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      if (d == 0) {
+        __hip_atomic_store(p.pm + slot, wg_ml[0][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.pl + slot, wg_ml[1][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (!p.fused) {
+    if (last && tid == 0) {
       __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    s_last = last ? 1 : 0;
+    return;
+  }
+  if (!last) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0) atomicAdd(arrive + kPubWord, 1u);
+    return;
+  }
+  if (tid == 0) {
+    const unsigned int want = (unsigned int)p.n_splits - 1u;
+    for (int it = 0; it < kSpinCap; ++it) {
+      if (__hip_atomic_load(arrive + kPubWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= want)
+        break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(arrive + kPubWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  if (!s_last || !p.fused) return;
-
-  const bool q16 = p.q_dtype == FC_F16;
-  if (p.raw_dtype == p.q_dtype) {
-    if (q16)
-      fused_merge<D, f16_t, f16_t>(p, b, hkv, g0, G, tid, &s_lds[0][0][0]);
-    else
-      fused_merge<D, bf16_t, bf16_t>(p, b, hkv, g0, G, tid, &s_lds[0][0][0]);
-  } else {
-    fused_merge<D, void, void>(p, b, hkv, g0, G, tid, &s_lds[0][0][0]);
-  }
+  fused_merge<D>(p, b, hkv, g0, G, split, tid, part_lds, wg_ml[0], wg_ml[1]);
 }
 
 template <int... Vs, typename F>
