@@ -56,6 +56,7 @@ SIGNATURES = {
                              _i64, _i64, _i64, _i64, _vp]),
     "fc_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _int]),
     "fc_attention_default_splits": (_int, [_i64, _i64, _i64, _i64, _int]),
+    "fc_attention_splits": (_int, [_int, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _int]),
     "fc_decode_attention": _ATTN_SIG,
     "fc_decode_attention_split": _ATTN_SIG,
     "fc_decode_attention_merge": _ATTN_SIG,

@@ -131,7 +131,8 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
     out = torch.empty_like(q)
     dev = q.device
     L = N.lib()
-    n_splits = L.fc_attention_default_splits(nb, B, Hkv, Hq // Hkv, N.num_cus(dev))
+    n_splits = L.fc_attention_splits(kind, N.dtype_code(ks.dtype), N.dtype_code(q.dtype), s, nb,
+                                     B, Hkv, Hq // Hkv, D, N.num_cus(dev))
     if _n_splits is not None and nb:
         # split count override (tests / tuning); trimmed to non-empty splits
         per = -(-nb // max(1, int(_n_splits)))

@@ -655,6 +655,54 @@ int attn_with_int(int v, F&& f) {
   return hit ? rc : FC_ERR_UNSUPPORTED;
 }
 
+// Workgroups per compute unit of the vector-ALU split pass that would run
+// for this store (kernel occupancy, cached per instantiation); 0 if the
+// runtime cannot report it.
+template <typename TS, int KIND, bool SREG, int GM>
+int valu_occupancy_of() {
+  static int cached = -1;
+  if (cached < 0) {
+    int n = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &n, reinterpret_cast<const void*>(&attn_split_kernel<TS, KIND, SREG, 8, GM>),
+        kAttnThreads, 0);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    cached = n;
+  }
+  return cached;
+}
+
+int valu_split_occupancy(int store_kind, int stream_dtype, int s, int gm) {
+  const bool sreg = s <= 8;
+  return attn_with_int<1, 2, 4, 8>(gm, [&](auto gc) -> int {
+    constexpr int GM = decltype(gc)::value;
+    using KI8 = std::integral_constant<int, FC_STORE_JPEG_I8>;
+    using KFP = std::integral_constant<int, FC_STORE_JPEG_FP>;
+    using KPNG = std::integral_constant<int, FC_STORE_PNG>;
+    auto by_dtype = [&](auto kc, auto sc) -> int {
+      constexpr int KIND = decltype(kc)::value;
+      constexpr bool SREG = decltype(sc)::value;
+      switch (stream_dtype) {
+        case FC_F32: return valu_occupancy_of<float, KIND, SREG, GM>();
+        case FC_F16: return valu_occupancy_of<f16_t, KIND, SREG, GM>();
+        case FC_BF16: return valu_occupancy_of<bf16_t, KIND, SREG, GM>();
+        default: return 0;
+      }
+    };
+    if (store_kind == FC_STORE_JPEG_I8)
+      return sreg ? valu_occupancy_of<float, FC_STORE_JPEG_I8, true, GM>()
+                  : valu_occupancy_of<float, FC_STORE_JPEG_I8, false, GM>();
+    if (store_kind == FC_STORE_PNG) return by_dtype(KPNG{}, std::true_type{});
+    if (store_kind == FC_STORE_JPEG_FP)
+      return sreg ? by_dtype(KFP{}, std::true_type{}) : by_dtype(KFP{}, std::false_type{});
+    (void)KI8{};
+    return 0;
+  });
+}
+
 }  // namespace fc
 
 using namespace fc;
@@ -697,6 +745,27 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G, i
   want = std::min<int64_t>(want, (nb + 15) / 16);
   want = std::max<int64_t>(1, std::min<int64_t>(want, kMaxSplits));
   // splits that are actually non-empty
+  const int64_t bps = (nb + want - 1) / want;
+  return (int)((nb + bps - 1) / bps);
+}
+
+int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, int64_t nb,
+                        int64_t B, int64_t Hkv, int64_t G, int64_t D, int n_cu) {
+  if (nb <= 0) return 0;
+  const bool mfma = store_kind == FC_STORE_JPEG_I8 && (q_dtype == FC_F16 || q_dtype == FC_BF16) &&
+                    (D == 64 || D == 128 || D == 256) && (s == 1 || s == 2 || s == 4) &&
+                    fc::mfma_split_allowed();
+  if (mfma) return fc_attention_default_splits(nb, B, Hkv, G, n_cu);
+  if (n_cu <= 0) n_cu = 256;
+  // vector-ALU split pass: one round of its workgroups at the occupancy the
+  // kernel reaches on this device (two per compute unit if it cannot be read)
+  const int gm = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
+  int per_cu = fc::valu_split_occupancy(store_kind, stream_dtype, s, gm);
+  if (per_cu <= 0) per_cu = 2;
+  const int64_t cols = std::max<int64_t>(1, B * Hkv * ((G + gm - 1) / gm));
+  int64_t want = ((int64_t)per_cu * n_cu + cols - 1) / cols;
+  want = std::min<int64_t>(want, (nb + 15) / 16);
+  want = std::max<int64_t>(1, std::min<int64_t>(want, fc::kMaxSplits));
   const int64_t bps = (nb + want - 1) / want;
   return (int)((nb + bps - 1) / bps);
 }

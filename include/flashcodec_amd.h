@@ -184,6 +184,20 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G,
                                  int n_cu);
 
 /*
+ * Split count for a fc_decode_attention call over stores of `store_kind`
+ * (stream dtype, query dtype, s stored rows per block, head size D): one
+ * round of workgroups of the split pass that will run — the matrix-core
+ * pass for int8 jpeg archives with fp16/bf16 queries (as
+ * fc_attention_default_splits), otherwise the vector-ALU pass at the
+ * occupancy it reaches on the current device.  0 when nb == 0.
+ * Replaces the split heuristic ns = max(1, min(32, ceil(n / 64))) of
+ * flashcodec/triton_attention.py:191.
+ */
+int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s,
+                        int64_t nb, int64_t B, int64_t Hkv, int64_t G, int64_t D,
+                        int n_cu);
+
+/*
  * Materialisation-free decode attention of one query token per sequence:
  *   q (B, Hq, 1, D) in q_dtype with element strides q_sb, q_sh
  *   K/V archives of nb blocks with s stored rows each, synthesis matrix

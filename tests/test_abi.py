@@ -51,6 +51,22 @@ def test_workspace_and_split_policy():
             assert bps * (ns - 1) < nb          # no empty split
 
 
+def test_store_aware_split_count():
+    """int8 jpeg stores with half-precision queries take the matrix-core
+    split count; other stores one round of the vector-ALU pass (two
+    workgroups per compute unit when no device reports the occupancy)."""
+    L = N.lib()
+    assert L.fc_attention_splits(N.STORE_PNG, N.F32, N.F32, 16, 0, 2, 8, 4, 128, 256) == 0
+    for nb in (1, 7, 1024, 4096, 100000):
+        for cols in ((8, 8, 4), (2, 8, 4), (1, 32, 1)):
+            assert (L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, 4, nb, *cols, 128, 256)
+                    == L.fc_attention_default_splits(nb, *cols, 256))
+            for kind, s in ((N.STORE_PNG, 16), (N.STORE_JPEG_FP, 2), (N.STORE_JPEG_I8, 4)):
+                ns = L.fc_attention_splits(kind, N.F32, N.F32, s, nb, *cols, 128, 256)
+                assert 1 <= ns <= 256
+                assert -(-nb // ns) * (ns - 1) < nb   # no empty split
+
+
 def test_argument_validation_needs_no_device():
     L = N.lib()
     # k > r, bad quant bits, store overflow, bad dtype: rejected up front
