@@ -9,7 +9,7 @@ hand-written HIP kernels for gfx950 behind a C ABI (libflashcodec_amd.so,
 include/flashcodec_amd.h).  Public names follow flashcodec/__init__.py:13-37.
 """
 
-from .attention import block_basis, codec_decode_attention
+from .attention import block_basis, codec_decode_attention, codec_decode_step
 from .cache import HAS_HF_CACHE, CodecKVCache, FlashCodecCache, FlashCodecLayer, make_codec
 from .codecs import (JPEGCodec, PNGCodec, dct_basis, dct_compress, dct_decompress,
                      dequantize_coeffs, png_filter, png_reconstruct, quantize_coeffs)

@@ -35,6 +35,27 @@ class StreamView(ctypes.Structure):
     ]
 
 
+class StepStream(ctypes.Structure):
+    """fc_step_stream: one stream of a layer for fc_decode_step."""
+    _fields_ = [
+        ("rows", _vp), ("scales", _vp), ("anchors", _vp), ("cap", _i64), ("tail", _vp),
+        ("token", _vp), ("tok_sb", _i64), ("tok_sh", _i64),
+    ]
+
+
+class StepArgs(ctypes.Structure):
+    """fc_step_args: the arguments of fc_decode_step."""
+    _fields_ = [
+        ("q", _vp), ("q_dtype", _int), ("q_sb", _i64), ("q_sh", _i64),
+        ("B", _i64), ("Hq", _i64), ("Hkv", _i64), ("D", _i64),
+        ("store_kind", _int), ("stream_dtype", _int), ("r", _int), ("s", _int),
+        ("quant_bits", _int), ("keep_m", _int), ("n_blocks", _i64), ("n_tail", _i64),
+        ("basis", _vp), ("A", _vp), ("scale", _fp), ("out", _vp), ("o_sb", _i64), ("o_sh", _i64),
+        ("workspace", _vp), ("workspace_bytes", _i64), ("n_cu", _int), ("stream", _vp),
+        ("key", StepStream), ("value", StepStream),
+    ]
+
+
 _ATTN_SIG = (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _i64,
                     ctypes.POINTER(StreamView), ctypes.POINTER(StreamView), _i64, _vp, _fp, _vp,
                     _i64, _i64, _vp, _int, _vp])
@@ -61,6 +82,7 @@ SIGNATURES = {
     "fc_decode_attention_split": _ATTN_SIG,
     "fc_decode_attention_merge": _ATTN_SIG,
     "fc_png_topm_mask_host": (ctypes.c_uint64, [_vp, _int, _int]),
+    "fc_decode_step": (_int, [ctypes.POINTER(StepArgs)]),
 }
 
 _LIB = None
@@ -121,7 +143,14 @@ def require_gpu(*tensors):
                 f"got a tensor on {t.device}. Move the KV tensors to a ROCm device.")
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device):
+    """hipStream_t of torch's current stream on `device`."""
+    if _RAW_STREAM is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _RAW_STREAM(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -13,10 +13,13 @@ head's rows read once per group of up to eight query heads) and a merge pass
 that folds in the raw tail.
 """
 
+import ctypes
+
 import torch
 
 from . import _native as N
 from .codecs import dct_basis
+from .codecs.jpeg import device_basis as dct_basis_device
 
 _A_CACHE = {}
 _WORKSPACES = {}
@@ -47,8 +50,7 @@ def workspace(device, nbytes):
     one stream (which run in order) share it.  Calls on other streams get
     their own."""
     device = torch.device(device)
-    stream = torch.cuda.current_stream(device).cuda_stream
-    key = (device.index, stream)
+    key = (device.index, N.stream_ptr(device))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
@@ -148,4 +150,100 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
         N.dtype_code(ks.dtype), r, s, nb, kv, vv, n_raw, N.ptr(A), scale, out.data_ptr(),
         out.stride(0), out.stride(1), N.ptr(ws), n_splits, N.stream_ptr(dev))
     N.check(rc, "fc_decode_attention")
+    return out
+
+
+def _step_args(ks, vs, query, tokens):
+    """The fc_step_args of a (key, value) stream pair with the fields that do
+    not change between decode steps filled in (cached on the key stream)."""
+    plan = getattr(ks, "_step_plan", None)
+    B, Hq, _, D = query.shape
+    Hkv = tokens.shape[1]
+    dev = query.device
+    key = (id(vs), B, Hq, Hkv, D, query.dtype, ks.dtype, dev)
+    if plan is not None and plan[0] == key:
+        return plan[1], plan[2]
+    c = ks.codec
+    r = c.block_size
+    a = N.StepArgs()
+    a.q_dtype = N.dtype_code(query.dtype)
+    a.B, a.Hq, a.Hkv, a.D = B, Hq, Hkv, D
+    if c.name == "jpeg":
+        a.store_kind = N.STORE_JPEG_I8 if c.quantized else N.STORE_JPEG_FP
+        a.s = c.keep_freqs
+        a.quant_bits = c.quant_bits
+        a.basis = dct_basis_device(r, c.keep_freqs, dev).data_ptr()
+    else:
+        a.store_kind = N.STORE_PNG
+        a.s = r
+        a.keep_m = c.keep_m
+    a.stream_dtype = N.dtype_code(ks.dtype)
+    a.r = r
+    a.A = _device_A(c, r, dev).data_ptr()
+    a.n_cu = N.num_cus(dev)
+    L = N.lib()
+    most = L.fc_attention_splits(a.store_kind, a.stream_dtype, a.q_dtype, a.s, 1 << 40, B, Hkv,
+                                 Hq // Hkv, D, a.n_cu)
+    ws_bytes = L.fc_attention_workspace_bytes(B, Hq, D, most)
+    ks._step_plan = (key, a, ws_bytes)
+    return a, ws_bytes
+
+
+def codec_decode_step(query, key_tokens, value_tokens, key_stream, value_stream, scale=None):
+    """One decode step of a layer in one library call: appends the step's
+    key and value tokens (B, Hkv, 1, D) to their streams and attends the
+    query (B, Hq, 1, D) over the result; the same as
+    ``key_stream.append(key_tokens); value_stream.append(value_tokens);
+    codec_decode_attention(query, key_stream, value_stream, scale)``
+    (flashcodec/patch_attention.py:95-98), which it falls back to when the
+    streams are not yet initialised or the shapes do not allow the fused
+    call."""
+    ks, vs = key_stream, value_stream
+    B, Hq, Sq, D = query.shape
+    fused = (Sq == 1 and key_tokens.shape[-2] == 1 and value_tokens.shape[-2] == 1
+             and ks.meta is not None and vs.meta is not None and ks.codec is vs.codec
+             and key_tokens.dtype == ks.dtype and value_tokens.dtype == vs.dtype
+             and ks.dtype == vs.dtype and ks.n_blocks == vs.n_blocks
+             and ks._n_raw == vs._n_raw and key_tokens.shape == value_tokens.shape
+             and key_tokens.shape[0] == B and ks.meta[:3] == vs.meta[:3]
+             and ks.meta[0] == B and ks.meta[1] == key_tokens.shape[1]
+             and query.is_cuda and key_tokens.is_cuda and value_tokens.is_cuda
+             and query.stride(-1) == 1 and key_tokens.stride(-1) == 1
+             and value_tokens.stride(-1) == 1 and Hq % key_tokens.shape[1] == 0)
+    if not fused:
+        ks.append(key_tokens)
+        vs.append(value_tokens)
+        return codec_decode_attention(query, ks, vs, scale=scale)
+    r = ks.codec.block_size
+    t, nb = ks._n_raw, ks.n_blocks
+    for st, tok in ((ks, key_tokens), (vs, value_tokens)):
+        st._tail_buffer(tok)
+        if st._capacity == 0 or (t + 1 == r and nb + 1 > st._capacity):
+            st._grow(nb + 1, tok)
+    a, ws_bytes = _step_args(ks, vs, query, key_tokens)
+    dev = query.device
+    out = torch.empty_like(query)
+    a.q, a.q_sb, a.q_sh = query.data_ptr(), query.stride(0), query.stride(1)
+    a.n_blocks, a.n_tail = nb, t
+    a.scale = D ** -0.5 if scale is None else float(scale)
+    a.out, a.o_sb, a.o_sh = out.data_ptr(), out.stride(0), out.stride(1)
+    ws = workspace(dev, ws_bytes)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    a.stream = N.stream_ptr(dev)
+    for sv, st, tok in ((a.key, ks, key_tokens), (a.value, vs, value_tokens)):
+        rows, extra = st._archive_tensors()[0], st._archive_tensors()[1:]
+        sv.rows = rows.data_ptr()
+        sv.scales = extra[0].data_ptr() if (st.codec.name == "jpeg" and extra) else None
+        sv.anchors = extra[0].data_ptr() if st.codec.name == "png" else None
+        sv.cap = st._capacity
+        sv.tail = st._raw_buf.data_ptr()
+        sv.token, sv.tok_sb, sv.tok_sh = tok.data_ptr(), tok.stride(0), tok.stride(1)
+    N.check(N.lib().fc_decode_step(ctypes.byref(a)), "fc_decode_step")
+    if t + 1 == r:
+        for st in (ks, vs):
+            st.n_blocks += 1
+            st.n_archived += r
+            st._n_raw = 0
+    else:
+        ks._n_raw = vs._n_raw = t + 1
     return out

@@ -3,7 +3,9 @@ transformers-5.x Cache/DynamicLayer backends.
 
 Mirrors flashcodec/cache.py:39-654.  A stream (one K or V tensor of one
 layer, layout (B, H, S, D), codec axis -2) keeps
-  * a raw tail of < r tokens at full fidelity (``raw``),
+  * a raw tail of < r tokens at full fidelity (``raw``: a view of the first
+    t rows of a preallocated (B, H, r, D) tail buffer, so appending a token
+    is one copy and a completed block is archived straight from the buffer),
   * an archive of complete blocks in capacity-doubling device buffers that
     are written in place by the archive kernels (``_coeffs``/``_scales`` for
     jpeg, ``_deltas``/``_anchors`` for png; reference layout, cache.py:94-104),
@@ -55,7 +57,8 @@ class _CodecStream:
 
     def __init__(self, codec):
         self.codec = codec
-        self.raw = None          # (B, H, t, D), t < r
+        self._raw_buf = None     # (B, H, r, D) tail buffer in the stream dtype
+        self._n_raw = 0          # tokens in the tail (t < r)
         self.n_archived = 0      # archived tokens
         self.n_blocks = 0        # archived blocks
         self.meta = None         # (B, H, D, element size)
@@ -74,8 +77,44 @@ class _CodecStream:
         return self.codec.block_size
 
     @property
+    def raw(self):
+        """Raw tail (B, H, t, D) with 0 < t < r, or None (cache.py:72-88): a
+        view of the tail buffer, valid until the tail next completes a
+        block."""
+        if self._n_raw == 0:
+            return None
+        return self._raw_buf[:, :, :self._n_raw]
+
+    @raw.setter
+    def raw(self, value):
+        if value is None or value.shape[-2] == 0:
+            self._n_raw = 0
+            return
+        t = value.shape[-2]
+        if t >= self.block_size:
+            raise ValueError(f"a raw tail holds fewer than block_size={self.block_size} tokens "
+                             f"(got {t})")
+        self._tail_buffer(value)
+        self._raw_buf[:, :, :t].copy_(value)
+        self._n_raw = t
+
+    def _tail_buffer(self, like):
+        """The (B, H, r, D) tail buffer, (re)allocated to match `like`."""
+        buf = self._raw_buf
+        B, H, D = like.shape[0], like.shape[1], like.shape[-1]
+        dtype = self.dtype if self.dtype is not None else like.dtype
+        if (buf is None or buf.shape[0] != B or buf.shape[1] != H or buf.shape[-1] != D
+                or buf.dtype != dtype or buf.device != like.device):
+            old = self._raw_buf
+            buf = torch.empty((B, H, self.block_size, D), dtype=dtype, device=like.device)
+            if self._n_raw and old is not None and old.shape == buf.shape:
+                buf[:, :, :self._n_raw].copy_(old[:, :, :self._n_raw])
+            self._raw_buf = buf
+        return buf
+
+    @property
     def seq_len(self):
-        return self.n_archived + (0 if self.raw is None else self.raw.shape[-2])
+        return self.n_archived + self._n_raw
 
     # ------------------------------------------------------------ storage
     def _archive_spec(self, cap, B, H, D):
@@ -132,20 +171,43 @@ class _CodecStream:
     # ------------------------------------------------------------ write
     def append(self, tokens):
         """Append (B, H, m, D) tokens; every block completed by them is
-        archived at once (cache.py:143-159)."""
+        archived at once (cache.py:143-159).  Tokens that do not complete a
+        block are copied into the tail buffer; a block completed by the tail
+        is archived from the tail buffer, whole blocks of the input straight
+        from the input (the archived bits depend only on each block's r
+        tokens, so they equal the reference's cat-then-archive)."""
         N.require_gpu(tokens)
         r = self.block_size
         if self.meta is None:
             self.meta = (tokens.shape[0], tokens.shape[1], tokens.shape[-1],
                          tokens.element_size())
             self.dtype = tokens.dtype
-        buf = tokens if self.raw is None else torch.cat([self.raw, tokens], dim=-2)
-        total = buf.shape[-2]
-        full = (total // r) * r
+        m = tokens.shape[-2]
+        if m == 0:
+            return
+        t = self._n_raw
+        if t + m < r:
+            # the tail grows: one copy (the common decode step)
+            self._tail_buffer(tokens)[:, :, t:t + m].copy_(tokens)
+            self._n_raw = t + m
+            return
+        pos = 0
+        if t:
+            # the tail completes a block
+            buf = self._tail_buffer(tokens)
+            pos = r - t
+            buf[:, :, t:].copy_(tokens[:, :, :pos])
+            self._archive(buf)
+            self.n_archived += r
+            self._n_raw = 0
+        full = ((m - pos) // r) * r
         if full:
-            self._archive(buf[..., :full, :])
+            self._archive(tokens[:, :, pos:pos + full])
             self.n_archived += full
-        self.raw = buf[..., full:, :].contiguous() if total > full else None
+        rem = m - pos - full
+        if rem:
+            self._tail_buffer(tokens)[:, :, :rem].copy_(tokens[:, :, pos + full:])
+        self._n_raw = rem
 
     # ------------------------------------------------------------ read
     def _decode_pending(self):
@@ -183,7 +245,8 @@ class _CodecStream:
         tokens from _rec (a view when there is no raw tail) followed by the
         raw tail (cache.py:203-220)."""
         if self.n_blocks == 0:
-            return self.raw
+            # a copy: the tail buffer's rows are rewritten once a block completes
+            return None if self.raw is None else self.raw.clone()
         self._decode_pending()
         view = self._rec[:, :, :self.n_archived]
         if self.raw is not None:
@@ -216,10 +279,8 @@ class _CodecStream:
             self.n_archived = keep_blocks * r
             self._rec_blocks = min(self._rec_blocks, keep_blocks)
             self.raw = self._rec[:, :, keep_blocks * r:keep, :].clone() if tail else None
-        elif tail == 0:
-            self.raw = None
         else:
-            self.raw = self.raw[..., :tail, :].contiguous()
+            self._n_raw = tail      # the first `tail` rows of the tail buffer stay
 
     def select_batch(self, idx):
         """Gather batch rows (beam-search reorder, batch expansion)

@@ -1,0 +1,130 @@
+// Fused decode step of one attention layer on a codec KV cache (gfx950).
+//
+// One call per layer and step: the new key and value tokens are written
+// into their streams' tail buffers (one launch for both streams), a tail
+// that completes a block is archived with the archive kernels of
+// fc_codec.hip, and the decode attention of fc_attention.hip /
+// fc_attn_mfma.hip runs over the archive plus the tail.  The reference does
+// the same work as two _CodecStream.append calls (cat, archive, contiguous
+// copy) and a codec_decode_attention call (flashcodec/cache.py:143-159,
+// flashcodec/attention.py:64-140, driven by
+// flashcodec/patch_attention.py:95-98); here the host crosses into the
+// library once.
+#include <hip/hip_runtime.h>
+
+#include "fc_attn_internal.h"
+#include "fc_common.h"
+
+namespace fc {
+
+constexpr int kTailThreads = 64;
+
+struct TailArgs {
+  const void* tok[2];  // new token of the key / value stream, (B, H, 1, D)
+  int64_t tsb[2], tsh[2];
+  void* tail[2];  // (B, H, r, D) contiguous tail buffers
+  int64_t H, D, r, t;
+};
+
+// tail[s][b][h][t][:] = tok[s][b][h][:]; blockIdx.x = b * H + h,
+// blockIdx.y = stream (0: key, 1: value).  T is a storage word of the
+// element size (the copy moves bits).
+template <typename T>
+__global__ __launch_bounds__(kTailThreads) void tail_append_kernel(TailArgs a) {
+  const int s = blockIdx.y;
+  const int64_t bh = blockIdx.x;
+  const int64_t b = bh / a.H, h = bh - b * a.H;
+  const T* src = static_cast<const T*>(a.tok[s]) + b * a.tsb[s] + h * a.tsh[s];
+  T* dst = static_cast<T*>(a.tail[s]) + (bh * a.r + a.t) * a.D;
+  for (int64_t d = threadIdx.x; d < a.D; d += kTailThreads) dst[d] = src[d];
+}
+
+}  // namespace fc
+
+using namespace fc;
+
+extern "C" {
+
+int fc_decode_step(const fc_step_args* a) {
+  if (!a) return FC_ERR_ARG;
+  const int64_t B = a->B, Hq = a->Hq, Hkv = a->Hkv, D = a->D;
+  const int r = a->r;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv) return FC_ERR_ARG;
+  if (r < 1 || r > FC_MAX_BLOCK || a->n_tail < 0 || a->n_tail >= r || a->n_blocks < 0)
+    return FC_ERR_ARG;
+  const int es = esize_of(a->stream_dtype);
+  if (es == 0 || a->stream_dtype == FC_I8) return FC_ERR_ARG;
+  const fc_step_stream* st[2] = {&a->key, &a->value};
+  for (const fc_step_stream* x : st)
+    if (!x->token || !x->tail || !x->rows) return FC_ERR_ARG;
+  if (a->store_kind == FC_STORE_JPEG_I8 && (!a->key.scales || !a->value.scales)) return FC_ERR_ARG;
+  if (a->store_kind == FC_STORE_PNG && (!a->key.anchors || !a->value.anchors)) return FC_ERR_ARG;
+  if (a->store_kind != FC_STORE_PNG && !a->basis) return FC_ERR_ARG;
+  const bool completes = a->n_tail + 1 == r;
+  if (completes && (a->n_blocks + 1 > a->key.cap || a->n_blocks + 1 > a->value.cap))
+    return FC_ERR_ARG;  // the caller grows the archives first
+  hipStream_t stream = (hipStream_t)a->stream;
+
+  // 1. the new tokens into the tails
+  TailArgs ta;
+  for (int i = 0; i < 2; ++i) {
+    ta.tok[i] = st[i]->token;
+    ta.tsb[i] = st[i]->tok_sb;
+    ta.tsh[i] = st[i]->tok_sh;
+    ta.tail[i] = st[i]->tail;
+  }
+  ta.H = Hkv;
+  ta.D = D;
+  ta.r = r;
+  ta.t = a->n_tail;
+  const dim3 grid((unsigned)(B * Hkv), 2);
+  if (es == 4)
+    tail_append_kernel<uint32_t><<<grid, kTailThreads, 0, stream>>>(ta);
+  else
+    tail_append_kernel<uint16_t><<<grid, kTailThreads, 0, stream>>>(ta);
+  int rc = check_launch();
+  if (rc != FC_OK) return rc;
+
+  // 2. a completed tail becomes block n_blocks of each archive
+  int64_t nb = a->n_blocks, nt = a->n_tail + 1;
+  const int64_t tsb = Hkv * r * D, tsh = (int64_t)r * D;
+  if (completes) {
+    for (int i = 0; i < 2; ++i) {
+      const fc_step_stream* x = st[i];
+      if (a->store_kind == FC_STORE_PNG)
+        rc = fc_png_encode(x->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, r, 1, D, r, a->keep_m,
+                           static_cast<float*>(x->rows), x->anchors, x->cap, nb, a->stream);
+      else
+        rc = fc_jpeg_encode(x->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, r, 1, D, r, a->s,
+                            a->basis, x->rows, x->scales, x->cap, nb, a->quant_bits, a->stream);
+      if (rc != FC_OK) return rc;
+    }
+    ++nb;
+    nt = 0;
+  }
+
+  // 3. attention over the archive and the tail
+  fc_stream_view v[2];
+  for (int i = 0; i < 2; ++i) {
+    v[i].rows = st[i]->rows;
+    v[i].scales = st[i]->scales;
+    v[i].anchors = st[i]->anchors;
+    v[i].cap = st[i]->cap;
+    v[i].raw = nt ? st[i]->tail : nullptr;
+    v[i].raw_sb = tsb;
+    v[i].raw_sh = tsh;
+    v[i].raw_st = D;
+  }
+  int n_splits = 0;
+  if (nb > 0) {
+    n_splits = fc_attention_splits(a->store_kind, a->stream_dtype, a->q_dtype, a->s, nb, B, Hkv,
+                                   Hq / Hkv, D, a->n_cu);
+    if (!a->workspace || fc_attention_workspace_bytes(B, Hq, D, n_splits) > a->workspace_bytes)
+      return FC_ERR_ARG;
+  }
+  return fc_decode_attention(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, a->store_kind,
+                             a->stream_dtype, r, a->s, nb, &v[0], &v[1], nt, a->A, a->scale,
+                             a->out, a->o_sb, a->o_sh, a->workspace, n_splits, a->stream);
+}
+
+}  // extern "C"

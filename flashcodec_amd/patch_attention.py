@@ -5,8 +5,9 @@ coefficient-domain kernels (flashcodec/patch_attention.py:1-151).
 reconstructed view.  This patch replaces the forward of standard attention
 modules (q_proj / k_proj / v_proj / o_proj, optional q_norm / k_norm, plain
 or gated query projection) so that a single-token decode step on a codec
-layer runs projection + norm + RoPE as usual, appends K/V to the codec
-streams and attends with ``codec_decode_attention`` — no (S, D) view.
+layer runs projection + norm + RoPE as usual, then appends K/V to the codec
+streams and attends on the archive in one library call
+(``codec_decode_step``) — no (S, D) view.
 
 Guards (anything else calls the original forward): codec cache layer, eval
 mode, one query token, ``position_embeddings`` given, no sliding window, a
@@ -20,7 +21,7 @@ import importlib
 
 import torch
 
-from .attention import codec_decode_attention
+from .attention import codec_decode_step
 from .cache import FlashCodecLayer
 
 _ROPE_CACHE = {}
@@ -88,10 +89,10 @@ def _attention_forward(module, orig, hidden_states, position_embeddings=None,
         if st._rec is not None:
             st.discard_view()
     layer.keys = layer.values = None
-    layer._key_stream.append(k)
-    layer._value_stream.append(v)
-    out = codec_decode_attention(q, layer._key_stream, layer._value_stream,
-                                 scale=module.scaling)
+    # append both tokens and attend in one library call (two appends and an
+    # attention call in the reference, patch_attention.py:95-98)
+    out = codec_decode_step(q, k, v, layer._key_stream, layer._value_stream,
+                            scale=module.scaling)
     out = out.transpose(1, 2).reshape(*lead, -1).contiguous()
     if gated:
         out = out * torch.sigmoid(gate)

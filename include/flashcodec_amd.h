@@ -252,6 +252,64 @@ int fc_decode_attention_merge(const void* q, int q_dtype, int64_t q_sb,
                               int64_t o_sb, int64_t o_sh, void* workspace,
                               int n_splits, void* stream);
 
+/*
+ * One stream (key or value) of a layer for fc_decode_step: its archive
+ * buffers (as fc_stream_view), its (B, H, r, D) contiguous tail buffer in
+ * the stream dtype (the raw tail is its first n_tail token rows), and the
+ * step's new token (B, H, 1, D) with element strides tok_sb, tok_sh.
+ */
+typedef struct fc_step_stream {
+  void* rows;            /* jpeg: (B*H, cap, s, D) codes / coefficients; png: deltas */
+  float* scales;         /* jpeg int8: (B*H, cap, s); else NULL */
+  void* anchors;         /* png: (B*H, cap, D); else NULL */
+  int64_t cap;           /* capacity of the archive in blocks */
+  void* tail;            /* (B, H, r, D) tail buffer */
+  const void* token;     /* the new token */
+  int64_t tok_sb, tok_sh;
+} fc_step_stream;
+
+typedef struct fc_step_args {
+  const void* q;         /* (B, Hq, 1, D) query, element strides q_sb, q_sh */
+  int q_dtype;
+  int64_t q_sb, q_sh;
+  int64_t B, Hq, Hkv, D;
+  int store_kind;        /* FC_STORE_* */
+  int stream_dtype;      /* dtype of the tokens, tails (and jpeg fp stores) */
+  int r;                 /* block size */
+  int s;                 /* stored rows per block: keep_freqs (jpeg) or r (png) */
+  int quant_bits;        /* jpeg: 0 or 8 */
+  int keep_m;            /* png: deltas kept per (block, feature) */
+  int64_t n_blocks;      /* archived blocks before the step */
+  int64_t n_tail;        /* tail tokens before the step (< r) */
+  const float* basis;    /* jpeg: k x r DCT-II basis (device); png: NULL */
+  const float* A;        /* r x s synthesis matrix (device) */
+  float scale;           /* attention scale */
+  void* out;             /* (B, Hq, 1, D) output in q_dtype, strides o_sb, o_sh */
+  int64_t o_sb, o_sh;
+  void* workspace;       /* decode-attention workspace (zero-fill rule) */
+  int64_t workspace_bytes;
+  int n_cu;              /* compute units of the device (split count) */
+  void* stream;          /* hipStream_t */
+  fc_step_stream key, value;
+} fc_step_args;
+
+/*
+ * One decode step of one attention layer: appends the new key and value
+ * tokens to their tails; if that completes a block (n_tail + 1 == r) both
+ * tails are archived as block n_blocks (the caller grows the archives
+ * beforehand; cap <= n_blocks is FC_ERR_ARG) and the tails become empty;
+ * then the decode attention runs over the archives and tails as
+ * fc_decode_attention with the split count of fc_attention_splits
+ * (workspace_bytes must cover fc_attention_workspace_bytes for it).  After
+ * the call the caller's state is n_tail' = (n_tail + 1) % r and
+ * n_blocks' = n_blocks + (n_tail + 1 == r).
+ * Replaces the decode-step sequence key_stream.append(k);
+ * value_stream.append(v); codec_decode_attention(q, ...) of
+ * flashcodec/patch_attention.py:95-98 (flashcodec/cache.py:143-159,
+ * flashcodec/attention.py:64-140) with one call.
+ */
+int fc_decode_step(const fc_step_args* args);
+
 #ifdef __cplusplus
 }
 #endif

@@ -253,3 +253,57 @@ def test_split_counts_agree(n_splits, oracle, split_variant):
                          .astype(np.float32)).half().to(DEV)
     out = fc.codec_decode_attention(q, ks, vs, _n_splits=n_splits)
     assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "f16")
+
+
+def _archive_of(st):
+    return [t[:, :, :st.n_blocks] for t in st._archive_tensors()] if st.n_blocks else []
+
+
+@pytest.mark.parametrize("cfg,dt", [
+    (dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16"),
+    (dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8), "bf16"),
+    (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32"),
+    (dict(mode="png", block_size=8, keep_ratio=0.5), "f32"),
+    (dict(mode="png", block_size=4, keep_ratio=1.0), "bf16"),
+])
+def test_fused_decode_step_matches_append_then_attend(cfg, dt):
+    """codec_decode_step (one library call per layer step) leaves the same
+    archives, tails and counters as two appends, and its output matches
+    codec_decode_attention on them, across block boundaries; the first call
+    on uninitialised streams takes the two-call path."""
+    B, Hkv, G, D = 2, 2, 4, 64
+    Hq, r = Hkv * G, cfg["block_size"]
+    tdt = torch_dtype(dt)
+    print(f"case fused step {cfg} {dt}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    mk = lambda: fc.make_codec(**cfg)
+    ks_f, vs_f, ks_r, vs_r = _CodecStream(mk()), _CodecStream(mk()), _CodecStream(mk()), \
+        _CodecStream(mk())
+    for st_pair in ((ks_f, ks_r), (vs_f, vs_r)):
+        pre = torch.randn((B, Hkv, 2 * r + 3, D), generator=g, device=DEV).to(tdt)
+        for st in st_pair:
+            st.append(pre)
+    fresh_k, fresh_v = _CodecStream(mk()), _CodecStream(mk())
+    for step in range(3 * r + 2):
+        # HF-style strided views: (B, 1, H, D) projections transposed to (B, H, 1, D)
+        q = torch.randn((B, 1, Hq, D), generator=g, device=DEV).to(tdt).transpose(1, 2)
+        k = torch.randn((B, 1, Hkv, D), generator=g, device=DEV).to(tdt).transpose(1, 2)
+        v = torch.randn((B, 1, Hkv, D), generator=g, device=DEV).to(tdt).transpose(1, 2)
+        out_f = fc.codec_decode_step(q, k, v, ks_f, vs_f)
+        ks_r.append(k)
+        vs_r.append(v)
+        out_r = fc.codec_decode_attention(q, ks_r, vs_r)
+        for a, b in ((ks_f, ks_r), (vs_f, vs_r)):
+            assert a.n_blocks == b.n_blocks and a.seq_len == b.seq_len
+            for x, y in zip(_archive_of(a), _archive_of(b)):
+                assert torch.equal(x, y)
+            assert (a.raw is None) == (b.raw is None)
+            if a.raw is not None:
+                assert torch.equal(a.raw, b.raw)
+        assert_close(to_values(out_f), to_values(out_r), dt)
+        if step == 0:
+            out0 = fc.codec_decode_step(q, k, v, fresh_k, fresh_v)   # two-call path
+            assert fresh_k.seq_len == 1 and torch.equal(fresh_k.raw, k)
+            ref0 = torch.softmax((q.float() @ k.float().transpose(-1, -2).repeat_interleave(
+                G, dim=1)) * D ** -0.5, dim=-1) @ v.float().repeat_interleave(G, dim=1)
+            assert_close(to_values(out0), ref0.cpu().numpy(), dt)

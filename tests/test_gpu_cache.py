@@ -218,3 +218,53 @@ def test_capacity_growth_keeps_prefix():
     one.append(x)
     assert torch.equal(one._coeffs[:, :, :40], st._coeffs[:, :, :40])
     assert torch.equal(one.read(), st.read())
+
+
+@pytest.mark.parametrize("mode,kw", [("jpeg", dict(keep_freqs=4, quant_bits=8)),
+                                     ("jpeg", dict(keep_freqs=2)),
+                                     ("png", dict(keep_ratio=0.5))])
+def test_ragged_appends_keep_the_tail_and_equal_a_bulk_fill(seqs, mode, kw):
+    """Appends of mixed sizes (inside the tail, completing it, spanning
+    several blocks) leave the last seq_len % r input tokens as the raw tail
+    after every call and archive exactly what one bulk append archives."""
+    k_seq, _ = seqs
+    cfg = dict(mode=mode, block_size=R, **kw)
+    print(f"case ragged {mode} {kw}", flush=True)
+    bulk = _CodecStream(fc.make_codec(**cfg))
+    bulk.append(k_seq)
+    st = _CodecStream(fc.make_codec(**cfg))
+    sizes = [1, 3, 8, 13, 2, 5, 17, 1, 7, 9, 0, 16, 4]
+    pos, i = 0, 0
+    while pos < S:
+        m = min(sizes[i % len(sizes)], S - pos)
+        st.append(k_seq[..., pos:pos + m, :])
+        pos, i = pos + m, i + 1
+        t = pos % R
+        assert st.seq_len == pos and st.n_blocks == pos // R
+        if t:
+            assert torch.equal(st.raw, k_seq[..., pos - t:pos, :])
+        else:
+            assert st.raw is None
+    for a, b in zip(_archive(st), _archive(bulk)):
+        assert torch.equal(a, b)
+    assert torch.equal(st.read(), bulk.read())
+
+
+def test_tail_reads_are_copies_and_follow_batch_changes(seqs):
+    k_seq, _ = seqs
+    cfg = dict(mode="jpeg", block_size=R, keep_freqs=4, quant_bits=8)
+    st = _CodecStream(fc.make_codec(**cfg))
+    st.append(k_seq[..., :3, :])
+    r0 = st.read()
+    st.append(k_seq[..., 3:3 + R, :])          # completes a block, rewrites the tail
+    assert torch.equal(r0, k_seq[..., :3, :])
+    assert torch.equal(st.raw, k_seq[..., R:R + 3, :])
+    idx = torch.tensor([1, 0, 1], device=DEV)  # batch 2 -> 3 with a live tail
+    st.select_batch(idx)
+    assert torch.equal(st.raw, k_seq[idx][..., R:R + 3, :])
+    st.append(k_seq[idx][..., R + 3:2 * R + 1, :])
+    ref = _CodecStream(fc.make_codec(**cfg))
+    ref.append(k_seq[idx][..., :2 * R + 1, :])
+    for a, b in zip(_archive(st), _archive(ref)):
+        assert torch.equal(a, b)
+    assert torch.equal(st.raw, ref.raw) and torch.equal(st.read(), ref.read())
