@@ -335,8 +335,23 @@ def c5_mode(args):
                 nxt = out.logits[:, -1].argmax(-1, keepdim=True)
             torch.cuda.synchronize()
             t2 = time.perf_counter()
+        if steps == 0:
+            return {"prefill_s": round(t1 - t0, 4)}
         return {"prefill_s": round(t1 - t0, 4), "decode_ms_per_step": round((t2 - t1) / steps * 1e3, 3),
                 "decode_tokens_per_s": round(batch * steps / (t2 - t1), 1)}
+
+    if args.c5_steps is not None:
+        # one run of the named setting (for kernel traces: launches per step
+        # are the dispatch count of a run minus that of the same run with 0
+        # steps, divided by the steps)
+        if args.c5_kv == "codec":
+            fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8,
+                                 materialization_free=True)
+        run(2, 64, 4)                                        # warm-up, same in every run
+        one = run(args.c5_batch, args.c5_prompt, args.c5_steps)
+        print(json.dumps({"mode": "c5 single run", "kv": args.c5_kv, "batch": args.c5_batch,
+                          "prompt": args.c5_prompt, "steps": args.c5_steps, **one}))
+        return
 
     res = {"metric": "end-to-end decode tokens/s (C5)", "unit": "tokens/s", "n_gpus": 1,
            "config": {"workload": "C5 Qwen3-0.6B-shaped greedy decoding", "layers": 28,
@@ -420,6 +435,11 @@ def main():
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--splits", type=int, default=0, help="override the split count")
+    ap.add_argument("--c5-steps", type=int, default=None,
+                    help="c5: one run of this many decode steps (0: prefill only)")
+    ap.add_argument("--c5-batch", type=int, default=16)
+    ap.add_argument("--c5-prompt", type=int, default=4096)
+    ap.add_argument("--c5-kv", choices=["raw", "codec"], default="codec")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} "
