@@ -112,6 +112,21 @@ CASES += [
     ("i8-f16-d64-g4", I8, "f16", 2, 4, 4, 8 * 123 + 4, 64),
 ]
 
+P16 = dict(mode="png", block_size=16, keep_ratio=0.25)
+CASES += [
+    # png and unquantised jpeg stores: head groups of 1-16 (and partial
+    # ones), rows per block 1-16, tails, no tail, anchors in every dtype
+    ("fp-png-f32-r16-g4", P16, "f32", 2, 2, 4, 16 * 130 + 7, 128),
+    ("fp-png-bf16-r16-g8", P16, "bf16", 1, 2, 8, 16 * 64 + 3, 64),
+    ("fp-png-f16-r8-g16", dict(mode="png", block_size=8, keep_ratio=1.0), "f16", 1, 1, 16, 8 * 80 + 1, 128),
+    ("fp-png-f32-r4-g1", dict(mode="png", block_size=4, keep_ratio=0.5), "f32", 2, 3, 1, 4 * 90, 64),
+    ("fp-png-f32-tail-only", P16, "f32", 1, 2, 4, 11, 128),
+    ("fp-jpeg-f16-k3-g3", dict(mode="jpeg", block_size=8, keep_freqs=3), "f16", 2, 2, 3, 8 * 111 + 5, 128),
+    ("fp-jpeg-f32-k1-g2", dict(mode="jpeg", block_size=8, keep_freqs=1), "f32", 1, 4, 2, 8 * 300 + 2, 64),
+    ("fp-jpeg-bf16-k16-g4", dict(mode="jpeg", block_size=16, keep_freqs=16), "bf16", 1, 2, 4, 16 * 33 + 15, 128),
+    ("fp-jpeg-f32-k2-g5", dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 1, 2, 5, 8 * 1000 + 3, 128),
+]
+
 
 @pytest.fixture(params=["auto", "valu"])
 def split_variant(request, monkeypatch):
