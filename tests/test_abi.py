@@ -5,6 +5,8 @@ Top-M selection matches the oracle (torch's CPU topk order)."""
 import ctypes
 import os
 import re
+import shutil
+import subprocess
 
 import numpy as np
 import pytest
@@ -132,3 +134,32 @@ def test_host_topm_adversarial_orders(oracle):
         for v in cols:
             for m in range(1, n):
                 assert np.array_equal(_topm_host(v, m), oracle.topk_keep(np.abs(v), m)), (n, m)
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layouts_match_the_header(tmp_path):
+    """The ctypes mirrors of fc_stream_view, fc_step_stream and fc_step_args
+    have the C compiler's field offsets and sizes."""
+    structs = {"fc_stream_view": N.StreamView, "fc_step_stream": N.StepStream,
+               "fc_step_args": N.StepArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "flashcodec_amd.h"',
+             'int main(void) {']
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in py._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ['  return 0;', '}']
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", f"-I{os.path.join(ROOT, 'include')}", str(src), "-o", str(exe)],
+                   check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    got = {}
+    for line in out.splitlines():
+        cname, field, val = line.split()
+        got[(cname, field)] = int(val)
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for field, _ in py._fields_:
+            assert got[(cname, field)] == getattr(py, field).offset, (cname, field)
