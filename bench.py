@@ -485,7 +485,8 @@ def main():
     assert ks.n_blocks == NB and ks.raw.shape[-2] == TAIL
 
     L = N.lib()
-    n_splits = args.splits or L.fc_attention_default_splits(NB, B, HKV, HQ // HKV, N.num_cus(dev))
+    n_splits = args.splits or L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, K, NB, B, HKV,
+                                                    HQ // HKV, D, N.num_cus(dev))
     keep = []
     kv, vv = _view(ks, keep), _view(vs, keep)
     A = _device_A(ks.codec, R, dev)

@@ -70,8 +70,9 @@ def _view(stream, keep):
             v.rows = stream._deltas.data_ptr()
             v.anchors = stream._anchors.data_ptr()
         v.cap = stream._capacity
-    if stream.raw is not None:
-        raw = stream.raw if stream.raw.stride(-1) == 1 else stream.raw.contiguous()
+    if stream._n_raw:
+        # the raw tail is the first _n_raw rows of the (B, H, r, D) tail buffer
+        raw = stream._raw_buf
         keep.append(raw)
         v.raw = raw.data_ptr()
         v.raw_sb, v.raw_sh, v.raw_st = raw.stride(0), raw.stride(1), raw.stride(2)
@@ -110,11 +111,13 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
     nb = ks.n_blocks
     if vs.n_blocks != nb or vs.n_archived != ks.n_archived:
         raise ValueError("key and value streams hold different token counts")
-    n_raw = 0 if ks.raw is None else ks.raw.shape[-2]
+    n_raw = ks._n_raw
+    if vs._n_raw != n_raw:
+        raise ValueError("key and value streams hold different token counts")
     if nb == 0 and n_raw == 0:
         return torch.zeros_like(query)                   # empty cache
     N.require_gpu(query)
-    like = ks.raw if nb == 0 else ks._archive_tensors()[0]
+    like = ks._raw_buf if nb == 0 else ks._archive_tensors()[0]
     N.require_gpu(like)
     Hkv = like.shape[1]
     assert Hq % Hkv == 0, f"query heads ({Hq}) must be a multiple of kv heads ({Hkv})"

@@ -755,8 +755,25 @@ int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, in
   const bool mfma = store_kind == FC_STORE_JPEG_I8 && (q_dtype == FC_F16 || q_dtype == FC_BF16) &&
                     (D == 64 || D == 128 || D == 256) && (s == 1 || s == 2 || s == 4) &&
                     fc::mfma_split_allowed();
-  if (mfma) return fc_attention_default_splits(nb, B, Hkv, G, n_cu);
   if (n_cu <= 0) n_cu = 256;
+  if (mfma) {
+    // one round of matrix-core workgroups (two per compute unit), but at
+    // least one pass (64 rows; 32 at D = 256) per wavefront, and no more
+    // than 16 splits or a tenth of the passes (each split adds a partial to
+    // the final merge): measured on the MI355X, 16 splits take 14.9 us at
+    // B=1, Hkv=8, G=2, k=2, S=16K where 64 take 25.9, 24 splits 20.3 us at
+    // S=64K where 64 take 28.6
+    const int64_t groups = (G + 15) / 16;
+    const int64_t cols = std::max<int64_t>(1, B * Hkv * groups);
+    int64_t want = (2 * (int64_t)n_cu + cols - 1) / cols;
+    const int64_t pr = D == 256 ? 32 : 64;
+    const int64_t npass = (nb * s + pr - 1) / pr;
+    want = std::min<int64_t>(want, std::max<int64_t>(1, npass / 4));
+    want = std::min<int64_t>(want, std::max<int64_t>(16, npass / 10));
+    want = std::max<int64_t>(1, std::min<int64_t>(want, fc::kMaxSplits));
+    const int64_t bps = (nb + want - 1) / want;
+    return (int)((nb + bps - 1) / bps);
+  }
   // vector-ALU split pass: one round of its workgroups at the occupancy the
   // kernel reaches on this device (two per compute unit if it cannot be read)
   const int gm = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));

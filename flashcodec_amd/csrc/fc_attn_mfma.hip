@@ -208,81 +208,93 @@ __device__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int6
 // out = sum_s w_s acc_s / sum_s w_s l_s over the n_splits partials of its G
 // query heads, w_s = 2^(m_s - max_s m_s).  This workgroup's own partial is
 // read from LDS (own_acc [16][D], own_m, own_l), the others with
-// device-scope loads; the raw tail is part of split 0's partial.  Each
-// thread owns an output task (head, 4 features) and reduces its head's
-// statistics itself, so the merge needs no barrier.
+// device-scope loads; the raw tail is part of split 0's partial.  The
+// statistics of all splits come in with one load per thread; then each
+// thread owns an output task (head, 4 features) and requests its partials
+// kPre splits at a time.  `lds` holds >= 2 * 16 * kFuseMaxSplits floats.
 template <int D>
 __device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
-                            int split, int tid, const float* own_acc, const float* own_m,
-                            const float* own_l) {
+                            int split, int tid, float* lds, const float* own_acc,
+                            const float* own_m, const float* own_l) {
   constexpr int C4 = D / 4;  // float4 chunks of a head's output
-  constexpr int kPre = 8;    // splits held in registers by one task
+  constexpr int kPre = 16;   // partials in flight per task
   const int ns = p.n_splits;
   const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;  // slot of head 0 of the group
+  float* wsp = lds;                        // [16][kFuseMaxSplits] split maxima
+  float* plv = wsp + 16 * kFuseMaxSplits;  // [16][kFuseMaxSplits] split sums
 
-  // device-scope (L2-missing) loads of the group's partials
+  // device-scope (L2-missing) loads of the group's partials and statistics
   const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, G * ns * D * 4);
+  const __amdgpu_buffer_rsrc_t rm = buf_rsrc(p.pm + bq0 * ns, G * ns * 4);
+  const __amdgpu_buffer_rsrc_t rl = buf_rsrc(p.pl + bq0 * ns, G * ns * 4);
   auto part = [&](int h, int sp, int c) {
-    if (sp == split) return *reinterpret_cast<const float4*>(own_acc + h * D + 4 * c);
-    return __builtin_bit_cast(
-        float4, __builtin_amdgcn_raw_buffer_load_b128(rp, ((h * ns + sp) * C4 + c) * 16, 0,
-                                                      kCachePolicySc1));
+    const float4_t v = __builtin_bit_cast(
+        float4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, ((h * ns + sp) * C4 + c) * 16, 0,
+                                                        kCachePolicySc1));
+    return sp == split ? *reinterpret_cast<const float4_t*>(own_acc + h * D + 4 * c) : v;
   };
-  auto stat = [&](const float* v, const float* own, int h, int sp) {
-    return sp == split ? own[h]
-                       : __hip_atomic_load(v + (bq0 + h) * ns + sp, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+  auto fma4 = [](float w, const float4_t& v, float4_t& o) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(w, v[i], o[i]);
   };
-  auto fma4 = [](float w, const float4& v, float4& o) {
-    o.x = __builtin_fmaf(w, v.x, o.x);
-    o.y = __builtin_fmaf(w, v.y, o.y);
-    o.z = __builtin_fmaf(w, v.z, o.z);
-    o.w = __builtin_fmaf(w, v.w, o.w);
-  };
-  auto finish_out = [&](int h, int c, const float4& o, float l) {
-    const float iv = 1.0f / l;
-    const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
-    store_any(p.out, p.q_dtype, ob + 0, o.x * iv);
-    store_any(p.out, p.q_dtype, ob + 1, o.y * iv);
-    store_any(p.out, p.q_dtype, ob + 2, o.z * iv);
-    store_any(p.out, p.q_dtype, ob + 3, o.w * iv);
-  };
-  for (int task = tid; task < G * C4; task += kMThreads) {
-    const int h = task / C4, c = task - h * C4;
-    float mx = -INFINITY, l = 0.f;
-    float4 o = {0.f, 0.f, 0.f, 0.f};
-    // kPre splits at a time, every load of a chunk in flight at once
+  auto task_out = [&](int h, int c, const float* wh, const float* lh, float4_t (&pre)[kPre],
+                      bool have0) {
+    float mx = -INFINITY;
+    for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, wh[sp]);
+    float l = 0.f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
     for (int sp0 = 0; sp0 < ns; sp0 += kPre) {
-      float4 pre[kPre];
-      float pm[kPre], pl[kPre];
+      if (sp0 > 0 || !have0) {
+#pragma unroll
+        for (int j = 0; j < kPre; ++j)
+          if (sp0 + j < ns) pre[j] = part(h, sp0 + j, c);
+      }
 #pragma unroll
       for (int j = 0; j < kPre; ++j)
         if (sp0 + j < ns) {
-          pre[j] = part(h, sp0 + j, c);
-          pm[j] = stat(p.pm, own_m, h, sp0 + j);
-          pl[j] = stat(p.pl, own_l, h, sp0 + j);
-        }
-      float nm = mx;
-#pragma unroll
-      for (int j = 0; j < kPre; ++j)
-        if (sp0 + j < ns) nm = fmaxf(nm, pm[j]);
-      if (nm == -INFINITY) continue;  // empty partials only so far
-      const float f = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mx - nm);
-      l *= f;
-      o.x *= f;
-      o.y *= f;
-      o.z *= f;
-      o.w *= f;
-#pragma unroll
-      for (int j = 0; j < kPre; ++j)
-        if (sp0 + j < ns) {
-          const float w = pm[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[j] - nm);
-          l = __builtin_fmaf(w, pl[j], l);
+          const float pmv = wh[sp0 + j];
+          const float w = pmv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pmv - mx);
+          l = __builtin_fmaf(w, lh[sp0 + j], l);
           fma4(w, pre[j], o);
         }
-      mx = nm;
     }
-    finish_out(h, c, o, l);
+    const float iv = 1.0f / l;
+    const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_any(p.out, p.q_dtype, ob + i, o[i] * iv);
+  };
+  auto stats = [&]() {
+    for (int u = tid; u < G * ns; u += kMThreads) {
+      const int h = u / ns, sp = u - h * ns;
+      const bool own = sp == split;
+      const float mv = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rm, u * 4, 0, kCachePolicySc1));
+      const float lv = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rl, u * 4, 0, kCachePolicySc1));
+      wsp[h * kFuseMaxSplits + sp] = own ? own_m[h] : mv;
+      plv[h * kFuseMaxSplits + sp] = own ? own_l[h] : lv;
+    }
+  };
+  float4_t pre[kPre];
+  if (G * C4 <= kMThreads) {
+    // one task per thread: its first kPre partials fly with the statistics
+    const bool act = tid < G * C4;
+    const int h = act ? tid / C4 : 0, c = tid - h * C4;
+    if (act) {
+#pragma unroll
+      for (int j = 0; j < kPre; ++j)
+        if (j < ns) pre[j] = part(h, j, c);
+    }
+    stats();
+    __syncthreads();
+    if (act) task_out(h, c, wsp + h * kFuseMaxSplits, plv + h * kFuseMaxSplits, pre, true);
+    return;
+  }
+  stats();
+  __syncthreads();
+  for (int task = tid; task < G * C4; task += kMThreads) {
+    const int h = task / C4, c = task - h * C4;
+    task_out(h, c, wsp + h * kFuseMaxSplits, plv + h * kFuseMaxSplits, pre, false);
   }
 }
 
@@ -746,7 +758,7 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
     __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  fused_merge<D>(p, b, hkv, g0, G, split, tid, part_lds, wg_ml[0], wg_ml[1]);
+  fused_merge<D>(p, b, hkv, g0, G, split, tid, &s_lds[0][0][0], part_lds, wg_ml[0], wg_ml[1]);
 }
 
 template <int... Vs, typename F>

@@ -55,14 +55,23 @@ def test_workspace_and_split_policy():
 
 def test_store_aware_split_count():
     """int8 jpeg stores with half-precision queries take the matrix-core
-    split count; other stores one round of the vector-ALU pass (two
+    split count (at most one round, at least one pass per wavefront, at most
+    max(16, passes / 10)); other stores one round of the vector-ALU pass (two
     workgroups per compute unit when no device reports the occupancy)."""
     L = N.lib()
     assert L.fc_attention_splits(N.STORE_PNG, N.F32, N.F32, 16, 0, 2, 8, 4, 128, 256) == 0
+    # the measured shapes: C3, C5, and the reference's published ones
+    assert L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, 4, 4096, 8, 8, 4, 128, 256) == 8
+    assert L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, 4, 512, 16, 8, 2, 128, 256) == 4
+    assert L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, 2, 2048, 1, 8, 2, 128, 256) == 16
+    assert L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, 2, 8192, 1, 8, 2, 128, 256) == 25
     for nb in (1, 7, 1024, 4096, 100000):
         for cols in ((8, 8, 4), (2, 8, 4), (1, 32, 1)):
-            assert (L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, 4, nb, *cols, 128, 256)
-                    == L.fc_attention_default_splits(nb, *cols, 256))
+            ns = L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, 4, nb, *cols, 128, 256)
+            assert 1 <= ns <= L.fc_attention_default_splits(nb, *cols, 256)
+            passes = -(-nb * 4 // 64)
+            assert ns <= max(1, passes // 4)
+            assert -(-nb // ns) * (ns - 1) < nb       # no empty split
             for kind, s in ((N.STORE_PNG, 16), (N.STORE_JPEG_FP, 2), (N.STORE_JPEG_I8, 4)):
                 ns = L.fc_attention_splits(kind, N.F32, N.F32, s, nb, *cols, 128, 256)
                 assert 1 <= ns <= 256
