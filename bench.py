@@ -340,6 +340,47 @@ def c5_mode(args):
         return {"prefill_s": round(t1 - t0, 4), "decode_ms_per_step": round((t2 - t1) / steps * 1e3, 3),
                 "decode_tokens_per_s": round(batch * steps / (t2 - t1), 1)}
 
+    def run_graph(batch, prompt, steps, warmup=2):
+        """Prefill eagerly, then `steps` greedy decode steps of which the
+        first `warmup` run eagerly and the rest replay a captured HIP graph
+        of one step (flashcodec_amd.graph); decode time over the replays."""
+        from flashcodec_amd import graph
+        g = torch.Generator().manual_seed(1)
+        ids = torch.randint(1, cfg.vocab_size, (batch, prompt), generator=g).to(dev)
+        with torch.no_grad():
+            out = model(input_ids=ids, use_cache=True, logits_to_keep=1)
+            nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            dec = graph.GraphDecoder(model, out.past_key_values, nxt, position=prompt,
+                                     max_new_tokens=steps, warmup=warmup)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            dec.generate(warmup)
+            for _ in range(steps - warmup):
+                dec.step()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            dec.close()
+        n = steps - warmup
+        return {"warmup_and_capture_s": round(t1 - t0, 4),
+                "decode_ms_per_step": round((t2 - t1) / n * 1e3, 3),
+                "decode_tokens_per_s": round(batch * n / (t2 - t1), 1), "graph_steps": n}
+
+    if args.c5_graph:
+        # codec decoding with each step replayed from a captured HIP graph
+        fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8,
+                             materialization_free=True)
+        run(2, 64, 4)
+        res = {"metric": "end-to-end decode tokens/s (C5), codec, HIP-graph decode steps",
+               "unit": "tokens/s", "n_gpus": 1,
+               "codec_graph_b16": run_graph(16, 4096, 256),
+               "codec_graph_b1": run_graph(1, 4096, 32)}
+        res["value"] = res["codec_graph_b16"]["decode_tokens_per_s"]
+        log(f"bench c5 graph: {res}")
+        print(json.dumps(res))
+        return
+
     if args.c5_steps is not None:
         # one run of the named setting (for kernel traces: launches per step
         # are the dispatch count of a run minus that of the same run with 0
@@ -440,6 +481,8 @@ def main():
     ap.add_argument("--c5-batch", type=int, default=16)
     ap.add_argument("--c5-prompt", type=int, default=4096)
     ap.add_argument("--c5-kv", choices=["raw", "codec"], default="codec")
+    ap.add_argument("--c5-graph", action="store_true",
+                    help="c5: codec decode steps replayed from a captured HIP graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} "

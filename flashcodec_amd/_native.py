@@ -52,7 +52,7 @@ class StepArgs(ctypes.Structure):
         ("quant_bits", _int), ("keep_m", _int), ("n_blocks", _i64), ("n_tail", _i64),
         ("basis", _vp), ("A", _vp), ("scale", _fp), ("out", _vp), ("o_sb", _i64), ("o_sh", _i64),
         ("workspace", _vp), ("workspace_bytes", _i64), ("n_cu", _int), ("stream", _vp),
-        ("key", StepStream), ("value", StepStream),
+        ("key", StepStream), ("value", StepStream), ("state", _vp),
     ]
 
 

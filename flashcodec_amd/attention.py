@@ -203,6 +203,10 @@ def codec_decode_step(query, key_tokens, value_tokens, key_stream, value_stream,
     call."""
     ks, vs = key_stream, value_stream
     B, Hq, Sq, D = query.shape
+    dev_state = getattr(ks, "_dev_state", None)
+    if dev_state is not None:
+        return _decode_step_device_state(query, key_tokens, value_tokens, ks, vs, scale,
+                                         dev_state)
     fused = (Sq == 1 and key_tokens.shape[-2] == 1 and value_tokens.shape[-2] == 1
              and ks.meta is not None and vs.meta is not None and ks.codec is vs.codec
              and key_tokens.dtype == ks.dtype and value_tokens.dtype == vs.dtype
@@ -249,4 +253,41 @@ def codec_decode_step(query, key_tokens, value_tokens, key_stream, value_stream,
             st._n_raw = 0
     else:
         ks._n_raw = vs._n_raw = t + 1
+    return out
+
+
+def _decode_step_device_state(query, key_tokens, value_tokens, ks, vs, scale, state):
+    """codec_decode_step with the stream counters on the device (graph
+    decoding): the enqueued work reads and advances `state` = (n_blocks,
+    n_tail) there and is the same at every step; the host counters are
+    advanced by the caller once the work has run (graph.advance_host)."""
+    if query.shape[-2] != 1 or key_tokens.shape[-2] != 1 or value_tokens.shape[-2] != 1:
+        raise ValueError("device-state decode steps take one token per sequence")
+    a, ws_bytes = _step_args(ks, vs, query, key_tokens)
+    dev = query.device
+    out = torch.empty_like(query)
+    a.q, a.q_sb, a.q_sh = query.data_ptr(), query.stride(0), query.stride(1)
+    a.n_blocks, a.n_tail = max(1, ks.n_blocks), ks._n_raw
+    a.scale = query.shape[-1] ** -0.5 if scale is None else float(scale)
+    a.out, a.o_sb, a.o_sh = out.data_ptr(), out.stride(0), out.stride(1)
+    key = (dev.index, N.stream_ptr(dev))
+    ws = _WORKSPACES.get(key)
+    if (ws is None or ws.numel() < ws_bytes) and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("run one decode step on the capture stream before capturing: the "
+                           "decode-attention workspace must exist (zero-filled) beforehand")
+    ws = workspace(dev, ws_bytes)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    a.stream = N.stream_ptr(dev)
+    for sv, st, tok in ((a.key, ks, key_tokens), (a.value, vs, value_tokens)):
+        sv.rows = st._coeffs.data_ptr()
+        sv.scales = st._scales.data_ptr()
+        sv.anchors = None
+        sv.cap = st._capacity
+        sv.tail = st._raw_buf.data_ptr()
+        sv.token, sv.tok_sb, sv.tok_sh = tok.data_ptr(), tok.stride(0), tok.stride(1)
+    a.state = state.data_ptr()
+    try:
+        N.check(N.lib().fc_decode_step(ctypes.byref(a)), "fc_decode_step")
+    finally:
+        a.state = None
     return out

@@ -856,7 +856,7 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
     int lg = 0;
     while ((int64_t(1) << lg) < chunks) ++lg;
     const int gm = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
-    AttnArgs a;
+    AttnArgs a{};
     a.q = q;
     a.q_dtype = q_dtype;
     a.q_sb = q_sb;
@@ -928,7 +928,7 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
   }
   if (!(parts & kPartMerge)) return FC_OK;
 
-  MergeArgs mg;
+  MergeArgs mg{};
   mg.q = q;
   mg.q_dtype = q_dtype;
   mg.q_sb = q_sb;
@@ -960,6 +960,42 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
     attn_merge_kernel<<<dim3((unsigned)(B * Hkv)), kAttnThreads, 0, st>>>(mg);
   }
   return check_launch();
+}
+
+int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
+                           int64_t Hq, int64_t Hkv, int64_t D, int stream_dtype, int r, int s,
+                           int64_t nb_hint, const fc_stream_view* key, const fc_stream_view* value,
+                           const float* A, float scale, void* out, int64_t o_sb, int64_t o_sh,
+                           void* workspace, int64_t workspace_bytes, int n_cu,
+                           const int64_t* state, void* stream) {
+  if (!state || !q || !out || !key || !value || !A || !workspace || nb_hint < 1) return FC_ERR_ARG;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv) return FC_ERR_ARG;
+  if (r < 1 || r > FC_MAX_BLOCK || s < 1 || s > r) return FC_ERR_ARG;
+  if (!key->rows || !value->rows || !key->scales || !value->scales || !key->raw || !value->raw)
+    return FC_ERR_ARG;
+  const int64_t G = Hq / Hkv;
+  if (!split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) ||
+      !mfma_split_allowed() || 2 * B * Hkv * ((G + 15) / 16) * kCounterStride > kCounterWords)
+    return FC_ERR_UNSUPPORTED;
+  const int n_splits =
+      fc_attention_splits(FC_STORE_JPEG_I8, stream_dtype, q_dtype, s, nb_hint, B, Hkv, G, D, n_cu);
+  if (n_splits < 1 || !split_i8_mfma_fusable(n_splits)) return FC_ERR_UNSUPPORTED;
+  if (fc_attention_workspace_bytes(B, Hq, D, n_splits) > workspace_bytes) return FC_ERR_ARG;
+  const int64_t ws_head = (B * Hq * (int64_t)n_splits + 3) / 4 * 4;
+  unsigned int* counters = static_cast<unsigned int*>(workspace);
+  float* pm = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  float* pl = pm + ws_head;
+  float* pacc = pl + ws_head;
+  MfmaFuse fz{};
+  fz.raw_dtype = stream_dtype;
+  fz.n_raw = 0;  // taken from the state
+  fz.out = out;
+  fz.o_sb = o_sb;
+  fz.o_sh = o_sh;
+  fz.state = state;
+  return launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb_hint, key, value,
+                              A, scale * kLog2e, pm, pl, pacc, n_splits, counters, kCounterWords,
+                              kCounterStride, &fz, (hipStream_t)stream);
 }
 
 }  // namespace fc

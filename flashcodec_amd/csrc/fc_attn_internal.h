@@ -21,6 +21,9 @@ struct MfmaFuse {
   int64_t n_raw;
   void* out;
   int64_t o_sb, o_sh;
+  // decode-step state on the device, (n_blocks, n_tail) before the step's
+  // token, or NULL: the kernel then takes the block and tail counts from it
+  const int64_t* state = nullptr;
 };
 
 bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
@@ -35,5 +38,22 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
                          unsigned int* counters, int64_t counter_words, int64_t stride,
                          const MfmaFuse* fuse, hipStream_t st);
+
+// Decode attention over a graph-capturable decode step (fc_decode_step with
+// a device state): the fused matrix-core pass only, block and tail counts
+// read from `state` on the device; nb_hint (> 0) sizes the split count.
+int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
+                           int64_t Hq, int64_t Hkv, int64_t D, int stream_dtype, int r, int s,
+                           int64_t nb_hint, const fc_stream_view* key, const fc_stream_view* value,
+                           const float* A, float scale, void* out, int64_t o_sb, int64_t o_sh,
+                           void* workspace, int64_t workspace_bytes, int n_cu,
+                           const int64_t* state, void* stream);
+
+// jpeg archive of one block of a decode step's tail, gated on the device:
+// runs only when gate[1] == r - 1 and writes block gate[0] (< cap).
+int jpeg_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
+                      int64_t x_sh, int64_t x_ss, int64_t D, int r, int k, const float* basis,
+                      void* coeffs, float* scales, int64_t cap, int quant_bits, void* stream,
+                      const int64_t* gate);
 
 }  // namespace fc

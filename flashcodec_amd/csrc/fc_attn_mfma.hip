@@ -85,6 +85,9 @@ struct MfmaArgs {
   int64_t n_raw;
   void* out;
   int64_t o_sb, o_sh;
+  // decode-step state on the device (or NULL): (n_blocks, n_tail) before
+  // the step's token; nb and n_raw are then taken from it (graph replays)
+  const int64_t* state;
 };
 
 constexpr int kMThreads = 256;
@@ -151,9 +154,8 @@ __device__ __forceinline__ void st_elem(void* ptr, int dt, int64_t i, float v) {
 // 16 * FC_MAX_BLOCK floats; every thread of the workgroup takes part.
 template <int D>
 __device__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
-                                 int tid, float* etl, float* acc, float* tm, float* tl) {
+                                 int nr, int tid, float* etl, float* acc, float* tm, float* tl) {
   const int lane = tid & 63, wave = tid >> 6;
-  const int nr = (int)p.n_raw;
   {
     // logits: 16 lanes per (head, token), features strided by 16
     const int grp = tid >> 4, gl = tid & 15;
@@ -339,7 +341,14 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   // The group's rows are cut into passes of PR rows; every wavefront of the
   // group's n_splits workgroups takes the next untaken pass from the group's
   // queue until none is left, so faster wavefronts take more passes.
-  const int64_t rows_total = p.nb * SROWS;
+  int64_t nb = p.nb, n_raw = p.n_raw;
+  if (p.state) {
+    // counts of the step's view, kept inside the buffers whatever the words hold
+    const int64_t t = min<int64_t>(max<int64_t>(p.state[1], 0), p.r - 1) + 1;
+    nb = min<int64_t>(max<int64_t>(p.state[0], 0) + (t == p.r ? 1 : 0), min(p.kcap, p.vcap));
+    n_raw = t == p.r ? 0 : t;
+  }
+  const int64_t rows_total = nb * SROWS;
   const int64_t npass = (rows_total + PR - 1) / PR;
   unsigned int* passq = p.passq + g * p.cstride;
   auto grab = [&]() -> unsigned int {  // result in lane 0, read when needed
@@ -514,10 +523,11 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
 
   // raw tail (fused calls): split 0 computes its partial before the passes
   // and folds it into its own, so the final merge reads partials only
-  const bool fold_tail = p.fused && split == 0 && p.n_raw > 0;
+  const bool fold_tail = p.fused && split == 0 && n_raw > 0;
   if (fold_tail)
-    raw_tail_partial<D>(p, b, hkv, g0, G, tid, reinterpret_cast<float*>(&w_lds[0][0][0]),
-                        part_lds, tail_ml[0], tail_ml[1]);
+    raw_tail_partial<D>(p, b, hkv, g0, G, (int)n_raw, tid,
+                        reinterpret_cast<float*>(&w_lds[0][0][0]), part_lds, tail_ml[0],
+                        tail_ml[1]);
 
   __syncthreads();  // a_lds; the tail's scratch (w_lds) is free again
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
@@ -826,6 +836,7 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
     a.out = fuse->out;
     a.o_sb = fuse->o_sb;
     a.o_sh = fuse->o_sh;
+    a.state = fuse->state;
   }
   const int64_t G = Hq / Hkv;
   const int gg = (int)std::min<int64_t>(G, 16);

@@ -62,12 +62,19 @@ __device__ __forceinline__ float quant_code(float c, float s, float rs) {
 
 // ---------------------------------------------------------------- jpeg encode
 
-template <typename T, int VEC, int RMAX, bool QUANT>
+template <typename T, int VEC, int RMAX, bool QUANT, bool GATED = false>
 __global__ __launch_bounds__(kThreads) void jpeg_encode_kernel(
     const T* __restrict__ x, int64_t sb, int64_t sh, int64_t ss, int64_t H, int64_t m,
     int64_t D, int64_t s_valid, int r, int k, const float* __restrict__ basis,
     void* __restrict__ out, float* __restrict__ scales, int64_t cap, int64_t n0,
-    int64_t items, int lpi_log2) {
+    int64_t items, int lpi_log2, const int64_t* __restrict__ gate = nullptr) {
+  if constexpr (GATED) {
+    // gate = device (n_blocks, n_tail) of a decode step: the block is
+    // archived only when the tail completes it, at block n_blocks
+    if (gate[1] != r - 1) return;
+    n0 = gate[0];
+    if (n0 < 0 || n0 + m > cap) return;
+  }
   const ItemMap im = item_of_thread(lpi_log2);
   // Dead lanes still take part in the group shuffles below; they work on
   // item 0 and store nothing.
@@ -249,12 +256,19 @@ __device__ __forceinline__ u32x2 quantize8(const float (&c)[8], float s) {
 // rounding, scale and codes) with the block loads unconditional, the row
 // absmax on DPP, the divisions replaced by exact shortcuts and KT (the
 // kept frequencies, 0 = runtime k) unrolled.
-template <typename T, int KT>
+template <typename T, int KT, bool GATED = false>
 __global__ __launch_bounds__(kThreads) void jpeg_encode_r8q_kernel(
     const T* __restrict__ x, int64_t sb, int64_t sh, int64_t ss, int64_t H, int64_t m,
     int64_t D, int k_rt, const float* __restrict__ basis, int8_t* __restrict__ out,
-    float* __restrict__ scales, int64_t cap, int64_t n0, int64_t items, int lpi_log2) {
+    float* __restrict__ scales, int64_t cap, int64_t n0, int64_t items, int lpi_log2,
+    const int64_t* __restrict__ gate = nullptr) {
   constexpr int R = 8, VEC = 8;
+  if constexpr (GATED) {
+    // gate = device (n_blocks, n_tail): archive only a completed tail
+    if (gate[1] != R - 1) return;
+    n0 = gate[0];
+    if (n0 < 0 || n0 + m > cap) return;
+  }
   const int k = KT > 0 ? KT : k_rt;
   const ItemMap im = item_of_thread(lpi_log2);
   const bool live = im.item < items;
@@ -764,10 +778,16 @@ const char* fc_status_string(int status) {
 
 int fc_last_hip_error(void) { return g_last_hip_error; }
 
-int fc_jpeg_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb, int64_t x_sh,
-                   int64_t x_ss, int64_t s_valid, int64_t m, int64_t D, int r, int k,
-                   const float* basis, void* coeffs, float* scales, int64_t cap, int64_t n0,
-                   int quant_bits, void* stream) {
+}  // extern "C"
+
+namespace fc {
+
+template <bool GATED>
+static int jpeg_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
+                              int64_t x_sh, int64_t x_ss, int64_t s_valid, int64_t m, int64_t D,
+                              int r, int k, const float* basis, void* coeffs, float* scales,
+                              int64_t cap, int64_t n0, int quant_bits, void* stream,
+                              const int64_t* gate) {
   if (B < 0 || H < 0 || m < 0 || D <= 0 || r < 1 || k < 1 || k > r) return FC_ERR_ARG;
   if (quant_bits != 0 && quant_bits != 8) return FC_ERR_ARG;
   if (n0 < 0 || n0 + m > cap) return FC_ERR_ARG;
@@ -789,9 +809,9 @@ int fc_jpeg_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_s
       using T = decltype(tv);
       return with_int<2, 4, 8, 0>(k == 2 || k == 4 || k == 8 ? k : 0, [&](auto kc) {
         constexpr int KT = decltype(kc)::value;
-        jpeg_encode_r8q_kernel<T, KT><<<grid, kThreads, 0, st>>>(
+        jpeg_encode_r8q_kernel<T, KT, GATED><<<grid, kThreads, 0, st>>>(
             (const T*)x, x_sb, x_sh, x_ss, H, m, D, k, basis, (int8_t*)coeffs, scales, cap, n0,
-            items, lg);
+            items, lg, gate);
         return FC_OK;
       });
     });
@@ -804,18 +824,39 @@ int fc_jpeg_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_s
       return with_int<8, 16, 0>(rmax, [&](auto rc_) {
         constexpr int RMAX = decltype(rc_)::value;
         if (quant_bits)
-          jpeg_encode_kernel<T, VEC, RMAX, true><<<grid, kThreads, 0, st>>>(
+          jpeg_encode_kernel<T, VEC, RMAX, true, GATED><<<grid, kThreads, 0, st>>>(
               (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, k, basis, coeffs, scales, cap,
-              n0, items, lg);
+              n0, items, lg, gate);
         else
-          jpeg_encode_kernel<T, VEC, RMAX, false><<<grid, kThreads, 0, st>>>(
+          jpeg_encode_kernel<T, VEC, RMAX, false, GATED><<<grid, kThreads, 0, st>>>(
               (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, k, basis, coeffs, scales, cap,
-              n0, items, lg);
+              n0, items, lg, gate);
         return FC_OK;
       });
     });
   });
   return rc != FC_OK ? rc : check_launch();
+}
+
+int jpeg_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
+                      int64_t x_sh, int64_t x_ss, int64_t D, int r, int k, const float* basis,
+                      void* coeffs, float* scales, int64_t cap, int quant_bits, void* stream,
+                      const int64_t* gate) {
+  if (!gate || cap < 1) return FC_ERR_ARG;
+  return jpeg_encode_launch<true>(x, x_dtype, B, H, x_sb, x_sh, x_ss, r, 1, D, r, k, basis,
+                                  coeffs, scales, cap, 0, quant_bits, stream, gate);
+}
+
+}  // namespace fc
+
+extern "C" {
+
+int fc_jpeg_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb, int64_t x_sh,
+                   int64_t x_ss, int64_t s_valid, int64_t m, int64_t D, int r, int k,
+                   const float* basis, void* coeffs, float* scales, int64_t cap, int64_t n0,
+                   int quant_bits, void* stream) {
+  return jpeg_encode_launch<false>(x, x_dtype, B, H, x_sb, x_sh, x_ss, s_valid, m, D, r, k, basis,
+                                   coeffs, scales, cap, n0, quant_bits, stream, nullptr);
 }
 
 int fc_jpeg_decode(const void* store, int store_dtype, const float* scales, int64_t B,

@@ -24,6 +24,7 @@ struct TailArgs {
   int64_t tsb[2], tsh[2];
   void* tail[2];  // (B, H, r, D) contiguous tail buffers
   int64_t H, D, r, t;
+  const int64_t* state;  // device (n_blocks, n_tail): t = state[1] (or NULL)
 };
 
 // tail[s][b][h][t][:] = tok[s][b][h][:]; blockIdx.x = b * H + h,
@@ -34,9 +35,76 @@ __global__ __launch_bounds__(kTailThreads) void tail_append_kernel(TailArgs a) {
   const int s = blockIdx.y;
   const int64_t bh = blockIdx.x;
   const int64_t b = bh / a.H, h = bh - b * a.H;
+  const int64_t t = a.state ? a.state[1] : a.t;
+  if (t < 0 || t >= a.r) return;  // a tail row exists only for 0 <= t < r
   const T* src = static_cast<const T*>(a.tok[s]) + b * a.tsb[s] + h * a.tsh[s];
-  T* dst = static_cast<T*>(a.tail[s]) + (bh * a.r + a.t) * a.D;
+  T* dst = static_cast<T*>(a.tail[s]) + (bh * a.r + t) * a.D;
   for (int64_t d = threadIdx.x; d < a.D; d += kTailThreads) dst[d] = src[d];
+}
+
+// state = (n_blocks, n_tail) after the step's token: one lane per word, so
+// the update goes out as ordinary vector stores
+__global__ void state_advance_kernel(int64_t* state, int64_t r) {
+  const int i = threadIdx.x;
+  if (i >= 2) return;
+  const int64_t nb = state[0], t = state[1] + 1;
+  const int64_t v[2] = {t == r ? nb + 1 : nb, t == r ? 0 : t};
+  state[i] = v[i];
+}
+
+// The step with its counters on the device (a->state): every launch reads
+// them there, so one captured graph of the step is valid at every step.
+static int decode_step_state(const fc_step_args* a) {
+  if (a->store_kind != FC_STORE_JPEG_I8 || a->quant_bits != 8) return FC_ERR_UNSUPPORTED;
+  if (a->n_blocks < 1) return FC_ERR_ARG;  // the archive holds a block before capture
+  const int64_t B = a->B, Hkv = a->Hkv, D = a->D;
+  const int r = a->r;
+  hipStream_t stream = (hipStream_t)a->stream;
+  const fc_step_stream* st[2] = {&a->key, &a->value};
+  TailArgs ta{};
+  for (int i = 0; i < 2; ++i) {
+    ta.tok[i] = st[i]->token;
+    ta.tsb[i] = st[i]->tok_sb;
+    ta.tsh[i] = st[i]->tok_sh;
+    ta.tail[i] = st[i]->tail;
+  }
+  ta.H = Hkv;
+  ta.D = D;
+  ta.r = r;
+  ta.t = 0;
+  ta.state = a->state;
+  const dim3 grid((unsigned)(B * Hkv), 2);
+  if (esize_of(a->stream_dtype) == 4)
+    tail_append_kernel<uint32_t><<<grid, kTailThreads, 0, stream>>>(ta);
+  else
+    tail_append_kernel<uint16_t><<<grid, kTailThreads, 0, stream>>>(ta);
+  int rc = check_launch();
+  if (rc != FC_OK) return rc;
+  const int64_t tsb = Hkv * r * D, tsh = (int64_t)r * D;
+  for (int i = 0; i < 2; ++i) {
+    rc = jpeg_encode_gated(st[i]->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, D, r, a->s,
+                           a->basis, st[i]->rows, st[i]->scales, st[i]->cap, 8, a->stream,
+                           a->state);
+    if (rc != FC_OK) return rc;
+  }
+  fc_stream_view v[2];
+  for (int i = 0; i < 2; ++i) {
+    v[i].rows = st[i]->rows;
+    v[i].scales = st[i]->scales;
+    v[i].anchors = nullptr;
+    v[i].cap = st[i]->cap;
+    v[i].raw = st[i]->tail;
+    v[i].raw_sb = tsb;
+    v[i].raw_sh = tsh;
+    v[i].raw_st = D;
+  }
+  rc = decode_attention_state(a->q, a->q_dtype, a->q_sb, a->q_sh, B, a->Hq, Hkv, D,
+                              a->stream_dtype, r, a->s, a->n_blocks, &v[0], &v[1], a->A, a->scale,
+                              a->out, a->o_sb, a->o_sh, a->workspace, a->workspace_bytes,
+                              a->n_cu, a->state, a->stream);
+  if (rc != FC_OK) return rc;
+  state_advance_kernel<<<1, 64, 0, stream>>>(const_cast<int64_t*>(a->state), r);
+  return check_launch();
 }
 
 }  // namespace fc
@@ -60,13 +128,14 @@ int fc_decode_step(const fc_step_args* a) {
   if (a->store_kind == FC_STORE_JPEG_I8 && (!a->key.scales || !a->value.scales)) return FC_ERR_ARG;
   if (a->store_kind == FC_STORE_PNG && (!a->key.anchors || !a->value.anchors)) return FC_ERR_ARG;
   if (a->store_kind != FC_STORE_PNG && !a->basis) return FC_ERR_ARG;
+  if (a->state) return decode_step_state(a);
   const bool completes = a->n_tail + 1 == r;
   if (completes && (a->n_blocks + 1 > a->key.cap || a->n_blocks + 1 > a->value.cap))
     return FC_ERR_ARG;  // the caller grows the archives first
   hipStream_t stream = (hipStream_t)a->stream;
 
   // 1. the new tokens into the tails
-  TailArgs ta;
+  TailArgs ta{};
   for (int i = 0; i < 2; ++i) {
     ta.tok[i] = st[i]->token;
     ta.tsb[i] = st[i]->tok_sb;
@@ -77,6 +146,7 @@ int fc_decode_step(const fc_step_args* a) {
   ta.D = D;
   ta.r = r;
   ta.t = a->n_tail;
+  ta.state = nullptr;  // host counters
   const dim3 grid((unsigned)(B * Hkv), 2);
   if (es == 4)
     tail_append_kernel<uint32_t><<<grid, kTailThreads, 0, stream>>>(ta);

@@ -292,6 +292,7 @@ typedef struct fc_step_args {
   int n_cu;              /* compute units of the device (split count) */
   void* stream;          /* hipStream_t */
   fc_step_stream key, value;
+  int64_t* state;        /* device (n_blocks, n_tail), or NULL: see below */
 } fc_step_args;
 
 /*
@@ -310,6 +311,15 @@ typedef struct fc_step_args {
  * flashcodec/attention.py:64-140) with one call.
  */
 int fc_decode_step(const fc_step_args* args);
+/*
+ * With args->state != NULL (int8 jpeg archives, the matrix-core decode
+ * attention), the step takes n_blocks and n_tail from the two int64 words
+ * at `state` on the device and advances them there (n_tail + 1 == r moves a
+ * block into the archive), so the enqueued work is the same at every step
+ * and a captured HIP graph of it stays valid.  args->n_blocks (>= 1) then
+ * only sizes the split count; the archives must hold every block the
+ * replayed steps will add (a block past `cap` is not written).
+ */
 
 #ifdef __cplusplus
 }
