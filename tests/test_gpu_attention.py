@@ -128,22 +128,34 @@ CASES += [
 ]
 
 
+def _use_variant(monkeypatch, variant):
+    """auto: the default split pass (matrix cores for int8 jpeg); valu: the
+    vector-ALU pass, the only one for fp stores."""
+    if variant == "valu":
+        monkeypatch.setenv("FLASHCODEC_AMD_ATTN", "valu")
+    else:
+        monkeypatch.delenv("FLASHCODEC_AMD_ATTN", raising=False)
+
+
 @pytest.fixture(params=["auto", "valu"])
 def split_variant(request, monkeypatch):
     """Run int8 cases on the matrix-core split pass (auto) and on the
     vector-ALU one."""
-    if request.param == "valu":
-        monkeypatch.setenv("FLASHCODEC_AMD_ATTN", "valu")
-    else:
-        monkeypatch.delenv("FLASHCODEC_AMD_ATTN", raising=False)
+    _use_variant(monkeypatch, request.param)
     return request.param
 
 
-@pytest.mark.parametrize("name,cfg,dt,B,Hk,G,S,D", CASES, ids=[c[0] for c in CASES])
-def test_decode_attention_matches_oracle(name, cfg, dt, B, Hk, G, S, D, oracle, split_variant):
-    if split_variant == "valu" and not cfg.get("quant_bits"):
-        pytest.skip("one split pass only for non-int8 stores")
-    print(f"case attention/{name} [{split_variant}]", flush=True)
+# int8 cases on both split passes, fp-store cases on their one pass
+ORACLE_CASES = [(c, "auto") for c in CASES] + [(c, "valu") for c in CASES
+                                                if c[1].get("quant_bits")]
+
+
+@pytest.mark.parametrize("case,variant", ORACLE_CASES,
+                         ids=[f"{v}-{c[0]}" for c, v in ORACLE_CASES])
+def test_decode_attention_matches_oracle(case, variant, oracle, monkeypatch):
+    name, cfg, dt, B, Hk, G, S, D = case
+    _use_variant(monkeypatch, variant)
+    print(f"case attention/{name} [{variant}]", flush=True)
     seed = seed_of(name)
     ks, vs = build_streams(cfg, dt, B, Hk, S, D, seed % 10000, oracle)
     rng = np.random.default_rng(seed)

@@ -89,3 +89,37 @@ def test_stream_empty_state():
     assert st.seq_len == 0
     with pytest.raises(ValueError):
         st.crop(2)
+
+
+def test_graph_host_counters_advance_like_appends():
+    """graph.advance_host moves a layer's host counters the way one-token
+    appends do: the tail grows to r - 1, then a block moves to the archive."""
+    pytest.importorskip("transformers")
+    from flashcodec_amd import graph
+    from flashcodec_amd.cache import FlashCodecLayer
+
+    class Cache:
+        pass
+
+    r = 8
+    layer = FlashCodecLayer(mode="jpeg", block_size=r, keep_freqs=4, quant_bits=8)
+    cache = Cache()
+    cache.layers = [layer, object()]             # non-codec layers are left alone
+    for st in (layer._key_stream, layer._value_stream):
+        st.n_blocks, st.n_archived, st._n_raw = 3, 3 * r, 5
+    seen = []
+    for _ in range(13):
+        graph.advance_host(cache)
+        st = layer._key_stream
+        seen.append((st.n_blocks, st._n_raw))
+    assert seen[:4] == [(3, 6), (3, 7), (4, 0), (4, 1)]
+    assert seen[-1] == (5, 2)                    # 3 blocks + 5 + 13 = 42 tokens = 5 * 8 + 2
+    twin = FlashCodecLayer(mode="jpeg", block_size=r, keep_freqs=4, quant_bits=8)
+    cache2 = Cache()
+    cache2.layers = [twin]
+    for st in (twin._key_stream, twin._value_stream):
+        st.n_blocks, st.n_archived, st._n_raw = 3, 3 * r, 5
+    graph.advance_host(cache2, steps=13)
+    for a, b in ((layer._key_stream, twin._key_stream), (layer._value_stream, twin._value_stream)):
+        assert (a.n_blocks, a.n_archived, a._n_raw) == (b.n_blocks, b.n_archived, b._n_raw)
+        assert a.n_archived == r * a.n_blocks
