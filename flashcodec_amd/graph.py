@@ -29,8 +29,13 @@ def _codec_layers(cache):
 
 def prepare(cache, extra_tokens):
     """Put the counters of every codec layer of `cache` on the device and
-    grow its archives for `extra_tokens` more tokens.  Each layer must hold
-    at least one archived block (a prefill of >= block_size tokens)."""
+    grow its archives for `extra_tokens` more tokens.  Every layer must be a
+    codec layer (other cache layers grow by concatenation, which a replayed
+    graph cannot do) holding at least one archived block (a prefill of
+    >= block_size tokens)."""
+    layers = list(getattr(cache, "layers", []))
+    if not layers or len(_codec_layers(cache)) != len(layers):
+        raise NotImplementedError("graph decoding needs a cache whose layers are all codec layers")
     for layer in _codec_layers(cache):
         ks, vs = layer._key_stream, layer._value_stream
         c = ks.codec

@@ -123,3 +123,21 @@ def test_graph_host_counters_advance_like_appends():
     for a, b in ((layer._key_stream, twin._key_stream), (layer._value_stream, twin._value_stream)):
         assert (a.n_blocks, a.n_archived, a._n_raw) == (b.n_blocks, b.n_archived, b._n_raw)
         assert a.n_archived == r * a.n_blocks
+
+
+def test_graph_prepare_refuses_mixed_caches():
+    pytest.importorskip("transformers")
+    from flashcodec_amd import graph
+    from flashcodec_amd.cache import FlashCodecLayer
+
+    class Cache:
+        pass
+
+    cache = Cache()
+    cache.layers = [FlashCodecLayer(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8),
+                    object()]
+    with pytest.raises(NotImplementedError):
+        graph.prepare(cache, 16)
+    cache.layers = [FlashCodecLayer(mode="png", block_size=8)]
+    with pytest.raises(NotImplementedError):
+        graph.prepare(cache, 16)
