@@ -168,7 +168,7 @@ def c2_mode(args):
         "hbm_frac_read": round(alg / (t_read * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "algorithmic_bytes": alg,
         "append_us_per_token": round(t_tok * 1e6, 2),
-        "append_launches_per_token": "2 copies (raw tail concat + contiguous) + 1 archive launch per 8 tokens",
+        "append_launches_per_token": "1 tail-row copy per token + 1 archive launch per 8 tokens",
         "token_by_token_codes_equal_bulk": same,
         "config": {"workload": "C2 jpeg int8 archive + read", "B": b_, "H": h_, "S": s_, "D": d_,
                    "block": r, "keep_freqs": k, "dtype": "fp16"},

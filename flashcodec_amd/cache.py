@@ -59,6 +59,8 @@ class _CodecStream:
         self.codec = codec
         self._raw_buf = None     # (B, H, r, D) tail buffer in the stream dtype
         self._n_raw = 0          # tokens in the tail (t < r)
+        self._tail_rows = None   # per-row (B, H, 1, D) views of the tail buffer
+        self._tail_key = None    # (shape, dtype, device) the tail buffer was checked for
         self.n_archived = 0      # archived tokens
         self.n_blocks = 0        # archived blocks
         self.meta = None         # (B, H, D, element size)
@@ -110,6 +112,8 @@ class _CodecStream:
             if self._n_raw and old is not None and old.shape == buf.shape:
                 buf[:, :, :self._n_raw].copy_(old[:, :, :self._n_raw])
             self._raw_buf = buf
+            self._tail_rows = [buf[:, :, t:t + 1] for t in range(self.block_size)]
+            self._tail_key = None
         return buf
 
     @property
@@ -176,8 +180,15 @@ class _CodecStream:
         is archived from the tail buffer, whole blocks of the input straight
         from the input (the archived bits depend only on each block's r
         tokens, so they equal the reference's cat-then-archive)."""
-        N.require_gpu(tokens)
         r = self.block_size
+        t = self._n_raw
+        if (t + 1 < r and self._tail_key is not None
+                and self._tail_key == (tokens.shape, tokens.dtype, tokens.device)):
+            # one token for a buffer already checked against this token shape
+            self._tail_rows[t].copy_(tokens)
+            self._n_raw = t + 1
+            return
+        N.require_gpu(tokens)
         if self.meta is None:
             self.meta = (tokens.shape[0], tokens.shape[1], tokens.shape[-1],
                          tokens.element_size())
@@ -185,7 +196,9 @@ class _CodecStream:
         m = tokens.shape[-2]
         if m == 0:
             return
-        t = self._n_raw
+        if m == 1 and tokens.dtype == self.dtype:
+            self._tail_buffer(tokens)
+            self._tail_key = (tokens.shape, tokens.dtype, tokens.device)
         if t + m < r:
             # the tail grows: one copy (the common decode step)
             self._tail_buffer(tokens)[:, :, t:t + m].copy_(tokens)
