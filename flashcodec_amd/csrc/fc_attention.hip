@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
+#include <type_traits>
 
 #include "fc_attn_internal.h"
 #include "fc_common.h"
@@ -69,6 +70,20 @@ struct AttnArgs {
   float* pm;
   float* pl;
   float* pacc;
+  // Fused merge (arrive != NULL): split 0 folds the raw tail into its
+  // partial, every workgroup publishes its partial and counts its arrival
+  // in its group's word (arrive + group * cstride, zero between calls), and
+  // the last workgroup of the group merges the partials into `out`.
+  // Otherwise n_raw is 0 here and the merge kernel runs afterwards.
+  unsigned int* arrive;
+  int64_t cstride;
+  const void* kraw;
+  const void* vraw;
+  int raw_dtype;
+  int64_t kr_sb, kr_sh, kr_st, vr_sb, vr_sh, vr_st;
+  int64_t n_raw;
+  void* out;
+  int64_t o_sb, o_sh;
 };
 
 // v + (v from the lane selected by a DPP pattern); patterns stay inside a
@@ -86,6 +101,38 @@ __device__ __forceinline__ float row_sum(float v, int lpr) {
   if (lpr >= 16) v = FC_DPP_ADD(v, 0x140); // row_mirror
   if (lpr >= 32) v += __shfl_xor(v, 16, 64);
   if (lpr >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// DPP lane v + (v from `n` lanes below / above inside the 16-lane row;
+// lanes without a source add 0)
+#define FC_DPP_SHR(v, n) \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x110 + (n), 0xf, 0xf, true))
+#define FC_DPP_SHL(v, n) \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + (n), 0xf, 0xf, true))
+
+// Inclusive prefix sum (lane t: sum of lanes <= t) and suffix sum (lane t:
+// sum of lanes >= t) inside each 16-lane row.
+__device__ __forceinline__ float row16_prefix(float v) {
+  v += FC_DPP_SHR(v, 1);
+  v += FC_DPP_SHR(v, 2);
+  v += FC_DPP_SHR(v, 4);
+  v += FC_DPP_SHR(v, 8);
+  return v;
+}
+__device__ __forceinline__ float row16_suffix(float v) {
+  v += FC_DPP_SHL(v, 1);
+  v += FC_DPP_SHL(v, 2);
+  v += FC_DPP_SHL(v, 4);
+  v += FC_DPP_SHL(v, 8);
+  return v;
+}
+// Maximum over the 16-lane row, in every lane of it.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false)));
   return v;
 }
 
@@ -248,14 +295,124 @@ __device__ __forceinline__ float pair_weights(float* sc, float* wo, int st, cons
   return es;
 }
 
+// Merge of one (batch, kv head, group of ng <= GM query heads) by the last
+// workgroup of the split pass to finish it: out = sum_s w_s acc_s /
+// sum_s w_s l_s over the n_splits published partials, w_s = 2^(m_s - max m)
+// (the raw tail is part of split 0's partial).  Partials and statistics are
+// read with device-scope loads.  Each output task (head, 4 features) is
+// shared by nsub adjacent lanes that take every nsub-th split, kPre partial
+// loads per lane in flight at a time; the first sweep's first loads are
+// requested together with the statistics, so a merge of up to kPre * nsub
+// splits per task costs one round trip.  `lds` holds >= 2 * GM * kMaxSplits
+// floats.
+template <int GM>
+__device__ void merge_group(const AttnArgs& p, int64_t b, int64_t hkv, int64_t g0, int ng, int tid,
+                            float* lds) {
+  constexpr int kPre = GM >= 4 ? 24 : 8;  // fewer heads: more lanes per task
+  const int ns = p.n_splits;
+  const int D = (int)p.D, C4 = D / 4;
+  const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;
+  float* const wsp = lds;                    // [ng][ns] split maxima
+  float* const plv = lds + GM * kMaxSplits;  // [ng][ns] split sums
+  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, ng * ns * D * 4);
+  const __amdgpu_buffer_rsrc_t rm = buf_rsrc(p.pm + bq0 * ns, ng * ns * 4);
+  const __amdgpu_buffer_rsrc_t rl = buf_rsrc(p.pl + bq0 * ns, ng * ns * 4);
+  const int ntask = ng * C4;
+  int lsub = 0;  // nsub = 2^lsub lanes per task, up to 16
+  while (lsub < 4 && (ntask << (lsub + 1)) <= kAttnThreads) ++lsub;
+  const int nsub = 1 << lsub;
+  const int sub = tid & (nsub - 1);
+  float4_t pre[kPre];
+  auto fetch = [&](bool act, int h, int c, int sp0) {
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      const int sp = sp0 + j * nsub;
+      pre[j] = (act && sp < ns)
+                   ? __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rp, ((h * ns + sp) * C4 + c) * 16, 0,
+                                                      kCachePolicySc1))
+                   : (float4_t){0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  {
+    const int task = tid >> lsub;
+    const bool act = task < ntask;
+    const int h = act ? task / C4 : 0;
+    fetch(act, h, act ? task - h * C4 : 0, sub);
+  }
+  for (int u = tid; u < ng * ns; u += kAttnThreads) {
+    wsp[u] = __builtin_bit_cast(float,
+                                __builtin_amdgcn_raw_buffer_load_b32(rm, u * 4, 0, kCachePolicySc1));
+    plv[u] = __builtin_bit_cast(float,
+                                __builtin_amdgcn_raw_buffer_load_b32(rl, u * 4, 0, kCachePolicySc1));
+  }
+  __syncthreads();
+  for (int t0 = 0; t0 < ntask; t0 += kAttnThreads >> lsub) {  // uniform trip count
+    const int task = t0 + (tid >> lsub);
+    const bool act = task < ntask;
+    const int h = act ? task / C4 : 0, c = act ? task - h * C4 : 0;
+    const float* wh = wsp + h * ns;
+    const float* lh = plv + h * ns;
+    float mx = -INFINITY;
+    for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, wh[sp]);
+    float l = 0.f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
+    for (int sp0 = sub; sp0 < ns; sp0 += kPre * nsub) {
+      if (t0 > 0 || sp0 > sub) fetch(act, h, c, sp0);
+#pragma unroll
+      for (int j = 0; j < kPre; ++j) {
+        const int sp = sp0 + j * nsub;
+        if (sp < ns) {
+          const float w = wh[sp] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wh[sp] - mx);
+          l = __builtin_fmaf(w, lh[sp], l);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(w, pre[j][i], o[i]);
+        }
+      }
+    }
+    for (int m = 1; m < nsub; m <<= 1) {
+      l += __shfl_xor(l, m, 64);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] += __shfl_xor(o[i], m, 64);
+    }
+    if (act && sub == 0) {
+      const float iv = 1.0f / l;
+      const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) store_any(p.out, p.q_dtype, ob + i, o[i] * iv);
+    }
+  }
+}
+
+// 3 waves per SIMD (12 per CU, 3 workgroups) up to 4 heads per workgroup,
+// except the 16-bit png variants, which would spill at that register budget
 template <typename TS, int KIND, bool SREG, int VEC, int GM>
-__global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs p) {
+constexpr int split_waves_per_eu() {
+  return (GM >= 8 || (KIND == FC_STORE_PNG && sizeof(TS) == 2)) ? 2 : 3;
+}
+
+template <typename TS, int KIND, bool SREG, int VEC, int GM>
+__global__ __launch_bounds__(kAttnThreads)
+__attribute__((amdgpu_waves_per_eu(split_waves_per_eu<TS, KIND, SREG, VEC, GM>())))
+void attn_split_kernel(AttnArgs p) {
   // scores, then weights, per (row, head); the generic-s variant keeps the
   // weights in a second region
   constexpr int kSwRegions = (KIND != FC_STORE_PNG && !SREG) ? 2 : 1;
-  __shared__ float sw[kPassRows * GM * kSwRegions];
-  float* const wts = sw + (kSwRegions - 1) * kPassRows * GM;
+  // rows whose loads one thread keeps in flight (fewer at 8 heads per
+  // workgroup, whose accumulators already hold most registers)
+  constexpr int kRB = GM >= 8 ? 2 : 4;
+  // layout: block nl of the pass at nl * bst, row j of it at + j * GM, head
+  // g at + g.  The block stride bst = (s | 1) * GM is an odd multiple of GM,
+  // so the (block, head) pairs of phase B, which read their blocks' rows in
+  // lockstep, fall in different LDS banks.  A pass of floor(kPassRows / s)
+  // blocks then spans at most 1.5 * kPassRows * GM floats (at s = 2).
+  constexpr int kRegion = kPassRows * GM * 3 / 2;
+  static_assert(kRegion * kSwRegions >= 2 * GM * kMaxSplits, "merge statistics fit the region");
+  static_assert(kRegion * kSwRegions >= 2 * 64 * GM, "tail logits fit the region");
+  __shared__ float sw[kRegion * kSwRegions];
+  float* const wts = sw + (kSwRegions - 1) * kRegion;
   __shared__ float red[(kAttnThreads / 64) * GM];
+  __shared__ float qs[GM * FC_MAX_HEAD_DIM];
 
   const int split = blockIdx.x;
   const int64_t bh = blockIdx.y;  // b * Hkv + hkv
@@ -270,16 +427,23 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs p) {
   const bool dact = d0 < p.D;
   const int s = p.s, r = p.r;
 
-  // query heads of this group, as fp32, for this lane's features
+  // query heads of this group, as fp32, for this lane's features.  Every
+  // workgroup of a kv head reads the same few query rows, so the workgroup
+  // stages them in LDS with one coalesced pass instead of letting each lane
+  // fetch its own features (which crowds the L2 lines that hold them).
+  {
+    const int64_t qb = b * p.q_sb + (hkv * p.G + g0) * p.q_sh;
+    for (int64_t i = tid; i < GM * p.D; i += kAttnThreads) {
+      const int64_t g = i / p.D, d = i - g * p.D;
+      qs[i] = (g0 + g) < p.G ? load_q(p.q, p.q_dtype, qb + g * p.q_sh + d) : 0.f;
+    }
+  }
+  __syncthreads();
   float qv[GM][VEC];
 #pragma unroll
-  for (int g = 0; g < GM; ++g) {
-    const int64_t hq = hkv * p.G + g0 + g;
-    const bool ok = dact && (g0 + g) < p.G;
+  for (int g = 0; g < GM; ++g)
 #pragma unroll
-    for (int v = 0; v < VEC; ++v)
-      qv[g][v] = ok ? load_q(p.q, p.q_dtype, b * p.q_sb + hq * p.q_sh + d0 + v) : 0.f;
-  }
+    for (int v = 0; v < VEC; ++v) qv[g][v] = dact ? qs[g * p.D + d0 + v] : 0.f;
 
   float acc[GM][VEC];
 #pragma unroll
@@ -293,20 +457,46 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs p) {
     l_run[g] = 0.f;
   }
 
-  const int64_t nb_begin = (int64_t)split * p.blocks_per_split;
-  const int64_t nb_end = min(p.nb, nb_begin + p.blocks_per_split);
-  const int cb_max = max(1, kPassRows / s);
-
-  for (int64_t nb0 = nb_begin; nb0 < nb_end; nb0 += cb_max) {
-    const int cb = (int)min((int64_t)cb_max, nb_end - nb0);
-    const int nrows = cb * s;
-
-    // ---- A: scores q . S_j for every row of the pass
-    for (int rho = slot; rho < nrows; rho += nslot) {
-      const int nl = rho / s, j = rho - nl * s;
+  // ---- raw tail (fused merge only): split 0 starts its partial with the
+  // n_raw < FC_MAX_BLOCK tail tokens at full precision
+  if (split == 0 && p.n_raw > 0) {
+    const int nt = (int)p.n_raw;
+    const int lane = tid & 63;
+    float* const tsc = sw;            // [nt][GM] base-2 logits
+    float* const tex = sw + 64 * GM;  // [nt][GM] exponentials
+    // VEC elements from d0 of tail row t (row 0 for lanes without one: a
+    // valid address whose values are dropped), all loads in flight together.
+    // The tail is in the stream dtype, which is TS except for int8 archives.
+    auto raw_row = [&](const void* base, int64_t off0, int64_t st, int t, bool ok,
+                       float (&x)[VEC]) {
+      const int64_t off = ok ? off0 + t * st + d0 : off0;
+      const int dt = KIND == FC_STORE_JPEG_I8 ? p.raw_dtype
+                     : std::is_same_v<TS, f16_t> ? FC_F16
+                     : std::is_same_v<TS, bf16_t> ? FC_BF16 : FC_F32;
+      switch (dt) {
+        case FC_F16: {
+          const f16_t* ptr = static_cast<const f16_t*>(base) + off;
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) x[v] = to_f32(ptr[ok ? v : 0]);
+        } break;
+        case FC_BF16: {
+          const bf16_t* ptr = static_cast<const bf16_t*>(base) + off;
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) x[v] = to_f32(ptr[ok ? v : 0]);
+        } break;
+        default: {
+          const float* ptr = static_cast<const float*>(base) + off;
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) x[v] = ptr[ok ? v : 0];
+        } break;
+      }
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) x[v] = ok ? x[v] : 0.f;
+    };
+    for (int t0 = 0; t0 < nt; t0 += nslot) {
+      const int t = t0 + slot;
       float x[VEC];
-      const float rs = load_row<TS, KIND, VEC>(p.krows, p.kscales, p.kanch, p.kcap, bh,
-                                               nb0 + nl, j, s, r, p.D, d0, dact, x);
+      raw_row(p.kraw, b * p.kr_sb + hkv * p.kr_sh, p.kr_st, t, t < nt && dact, x);
       float pd[GM];
 #pragma unroll
       for (int g = 0; g < GM; ++g) {
@@ -315,25 +505,132 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs p) {
         for (int v = 0; v < VEC; ++v) a = __builtin_fmaf(qv[g][v], x[v], a);
         pd[g] = row_sum(a, lpr);
       }
-      if (lir == 0) {
+      if (lir == 0 && t < nt) {
 #pragma unroll
-        for (int g = 0; g < GM; ++g) sw[rho * GM + g] = pd[g] * rs;
+        for (int g = 0; g < GM; ++g) tsc[t * GM + g] = pd[g] * p.scale_log2;
+      }
+    }
+    __syncthreads();
+    // every wavefront: per head, lanes = tokens
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+      const float lg = lane < nt ? tsc[lane * GM + g] : -INFINITY;
+      float mx = lg;
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+      const float e = lane < nt ? __builtin_amdgcn_exp2f(lg - mx) : 0.f;
+      float l = e;
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
+      m_run[g] = mx;
+      l_run[g] = l;
+      if (tid < nt) tex[tid * GM + g] = e;
+    }
+    __syncthreads();
+    for (int t0 = 0; t0 < nt; t0 += nslot) {
+      const int t = t0 + slot;
+      float x[VEC];
+      raw_row(p.vraw, b * p.vr_sb + hkv * p.vr_sh, p.vr_st, t, t < nt && dact, x);
+      if (t < nt) {
+#pragma unroll
+        for (int g = 0; g < GM; ++g) {
+          const float w = tex[t * GM + g];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[g][v] = __builtin_fmaf(w, x[v], acc[g][v]);
+        }
+      }
+    }
+    __syncthreads();  // sw is reused by the passes
+  }
+
+  const int64_t nb_begin = (int64_t)split * p.blocks_per_split;
+  const int64_t nb_end = min(p.nb, nb_begin + p.blocks_per_split);
+  const int cb_max = max(1, kPassRows / s);
+  const int bst = (s | 1) * GM;
+  // V rows rho0, rho0 + nslot, ... (kRB of them) of the pass at block nb0
+  auto load_v_batch = [&](int rho0, int nrows, int64_t nb0, float (&x)[kRB][VEC]) {
+#pragma unroll
+    for (int u = 0; u < kRB; ++u) {
+      const int rho = rho0 + u * nslot;
+      const bool ok = rho < nrows;
+      const int nl = ok ? rho / s : 0, j = ok ? rho - nl * s : 0;
+      load_row<TS, KIND, VEC>(p.vrows, nullptr, p.vanch, p.vcap, bh, nb0 + nl, j, s, r, p.D, d0,
+                              dact && ok, x[u]);
+    }
+  };
+
+  for (int64_t nb0 = nb_begin; nb0 < nb_end; nb0 += cb_max) {
+    const int cb = (int)min((int64_t)cb_max, nb_end - nb0);
+    const int nrows = cb * s;
+
+    // ---- A: scores q . S_j for every row of the pass; each thread issues
+    // the loads of kRB rows before it reduces any of them
+    for (int rho0 = slot; rho0 < nrows; rho0 += kRB * nslot) {
+      float x[kRB][VEC], rs[kRB];
+#pragma unroll
+      for (int u = 0; u < kRB; ++u) {
+        const int rho = rho0 + u * nslot;
+        const bool ok = rho < nrows;
+        const int nl = ok ? rho / s : 0, j = ok ? rho - nl * s : 0;
+        rs[u] = load_row<TS, KIND, VEC>(p.krows, p.kscales, p.kanch, p.kcap, bh, nb0 + nl, j, s,
+                                        r, p.D, d0, dact && ok, x[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kRB; ++u) {
+        const int rho = rho0 + u * nslot;
+        float pd[GM];
+#pragma unroll
+        for (int g = 0; g < GM; ++g) {
+          float a = 0.f;
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) a = __builtin_fmaf(qv[g][v], x[u][v], a);
+          pd[g] = row_sum(a, lpr);
+        }
+        if (lir == 0 && rho < nrows) {
+          const int nl = rho / s, so = nl * bst + (rho - nl * s) * GM;
+#pragma unroll
+          for (int g = 0; g < GM; ++g) sw[so + g] = pd[g] * rs[u];
+        }
       }
     }
     __syncthreads();
 
+    // the first batch of V rows is requested now, so that its loads are in
+    // flight while phase B works on the scores
+    float xv[kRB][VEC];
+    load_v_batch(slot, nrows, nb0, xv);
+
     // ---- B: logits, running max, weights (in place of the scores)
     const int npairs = cb * GM;
-    const int gsel = tid % GM;  // every pair this thread handles has this head
+    // png with r <= 16: one 16-lane row per (block, head) pair, lane t =
+    // token t (prefix sums for the logits, suffix sums for the weights);
+    // otherwise one thread per pair.  Either way every pair a thread
+    // handles has head gsel.
+    const bool rows16 = KIND == FC_STORE_PNG && r <= 16;
+    const int gsel = rows16 ? (tid >> 4) % GM : tid % GM;
+    const int l16 = tid & 15;
     float pmax[GM];
 #pragma unroll
     for (int g = 0; g < GM; ++g) pmax[g] = -INFINITY;
-    for (int u = tid; u < npairs; u += kAttnThreads) {
-      const float mx = pair_max<KIND, SREG>(sw + (u / GM) * s * GM + gsel, GM, p.A, r, s,
-                                            p.scale_log2);
+    if (rows16) {
+      for (int u = tid >> 4; u - (tid >> 4) < npairs; u += kAttnThreads / 16) {
+        const bool ok = u < npairs && l16 < r;  // uniform loop bound over the row
+        const float sc = ok ? sw[(u / GM) * bst + l16 * GM + gsel] : 0.f;
+        // the row operations run in all 16 lanes (their DPP sources must be active)
+        const float pre = row16_prefix(sc);
+        const float mx = row16_max(ok ? pre * p.scale_log2 : -INFINITY);
 #pragma unroll
-      for (int g = 0; g < GM; ++g)
-        if (g == gsel) pmax[g] = fmaxf(pmax[g], mx);
+        for (int g = 0; g < GM; ++g)
+          if (g == gsel) pmax[g] = fmaxf(pmax[g], mx);
+      }
+    } else {
+      for (int u = tid; u < npairs; u += kAttnThreads) {
+        const float mx = pair_max<KIND, SREG>(sw + (u / GM) * bst + gsel, GM, p.A, r, s,
+                                              p.scale_log2);
+#pragma unroll
+        for (int g = 0; g < GM; ++g)
+          if (g == gsel) pmax[g] = fmaxf(pmax[g], mx);
+      }
     }
     wg_reduce<GM>(pmax, red, true);
     float alpha[GM];
@@ -348,15 +645,32 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs p) {
     float psum[GM];
 #pragma unroll
     for (int g = 0; g < GM; ++g) psum[g] = 0.f;
-    for (int u = tid; u < npairs; u += kAttnThreads) {
-      const int nl = u / GM;
-      const float* vsc = KIND == FC_STORE_JPEG_I8 ? p.vscales + (bh * p.vcap + nb0 + nl) * s
-                                                  : nullptr;
-      const float es = pair_weights<KIND, SREG>(sw + nl * s * GM + gsel, wts + nl * s * GM + gsel,
-                                                GM, p.A, r, s, p.scale_log2, mg, vsc);
+    if (rows16) {
+      float es = 0.f;
+      for (int u = tid >> 4; u - (tid >> 4) < npairs; u += kAttnThreads / 16) {
+        const bool ok = u < npairs && l16 < r;
+        float* const at = sw + (u / GM) * bst + l16 * GM + gsel;
+        const float sc = ok ? *at : 0.f;
+        const float lg = row16_prefix(sc) * p.scale_log2;
+        const float e = ok ? __builtin_amdgcn_exp2f(lg - mg) : 0.f;
+        es += e;
+        const float w = row16_suffix(e);  // w_j = sum_{t >= j} e_t
+        if (ok) *at = w;
+      }
 #pragma unroll
       for (int g = 0; g < GM; ++g)
-        if (g == gsel) psum[g] += es;
+        if (g == gsel) psum[g] = es;
+    } else {
+      for (int u = tid; u < npairs; u += kAttnThreads) {
+        const int nl = u / GM;
+        const float* vsc = KIND == FC_STORE_JPEG_I8 ? p.vscales + (bh * p.vcap + nb0 + nl) * s
+                                                    : nullptr;
+        const float es = pair_weights<KIND, SREG>(sw + nl * bst + gsel, wts + nl * bst + gsel,
+                                                  GM, p.A, r, s, p.scale_log2, mg, vsc);
+#pragma unroll
+        for (int g = 0; g < GM; ++g)
+          if (g == gsel) psum[g] += es;
+      }
     }
     wg_reduce<GM>(psum, red, false);
 #pragma unroll
@@ -367,63 +681,100 @@ __global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(AttnArgs p) {
     }
     // (wg_reduce ended with a barrier, so the weights are visible)
 
-    // ---- C: values
-    for (int rho = slot; rho < nrows; rho += nslot) {
-      const int nl = rho / s, j = rho - nl * s;
-      float x[VEC];
-      load_row<TS, KIND, VEC>(p.vrows, nullptr, p.vanch, p.vcap, bh, nb0 + nl, j, s, r, p.D,
-                              d0, dact, x);
+    // ---- C: values, kRB rows of loads in flight per thread (xv holds the
+    // batch at rho0; the next batch is requested once it is consumed)
+    for (int rho0 = slot; rho0 < nrows; rho0 += kRB * nslot) {
 #pragma unroll
-      for (int g = 0; g < GM; ++g) {
-        const float w = wts[rho * GM + g];
+      for (int u = 0; u < kRB; ++u) {
+        const int rho = rho0 + u * nslot;
+        if (rho >= nrows) break;  // uniform over the lanes of a row
+        const int nl = rho / s, so = nl * bst + (rho - nl * s) * GM;
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[g][v] = __builtin_fmaf(w, x[v], acc[g][v]);
+        for (int g = 0; g < GM; ++g) {
+          const float w = wts[so + g];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[g][v] = __builtin_fmaf(w, xv[u][v], acc[g][v]);
+        }
       }
+      if (rho0 + kRB * nslot < nrows) load_v_batch(rho0 + kRB * nslot, nrows, nb0, xv);
     }
     __syncthreads();
   }
 
-  // ---- combine the row slots: lanes of a wavefront with equal `lir`, then
-  // the wavefronts through LDS (reusing sw), one head at a time.
+  // ---- combine the row slots: lanes of a wavefront with equal `lir` (all
+  // GM * VEC exchanges of one distance in flight together), then the
+  // wavefronts through LDS (reusing sw) over the flattened (head, feature)
+  // range, in as few chunks as the LDS region allows (one at GM * D <= 768).
+  for (int m = lpr; m < 64; m <<= 1) {
 #pragma unroll
-  for (int g = 0; g < GM; ++g)
+    for (int g = 0; g < GM; ++g)
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      float x = acc[g][v];
-      for (int m = lpr; m < 64; m <<= 1) x += __shfl_xor(x, m, 64);
-      acc[g][v] = x;
-    }
+      for (int v = 0; v < VEC; ++v) acc[g][v] += __shfl_xor(acc[g][v], m, 64);
+  }
   const int lane = tid & 63, wave = tid >> 6;
-  const int nwave = kAttnThreads / 64;
+  constexpr int nwave = kAttnThreads / 64;
+  constexpr int kChunk = kRegion * kSwRegions / nwave;
+  const int64_t ng = min((int64_t)GM, p.G - g0);  // heads of this group
+  const int64_t total = ng * p.D;
+  const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;
+  // with the fused merge the partials are stored at device scope (read back
+  // by another workgroup of this kernel)
+  const bool fused = p.arrive != nullptr;
+  auto publish = [&](float* at, float v) {
+    if (fused)
+      __hip_atomic_store(at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      *at = v;
+  };
+  for (int64_t c = 0; c < total; c += kChunk) {
+    const int64_t span = min((int64_t)kChunk, total - c);
+    if (c > 0) __syncthreads();  // the previous chunk's sums are read
+    if (lane < lpr && dact) {
 #pragma unroll
-  for (int g = 0; g < GM; ++g) {
-    if (g0 + g >= p.G) break;  // uniform
-    for (int64_t c = 0; c < p.D; c += kPassRows * GM / nwave) {
-      const int64_t span = min((int64_t)(kPassRows * GM / nwave), p.D - c);
-      // wavefront `wave` writes features [c, c+span) it owns
-      if (lane < lpr && dact) {
+      for (int g = 0; g < GM; ++g)
 #pragma unroll
         for (int v = 0; v < VEC; ++v) {
-          const int64_t d = d0 + v - c;
-          if (d >= 0 && d < span) sw[wave * span + d] = acc[g][v];
+          const int64_t i = g * p.D + d0 + v - c;
+          if (g < ng && i >= 0 && i < span) sw[wave * span + i] = acc[g][v];
         }
-      }
-      __syncthreads();
-      const int64_t bq = b * (p.Hkv * p.G) + hkv * p.G + g0 + g;
-      const int64_t slot_out = bq * p.n_splits + split;
-      for (int64_t d = tid; d < span; d += kAttnThreads) {
-        float x = 0.f;
-        for (int w = 0; w < nwave; ++w) x += sw[w * span + d];
-        p.pacc[slot_out * p.D + c + d] = x;
-      }
-      __syncthreads();
     }
-    if (tid == 0) {
-      const int64_t bq = b * (p.Hkv * p.G) + hkv * p.G + g0 + g;
-      p.pm[bq * p.n_splits + split] = m_run[g];
-      p.pl[bq * p.n_splits + split] = l_run[g];
+    __syncthreads();
+    for (int64_t i = tid; i < span; i += kAttnThreads) {
+      float x = 0.f;
+#pragma unroll
+      for (int w = 0; w < nwave; ++w) x += sw[w * span + i];
+      const int64_t g = (c + i) / p.D, d = (c + i) - g * p.D;
+      publish(p.pacc + ((bq0 + g) * p.n_splits + split) * p.D + d, x);
     }
   }
+  if (tid < ng) {
+#pragma unroll
+    for (int g = 0; g < GM; ++g)
+      if (g == tid) {
+        publish(p.pm + (bq0 + g) * p.n_splits + split, m_run[g]);
+        publish(p.pl + (bq0 + g) * p.n_splits + split, l_run[g]);
+      }
+  }
+  if (!fused) return;
+
+  // ---- arrival: every thread's stores are complete before the workgroup
+  // counts itself, so the workgroup that counts last finds every partial of
+  // its group published; it returns the word to zero and merges.
+  __shared__ int s_last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (tid == 0) {
+    unsigned int* word = p.arrive + ((int64_t)blockIdx.y * gridDim.z + blockIdx.z) * p.cstride;
+    const unsigned int old = atomicAdd(word, 1u);
+    const bool last = old + 1 == (unsigned int)p.n_splits;
+    if (last) __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  merge_group<GM>(p, b, hkv, g0, (int)ng, tid, sw);
 }
 
 struct MergeArgs {
@@ -884,7 +1235,27 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
     a.pl = pl;
     a.pacc = pacc;
     if ((a.blocks_per_split * (n_splits - 1)) >= nb) return FC_ERR_ARG;  // empty split
-    const dim3 grid((unsigned)n_splits, (unsigned)(B * Hkv), (unsigned)((G + gm - 1) / gm));
+    // the merge runs inside the split pass when every group has a counter
+    const int64_t zg = (G + gm - 1) / gm;
+    const bool fuse = (parts & kPartMerge) && B * Hkv * zg * kCounterStride <= kCounterWords;
+    if (fuse) {
+      a.arrive = counters;
+      a.cstride = kCounterStride;
+      a.kraw = key->raw;
+      a.vraw = value->raw;
+      a.raw_dtype = stream_dtype;
+      a.kr_sb = key->raw_sb;
+      a.kr_sh = key->raw_sh;
+      a.kr_st = key->raw_st;
+      a.vr_sb = value->raw_sb;
+      a.vr_sh = value->raw_sh;
+      a.vr_st = value->raw_st;
+      a.n_raw = n_raw;
+      a.out = out;
+      a.o_sb = o_sb;
+      a.o_sh = o_sh;
+    }
+    const dim3 grid((unsigned)n_splits, (unsigned)(B * Hkv), (unsigned)zg);
     const bool sreg = s <= 8;
     auto go = [&](auto ts, auto kc, auto sc) {
       using TS = decltype(ts);
@@ -921,7 +1292,7 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
     }
     if (rc != FC_OK) return rc;
     rc = check_launch();
-    if (rc != FC_OK) return rc;
+    if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0) {
     // merge only: the split geometry must still be consistent
     if (D % 8) return FC_ERR_UNSUPPORTED;

@@ -10,6 +10,18 @@
 
 namespace fc {
 
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor: 32-bit data format
+constexpr int kCachePolicySc1 = 16;    // buffer load cache policy: device scope (sc1)
+constexpr int kWaitVmcnt0 = 0x0F70;    // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
+
+// buffer descriptor over `bytes` bytes at `base`: loads at offsets past the
+// end return zero
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kBufWord3);
+}
+
 int check_launch();
 int esize_of(int dt);
 

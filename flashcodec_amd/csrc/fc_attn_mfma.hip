@@ -48,7 +48,6 @@ namespace fc {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
@@ -99,10 +98,7 @@ constexpr int kSPad = kPassRowsW + 4;  // float stride of a score row in LDS
 constexpr int kWPad = kPassRowsW + 8;  // half stride of a weight row in LDS
 constexpr float kLazyMax = 8.f;        // exponentials may reach 2^8 before a rescale
 constexpr int kTapsUnrolled = 16;      // softmax taps unrolled (block sizes up to 16)
-constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor: 32-bit data format
-constexpr int kCachePolicySc1 = 16;    // buffer load cache policy: device scope (sc1)
 constexpr int kCachePolicyNt = 2;      // buffer load cache policy: nontemporal (streaming)
-constexpr int kWaitVmcnt0 = 0x0F70;    // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15)
 constexpr int kPubWord = 1;            // publication counter: word 1 of a group's arrival line
 constexpr int kSpinCap = 1 << 24;      // polls of the publication counter before giving up
 
@@ -122,11 +118,6 @@ __device__ __forceinline__ int pow2_exp_for(float x, int target) {
   return e - target;
 }
 
-// buffer descriptor over `bytes` bytes at `base`: loads at offsets past the
-// end return zero (rows past the end of a pass read as code 0 / scale 0)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, kBufWord3);
-}
 
 // Element load / store with the dtype fixed at compile time (T = f16_t,
 // bf16_t) or read at run time (T = void).

@@ -334,3 +334,51 @@ def test_fused_decode_step_matches_append_then_attend(cfg, dt):
             ref0 = torch.softmax((q.float() @ k.float().transpose(-1, -2).repeat_interleave(
                 G, dim=1)) * D ** -0.5, dim=-1) @ v.float().repeat_interleave(G, dim=1)
             assert_close(to_values(out0), ref0.cpu().numpy(), dt)
+
+
+@pytest.mark.parametrize("name,cfg,dt,B,Hk,G,S,D", [
+    ("jpeg-i8-f16", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16", 2, 2, 4, 8 * 300 + 5, 128),
+    ("png-f32-r16", dict(mode="png", block_size=16, keep_ratio=0.25), "f32", 2, 2, 4, 16 * 90 + 13, 128),
+    ("jpeg-fp-bf16", dict(mode="jpeg", block_size=8, keep_freqs=2), "bf16", 1, 2, 8, 8 * 70 + 7, 64),
+    ("png-f16-g3", dict(mode="png", block_size=8, keep_ratio=1.0), "f16", 1, 3, 3, 8 * 40 + 1, 64),
+], ids=lambda x: x if isinstance(x, str) else None)
+def test_split_then_merge_entry_points(name, cfg, dt, B, Hk, G, S, D, oracle):
+    """fc_decode_attention_split followed by fc_decode_attention_merge (the
+    partials with the raw tail merged by the separate pass) gives the same
+    attention as fc_decode_attention (merge fused into the split pass, the
+    tail folded into split 0)."""
+    from flashcodec_amd import _native as N
+    from flashcodec_amd.attention import _device_A, _view, workspace
+    print(f"case split+merge {name}", flush=True)
+    ks, vs = build_streams(cfg, dt, B, Hk, S, D, seed_of("split-merge", name), oracle)
+    assert ks._n_raw > 0
+    rng = np.random.default_rng(seed_of("split-merge-q", name))
+    q = torch.from_numpy((rng.standard_normal((B, Hk * G, 1, D)) / math.sqrt(D))
+                         .astype(np.float32)).to(torch_dtype(dt)).to(DEV)
+    fused = fc.codec_decode_attention(q, ks, vs)
+    c, r, nb = ks.codec, ks.block_size, ks.n_blocks
+    if c.name == "jpeg":
+        kind = N.STORE_JPEG_I8 if c.quantized else N.STORE_JPEG_FP
+        s = c.keep_freqs
+    else:
+        kind, s = N.STORE_PNG, r
+    L = N.lib()
+    dev = q.device
+    ns = L.fc_attention_splits(kind, N.dtype_code(ks.dtype), N.dtype_code(q.dtype), s, nb, B, Hk,
+                               G, D, N.num_cus(dev))
+    ws = workspace(dev, L.fc_attention_workspace_bytes(B, Hk * G, D, ns))
+    A = _device_A(c, r, dev)
+    keep = []
+    kv, vv = _view(ks, keep), _view(vs, keep)
+    out = torch.empty_like(q)
+    args = (q.data_ptr(), N.dtype_code(q.dtype), q.stride(0), q.stride(1), B, Hk * G, Hk, D, kind,
+            N.dtype_code(ks.dtype), r, s, nb, kv, vv, ks._n_raw, N.ptr(A), D ** -0.5,
+            out.data_ptr(), out.stride(0), out.stride(1), N.ptr(ws), ns, N.stream_ptr(dev))
+    N.check(L.fc_decode_attention_split(*args), "fc_decode_attention_split")
+    N.check(L.fc_decode_attention_merge(*args), "fc_decode_attention_merge")
+    ref = oracle_out(oracle, q, ks, vs, D ** -0.5)
+    assert_close(to_values(out)[:, :, 0], ref, dt)
+    assert_close(to_values(fused)[:, :, 0], ref, dt)
+    # the workspace counters are back at zero: a second fused call agrees
+    again = fc.codec_decode_attention(q, ks, vs)
+    assert_close(to_values(again)[:, :, 0], ref, dt)
