@@ -322,7 +322,13 @@ def c5_mode(args):
         g = torch.Generator().manual_seed(1)
         ids = torch.randint(1, cfg.vocab_size, (batch, prompt), generator=g).to(dev)
         with torch.no_grad():
+            # memory as flashcodec benchmarks/bench_e2e.py:68-80 reports it:
+            # peak = most allocated during the run, steady = still allocated
+            # after it (the cache), both above what was allocated before
             torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            torch.cuda.reset_peak_memory_stats()
+            base = torch.cuda.memory_allocated()
             t0 = time.perf_counter()
             out = model(input_ids=ids, use_cache=True, logits_to_keep=1)
             pkv = out.past_key_values
@@ -335,10 +341,14 @@ def c5_mode(args):
                 nxt = out.logits[:, -1].argmax(-1, keepdim=True)
             torch.cuda.synchronize()
             t2 = time.perf_counter()
+            del out
+            mem = {"peak_MB": round((torch.cuda.max_memory_allocated() - base) / 1e6, 1),
+                   "steady_MB": round((torch.cuda.memory_allocated() - base) / 1e6, 1)}
+            del pkv, nxt
         if steps == 0:
-            return {"prefill_s": round(t1 - t0, 4)}
+            return {"prefill_s": round(t1 - t0, 4), **mem}
         return {"prefill_s": round(t1 - t0, 4), "decode_ms_per_step": round((t2 - t1) / steps * 1e3, 3),
-                "decode_tokens_per_s": round(batch * steps / (t2 - t1), 1)}
+                "decode_tokens_per_s": round(batch * steps / (t2 - t1), 1), **mem}
 
     def run_graph(batch, prompt, steps, warmup=2):
         """Prefill eagerly, then `steps` greedy decode steps of which the

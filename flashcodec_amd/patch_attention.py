@@ -15,6 +15,13 @@ RoPE function in the model's module, and either batch 1 or no attention mask
 (transformers passes no mask to SDPA-style attention when nothing is padded,
 so unpadded batched decoding takes the codec path too; the reference stops
 at batch 1, patch_attention.py:52).
+
+Prefill (several query tokens) runs the original forward, which attends on
+the reconstructed view the cache returns; on a codec layer that decode steps
+can serve from the archive the view is released as soon as that forward
+returns, so a prefill holds one layer's view at a time instead of every
+layer's until the first decode step (the reference drops each view on the
+layer's first decode step, patch_attention.py:90-94).
 """
 
 import importlib
@@ -46,19 +53,32 @@ def _codec_layer(module, past_key_values):
     return layer if isinstance(layer, FlashCodecLayer) else None
 
 
+def _release_view(layer):
+    """Drop a codec layer's reconstructed view (the streams' _rec and the
+    layer's references to it); the archives and tails stay."""
+    for st in (layer._key_stream, layer._value_stream):
+        if st._rec is not None:
+            st.discard_view()
+    layer.keys = layer.values = None
+
+
 def _attention_forward(module, orig, hidden_states, position_embeddings=None,
                        attention_mask=None, past_key_values=None, **kwargs):
     layer = _codec_layer(module, past_key_values)
-    usable = (layer is not None
-              and not module.training
+    codec_ok = (layer is not None
+                and not module.training
+                and position_embeddings is not None
+                and getattr(module, "sliding_window", None) is None
+                and _rope_fn(module) is not None)
+    usable = (codec_ok
               and hidden_states.shape[-2] == 1
-              and (hidden_states.shape[0] == 1 or attention_mask is None)
-              and position_embeddings is not None
-              and getattr(module, "sliding_window", None) is None
-              and _rope_fn(module) is not None)
+              and (hidden_states.shape[0] == 1 or attention_mask is None))
     if not usable:
-        return orig(hidden_states, position_embeddings=position_embeddings,
-                    attention_mask=attention_mask, past_key_values=past_key_values, **kwargs)
+        out = orig(hidden_states, position_embeddings=position_embeddings,
+                   attention_mask=attention_mask, past_key_values=past_key_values, **kwargs)
+        if codec_ok and hidden_states.shape[-2] > 1 and layer.is_initialized:
+            _release_view(layer)  # prefill done: decode attends on the archive
+        return out
 
     lead = hidden_states.shape[:-1]
     hd = module.head_dim
@@ -85,10 +105,7 @@ def _attention_forward(module, orig, hidden_states, position_embeddings=None,
     if not layer.is_initialized:
         layer.lazy_initialization(k, v)
     # the prefill view is dead weight once decoding attends on the archive
-    for st in (layer._key_stream, layer._value_stream):
-        if st._rec is not None:
-            st.discard_view()
-    layer.keys = layer.values = None
+    _release_view(layer)
     # append both tokens and attend in one library call (two appends and an
     # attention call in the reference, patch_attention.py:95-98)
     out = codec_decode_step(q, k, v, layer._key_stream, layer._value_stream,
