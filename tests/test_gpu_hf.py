@@ -195,3 +195,27 @@ def test_batched_materialization_free_decoding_qwen3():
             break
         n_same += 1
     assert n_same >= 4
+
+
+def test_prefill_view_released_per_layer():
+    """With the attention patch a prefill forward leaves no reconstructed
+    view behind on any codec layer (each is released when its layer's
+    forward returns), and the next decode step still matches the unpatched
+    materialised codec path."""
+    ids = torch.randint(1, VOCAB, (2, 37), generator=torch.Generator().manual_seed(5)).to(DEV)
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+    mat, mf = tiny_qwen3(), tiny_qwen3()
+    fc.apply_flash_codec(mat, **cfg)
+    fc.apply_flash_codec(mf, materialization_free=True, **cfg)
+    with torch.no_grad():
+        out_m = mat(input_ids=ids, use_cache=True)
+        out_f = mf(input_ids=ids, use_cache=True)
+        assert torch.equal(out_m.logits, out_f.logits)  # prefill is the same computation
+        for layer in out_f.past_key_values.layers:
+            assert layer._key_stream._rec is None and layer._value_stream._rec is None
+            assert layer.keys is None and layer.values is None
+        nxt = out_m.logits[:, -1:].argmax(-1)
+        step_m = mat(input_ids=nxt, past_key_values=out_m.past_key_values, use_cache=True)
+        step_f = mf(input_ids=nxt, past_key_values=out_f.past_key_values, use_cache=True)
+    a, b = step_m.logits.float(), step_f.logits.float()
+    assert (a - b).abs().max().item() <= 3e-2 * a.abs().max().item()
