@@ -208,9 +208,11 @@ int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s,
  * scale * q . (A S)[p]; softmax in fp32; output (p A) S + p_raw V_raw.
  * Every query head reads its kv head's rows once per group of up to 16
  * query heads.  `workspace` must hold fc_attention_workspace_bytes(...) and
- * follow its zero-fill rule.  int8 jpeg archives with fp16/bf16 queries and
- * D in {64, 128, 256} run as one launch (the split pass merges its own
- * partials); other cases launch the split and merge passes.
+ * follow its zero-fill rule.  With archived blocks the call is normally
+ * one launch: the split pass's last workgroup per (batch, kv head, head
+ * group) merges the partials and the raw tail into `out`.  Shapes beyond
+ * the workspace's counters or the fused merge's split limit run the merge
+ * pass as a second launch; a tail-only call (nb == 0) is one merge launch.
  *
  * Replaces codec_decode_attention's jpeg Triton path and its png / torch
  * path (flashcodec/attention.py:64-140;
