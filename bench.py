@@ -94,6 +94,18 @@ def split_kernel_name():
     return "attn_split_i8_mfma<4,4,4> (merge fused)"
 
 
+def cpu_rate(fn, nbytes, min_seconds=1.0):
+    """GB/s of `fn` (a CPU oracle call over `nbytes` algorithmic bytes),
+    repeated until min_seconds have passed (one host thread)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            return round(nbytes * n / dt / 1e9, 3)
+
+
 def timed(fn, steps, warmup):
     """Average ms of fn() over `steps` calls between events on the current
     stream, after `warmup` calls."""
@@ -159,6 +171,19 @@ def c2_mode(args):
     t_tok = (time.perf_counter() - t0) / n_tok
     same = bool(torch.equal(st._coeffs[:, :, :n_tok // r], coeffs[:, :, :n_tok // r]) and
                 torch.equal(st._scales[:, :, :n_tok // r], scales[:, :, :n_tok // r]))
+
+    # the CPU oracle (the reference's algorithm restated in C++) on the whole
+    # workload, one host thread
+    from oracle import oracle as O
+    basis = fc.dct_basis(r, k).numpy()
+    xs = x.float().cpu().numpy()
+    _, cs, ss = O.jpeg_encode(xs, r, k, basis, "f16", quant=True)
+    alg_s = alg
+    cpu = {"unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": "the whole workload (128 sequences of 8192 tokens), C++ oracle",
+           "archive": cpu_rate(lambda: O.jpeg_encode(xs, r, k, basis, "f16", quant=True), alg_s),
+           "read": cpu_rate(lambda: O.jpeg_decode(None, r, basis, "f16", codes=cs, scales=ss),
+                            alg_s)}
     print(json.dumps({
         "metric": "jpeg int8 archive / read GB/s (C2)", "unit": "GB/s", "n_gpus": 1,
         "archive_GBs": round(alg / (t_arch * 1e-3) / 1e9, 1),
@@ -170,6 +195,7 @@ def c2_mode(args):
         "append_us_per_token": round(t_tok * 1e6, 2),
         "append_launches_per_token": "1 tail-row copy per token + 1 archive launch per 8 tokens",
         "token_by_token_codes_equal_bulk": same,
+        "cpu_baseline": cpu,
         "config": {"workload": "C2 jpeg int8 archive + read", "B": b_, "H": h_, "S": s_, "D": d_,
                    "block": r, "keep_freqs": k, "dtype": "fp16"},
         "data": "synthetic AR(1) rho=0.95, per-channel scale log-uniform [0.1, 10]"}))
@@ -233,6 +259,29 @@ def c4_mode(args):
             p_ = torch.softmax((q @ kk.transpose(-1, -2).contiguous()) * d_ ** -0.5, dim=-1)
             ref = p_ @ vv
             res[tag]["vs_dense_max_abs_err"] = float((o - ref).abs().max())
+        # the CPU oracle on the whole stream (one host thread); attention on
+        # one of the 16 (batch, kv head) sequences
+        from oracle import oracle as O
+        xs = x["k"].cpu().numpy()
+        dl, an = O.png_encode(xs, r, keep)
+        alg_s = alg_codec
+        cpu = {"unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": "archive / read: the whole stream; attention: 1 of the 16 (batch, kv "
+                         "head) sequences (16384 tokens, 4 query heads); C++ oracle",
+               "archive": cpu_rate(lambda: O.png_encode(xs, r, keep), alg_s),
+               "read": cpu_rate(lambda: O.png_decode(dl, an, "f32"), alg_s)}
+        if keep == 1.0:
+            # fp64 decode attention of the sample's 4 query heads over its
+            # stored rows (png rows -> fp64 as the oracle defines them)
+            rk = O.stored_rows_png(ks._deltas[:1, :1, :nb].cpu().numpy(),
+                                   ks._anchors[:1, :1, :nb].cpu().numpy())
+            rv = O.stored_rows_png(vs._deltas[:1, :1, :nb].cpu().numpy(),
+                                   vs._anchors[:1, :1, :nb].cpu().numpy())
+            qs = q[:1, :hq // h_, 0].cpu().numpy()
+            A = O.synthesis_matrix("png", r)
+            cpu["attention"] = cpu_rate(
+                lambda: O.attention(qs, rk, rv, None, None, A, d_ ** -0.5), alg_attn // (b_ * h_))
+        res[tag]["cpu_baseline"] = cpu
         log(f"bench c4 keep {keep}: {res[tag]}")
     print(json.dumps(res))
 
@@ -261,6 +310,11 @@ def c1_mode(args):
     xn = x.cpu().numpy()
     coef = O.jpeg_encode(xn, r, k, basis, "f32")
     ref = O.jpeg_decode(coef, r, basis, "f32")
+    cpu = {"unit": "GB/s", "cores": 1, "kind": "port", "sample": "the whole C1 stream, C++ oracle",
+           "archive": cpu_rate(lambda: O.jpeg_encode(xn, r, k, basis, "f32"),
+                               b_ * h_ * s_ * d_ * 4 + b_ * h_ * (s_ // r) * k * d_ * 4),
+           "read": cpu_rate(lambda: O.jpeg_decode(coef, r, basis, "f32"),
+                            b_ * h_ * s_ * d_ * 4 + b_ * h_ * (s_ // r) * k * d_ * 4)}
     bit_exact = bool(np.array_equal(rec.cpu().numpy().view(np.uint32), np.asarray(ref, np.float32).view(np.uint32)))
     alg = b_ * h_ * s_ * d_ * 4 + b_ * h_ * (s_ // r) * k * d_ * 4
     t_arch = timed(lambda: _CodecStream(st.codec).append(x), args.steps, args.warmup)
@@ -269,6 +323,7 @@ def c1_mode(args):
                       "bit_exact_vs_oracle": bit_exact,
                       "archive_us": round(t_arch * 1e3, 2),
                       "archive_GBs": round(alg / (t_arch * 1e-3) / 1e9, 1),
+                      "cpu_baseline": cpu,
                       "config": {"workload": "C1 jpeg round trip", "B": b_, "H": h_, "S": s_, "D": d_,
                                  "block": r, "keep_freqs": k, "dtype": "fp32"},
                       "data": "synthetic AR(1) rho=0.97, unit variance"}))
