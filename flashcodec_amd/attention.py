@@ -279,9 +279,10 @@ def _decode_step_device_state(query, key_tokens, value_tokens, ks, vs, scale, st
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     a.stream = N.stream_ptr(dev)
     for sv, st, tok in ((a.key, ks, key_tokens), (a.value, vs, value_tokens)):
-        sv.rows = st._coeffs.data_ptr()
-        sv.scales = st._scales.data_ptr()
-        sv.anchors = None
+        rows, extra = st._archive_tensors()[0], st._archive_tensors()[1:]
+        sv.rows = rows.data_ptr()
+        sv.scales = extra[0].data_ptr() if (st.codec.name == "jpeg" and extra) else None
+        sv.anchors = extra[0].data_ptr() if st.codec.name == "png" else None
         sv.cap = st._capacity
         sv.tail = st._raw_buf.data_ptr()
         sv.token, sv.tok_sb, sv.tok_sh = tok.data_ptr(), tok.stride(0), tok.stride(1)

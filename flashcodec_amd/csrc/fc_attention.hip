@@ -84,6 +84,9 @@ struct AttnArgs {
   int64_t n_raw;
   void* out;
   int64_t o_sb, o_sh;
+  // device (n_blocks, n_tail) before a decode step's token, or NULL: the
+  // kernel then takes nb, the tail length and the split ranges from it
+  const int64_t* state;
 };
 
 // v + (v from the lane selected by a DPP pattern); patterns stay inside a
@@ -457,10 +460,21 @@ void attn_split_kernel(AttnArgs p) {
     l_run[g] = 0.f;
   }
 
+  // block and tail counts: the arguments, or the decode-step state on the
+  // device (tail after the step's token: t = n_tail + 1 tokens, archived as
+  // block n_blocks when t == r; clamped to the archive capacity)
+  int64_t nb = p.nb, n_raw = p.n_raw, bps = p.blocks_per_split;
+  if (p.state) {
+    const int64_t t = min(max(p.state[1], (int64_t)0), (int64_t)(r - 1)) + 1;
+    nb = min(max(p.state[0], (int64_t)0) + (t == r ? 1 : 0), min(p.kcap, p.vcap));
+    n_raw = t == r ? 0 : t;
+    bps = (nb + p.n_splits - 1) / p.n_splits;  // trailing splits may be empty
+  }
+
   // ---- raw tail (fused merge only): split 0 starts its partial with the
-  // n_raw < FC_MAX_BLOCK tail tokens at full precision
-  if (split == 0 && p.n_raw > 0) {
-    const int nt = (int)p.n_raw;
+  // n_raw <= FC_MAX_BLOCK tail tokens at full precision
+  if (split == 0 && n_raw > 0) {
+    const int nt = (int)n_raw;
     const int lane = tid & 63;
     float* const tsc = sw;            // [nt][GM] base-2 logits
     float* const tex = sw + 64 * GM;  // [nt][GM] exponentials
@@ -543,8 +557,8 @@ void attn_split_kernel(AttnArgs p) {
     __syncthreads();  // sw is reused by the passes
   }
 
-  const int64_t nb_begin = (int64_t)split * p.blocks_per_split;
-  const int64_t nb_end = min(p.nb, nb_begin + p.blocks_per_split);
+  const int64_t nb_begin = (int64_t)split * bps;
+  const int64_t nb_end = min(nb, nb_begin + bps);
   const int cb_max = max(1, kPassRows / s);
   const int bst = (s | 1) * GM;
   // V rows rho0, rho0 + nslot, ... (kRB of them) of the pass at block nb0
@@ -1142,6 +1156,120 @@ int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, in
 
 namespace fc {
 
+// Groups of the vector-ALU pass: (batch, kv head, group of <= 8 query heads).
+static int64_t valu_groups(int64_t B, int64_t Hkv, int64_t G) {
+  const int gm = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
+  return B * Hkv * ((G + gm - 1) / gm);
+}
+
+// Whether the workspace holds a merge counter for every group.
+static bool valu_fusable(int64_t B, int64_t Hkv, int64_t G) {
+  return valu_groups(B, Hkv, G) * kCounterStride <= kCounterWords;
+}
+
+// Enqueues the vector-ALU split pass (VEC = 8 features per lane, LPR =
+// lanes per row).  counters != NULL: the merge is fused (split 0 folds the
+// n_raw tail tokens in, the last workgroup per group writes `out`).
+// state != NULL (fused only): the block and tail counts come from the
+// device pair (n_blocks, n_tail) before the step's token, nb sizing nothing
+// but the caller's split count.
+static int launch_split_valu(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
+                             int64_t Hkv, int64_t G, int64_t D, int store_kind, int stream_dtype,
+                             int r, int s, int64_t nb, const fc_stream_view* key,
+                             const fc_stream_view* value, int64_t n_raw, const float* A,
+                             float scale_log2, void* out, int64_t o_sb, int64_t o_sh, float* pm,
+                             float* pl, float* pacc, int n_splits, unsigned int* counters,
+                             const int64_t* state, hipStream_t st) {
+  if (D % 8) return FC_ERR_UNSUPPORTED;
+  const int64_t chunks = D / 8;
+  int lg = 0;
+  while ((int64_t(1) << lg) < chunks) ++lg;
+  const int gm = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
+  AttnArgs a{};
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.krows = key->rows;
+  a.kscales = key->scales;
+  a.kanch = key->anchors;
+  a.kcap = key->cap;
+  a.vrows = value->rows;
+  a.vscales = value->scales;
+  a.vanch = value->anchors;
+  a.vcap = value->cap;
+  a.A = A;
+  a.Hkv = Hkv;
+  a.G = G;
+  a.D = D;
+  a.nb = nb;
+  a.r = r;
+  a.s = s;
+  a.scale_log2 = scale_log2;
+  a.lpr_log2 = lg;
+  a.blocks_per_split = (nb + n_splits - 1) / n_splits;
+  a.n_splits = n_splits;
+  a.pm = pm;
+  a.pl = pl;
+  a.pacc = pacc;
+  a.state = state;
+  const int64_t zg = (G + gm - 1) / gm;
+  if (counters) {
+    a.arrive = counters;
+    a.cstride = kCounterStride;
+    a.kraw = key->raw;
+    a.vraw = value->raw;
+    a.raw_dtype = stream_dtype;
+    a.kr_sb = key->raw_sb;
+    a.kr_sh = key->raw_sh;
+    a.kr_st = key->raw_st;
+    a.vr_sb = value->raw_sb;
+    a.vr_sh = value->raw_sh;
+    a.vr_st = value->raw_st;
+    a.n_raw = n_raw;
+    a.out = out;
+    a.o_sb = o_sb;
+    a.o_sh = o_sh;
+  }
+  const dim3 grid((unsigned)n_splits, (unsigned)(B * Hkv), (unsigned)zg);
+  const bool sreg = s <= 8;
+  auto go = [&](auto ts, auto kc, auto sc) {
+    using TS = decltype(ts);
+    constexpr int KIND = decltype(kc)::value;
+    constexpr bool SREG = decltype(sc)::value;
+    return attn_with_int<1, 2, 4, 8>(gm, [&](auto gc) {
+      constexpr int GM = decltype(gc)::value;
+      attn_split_kernel<TS, KIND, SREG, 8, GM><<<grid, kAttnThreads, 0, st>>>(a);
+      return FC_OK;
+    });
+  };
+  using KI8 = std::integral_constant<int, FC_STORE_JPEG_I8>;
+  using KFP = std::integral_constant<int, FC_STORE_JPEG_FP>;
+  using KPNG = std::integral_constant<int, FC_STORE_PNG>;
+  using ST = std::true_type;
+  using SF = std::false_type;
+  int rc = FC_ERR_ARG;
+  if (store_kind == FC_STORE_JPEG_I8) {
+    // int8 rows do not depend on the stream dtype (the tail's dtype is read
+    // at run time)
+    rc = sreg ? go(float{}, KI8{}, ST{}) : go(float{}, KI8{}, SF{});
+  } else if (store_kind == FC_STORE_JPEG_FP || store_kind == FC_STORE_PNG) {
+    const bool png = store_kind == FC_STORE_PNG;
+    auto pick = [&](auto ts) {
+      if (png) return go(ts, KPNG{}, ST{});
+      return sreg ? go(ts, KFP{}, ST{}) : go(ts, KFP{}, SF{});
+    };
+    switch (stream_dtype) {
+      case FC_F32: rc = pick(float{}); break;
+      case FC_F16: rc = pick(f16_t{}); break;
+      case FC_BF16: rc = pick(bf16_t{}); break;
+      default: return FC_ERR_ARG;
+    }
+  }
+  if (rc != FC_OK) return rc;
+  return check_launch();
+}
+
 constexpr int kPartSplit = 1, kPartMerge = 2;
 
 // Validates the arguments and enqueues the requested parts: the split pass
@@ -1201,97 +1329,14 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
                                         kCounterWords, kCounterStride, fuse ? &fz : nullptr, st);
     if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit)) {
-    // VEC = 8 features per lane; LPR = lanes per row
-    if (D % 8) return FC_ERR_UNSUPPORTED;
-    const int64_t chunks = D / 8;
-    int lg = 0;
-    while ((int64_t(1) << lg) < chunks) ++lg;
-    const int gm = G >= 8 ? 8 : (G >= 4 ? 4 : (G >= 2 ? 2 : 1));
-    AttnArgs a{};
-    a.q = q;
-    a.q_dtype = q_dtype;
-    a.q_sb = q_sb;
-    a.q_sh = q_sh;
-    a.krows = key->rows;
-    a.kscales = key->scales;
-    a.kanch = key->anchors;
-    a.kcap = key->cap;
-    a.vrows = value->rows;
-    a.vscales = value->scales;
-    a.vanch = value->anchors;
-    a.vcap = value->cap;
-    a.A = A;
-    a.Hkv = Hkv;
-    a.G = G;
-    a.D = D;
-    a.nb = nb;
-    a.r = r;
-    a.s = s;
-    a.scale_log2 = scale_log2;
-    a.lpr_log2 = lg;
-    a.blocks_per_split = (nb + n_splits - 1) / n_splits;
-    a.n_splits = n_splits;
-    a.pm = pm;
-    a.pl = pl;
-    a.pacc = pacc;
-    if ((a.blocks_per_split * (n_splits - 1)) >= nb) return FC_ERR_ARG;  // empty split
     // the merge runs inside the split pass when every group has a counter
-    const int64_t zg = (G + gm - 1) / gm;
-    const bool fuse = (parts & kPartMerge) && B * Hkv * zg * kCounterStride <= kCounterWords;
-    if (fuse) {
-      a.arrive = counters;
-      a.cstride = kCounterStride;
-      a.kraw = key->raw;
-      a.vraw = value->raw;
-      a.raw_dtype = stream_dtype;
-      a.kr_sb = key->raw_sb;
-      a.kr_sh = key->raw_sh;
-      a.kr_st = key->raw_st;
-      a.vr_sb = value->raw_sb;
-      a.vr_sh = value->raw_sh;
-      a.vr_st = value->raw_st;
-      a.n_raw = n_raw;
-      a.out = out;
-      a.o_sb = o_sb;
-      a.o_sh = o_sh;
-    }
-    const dim3 grid((unsigned)n_splits, (unsigned)(B * Hkv), (unsigned)zg);
-    const bool sreg = s <= 8;
-    auto go = [&](auto ts, auto kc, auto sc) {
-      using TS = decltype(ts);
-      constexpr int KIND = decltype(kc)::value;
-      constexpr bool SREG = decltype(sc)::value;
-      return attn_with_int<1, 2, 4, 8>(gm, [&](auto gc) {
-        constexpr int GM = decltype(gc)::value;
-        attn_split_kernel<TS, KIND, SREG, 8, GM><<<grid, kAttnThreads, 0, st>>>(a);
-        return FC_OK;
-      });
-    };
-    using KI8 = std::integral_constant<int, FC_STORE_JPEG_I8>;
-    using KFP = std::integral_constant<int, FC_STORE_JPEG_FP>;
-    using KPNG = std::integral_constant<int, FC_STORE_PNG>;
-    using ST = std::true_type;
-    using SF = std::false_type;
-    int rc = FC_ERR_ARG;
-    if (store_kind == FC_STORE_JPEG_I8) {
-      // int8 rows do not depend on the stream dtype (the raw tail is merged
-      // separately)
-      rc = sreg ? go(float{}, KI8{}, ST{}) : go(float{}, KI8{}, SF{});
-    } else if (store_kind == FC_STORE_JPEG_FP || store_kind == FC_STORE_PNG) {
-      const bool png = store_kind == FC_STORE_PNG;
-      auto pick = [&](auto ts) {
-        if (png) return go(ts, KPNG{}, ST{});
-        return sreg ? go(ts, KFP{}, ST{}) : go(ts, KFP{}, SF{});
-      };
-      switch (stream_dtype) {
-        case FC_F32: rc = pick(float{}); break;
-        case FC_F16: rc = pick(f16_t{}); break;
-        case FC_BF16: rc = pick(bf16_t{}); break;
-        default: return FC_ERR_ARG;
-      }
-    }
-    if (rc != FC_OK) return rc;
-    rc = check_launch();
+    if (D % 8) return FC_ERR_UNSUPPORTED;
+    if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;  // empty split
+    const bool fuse = (parts & kPartMerge) && valu_fusable(B, Hkv, G);
+    const int rc = launch_split_valu(q, q_dtype, q_sb, q_sh, B, Hkv, G, D, store_kind, stream_dtype,
+                                     r, s, nb, key, value, fuse ? n_raw : 0, A, scale_log2, out,
+                                     o_sb, o_sh, pm, pl, pacc, n_splits,
+                                     fuse ? counters : nullptr, nullptr, st);
     if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0) {
     // merge only: the split geometry must still be consistent
@@ -1334,39 +1379,50 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
 }
 
 int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
-                           int64_t Hq, int64_t Hkv, int64_t D, int stream_dtype, int r, int s,
-                           int64_t nb_hint, const fc_stream_view* key, const fc_stream_view* value,
-                           const float* A, float scale, void* out, int64_t o_sb, int64_t o_sh,
-                           void* workspace, int64_t workspace_bytes, int n_cu,
-                           const int64_t* state, void* stream) {
+                           int64_t Hq, int64_t Hkv, int64_t D, int store_kind, int stream_dtype,
+                           int r, int s, int64_t nb_hint, const fc_stream_view* key,
+                           const fc_stream_view* value, const float* A, float scale, void* out,
+                           int64_t o_sb, int64_t o_sh, void* workspace, int64_t workspace_bytes,
+                           int n_cu, const int64_t* state, void* stream) {
   if (!state || !q || !out || !key || !value || !A || !workspace || nb_hint < 1) return FC_ERR_ARG;
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv) return FC_ERR_ARG;
   if (r < 1 || r > FC_MAX_BLOCK || s < 1 || s > r) return FC_ERR_ARG;
-  if (!key->rows || !value->rows || !key->scales || !value->scales || !key->raw || !value->raw)
-    return FC_ERR_ARG;
+  if (!key->rows || !value->rows || !key->raw || !value->raw) return FC_ERR_ARG;
+  if (store_kind == FC_STORE_JPEG_I8 && (!key->scales || !value->scales)) return FC_ERR_ARG;
+  if (store_kind == FC_STORE_PNG && (!key->anchors || !value->anchors || s != r)) return FC_ERR_ARG;
   const int64_t G = Hq / Hkv;
-  if (!split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) ||
-      !mfma_split_allowed() || 2 * B * Hkv * ((G + 15) / 16) * kCounterStride > kCounterWords)
-    return FC_ERR_UNSUPPORTED;
   const int n_splits =
-      fc_attention_splits(FC_STORE_JPEG_I8, stream_dtype, q_dtype, s, nb_hint, B, Hkv, G, D, n_cu);
-  if (n_splits < 1 || !split_i8_mfma_fusable(n_splits)) return FC_ERR_UNSUPPORTED;
+      fc_attention_splits(store_kind, stream_dtype, q_dtype, s, nb_hint, B, Hkv, G, D, n_cu);
+  if (n_splits < 1) return FC_ERR_UNSUPPORTED;
   if (fc_attention_workspace_bytes(B, Hq, D, n_splits) > workspace_bytes) return FC_ERR_ARG;
   const int64_t ws_head = (B * Hq * (int64_t)n_splits + 3) / 4 * 4;
   unsigned int* counters = static_cast<unsigned int*>(workspace);
   float* pm = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   float* pl = pm + ws_head;
   float* pacc = pl + ws_head;
-  MfmaFuse fz{};
-  fz.raw_dtype = stream_dtype;
-  fz.n_raw = 0;  // taken from the state
-  fz.out = out;
-  fz.o_sb = o_sb;
-  fz.o_sh = o_sh;
-  fz.state = state;
-  return launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb_hint, key, value,
-                              A, scale * kLog2e, pm, pl, pacc, n_splits, counters, kCounterWords,
-                              kCounterStride, &fz, (hipStream_t)stream);
+  hipStream_t st = (hipStream_t)stream;
+  // the same pass fc_attention_splits sized: matrix cores for int8 jpeg
+  // archives they support, else the vector-ALU pass; both with the merge
+  // fused (no second launch depends on the counts)
+  if (store_kind == FC_STORE_JPEG_I8 &&
+      split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) &&
+      mfma_split_allowed() && 2 * B * Hkv * ((G + 15) / 16) * kCounterStride <= kCounterWords) {
+    if (!split_i8_mfma_fusable(n_splits)) return FC_ERR_UNSUPPORTED;
+    MfmaFuse fz{};
+    fz.raw_dtype = stream_dtype;
+    fz.n_raw = 0;  // taken from the state
+    fz.out = out;
+    fz.o_sb = o_sb;
+    fz.o_sh = o_sh;
+    fz.state = state;
+    return launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb_hint, key, value,
+                                A, scale * kLog2e, pm, pl, pacc, n_splits, counters,
+                                kCounterWords, kCounterStride, &fz, st);
+  }
+  if (!valu_fusable(B, Hkv, G)) return FC_ERR_UNSUPPORTED;
+  return launch_split_valu(q, q_dtype, q_sb, q_sh, B, Hkv, G, D, store_kind, stream_dtype, r, s,
+                           nb_hint, key, value, 0, A, scale * kLog2e, out, o_sb, o_sh, pm, pl,
+                           pacc, n_splits, counters, state, st);
 }
 
 }  // namespace fc

@@ -52,14 +52,22 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          const MfmaFuse* fuse, hipStream_t st);
 
 // Decode attention over a graph-capturable decode step (fc_decode_step with
-// a device state): the fused matrix-core pass only, block and tail counts
-// read from `state` on the device; nb_hint (> 0) sizes the split count.
+// a device state): one launch with the merge fused (matrix-core pass for
+// int8 jpeg archives it supports, else the vector-ALU pass), block and tail
+// counts read from `state` on the device; nb_hint (> 0) sizes the split
+// count.
 int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
-                           int64_t Hq, int64_t Hkv, int64_t D, int stream_dtype, int r, int s,
-                           int64_t nb_hint, const fc_stream_view* key, const fc_stream_view* value,
-                           const float* A, float scale, void* out, int64_t o_sb, int64_t o_sh,
-                           void* workspace, int64_t workspace_bytes, int n_cu,
-                           const int64_t* state, void* stream);
+                           int64_t Hq, int64_t Hkv, int64_t D, int store_kind, int stream_dtype,
+                           int r, int s, int64_t nb_hint, const fc_stream_view* key,
+                           const fc_stream_view* value, const float* A, float scale, void* out,
+                           int64_t o_sb, int64_t o_sh, void* workspace, int64_t workspace_bytes,
+                           int n_cu, const int64_t* state, void* stream);
+
+// png archive of one block of a decode step's tail, gated like
+// jpeg_encode_gated.
+int png_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
+                     int64_t x_sh, int64_t x_ss, int64_t D, int r, int keep_m, float* deltas,
+                     void* anchors, int64_t cap, void* stream, const int64_t* gate);
 
 // jpeg archive of one block of a decode step's tail, gated on the device:
 // runs only when gate[1] == r - 1 and writes block gate[0] (< cap).

@@ -583,11 +583,19 @@ __device__ __forceinline__ uint64_t topm_mask(const uint32_t (&key)[RMAX], int n
   return topm_mask_exact(kk, n, m);
 }
 
-template <typename T, int VEC, int RMAX>
+template <typename T, int VEC, int RMAX, bool GATED = false>
 __global__ __launch_bounds__(kThreads) void png_encode_kernel(
     const T* __restrict__ x, int64_t sb, int64_t sh, int64_t ss, int64_t H, int64_t m,
     int64_t D, int64_t s_valid, int r, int keep_m, float* __restrict__ deltas,
-    T* __restrict__ anchors, int64_t cap, int64_t n0, int64_t items, int lpi_log2) {
+    T* __restrict__ anchors, int64_t cap, int64_t n0, int64_t items, int lpi_log2,
+    const int64_t* __restrict__ gate = nullptr) {
+  if constexpr (GATED) {
+    // gate = device (n_blocks, n_tail): archive only a completed tail, as
+    // block n_blocks
+    if (gate[1] != r - 1) return;
+    n0 = gate[0];
+    if (n0 < 0 || n0 + m > cap) return;
+  }
   const ItemMap im = item_of_thread(lpi_log2);
   if (im.item >= items) return;
   const int64_t bh = im.item / m, blk = im.item - bh * m;
@@ -847,6 +855,57 @@ int jpeg_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t 
                                   coeffs, scales, cap, 0, quant_bits, stream, gate);
 }
 
+template <bool GATED>
+static int png_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
+                             int64_t x_sh, int64_t x_ss, int64_t s_valid, int64_t m, int64_t D,
+                             int r, int keep_m, float* deltas, void* anchors, int64_t cap,
+                             int64_t n0, void* stream, const int64_t* gate) {
+  if (B < 0 || H < 0 || m < 0 || D <= 0 || r < 2 || keep_m < 0) return FC_ERR_ARG;
+  if (n0 < 0 || n0 + m > cap) return FC_ERR_ARG;
+  const int64_t items = B * H * m;
+  if (items == 0) return FC_OK;
+  if (!x || !deltas || !anchors) return FC_ERR_ARG;
+  if (r > FC_MAX_BLOCK || D > FC_MAX_HEAD_DIM) return FC_ERR_UNSUPPORTED;
+  const int es = esize_of(x_dtype);
+  if (!es || x_dtype == FC_I8) return FC_ERR_ARG;
+  // register-resident block bucket; rmax*vec <= 64 floats per lane
+  const int rmax = r <= 8 ? 8 : (r <= 16 ? 16 : (r <= 32 ? 32 : 64));
+  const int max_vec = rmax == 8 ? 8 : (rmax == 16 ? 4 : 1);
+  const int vec =
+      pick_vec(D, max_vec, {x_sb, x_sh, x_ss}, {{x, es}, {anchors, es}, {deltas, 4}});
+  if (!vec) return FC_ERR_UNSUPPORTED;
+  const int lg = log2_lanes(D, vec);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = grid_for(items, lg);
+  const int rc = with_float_type(x_dtype, [&](auto tv) {
+    using T = decltype(tv);
+    return with_int<1, 4, 8>(vec, [&](auto vc) {
+      constexpr int VEC = decltype(vc)::value;
+      return with_int<8, 16, 32, 64>(rmax, [&](auto rc_) {
+        constexpr int RMAX = decltype(rc_)::value;
+        if constexpr (RMAX * VEC <= 64) {
+          png_encode_kernel<T, VEC, RMAX, GATED><<<grid, kThreads, 0, st>>>(
+              (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, keep_m, deltas, (T*)anchors,
+              cap, n0, items, lg, gate);
+          return FC_OK;
+        } else {
+          return FC_ERR_UNSUPPORTED;
+        }
+      });
+    });
+  });
+  return rc != FC_OK ? rc : check_launch();
+}
+
+
+int png_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
+                     int64_t x_sh, int64_t x_ss, int64_t D, int r, int keep_m, float* deltas,
+                     void* anchors, int64_t cap, void* stream, const int64_t* gate) {
+  if (!gate || cap < 1) return FC_ERR_ARG;
+  return png_encode_launch<true>(x, x_dtype, B, H, x_sb, x_sh, x_ss, r, 1, D, r, keep_m, deltas,
+                                 anchors, cap, 0, stream, gate);
+}
+
 }  // namespace fc
 
 extern "C" {
@@ -963,41 +1022,8 @@ int fc_dequantize_rows(const int8_t* codes, const float* scales, int64_t n_rows,
 int fc_png_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb, int64_t x_sh,
                   int64_t x_ss, int64_t s_valid, int64_t m, int64_t D, int r, int keep_m,
                   float* deltas, void* anchors, int64_t cap, int64_t n0, void* stream) {
-  if (B < 0 || H < 0 || m < 0 || D <= 0 || r < 2 || keep_m < 0) return FC_ERR_ARG;
-  if (n0 < 0 || n0 + m > cap) return FC_ERR_ARG;
-  const int64_t items = B * H * m;
-  if (items == 0) return FC_OK;
-  if (!x || !deltas || !anchors) return FC_ERR_ARG;
-  if (r > FC_MAX_BLOCK || D > FC_MAX_HEAD_DIM) return FC_ERR_UNSUPPORTED;
-  const int es = esize_of(x_dtype);
-  if (!es || x_dtype == FC_I8) return FC_ERR_ARG;
-  // register-resident block bucket; rmax*vec <= 64 floats per lane
-  const int rmax = r <= 8 ? 8 : (r <= 16 ? 16 : (r <= 32 ? 32 : 64));
-  const int max_vec = rmax == 8 ? 8 : (rmax == 16 ? 4 : 1);
-  const int vec =
-      pick_vec(D, max_vec, {x_sb, x_sh, x_ss}, {{x, es}, {anchors, es}, {deltas, 4}});
-  if (!vec) return FC_ERR_UNSUPPORTED;
-  const int lg = log2_lanes(D, vec);
-  hipStream_t st = (hipStream_t)stream;
-  const dim3 grid = grid_for(items, lg);
-  const int rc = with_float_type(x_dtype, [&](auto tv) {
-    using T = decltype(tv);
-    return with_int<1, 4, 8>(vec, [&](auto vc) {
-      constexpr int VEC = decltype(vc)::value;
-      return with_int<8, 16, 32, 64>(rmax, [&](auto rc_) {
-        constexpr int RMAX = decltype(rc_)::value;
-        if constexpr (RMAX * VEC <= 64) {
-          png_encode_kernel<T, VEC, RMAX><<<grid, kThreads, 0, st>>>(
-              (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, keep_m, deltas, (T*)anchors,
-              cap, n0, items, lg);
-          return FC_OK;
-        } else {
-          return FC_ERR_UNSUPPORTED;
-        }
-      });
-    });
-  });
-  return rc != FC_OK ? rc : check_launch();
+  return png_encode_launch<false>(x, x_dtype, B, H, x_sb, x_sh, x_ss, s_valid, m, D, r, keep_m,
+                                  deltas, anchors, cap, n0, stream, nullptr);
 }
 
 int fc_png_decode(const float* deltas, const void* anchors, int anchor_dtype, int64_t B,

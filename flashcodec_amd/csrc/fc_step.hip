@@ -55,7 +55,10 @@ __global__ void state_advance_kernel(int64_t* state, int64_t r) {
 // The step with its counters on the device (a->state): every launch reads
 // them there, so one captured graph of the step is valid at every step.
 static int decode_step_state(const fc_step_args* a) {
-  if (a->store_kind != FC_STORE_JPEG_I8 || a->quant_bits != 8) return FC_ERR_UNSUPPORTED;
+  const int kind = a->store_kind;
+  if (kind == FC_STORE_JPEG_I8 && a->quant_bits != 8) return FC_ERR_ARG;
+  if (kind != FC_STORE_JPEG_I8 && kind != FC_STORE_JPEG_FP && kind != FC_STORE_PNG)
+    return FC_ERR_ARG;
   if (a->n_blocks < 1) return FC_ERR_ARG;  // the archive holds a block before capture
   const int64_t B = a->B, Hkv = a->Hkv, D = a->D;
   const int r = a->r;
@@ -82,23 +85,28 @@ static int decode_step_state(const fc_step_args* a) {
   if (rc != FC_OK) return rc;
   const int64_t tsb = Hkv * r * D, tsh = (int64_t)r * D;
   for (int i = 0; i < 2; ++i) {
-    rc = jpeg_encode_gated(st[i]->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, D, r, a->s,
-                           a->basis, st[i]->rows, st[i]->scales, st[i]->cap, 8, a->stream,
-                           a->state);
+    if (kind == FC_STORE_PNG)
+      rc = png_encode_gated(st[i]->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, D, r, a->keep_m,
+                            static_cast<float*>(st[i]->rows), st[i]->anchors, st[i]->cap,
+                            a->stream, a->state);
+    else
+      rc = jpeg_encode_gated(st[i]->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, D, r, a->s,
+                             a->basis, st[i]->rows, st[i]->scales, st[i]->cap,
+                             kind == FC_STORE_JPEG_I8 ? 8 : 0, a->stream, a->state);
     if (rc != FC_OK) return rc;
   }
   fc_stream_view v[2];
   for (int i = 0; i < 2; ++i) {
     v[i].rows = st[i]->rows;
     v[i].scales = st[i]->scales;
-    v[i].anchors = nullptr;
+    v[i].anchors = st[i]->anchors;
     v[i].cap = st[i]->cap;
     v[i].raw = st[i]->tail;
     v[i].raw_sb = tsb;
     v[i].raw_sh = tsh;
     v[i].raw_st = D;
   }
-  rc = decode_attention_state(a->q, a->q_dtype, a->q_sb, a->q_sh, B, a->Hq, Hkv, D,
+  rc = decode_attention_state(a->q, a->q_dtype, a->q_sb, a->q_sh, B, a->Hq, Hkv, D, kind,
                               a->stream_dtype, r, a->s, a->n_blocks, &v[0], &v[1], a->A, a->scale,
                               a->out, a->o_sb, a->o_sh, a->workspace, a->workspace_bytes,
                               a->n_cu, a->state, a->stream);

@@ -13,9 +13,10 @@ executed step (``advance_host``), so ``seq_len``, ``read()`` and the other
 stream APIs stay valid; ``release(cache)`` returns the layers to host-driven
 steps.
 
-Only int8 jpeg archives with fp16/bf16 models are supported (the matrix-core
-decode attention).  This is not part of the reference, which has no graph
-path (flashcodec/patch_attention.py decodes eagerly).
+Every store kind works (int8 jpeg on the matrix-core decode attention,
+unquantised jpeg and png on the vector-ALU one; both merge in the same
+launch).  This is not part of the reference, which has no graph path
+(flashcodec/patch_attention.py decodes eagerly).
 """
 
 import torch
@@ -39,17 +40,15 @@ def prepare(cache, extra_tokens):
     for layer in _codec_layers(cache):
         ks, vs = layer._key_stream, layer._value_stream
         c = ks.codec
-        if c.name != "jpeg" or not c.quantized:
-            raise NotImplementedError("graph decoding supports int8 jpeg archives only")
         if ks.n_blocks < 1 or ks.n_blocks != vs.n_blocks or ks._n_raw != vs._n_raw:
             raise ValueError("graph decoding needs a prefill of at least one block per layer")
         r = c.block_size
         need = ks.n_blocks + (ks._n_raw + extra_tokens) // r + 1
-        like = ks._coeffs
+        like = ks._archive_tensors()[0]
         for st in (ks, vs):
             st.discard_view()
             st._grow(need, like)
-            st._tail_buffer(st._coeffs)     # (B, H, r, D) in the stream dtype
+            st._tail_buffer(like)           # (B, H, r, D) in the stream dtype
         state = torch.tensor([ks.n_blocks, ks._n_raw], dtype=torch.int64, device=like.device)
         ks._dev_state = vs._dev_state = state
         layer.keys = layer.values = None

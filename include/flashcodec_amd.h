@@ -314,13 +314,14 @@ typedef struct fc_step_args {
  */
 int fc_decode_step(const fc_step_args* args);
 /*
- * With args->state != NULL (int8 jpeg archives, the matrix-core decode
- * attention), the step takes n_blocks and n_tail from the two int64 words
- * at `state` on the device and advances them there (n_tail + 1 == r moves a
- * block into the archive), so the enqueued work is the same at every step
- * and a captured HIP graph of it stays valid.  args->n_blocks (>= 1) then
- * only sizes the split count; the archives must hold every block the
- * replayed steps will add (a block past `cap` is not written).
+ * With args->state != NULL (any store kind), the step takes n_blocks and
+ * n_tail from the two int64 words at `state` on the device and advances
+ * them there (n_tail + 1 == r moves a block into the archive), so the
+ * enqueued work is the same at every step and a captured HIP graph of it
+ * stays valid: the archive kernels run gated on the state, the attention is
+ * one launch with its merge fused.  args->n_blocks (>= 1) then only sizes
+ * the split count; the archives must hold every block the replayed steps
+ * will add (a block past `cap` is not written).
  */
 
 #ifdef __cplusplus

@@ -1,6 +1,7 @@
 """GPU: decode steps replayed from a captured HIP graph (device-side stream
 counters) against the same steps run eagerly through the host-driven codec
-path, on a tiny Qwen3 decoder with int8 jpeg archives."""
+path, on a tiny Qwen3 decoder with int8 jpeg (matrix-core attention),
+unquantised jpeg and png archives (vector-ALU attention)."""
 
 import pytest
 import torch
@@ -13,15 +14,14 @@ pytestmark = pytest.mark.gpu
 transformers = pytest.importorskip("transformers")
 
 
-def tiny_qwen3(dtype):
+def tiny_qwen3(dtype, codec):
     from transformers import Qwen3Config, Qwen3ForCausalLM
     cfg = Qwen3Config(vocab_size=512, hidden_size=256, intermediate_size=512,
                       num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
                       head_dim=64, max_position_embeddings=4096, tie_word_embeddings=True)
     torch.manual_seed(0)
     model = Qwen3ForCausalLM(cfg).to(device="cuda", dtype=dtype).eval()
-    fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8,
-                         materialization_free=True)
+    fc.apply_flash_codec(model, materialization_free=True, **codec)
     return model
 
 
@@ -31,14 +31,21 @@ def prefill(model, prompt):
     return out.past_key_values
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_graph_replays_match_eager_steps(dtype):
-    model = tiny_qwen3(dtype)
+I8 = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+FP = dict(mode="jpeg", block_size=8, keep_freqs=4)
+PNG = dict(mode="png", block_size=8, keep_ratio=0.5)
+
+
+@pytest.mark.parametrize("dtype,codec", [(torch.float16, I8), (torch.bfloat16, I8),
+                                         (torch.bfloat16, FP), (torch.float16, PNG)],
+                         ids=["i8-f16", "i8-bf16", "fp-bf16", "png-f16"])
+def test_graph_replays_match_eager_steps(dtype, codec):
+    model = tiny_qwen3(dtype, codec)
     g = torch.Generator().manual_seed(5)
     B, P, steps = 2, 29, 21                      # 29 + 21 tokens cross three block boundaries
     prompt = torch.randint(1, 512, (B, P), generator=g).cuda()
     forced = torch.randint(1, 512, (B, steps), generator=g).cuda()
-    print(f"case graph decode {dtype}", flush=True)
+    print(f"case graph decode {dtype} {codec}", flush=True)
 
     # eager, host-driven codec steps
     cache_e = prefill(model, prompt)
@@ -72,8 +79,8 @@ def test_graph_replays_match_eager_steps(dtype):
     l0e, l0g = cache_e.layers[0], cache_g.layers[0]
     for se, sg in ((l0e._key_stream, l0g._key_stream), (l0e._value_stream, l0g._value_stream)):
         n = se.n_blocks
-        assert torch.equal(se._coeffs[:, :, :n], sg._coeffs[:, :, :n])
-        assert torch.equal(se._scales[:, :, :n], sg._scales[:, :, :n])
+        for te, tg in zip(se._archive_tensors(), sg._archive_tensors()):
+            assert torch.equal(te[:, :, :n], tg[:, :, :n])
         assert torch.equal(se.raw, sg.raw)
     # the cache keeps working eagerly after the graph is released
     with torch.no_grad():

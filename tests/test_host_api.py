@@ -125,7 +125,7 @@ def test_graph_host_counters_advance_like_appends():
         assert a.n_archived == r * a.n_blocks
 
 
-def test_graph_prepare_refuses_mixed_caches():
+def test_graph_prepare_refuses_mixed_and_empty_caches():
     pytest.importorskip("transformers")
     from flashcodec_amd import graph
     from flashcodec_amd.cache import FlashCodecLayer
@@ -139,5 +139,5 @@ def test_graph_prepare_refuses_mixed_caches():
     with pytest.raises(NotImplementedError):
         graph.prepare(cache, 16)
     cache.layers = [FlashCodecLayer(mode="png", block_size=8)]
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):               # no archived block to size the splits
         graph.prepare(cache, 16)
