@@ -20,13 +20,16 @@
 //      (base-2 domain, scale*log2(e) folded in), the pass maximum updates
 //      the running maximum, and the pair writes its s output weights
 //      w_j = sum_p 2^(logit_p - m) A[p][j] (times the V row scale) back in
-//      place of its scores;
+//      place of its scores (png with r <= 16: one pair per 16-lane row,
+//      DPP prefix / suffix sums); the first V rows are already requested;
 //   C. values: the same row tasks accumulate acc[g][d] += w_j * S_j[d].
 // The partial (m, l, acc[D]) of each (query head, split) goes to the
-// workspace.
-// Kernel 2 (merge): one workgroup per (batch, kv head) combines the split
-// partials of each query head with the raw tail tokens (attended at full
-// precision) and writes out = acc / l in the query dtype.
+// workspace.  With the merge fused (fc_decode_attention), split 0 starts
+// from the raw tail tokens (attended at full precision), and the last
+// workgroup of each (batch, kv head, head group) to publish its partial
+// combines all of them into out = acc / l in the query dtype.
+// Kernel 2 (merge, for the two-pass entry points): one workgroup per query
+// head combines the split partials with the raw tail tokens.
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
