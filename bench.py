@@ -14,8 +14,12 @@ the call:
   K+V int8 codes 2*134,217,728 + fp32 scales 2*4,194,304 + raw tails
   163,840 + q 65,536 + out 65,536 = 277,118,976 bytes per call.
 The roofline object covers that kernel, each launch timed with HIP events on
-the stream it is launched on.  `cpu_baseline` times the fp64 CPU oracle on
-the same workload's sequences for at least 10 s (one whole call or more).
+the stream it is launched on.  With `--rotating-sets N` (N >= 2) a
+`rotating_sets` object times the same launches cycling over N copies of the
+archives (as a decode step cycles over its layers' caches), so that no launch
+finds data a previous one left in the caches.  `cpu_baseline` times the fp64
+CPU oracle on the same workload's sequences for at least 10 s (one whole
+call or more).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1]
   python bench.py --mode copy     # plain copy, for PMC byte calibration
@@ -540,6 +544,8 @@ def main():
                     default="c3")
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--rotating-sets", type=int, default=0,
+                    help="c3: also time launches cycling over this many archive copies")
     ap.add_argument("--splits", type=int, default=0, help="override the split count")
     ap.add_argument("--c5-steps", type=int, default=None,
                     help="c5: one run of this many decode steps (0: prefill only)")
@@ -644,6 +650,42 @@ def main():
     achieved = ALG_BYTES_CALL / (launch_ms * 1e-3) / 1e9
     log(f"bench: kernel {launch_ms * 1e3:.1f} us per launch, {achieved:.0f} GB/s")
 
+    # optionally the same launches rotating over N copies of the archives
+    # (277 MB each), as a decode step does over its layers: no call finds
+    # its inputs in the caches a previous call left behind
+    rot = None
+    ROT_SETS = args.rotating_sets
+    rot_args = [abi_args]
+    copies = []
+    for _ in range(ROT_SETS - 1 if ROT_SETS >= 2 else 0):
+        views = []
+        for st in (ks, vs):
+            c = _CodecStream(st.codec)
+            c._coeffs, c._scales = st._coeffs.clone(), st._scales.clone()
+            c._capacity, c.n_blocks, c.n_archived = st._capacity, st.n_blocks, st.n_archived
+            c.dtype, c.meta = st.dtype, st.meta
+            c._raw_buf, c._n_raw = st._raw_buf.clone(), st._n_raw
+            copies.append(c)
+            views.append(_view(c, keep))
+        rot_args.append(abi_args[:13] + tuple(views) + abi_args[15:])
+    if copies:
+        for i in range(2 * ROT_SETS):
+            N.check(L.fc_decode_attention(*rot_args[i % ROT_SETS]), "fc_decode_attention")
+        torch.cuda.synchronize()
+        k0.record(stream)
+        for i in range(args.steps):
+            N.check(L.fc_decode_attention(*rot_args[i % ROT_SETS]), "fc_decode_attention")
+        k1.record(stream)
+        torch.cuda.synchronize()
+        rot_ms = k0.elapsed_time(k1) / args.steps
+        rot_achieved = ALG_BYTES_CALL / (rot_ms * 1e-3) / 1e9
+        log(f"bench: kernel over {ROT_SETS} rotating archive sets {rot_ms * 1e3:.1f} us per "
+            f"launch, {rot_achieved:.0f} GB/s")
+        rot = {"sets": ROT_SETS, "avg_launch_us": round(rot_ms * 1e3, 2),
+               "achieved": round(rot_achieved, 2), "frac": round(rot_achieved / HBM_PEAK_GBS, 4)}
+        del copies, rot_args
+        torch.cuda.empty_cache()
+
     result = {
         "metric": METRIC,
         "value": round(ALG_BYTES_CALL / (ms * 1e-3) / 1e9, 2),
@@ -674,6 +716,8 @@ def main():
                      "algorithmic_bytes_per_launch": ALG_BYTES_CALL,
                      "avg_launch_us": round(launch_ms * 1e3, 2)},
     }
+    if rot is not None:
+        result["rotating_sets"] = rot
     if not args.no_cpu_baseline:
         log("bench: cpu baseline (fp64 oracle, >= 10 s of the workload)")
         ref, cpu = cpu_baseline(q, ks, vs)
