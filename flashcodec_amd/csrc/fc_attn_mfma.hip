@@ -142,24 +142,35 @@ __device__ __forceinline__ void st_elem(void* ptr, int dt, int64_t i, float v) {
 // query heads the base-2 logits of the n_raw tail tokens at full precision,
 // their maximum tm[h], sum tl[h] = sum_t 2^(logit_t - tm[h]) and
 // acc[h][d] = sum_t 2^(logit_t - tm[h]) v_t[d].  `etl` holds
-// 16 * FC_MAX_BLOCK floats; every thread of the workgroup takes part.
-template <int D>
-__device__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
-                                 int nr, int tid, float* etl, float* acc, float* tm, float* tl) {
+// 16 * FC_MAX_BLOCK floats; every thread of the workgroup takes part.  QT /
+// RT are the query and tail element types: with them fixed at compile time
+// each thread issues all its loads before it uses any (this runs while the
+// other workgroups stream the archive, where every serialized load waits
+// several microseconds).
+template <int D, typename QT, typename RT>
+__device__ void raw_tail_partial_t(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
+                                   int nr, int tid, float* etl, float* acc, float* tm,
+                                   float* tl) {
   const int lane = tid & 63, wave = tid >> 6;
+  const QT* qb = static_cast<const QT*>(p.q) + b * p.q_sb;
+  const RT* kb = static_cast<const RT*>(p.kraw) + b * p.kr_sb + hkv * p.kr_sh;
+  const RT* vb = static_cast<const RT*>(p.vraw) + b * p.vr_sb + hkv * p.vr_sh;
   {
     // logits: 16 lanes per (head, token), features strided by 16
     const int grp = tid >> 4, gl = tid & 15;
     for (int u = grp; u < G * nr; u += kMThreads / 16) {
       const int h = u / nr, t = u - h * nr;
-      const int64_t hq = hkv * p.G + g0 + h;
+      const QT* qr = qb + (hkv * p.G + g0 + h) * p.q_sh + gl;
+      const RT* kr = kb + t * p.kr_st + gl;
+      float qv[D / 16], kv[D / 16];
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        qv[i] = to_f32(qr[16 * i]);
+        kv[i] = to_f32(kr[16 * i]);
+      }
       float a = 0.f;
 #pragma unroll
-      for (int i = 0; i < D / 16; ++i)
-        a = __builtin_fmaf(load_q(p.q, p.q_dtype, b * p.q_sb + hq * p.q_sh + gl + 16 * i),
-                           load_q(p.kraw, p.raw_dtype,
-                                  b * p.kr_sb + hkv * p.kr_sh + t * p.kr_st + gl + 16 * i),
-                           a);
+      for (int i = 0; i < D / 16; ++i) a = __builtin_fmaf(qv[i], kv[i], a);
 #pragma unroll
       for (int m = 8; m >= 1; m >>= 1) a += __shfl_xor(a, m, 16);
       if (gl == 0) etl[h * FC_MAX_BLOCK + t] = a * p.scale_log2;
@@ -185,14 +196,37 @@ __device__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int6
     }
   }
   __syncthreads();
+  constexpr int kT = 8;  // tail rows requested together
   for (int x = tid; x < G * D; x += kMThreads) {
     const int h = x / D, d = x - h * D;
     float o = 0.f;
-    for (int t = 0; t < nr; ++t)
-      o = __builtin_fmaf(etl[h * FC_MAX_BLOCK + t],
-                         load_q(p.vraw, p.raw_dtype, b * p.vr_sb + hkv * p.vr_sh + t * p.vr_st + d),
-                         o);
+    for (int t0 = 0; t0 < nr; t0 += kT) {
+      float vv[kT];
+#pragma unroll
+      for (int j = 0; j < kT; ++j) vv[j] = t0 + j < nr ? to_f32(vb[(t0 + j) * p.vr_st + d]) : 0.f;
+#pragma unroll
+      for (int j = 0; j < kT; ++j)
+        if (t0 + j < nr) o = __builtin_fmaf(etl[h * FC_MAX_BLOCK + t0 + j], vv[j], o);
+    }
     acc[h * D + d] = o;
+  }
+}
+
+template <int D>
+__device__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
+                                 int nr, int tid, float* etl, float* acc, float* tm, float* tl) {
+  // the matrix-core pass takes fp16 / bf16 queries; tails are in the stream dtype
+  auto with_q = [&](auto rt) {
+    using RT = decltype(rt);
+    if (p.q_dtype == FC_F16)
+      raw_tail_partial_t<D, f16_t, RT>(p, b, hkv, g0, G, nr, tid, etl, acc, tm, tl);
+    else
+      raw_tail_partial_t<D, bf16_t, RT>(p, b, hkv, g0, G, nr, tid, etl, acc, tm, tl);
+  };
+  switch (p.raw_dtype) {
+    case FC_F16: with_q(f16_t{}); break;
+    case FC_BF16: with_q(bf16_t{}); break;
+    default: with_q(float{}); break;
   }
 }
 
