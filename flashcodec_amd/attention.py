@@ -192,6 +192,17 @@ def _step_args(ks, vs, query, tokens):
     return a, ws_bytes
 
 
+def _same_codec(a, b):
+    """Whether two codec objects archive identically (same kind and
+    parameters); the fused step archives both streams with one setting."""
+    if a is b:
+        return True
+    return (a.name == b.name and a.block_size == b.block_size
+            and getattr(a, "keep_freqs", None) == getattr(b, "keep_freqs", None)
+            and getattr(a, "quant_bits", None) == getattr(b, "quant_bits", None)
+            and getattr(a, "keep_ratio", None) == getattr(b, "keep_ratio", None))
+
+
 def codec_decode_step(query, key_tokens, value_tokens, key_stream, value_stream, scale=None):
     """One decode step of a layer in one library call: appends the step's
     key and value tokens (B, Hkv, 1, D) to their streams and attends the
@@ -208,7 +219,7 @@ def codec_decode_step(query, key_tokens, value_tokens, key_stream, value_stream,
         return _decode_step_device_state(query, key_tokens, value_tokens, ks, vs, scale,
                                          dev_state)
     fused = (Sq == 1 and key_tokens.shape[-2] == 1 and value_tokens.shape[-2] == 1
-             and ks.meta is not None and vs.meta is not None and ks.codec is vs.codec
+             and ks.meta is not None and vs.meta is not None and _same_codec(ks.codec, vs.codec)
              and key_tokens.dtype == ks.dtype and value_tokens.dtype == vs.dtype
              and ks.dtype == vs.dtype and ks.n_blocks == vs.n_blocks
              and ks._n_raw == vs._n_raw and key_tokens.shape == value_tokens.shape
