@@ -141,3 +141,21 @@ def test_graph_prepare_refuses_mixed_and_empty_caches():
     cache.layers = [FlashCodecLayer(mode="png", block_size=8)]
     with pytest.raises(ValueError):               # no archived block to size the splits
         graph.prepare(cache, 16)
+
+
+def test_fused_step_codec_equality():
+    """The fused decode step archives both streams with one codec setting:
+    equal parameters qualify, any difference does not."""
+    from flashcodec_amd.attention import _same_codec
+    mk = fc.make_codec
+    assert _same_codec(mk(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8),
+                       mk(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8))
+    assert not _same_codec(mk(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8),
+                           mk(mode="jpeg", block_size=8, keep_freqs=4))
+    assert not _same_codec(mk(mode="jpeg", block_size=8, keep_freqs=4),
+                           mk(mode="jpeg", block_size=8, keep_freqs=2))
+    assert _same_codec(mk(mode="png", block_size=16, keep_ratio=0.25),
+                       mk(mode="png", block_size=16, keep_ratio=0.25))
+    assert not _same_codec(mk(mode="png", block_size=16, keep_ratio=0.25),
+                           mk(mode="png", block_size=16, keep_ratio=0.5))
+    assert not _same_codec(mk(mode="png", block_size=8), mk(mode="jpeg", block_size=8))
