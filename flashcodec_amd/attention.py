@@ -248,11 +248,12 @@ def codec_decode_step(query, key_tokens, value_tokens, key_stream, value_stream,
     ws = workspace(dev, ws_bytes)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     a.stream = N.stream_ptr(dev)
+    jpeg = ks.codec.name == "jpeg"
     for sv, st, tok in ((a.key, ks, key_tokens), (a.value, vs, value_tokens)):
-        rows, extra = st._archive_tensors()[0], st._archive_tensors()[1:]
-        sv.rows = rows.data_ptr()
-        sv.scales = extra[0].data_ptr() if (st.codec.name == "jpeg" and extra) else None
-        sv.anchors = extra[0].data_ptr() if st.codec.name == "png" else None
+        arch = st._archive_tensors()
+        sv.rows = arch[0].data_ptr()
+        sv.scales = arch[1].data_ptr() if (jpeg and len(arch) > 1) else None
+        sv.anchors = None if jpeg else arch[1].data_ptr()
         sv.cap = st._capacity
         sv.tail = st._raw_buf.data_ptr()
         sv.token, sv.tok_sb, sv.tok_sh = tok.data_ptr(), tok.stride(0), tok.stride(1)
@@ -289,11 +290,12 @@ def _decode_step_device_state(query, key_tokens, value_tokens, ks, vs, scale, st
     ws = workspace(dev, ws_bytes)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     a.stream = N.stream_ptr(dev)
+    jpeg = ks.codec.name == "jpeg"
     for sv, st, tok in ((a.key, ks, key_tokens), (a.value, vs, value_tokens)):
-        rows, extra = st._archive_tensors()[0], st._archive_tensors()[1:]
-        sv.rows = rows.data_ptr()
-        sv.scales = extra[0].data_ptr() if (st.codec.name == "jpeg" and extra) else None
-        sv.anchors = extra[0].data_ptr() if st.codec.name == "png" else None
+        arch = st._archive_tensors()
+        sv.rows = arch[0].data_ptr()
+        sv.scales = arch[1].data_ptr() if (jpeg and len(arch) > 1) else None
+        sv.anchors = None if jpeg else arch[1].data_ptr()
         sv.cap = st._capacity
         sv.tail = st._raw_buf.data_ptr()
         sv.token, sv.tok_sb, sv.tok_sh = tok.data_ptr(), tok.stride(0), tok.stride(1)
