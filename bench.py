@@ -98,6 +98,18 @@ def split_kernel_name():
     return "attn_split_i8_mfma<4,4,4> (merge fused)"
 
 
+def cpu_model():
+    """Host CPU model name (/proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_rate(fn, nbytes, min_seconds=1.0):
     """GB/s of `fn` (a CPU oracle call over `nbytes` algorithmic bytes),
     repeated until min_seconds have passed (one host thread)."""
@@ -183,7 +195,7 @@ def c2_mode(args):
     xs = x.float().cpu().numpy()
     _, cs, ss = O.jpeg_encode(xs, r, k, basis, "f16", quant=True)
     alg_s = alg
-    cpu = {"unit": "GB/s", "cores": 1, "kind": "port",
+    cpu = {"unit": "GB/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
            "sample": "the whole workload (128 sequences of 8192 tokens), C++ oracle",
            "archive": cpu_rate(lambda: O.jpeg_encode(xs, r, k, basis, "f16", quant=True), alg_s),
            "read": cpu_rate(lambda: O.jpeg_decode(None, r, basis, "f16", codes=cs, scales=ss),
@@ -269,7 +281,7 @@ def c4_mode(args):
         xs = x["k"].cpu().numpy()
         dl, an = O.png_encode(xs, r, keep)
         alg_s = alg_codec
-        cpu = {"unit": "GB/s", "cores": 1, "kind": "port",
+        cpu = {"unit": "GB/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
                "sample": "archive / read: the whole stream; attention: 1 of the 16 (batch, kv "
                          "head) sequences (16384 tokens, 4 query heads); C++ oracle",
                "archive": cpu_rate(lambda: O.png_encode(xs, r, keep), alg_s),
@@ -315,6 +327,7 @@ def c1_mode(args):
     coef = O.jpeg_encode(xn, r, k, basis, "f32")
     ref = O.jpeg_decode(coef, r, basis, "f32")
     cpu = {"unit": "GB/s", "cores": 1, "kind": "port", "sample": "the whole C1 stream, C++ oracle",
+           "cpu_model": cpu_model(),
            "archive": cpu_rate(lambda: O.jpeg_encode(xn, r, k, basis, "f32"),
                                b_ * h_ * s_ * d_ * 4 + b_ * h_ * (s_ // r) * k * d_ * 4),
            "read": cpu_rate(lambda: O.jpeg_decode(coef, r, basis, "f32"),
@@ -532,7 +545,7 @@ def cpu_baseline(q, ks, vs, min_seconds=10.0):
                   "sample": f"{done} sequences of the workload ({done / B:.2f} calls): int8 "
                             "codes -> fp64 rows (numpy) -> fp64 decode attention over 32 q "
                             "heads x (32768 archived + 5 raw tokens) (C++ oracle, OpenMP)",
-                  "seconds": round(dt, 3)}
+                  "seconds": round(dt, 3), "cpu_model": cpu_model()}
 
 
 def main():
