@@ -14,7 +14,8 @@ import torch
 from . import _build
 
 F32, F16, BF16, I8 = 0, 1, 2, 3
-OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP = 0, -1, -2, -3
+OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_INCOMPLETE = 0, -1, -2, -3, -4
+PASS_AUTO, PASS_VECTOR, PASS_STATIC = 0, 1, 2
 STORE_JPEG_I8, STORE_JPEG_FP, STORE_PNG = 0, 1, 2
 MAX_BLOCK = 64
 MAX_HEAD_DIM = 512
@@ -83,6 +84,10 @@ SIGNATURES = {
     "fc_decode_attention_merge": _ATTN_SIG,
     "fc_png_topm_mask_host": (ctypes.c_uint64, [_vp, _int, _int]),
     "fc_decode_step": (_int, [ctypes.POINTER(StepArgs)]),
+    "fc_attention_workspace_status": (_int, [_vp, _vp]),
+    "fc_set_attention_pass": (_int, [_int]),
+    "fc_get_attention_pass": (_int, []),
+    "fc_set_merge_wait_limit": (None, [_int]),
 }
 
 _LIB = None
@@ -114,6 +119,11 @@ class KernelError(RuntimeError):
     """A flashcodec_amd kernel entry point returned an error status."""
 
 
+class IncompleteMergeError(KernelError):
+    """A fused decode-attention merge gave up waiting for split partials:
+    outputs written since the workspace was last checked may be wrong."""
+
+
 def check(rc, what):
     if rc == OK:
         return
@@ -123,7 +133,23 @@ def check(rc, what):
         msg += f" (hipError {L.fc_last_hip_error()})"
     if rc == ERR_UNSUPPORTED:
         raise NotImplementedError(f"{what}: {msg}")
+    if rc == ERR_INCOMPLETE:
+        raise IncompleteMergeError(f"{what}: {msg}")
     raise KernelError(f"{what}: {msg}")
+
+
+def set_attention_pass(name):
+    """Select the decode-attention split pass process-wide: "auto" (matrix
+    cores for the int8 jpeg archives they support, passes from a queue),
+    "static" (the same with a fixed pass order: bitwise reproducible) or
+    "valu" (vector ALU for every store, for A/B measurements).  Returns the
+    previous name."""
+    names = {PASS_AUTO: "auto", PASS_VECTOR: "valu", PASS_STATIC: "static"}
+    L = lib()
+    prev = names[L.fc_get_attention_pass()]
+    code = {v: k for k, v in names.items()}[name]
+    check(L.fc_set_attention_pass(code), "fc_set_attention_pass")
+    return prev
 
 
 def dtype_code(dtype):

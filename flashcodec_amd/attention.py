@@ -7,10 +7,11 @@ token the scores are (q . S^T) A^T and the output (prob A) S, so the (S, D)
 reconstruction never exists (flashcodec/attention.py:1-27).
 
 `codec_decode_attention` keeps the reference signature
-(flashcodec/attention.py:64) and runs two HIP kernels of
-libflashcodec_amd.so: a split-K pass over the archived blocks (every kv
-head's rows read once per group of up to eight query heads) and a merge pass
-that folds in the raw tail.
+(flashcodec/attention.py:64) and runs the split-K decode attention of
+libflashcodec_amd.so: one launch whose workgroups walk the archived blocks
+(every kv head's rows read once per group of up to sixteen query heads) and
+whose last workgroup per head group merges the split partials with the raw
+tail.
 """
 
 import ctypes
@@ -41,6 +42,18 @@ def _device_A(codec, r, device):
         A = block_basis(codec, r, dtype=torch.float32).contiguous().to(device)
         _A_CACHE[key] = A
     return A
+
+
+def check_workspaces(device=None):
+    """Raise IncompleteMergeError if a decode attention since the last check
+    merged without every split partial (its bounded wait for the other
+    workgroups gave up; the output of that call may be wrong).  Synchronizes
+    the device's streams that own a workspace; clears the status."""
+    for (index, stream), ws in list(_WORKSPACES.items()):
+        if device is not None and torch.device(device).index not in (None, index):
+            continue
+        N.check(N.lib().fc_attention_workspace_status(ws.data_ptr(), stream),
+                "decode attention")
 
 
 def workspace(device, nbytes):
@@ -79,6 +92,25 @@ def _view(stream, keep):
     return v
 
 
+def _triton_refuses(query, ks, vs, D):
+    """Why impl="triton" raises in the reference for this call, or None.
+    The reference tries its Triton path for jpeg stores only (png stores go
+    to the torch path whatever `impl` says, flashcodec/attention.py:91) and
+    raises when that path returns None for them
+    (flashcodec/triton_attention.py:154-173, attention.py:96-99)."""
+    if ks.codec.name != "jpeg":
+        return None
+    if not query.is_cuda:
+        return "the query is not on a GPU"
+    if vs.codec.name != "jpeg":
+        return "key and value codecs differ"
+    if ks.n_blocks == 0:
+        return "an empty archive"
+    if D > 256:
+        return f"head size {D} > 256"
+    return None
+
+
 def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="auto",
                            _n_splits=None):
     """Attention of one new query token against a codec archive without
@@ -88,8 +120,14 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
         query: (B, Hq, 1, D) query of the current step.
         key_stream, value_stream: ``_CodecStream`` instances of one layer.
         scale: attention scale (default ``D ** -0.5``).
-        impl: ``"auto"`` / ``"hip"`` (``"triton"`` is accepted as the name of
-            the reference's accelerated path and runs the same HIP kernels).
+        impl: the reference's implementation selector
+            (flashcodec/attention.py:64-99).  Every value computes on this
+            build's HIP kernels (there is no other implementation); they keep
+            the reference's error behaviour: ``"triton"`` raises RuntimeError
+            for the jpeg cases the reference's Triton path does not support
+            (an empty archive, D > 256, a query off the GPU), while
+            ``"auto"``, ``"torch"`` (the reference's portable path) and any
+            other value run every case.
     Returns:
         (B, Hq, 1, D) attention output in the query dtype.
 
@@ -101,9 +139,11 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
     if Sq != 1:
         raise ValueError("codec_decode_attention only supports a single query token "
                          f"(got Sq={Sq}); prefill should use the materialized view")
-    if impl not in ("auto", "hip", "triton"):
-        raise ValueError(f"impl={impl!r}: this build computes on HIP kernels only "
-                         "(use 'auto' or 'hip')")
+    if impl == "triton":
+        why = _triton_refuses(query, key_stream, value_stream, D)
+        if why is not None:
+            raise RuntimeError("triton implementation does not support this case "
+                               f"({why}; see codec_decode_attention_triton)")
     scale = D ** -0.5 if scale is None else float(scale)
     ks, vs = key_stream, value_stream
     if ks.codec.name != vs.codec.name:

@@ -40,11 +40,19 @@
 
 namespace fc {
 
-// FLASHCODEC_AMD_ATTN=valu forces the vector-ALU split pass (A/B testing).
-static bool mfma_split_allowed() {
+// Split pass selection and merge wait limit: read from the environment once,
+// when the library is loaded (FLASHCODEC_AMD_ATTN=valu forces the vector-ALU
+// split pass, for A/B measurements), never on the call path.
+constexpr int kDefaultMergeWait = 1 << 24;  // polls of a publication counter
+static int g_attention_pass = [] {
   const char* v = getenv("FLASHCODEC_AMD_ATTN");
-  return !(v && v[0] == 'v');
-}
+  return (v && v[0] == 'v') ? FC_PASS_VECTOR : FC_PASS_AUTO;
+}();
+static int g_merge_wait = kDefaultMergeWait;
+
+bool mfma_split_allowed() { return g_attention_pass != FC_PASS_VECTOR; }
+bool static_pass_order() { return g_attention_pass == FC_PASS_STATIC; }
+int merge_wait_limit() { return g_merge_wait; }
 
 constexpr int kAttnThreads = 256;
 constexpr int kPassRows = 512;
@@ -1077,19 +1085,28 @@ using namespace fc;
 
 namespace fc {
 
-// Workspace of one call: kCounterWords 32-bit counters of the matrix-core
-// split pass (pass queues and arrival counts; a fixed region, so calls of any
-// shape find their counters at the same place), then pm | pl | pacc (fp32,
-// sections 16-byte aligned, 256-byte rounded).  The counters must be zero
-// before a workspace's first use; every call leaves them zero.
-constexpr int64_t kCounterWords = 262144;  // 1 MiB: 2 x 4096 counters, one per 128-byte line
-constexpr int64_t kCounterBytes = kCounterWords * 4;
-constexpr int64_t kCounterStride = 32;  // words between counters (no two share a line)
 static int64_t ws_partial_bytes(int64_t B, int64_t Hq, int64_t D, int n_splits) {
   const int64_t slots = B * Hq * (int64_t)n_splits;
   const int64_t head = (slots + 3) / 4 * 4;
   const int64_t bytes = (2 * head + slots * D) * (int64_t)sizeof(float);
   return (bytes + 255) / 256 * 256;
+}
+
+// Workspace of one call: the status line, kCounterWords 32-bit counters of
+// the split passes (a fixed region, so calls of any shape find their
+// counters at the same place), then pm | pl | pacc (fp32, sections 16-byte
+// aligned).  The counters must be zero before a workspace's first use;
+// every call leaves them zero.
+WsLayout ws_layout(void* workspace, int64_t B, int64_t Hq, int n_splits) {
+  WsLayout w;
+  unsigned int* base = static_cast<unsigned int*>(workspace);
+  w.status = base;
+  w.counters = base + kWsStatusWords;
+  const int64_t ws_head = (B * Hq * (int64_t)n_splits + 3) / 4 * 4;
+  w.pm = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  w.pl = w.pm + ws_head;
+  w.pacc = w.pl + ws_head;
+  return w;
 }
 
 }  // namespace fc
@@ -1273,11 +1290,9 @@ static int launch_split_valu(const void* q, int q_dtype, int64_t q_sb, int64_t q
   return check_launch();
 }
 
-constexpr int kPartSplit = 1, kPartMerge = 2;
-
 // Validates the arguments and enqueues the requested parts: the split pass
 // over the archived blocks and/or the merge pass (split partials + raw tail).
-static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                                   int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int store_kind,
                                   int stream_dtype, int r, int s, int64_t nb,
                                   const fc_stream_view* key, const fc_stream_view* value,
@@ -1305,12 +1320,12 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
   const int64_t G = Hq / Hkv;
   const float scale_log2 = scale * kLog2e;
   hipStream_t st = (hipStream_t)stream;
-  // workspace: counters | pm | pl | pacc, sections 16-byte aligned
-  const int64_t ws_head = (B * Hq * (int64_t)n_splits + 3) / 4 * 4;
-  unsigned int* counters = static_cast<unsigned int*>(workspace);
-  float* pm = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-  float* pl = pm + ws_head;
-  float* pacc = pl + ws_head;
+  // workspace: status | counters | pm | pl | pacc
+  const WsLayout ws = ws_layout(workspace, B, Hq, n_splits);
+  unsigned int* counters = ws.counters;
+  float* pm = ws.pm;
+  float* pl = ws.pl;
+  float* pacc = ws.pacc;
 
   if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_JPEG_I8 &&
       split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) &&
@@ -1329,7 +1344,8 @@ static int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int6
     }
     const int rc = launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb, key,
                                         value, A, scale_log2, pm, pl, pacc, n_splits, counters,
-                                        kCounterWords, kCounterStride, fuse ? &fz : nullptr, st);
+                                        kCounterWords, kCounterStride, ws.status,
+                                        fuse ? &fz : nullptr, st);
     if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit)) {
     // the merge runs inside the split pass when every group has a counter
@@ -1398,11 +1414,11 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
       fc_attention_splits(store_kind, stream_dtype, q_dtype, s, nb_hint, B, Hkv, G, D, n_cu);
   if (n_splits < 1) return FC_ERR_UNSUPPORTED;
   if (fc_attention_workspace_bytes(B, Hq, D, n_splits) > workspace_bytes) return FC_ERR_ARG;
-  const int64_t ws_head = (B * Hq * (int64_t)n_splits + 3) / 4 * 4;
-  unsigned int* counters = static_cast<unsigned int*>(workspace);
-  float* pm = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-  float* pl = pm + ws_head;
-  float* pacc = pl + ws_head;
+  const WsLayout ws = ws_layout(workspace, B, Hq, n_splits);
+  unsigned int* counters = ws.counters;
+  float* pm = ws.pm;
+  float* pl = ws.pl;
+  float* pacc = ws.pacc;
   hipStream_t st = (hipStream_t)stream;
   // the same pass fc_attention_splits sized: matrix cores for int8 jpeg
   // archives they support, else the vector-ALU pass; both with the merge
@@ -1420,7 +1436,7 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     fz.state = state;
     return launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb_hint, key, value,
                                 A, scale * kLog2e, pm, pl, pacc, n_splits, counters,
-                                kCounterWords, kCounterStride, &fz, st);
+                                kCounterWords, kCounterStride, ws.status, &fz, st);
   }
   if (!valu_fusable(B, Hkv, G)) return FC_ERR_UNSUPPORTED;
   return launch_split_valu(q, q_dtype, q_sb, q_sh, B, Hkv, G, D, store_kind, stream_dtype, r, s,
@@ -1453,5 +1469,29 @@ int fc_decode_attention_split(FC_ATTN_PARAMS) {
 int fc_decode_attention_merge(FC_ATTN_PARAMS) {
   return decode_attention_parts(FC_ATTN_ARGS, kPartMerge);
 }
+
+int fc_attention_workspace_status(void* workspace, void* stream) {
+  if (!workspace) return FC_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  unsigned int word = 0;
+  int rc = hip_status(hipMemcpyAsync(&word, workspace, sizeof(word), hipMemcpyDeviceToHost, st));
+  if (rc == FC_OK) rc = hip_status(hipStreamSynchronize(st));
+  if (rc != FC_OK) return rc;
+  if (word == 0) return FC_OK;
+  const unsigned int zero = 0;
+  rc = hip_status(hipMemcpyAsync(workspace, &zero, sizeof(zero), hipMemcpyHostToDevice, st));
+  if (rc == FC_OK) rc = hip_status(hipStreamSynchronize(st));
+  return rc != FC_OK ? rc : FC_ERR_INCOMPLETE;
+}
+
+int fc_set_attention_pass(int pass) {
+  if (pass != FC_PASS_AUTO && pass != FC_PASS_VECTOR && pass != FC_PASS_STATIC) return FC_ERR_ARG;
+  g_attention_pass = pass;
+  return FC_OK;
+}
+
+int fc_get_attention_pass(void) { return g_attention_pass; }
+
+void fc_set_merge_wait_limit(int polls) { g_merge_wait = polls; }
 
 }  // extern "C"

@@ -23,7 +23,36 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int
 }
 
 int check_launch();
+int hip_status(hipError_t e);  // FC_OK, or FC_ERR_HIP with the error recorded
 int esize_of(int dt);
+
+// Value of a workspace's status word after a fused merge merged without
+// every split partial (the bounded publication wait gave up).
+constexpr unsigned int FC_STATUS_MERGE_INCOMPLETE = 1;
+
+// Process-wide settings, read once when the library loads
+// (FLASHCODEC_AMD_ATTN=valu selects the vector-ALU split pass) and
+// changeable through fc_set_attention_pass / fc_set_merge_wait_limit.
+bool mfma_split_allowed();
+bool static_pass_order();  // matrix-core pass without its dynamic pass queue
+int merge_wait_limit();
+
+// Decode-attention workspace: a status line, the counter region (pass
+// queues, arrival and publication counts; zero between calls), then the
+// split partials pm | pl | pacc.
+constexpr int64_t kWsCounterRegionWords = 262144;  // 1 MiB
+constexpr int64_t kWsStatusWords = 64;              // status word + padding (two lines)
+constexpr int64_t kCounterWords = kWsCounterRegionWords - kWsStatusWords;
+constexpr int64_t kCounterBytes = kWsCounterRegionWords * 4;
+constexpr int64_t kCounterStride = 32;  // words between counters (no two share a line)
+struct WsLayout {
+  unsigned int* status;
+  unsigned int* counters;  // kCounterWords words
+  float* pm;
+  float* pl;
+  float* pacc;
+};
+WsLayout ws_layout(void* workspace, int64_t B, int64_t Hq, int n_splits);
 
 // Fused merge of the matrix-core split pass: the last workgroup of each
 // (batch, kv head, head group) combines the split partials with the raw
@@ -49,7 +78,19 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
                          unsigned int* counters, int64_t counter_words, int64_t stride,
-                         const MfmaFuse* fuse, hipStream_t st);
+                         unsigned int* status, const MfmaFuse* fuse, hipStream_t st);
+
+// fc_decode_attention's body: validates the arguments and enqueues the
+// requested parts (kPartSplit: the split pass over the archived blocks;
+// kPartMerge: the merge of the split partials with the raw tail, fused into
+// the split pass where it can be) with `workspace` as scratch.
+constexpr int kPartSplit = 1, kPartMerge = 2;
+int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
+                           int64_t Hq, int64_t Hkv, int64_t D, int store_kind, int stream_dtype,
+                           int r, int s, int64_t nb, const fc_stream_view* key,
+                           const fc_stream_view* value, int64_t n_raw, const float* A,
+                           float scale, void* out, int64_t o_sb, int64_t o_sh, void* workspace,
+                           int n_splits, void* stream, int parts);
 
 // Decode attention over a graph-capturable decode step (fc_decode_step with
 // a device state): one launch with the merge fused (matrix-core pass for

@@ -87,6 +87,16 @@ struct MfmaArgs {
   // decode-step state on the device (or NULL): (n_blocks, n_tail) before
   // the step's token; nb and n_raw are then taken from it (graph replays)
   const int64_t* state;
+  // status word of the workspace: set to FC_STATUS_MERGE_INCOMPLETE when a
+  // merging workgroup stops waiting for the other splits' publications
+  unsigned int* status;
+  // polls of the publication counter before the merge gives up (< 0: give
+  // up at once; a test knob that makes the give-up path run)
+  int spin_cap;
+  // static pass order (no queue): wavefront w of the group's n_splits * 4
+  // takes passes w, w + n_splits * 4, ...; fixed summation order, so the
+  // output is bitwise reproducible
+  int static_passes;
 };
 
 constexpr int kMThreads = 256;
@@ -100,7 +110,6 @@ constexpr float kLazyMax = 8.f;        // exponentials may reach 2^8 before a re
 constexpr int kTapsUnrolled = 16;      // softmax taps unrolled (block sizes up to 16)
 constexpr int kCachePolicyNt = 2;      // buffer load cache policy: nontemporal (streaming)
 constexpr int kPubWord = 1;            // publication counter: word 1 of a group's arrival line
-constexpr int kSpinCap = 1 << 24;      // polls of the publication counter before giving up
 
 // Orders this wavefront's LDS writes before its later LDS reads (lanes of a
 // wavefront exchange data through its private LDS region).
@@ -376,7 +385,11 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   const int64_t rows_total = nb * SROWS;
   const int64_t npass = (rows_total + PR - 1) / PR;
   unsigned int* passq = p.passq + g * p.cstride;
+  const unsigned int wslot = (unsigned int)(split * kWaves + wave);
+  const unsigned int wstride = (unsigned int)(p.n_splits * kWaves);
+  unsigned int wtaken = 0;
   auto grab = [&]() -> unsigned int {  // result in lane 0, read when needed
+    if (p.static_passes) return wslot + wstride * wtaken++;
     unsigned int v = 0;
     if (lane == 0) v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return v;
@@ -782,14 +795,29 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
     return;
   }
   if (tid == 0) {
+    // Ordering: every partial word was written by an agent-scope atomic
+    // store, which is performed at the device's coherence point (not held in
+    // the writer XCD's L2), and each publisher waited for its stores to
+    // complete (vmcnt(0)) before counting itself; the merge reads partials
+    // with agent-scope loads issued after it has seen the count, so no load
+    // can be served by a stale L2 line.  No cache-wide writeback or
+    // invalidate is needed (each costs ~0.1 us and they serialize per XCD).
     const unsigned int want = (unsigned int)p.n_splits - 1u;
-    for (int it = 0; it < kSpinCap; ++it) {
-      if (__hip_atomic_load(arrive + kPubWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= want)
-        break;
+    unsigned int seen = 0;
+    for (int it = 0; it < p.spin_cap; ++it) {
+      seen = __hip_atomic_load(arrive + kPubWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (seen >= want) break;
       __builtin_amdgcn_s_sleep(1);
     }
+    if (seen < want)  // merged without every partial: the host reads this word
+      __hip_atomic_store(p.status, (unsigned int)FC_STATUS_MERGE_INCOMPLETE, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(arrive + kPubWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // publications still in flight after a give-up add to the word later:
+    // subtracting what was expected (not storing 0) leaves it at zero once
+    // every publisher has counted itself, i.e. before the next call starts
+    __hip_atomic_fetch_add(arrive + kPubWord, 0u - want, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
@@ -822,7 +850,7 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
                          unsigned int* counters, int64_t counter_words, int64_t stride,
-                         const MfmaFuse* fuse, hipStream_t st) {
+                         unsigned int* status, const MfmaFuse* fuse, hipStream_t st) {
   MfmaArgs a{};
   a.q = q;
   a.q_dtype = q_dtype;
@@ -871,6 +899,9 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   if (!counters || 2 * a.ngroups * stride > counter_words) return FC_ERR_ARG;
   a.arrive = counters;
   a.passq = counters + counter_words / 2;
+  a.status = status;
+  a.spin_cap = merge_wait_limit();
+  a.static_passes = static_pass_order() ? 1 : 0;
   a.cstride = stride;
   const dim3 grid((unsigned)(a.ngroups * n_splits));
   const int rc = mfma_with_int<1, 2, 4>(s, [&](auto sc) {

@@ -714,6 +714,12 @@ int check_launch() {
   return FC_OK;
 }
 
+int hip_status(hipError_t e) {
+  if (e == hipSuccess) return FC_OK;
+  g_last_hip_error = (int)e;
+  return FC_ERR_HIP;
+}
+
 static bool aligned(const void* p, int64_t bytes) {
   return p == nullptr || ((uintptr_t)p % (uintptr_t)bytes) == 0;
 }
@@ -792,6 +798,9 @@ const char* fc_status_string(int status) {
     case FC_ERR_ARG: return "invalid argument";
     case FC_ERR_UNSUPPORTED: return "unsupported by this build's kernels";
     case FC_ERR_HIP: return "HIP runtime error";
+    case FC_ERR_INCOMPLETE:
+      return "a decode-attention merge stopped waiting for split partials; outputs written "
+             "since the workspace was last checked may be wrong";
     default: return "unknown status";
   }
 }

@@ -42,13 +42,18 @@ __global__ __launch_bounds__(kTailThreads) void tail_append_kernel(TailArgs a) {
   for (int64_t d = threadIdx.x; d < a.D; d += kTailThreads) dst[d] = src[d];
 }
 
-// state = (n_blocks, n_tail) after the step's token: one lane per word, so
-// the update goes out as ordinary vector stores
-__global__ void state_advance_kernel(int64_t* state, int64_t r) {
+// state = (n_blocks, n_tail, overflow) after the step's token: one lane per
+// word, so the update goes out as ordinary vector stores.  A block that
+// completes past the archives' capacity `cap` was not written by the gated
+// archive kernels (and the attention reads at most `cap` blocks): the
+// overflow word records it, sticky, for the host to check.
+__global__ void state_advance_kernel(int64_t* state, int64_t r, int64_t cap) {
   const int i = threadIdx.x;
-  if (i >= 2) return;
+  if (i >= 3) return;
   const int64_t nb = state[0], t = state[1] + 1;
-  const int64_t v[2] = {t == r ? nb + 1 : nb, t == r ? 0 : t};
+  const bool full = t == r;
+  const bool over = full && nb + 1 > cap;
+  const int64_t v[3] = {full ? nb + 1 : nb, full ? 0 : t, (state[2] != 0 || over) ? 1 : 0};
   state[i] = v[i];
 }
 
@@ -111,7 +116,9 @@ static int decode_step_state(const fc_step_args* a) {
                               a->out, a->o_sb, a->o_sh, a->workspace, a->workspace_bytes,
                               a->n_cu, a->state, a->stream);
   if (rc != FC_OK) return rc;
-  state_advance_kernel<<<1, 64, 0, stream>>>(const_cast<int64_t*>(a->state), r);
+  state_advance_kernel<<<1, 64, 0, stream>>>(const_cast<int64_t*>(a->state), r,
+                                             a->key.cap < a->value.cap ? a->key.cap
+                                                                       : a->value.cap);
   return check_launch();
 }
 

@@ -49,7 +49,9 @@ def prepare(cache, extra_tokens):
             st.discard_view()
             st._grow(need, like)
             st._tail_buffer(like)           # (B, H, r, D) in the stream dtype
-        state = torch.tensor([ks.n_blocks, ks._n_raw], dtype=torch.int64, device=like.device)
+        # (n_blocks, n_tail, overflow, padding)
+        state = torch.tensor([ks.n_blocks, ks._n_raw, 0, 0], dtype=torch.int64,
+                             device=like.device)
         ks._dev_state = vs._dev_state = state
         layer.keys = layer.values = None
 
@@ -69,19 +71,28 @@ def advance_host(cache, steps=1):
 
 
 def release(cache, check=True):
-    """Return the codec layers to host-driven decode steps; with `check`,
-    the device counters must equal the host ones."""
+    """Return the codec layers to host-driven decode steps.  With `check`,
+    the device counters must equal the host ones and no step may have run
+    past the archive capacity that prepare() reserved (a block completed
+    beyond it was not archived, so the outputs of the steps since are wrong):
+    RuntimeError otherwise."""
     for layer in _codec_layers(cache):
         ks, vs = layer._key_stream, layer._value_stream
         state = getattr(ks, "_dev_state", None)
         if state is None:
             continue
+        ks._dev_state = vs._dev_state = None
         if check:
-            nb, nt = (int(v) for v in state.cpu())
+            nb, nt, overflow = (int(v) for v in state[:3].cpu())
+            if overflow:
+                raise RuntimeError("graph decode steps ran past the archive capacity reserved "
+                                   "by prepare(); blocks past it were not archived")
             if (nb, nt) != (ks.n_blocks, ks._n_raw):
                 raise RuntimeError(f"device counters ({nb}, {nt}) differ from the host's "
                                    f"({ks.n_blocks}, {ks._n_raw})")
-        ks._dev_state = vs._dev_state = None
+    if check:
+        from .attention import check_workspaces
+        check_workspaces()
 
 
 class GraphDecoder:
@@ -103,7 +114,10 @@ class GraphDecoder:
         self.model, self.cache = model, cache
         dev = input_ids.device
         B = input_ids.shape[0]
-        prepare(cache, max_new_tokens + warmup)
+        # decode steps (eager warm-up ones included) the archives are sized for
+        self.capacity = int(max_new_tokens) + int(warmup)
+        self.steps = 0
+        prepare(cache, self.capacity)
         self.ids = input_ids.reshape(B, 1).clone()
         self.pos = torch.full((B, 1), int(position), dtype=torch.long, device=dev)
         cfg = model.config.get_text_config(decoder=True) if hasattr(model.config,
@@ -129,6 +143,7 @@ class GraphDecoder:
         return out.logits
 
     def _advance(self, logits):
+        self.steps += 1
         advance_host(self.cache)
         nxt = logits[:, -1].argmax(-1, keepdim=True)
         self.ids.copy_(nxt)
@@ -136,9 +151,15 @@ class GraphDecoder:
         self.pending.append(nxt.clone())
 
     def step(self):
-        """Replay one decode step; returns the (B, 1) greedy tokens."""
+        """Replay one decode step; returns the (B, 1) greedy tokens.  Raises
+        RuntimeError once the steps reserved at construction (max_new_tokens
+        + warmup) are used up: the archives hold no room for more blocks."""
+        if self.steps >= self.capacity:
+            raise RuntimeError(f"GraphDecoder reserved archive room for {self.capacity} decode "
+                               "steps (max_new_tokens + warmup); build a new decoder to go on")
         with torch.cuda.stream(self.stream):
             self.graph.replay()
+            self.steps += 1
             advance_host(self.cache)
             nxt = self.logits[:, -1].argmax(-1, keepdim=True)
             self.ids.copy_(nxt)

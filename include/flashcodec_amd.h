@@ -6,7 +6,8 @@
  * sizes, enqueues its kernels on the given HIP stream (`stream` is a
  * hipStream_t; NULL = the default stream) and returns an int status:
  * FC_OK (0) or one of the negative FC_ERR_* codes below.  Nothing here
- * allocates device memory, synchronises the stream or throws.
+ * allocates device memory or throws, and only fc_attention_workspace_status
+ * (which reads a result back) synchronises a stream.
  *
  * Layout conventions (all element strides, innermost dimension D is
  * contiguous, i.e. stride 1):
@@ -41,7 +42,9 @@ enum {
   FC_OK = 0,
   FC_ERR_ARG = -1,         /* invalid argument (shape, dtype, pointer)       */
   FC_ERR_UNSUPPORTED = -2, /* valid but outside this build's kernel limits   */
-  FC_ERR_HIP = -3          /* a HIP runtime call failed (see fc_last_hip_error) */
+  FC_ERR_HIP = -3,         /* a HIP runtime call failed (see fc_last_hip_error) */
+  FC_ERR_INCOMPLETE = -4   /* a fused decode-attention merge stopped waiting for
+                              split partials (fc_attention_workspace_status) */
 };
 
 /* Limits of the kernels in this library. */
@@ -256,6 +259,50 @@ int fc_decode_attention_merge(const void* q, int q_dtype, int64_t q_sb,
                               int n_splits, void* stream);
 
 /*
+ * Status of the decode attentions that used `workspace` since it was last
+ * checked: FC_OK, or FC_ERR_INCOMPLETE when a fused merge (the last
+ * workgroup of a head group) stopped waiting for the other splits'
+ * partials after its bounded wait and merged without them, so an output
+ * may be wrong.  Synchronizes `stream` (the one the calls were enqueued
+ * on), reads the workspace's status word and clears it.  Not for use
+ * inside a graph capture.  No reference counterpart (the reference's
+ * Triton path merges in a second kernel and has nothing to wait for,
+ * flashcodec/triton_attention.py:214-221).
+ */
+int fc_attention_workspace_status(void* workspace, void* stream);
+
+/* Split pass selection for fc_decode_attention / fc_decode_step. */
+enum {
+  FC_PASS_AUTO = 0,   /* matrix-core pass for the int8 jpeg archives it supports,
+                         its passes handed out by a queue (outputs may differ in
+                         the last bits between calls: fp32 summation order) */
+  FC_PASS_VECTOR = 1, /* vector-ALU pass for every store (A/B measurements) */
+  FC_PASS_STATIC = 2  /* as FC_PASS_AUTO with a fixed pass order: bitwise
+                         reproducible outputs, at some cost in balance */
+};
+
+/*
+ * Process-wide split pass selection (FC_PASS_*; FC_ERR_ARG otherwise) and
+ * its current value.  The initial value comes from the environment when
+ * the library is loaded (FLASHCODEC_AMD_ATTN=valu selects FC_PASS_VECTOR);
+ * calls never read the environment.  Changing it while calls are in flight
+ * on other threads is a race.  No reference counterpart (the reference picks
+ * Triton or torch per call through `impl`, flashcodec/attention.py:91-99).
+ */
+int fc_set_attention_pass(int pass);
+int fc_get_attention_pass(void);
+
+/*
+ * Polls of a publication counter before a fused merge gives up (default
+ * 2^24, several seconds; the other workgroups of the head group have
+ * arrived and need nothing more to finish).  A value <= 0 makes the merge
+ * give up at once: a test knob that runs the give-up path (status word,
+ * counter reset) with every kernel still exiting normally.  Process-wide;
+ * no reference counterpart.
+ */
+void fc_set_merge_wait_limit(int polls);
+
+/*
  * One stream (key or value) of a layer for fc_decode_step: its archive
  * buffers (as fc_stream_view), its (B, H, r, D) contiguous tail buffer in
  * the stream dtype (the raw tail is its first n_tail token rows), and the
@@ -294,7 +341,7 @@ typedef struct fc_step_args {
   int n_cu;              /* compute units of the device (split count) */
   void* stream;          /* hipStream_t */
   fc_step_stream key, value;
-  int64_t* state;        /* device (n_blocks, n_tail), or NULL: see below */
+  int64_t* state;        /* device (n_blocks, n_tail, overflow), or NULL: see below */
 } fc_step_args;
 
 /*
@@ -315,15 +362,16 @@ typedef struct fc_step_args {
 int fc_decode_step(const fc_step_args* args);
 /*
  * With args->state != NULL (any store kind), the step takes n_blocks and
- * n_tail from the two int64 words at `state` on the device and advances
- * them there (n_tail + 1 == r moves a block into the archive), so the
- * enqueued work is the same at every step and a captured HIP graph of it
- * stays valid: the archive kernels run gated on the state, the attention is
- * one launch with its merge fused.  args->n_blocks (>= 1) then only sizes
- * the split count; the archives must hold every block the replayed steps
- * will add (a block past `cap` is not written).
+ * n_tail from the first two of the three int64 words at `state` on the
+ * device and advances them there (n_tail + 1 == r moves a block into the
+ * archive), so the enqueued work is the same at every step and a captured
+ * HIP graph of it stays valid: the archive kernels run gated on the state,
+ * the attention is one launch with its merge fused.  args->n_blocks (>= 1)
+ * then only sizes the split count.  The archives must hold every block the
+ * replayed steps will add: a block past `cap` is not written, the attention
+ * reads at most `cap` blocks, and the third word (overflow, zero when the
+ * caller sets up the state) becomes 1 and stays 1, for the caller to check.
  */
-
 #ifdef __cplusplus
 }
 #endif

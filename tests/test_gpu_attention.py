@@ -128,20 +128,26 @@ CASES += [
 ]
 
 
-def _use_variant(monkeypatch, variant):
-    """auto: the default split pass (matrix cores for int8 jpeg); valu: the
-    vector-ALU pass, the only one for fp stores."""
-    if variant == "valu":
-        monkeypatch.setenv("FLASHCODEC_AMD_ATTN", "valu")
-    else:
-        monkeypatch.delenv("FLASHCODEC_AMD_ATTN", raising=False)
+@pytest.fixture
+def attention_pass():
+    """use(name) selects the split pass for this test ("auto": matrix cores
+    for int8 jpeg; "valu": the vector-ALU pass, the only one for fp stores);
+    the previous selection is restored afterwards."""
+    from flashcodec_amd import _native as N
+    prev = []
+
+    def use(name):
+        prev.append(N.set_attention_pass(name))
+    yield use
+    if prev:
+        N.set_attention_pass(prev[0])
 
 
 @pytest.fixture(params=["auto", "valu"])
-def split_variant(request, monkeypatch):
+def split_variant(request, attention_pass):
     """Run int8 cases on the matrix-core split pass (auto) and on the
     vector-ALU one."""
-    _use_variant(monkeypatch, request.param)
+    attention_pass(request.param)
     return request.param
 
 
@@ -152,9 +158,9 @@ ORACLE_CASES = [(c, "auto") for c in CASES] + [(c, "valu") for c in CASES
 
 @pytest.mark.parametrize("case,variant", ORACLE_CASES,
                          ids=[f"{v}-{c[0]}" for c, v in ORACLE_CASES])
-def test_decode_attention_matches_oracle(case, variant, oracle, monkeypatch):
+def test_decode_attention_matches_oracle(case, variant, oracle, attention_pass):
     name, cfg, dt, B, Hk, G, S, D = case
-    _use_variant(monkeypatch, variant)
+    attention_pass(variant)
     print(f"case attention/{name} [{variant}]", flush=True)
     seed = seed_of(name)
     ks, vs = build_streams(cfg, dt, B, Hk, S, D, seed % 10000, oracle)

@@ -1,0 +1,349 @@
+"""GPU: the decode attention at the BASELINE configurations' own shapes, on
+the kernel instantiations those configurations run, and through every entry
+that reaches it (plain call, fused decode step, device-state step, graph
+replay), each against the fp64 oracle on the streams' stored rows.
+
+Tolerances are the contract's (fp16 / bf16: 2e-3 of max|ref| plus half an
+ulp of the output dtype; fp32: 1e-5 absolute), as in test_gpu_attention.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import flashcodec_amd as fc
+from flashcodec_amd import _native as N
+from flashcodec_amd import attention as fa
+from flashcodec_amd.cache import _CodecStream
+from tests.conftest import to_values, torch_dtype
+from tests.test_gpu_attention import assert_close, build_streams, oracle_out
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+I8_C3 = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+
+
+def queries(B, Hq, D, seed, dt):
+    rng = np.random.default_rng(seed)
+    q = (rng.standard_normal((B, Hq, 1, D)) / math.sqrt(D)).astype(np.float32)
+    return torch.from_numpy(q).to(torch_dtype(dt)).to(DEV)
+
+
+@pytest.fixture
+def attention_pass():
+    """use(name) selects the split pass for one test; restored afterwards."""
+    prev = []
+
+    def use(name):
+        prev.append(N.set_attention_pass(name))
+    yield use
+    if prev:
+        N.set_attention_pass(prev[0])
+
+
+def test_c3_full_shape_every_sequence(oracle):
+    """BASELINE C3 as bench.py runs it: B=8, 32 q / 8 kv heads, D=128,
+    32768 archived tokens (r=8, k=4, int8) + 5 raw fp16 tokens, q fp16
+    N(0,1)/sqrt(D); the default split count (64 head groups x 8 splits, one
+    launch with the merge fused).  All 8 sequences against the oracle."""
+    B, Hkv, G, D, S = 8, 8, 4, 128, 32768 + 5
+    print("case c3 full shape", flush=True)
+    ks, vs = build_streams(I8_C3, "f16", B, Hkv, S, D, 303, oracle)
+    assert ks.n_blocks == 4096 and ks.raw.shape[-2] == 5
+    q = queries(B, Hkv * G, D, 304, "f16")
+    n_splits = N.lib().fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, 4, ks.n_blocks, B, Hkv,
+                                           G, D, N.num_cus(q.device))
+    assert 1 < n_splits <= 64                    # the fused (one-launch) merge
+    out = fc.codec_decode_attention(q, ks, vs)
+    fa.check_workspaces()
+    ref = oracle_out(oracle, q, ks, vs, D ** -0.5)
+    assert_close(to_values(out)[:, :, 0], ref, "f16")
+
+
+def test_c5_attention_instantiation(oracle):
+    """The decode attention of the C5 model's first decode step: bf16,
+    16 q / 8 kv heads (G=2), D=128, k=4 int8, batch 16 over a 4096-token
+    prompt plus the step's token (matrix-core pass <s=4, D=128, G=2>)."""
+    B, Hkv, G, D, S = 16, 8, 2, 128, 4096 + 1
+    print("case c5 attention shape", flush=True)
+    ks, vs = build_streams(I8_C3, "bf16", B, Hkv, S, D, 505, oracle)
+    q = queries(B, Hkv * G, D, 506, "bf16")
+    out = fc.codec_decode_attention(q, ks, vs)
+    fa.check_workspaces()
+    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "bf16")
+
+
+@pytest.mark.parametrize("keep", [0.25, 1.0])
+def test_c4_png_full_shape(keep, oracle):
+    """BASELINE C4: png fp32 (2, 8, 16384, 128), r=16, keep_ratio 0.25 and
+    1.0, decode attention with 32 q heads (fp32 queries: 1e-5 absolute)."""
+    B, Hkv, G, D, S = 2, 8, 4, 128, 16384
+    print(f"case c4 png keep={keep}", flush=True)
+    cfg = dict(mode="png", block_size=16, keep_ratio=keep)
+    ks, vs = build_streams(cfg, "f32", B, Hkv, S, D, 404, oracle)
+    assert ks.n_blocks == 1024 and ks.raw is None
+    q = queries(B, Hkv * G, D, 405, "f32")
+    out = fc.codec_decode_attention(q, ks, vs)
+    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "f32")
+
+
+@pytest.mark.parametrize("dt,G,D", [("f16", 4, 128), ("bf16", 2, 128), ("f16", 8, 64),
+                                    ("bf16", 4, 256)])
+def test_outlier_queries_on_matrix_cores(dt, G, D, oracle):
+    """Queries with a few features 100x (and one head with a 1000x
+    feature), the shape of real LLM queries: the matrix-core pass rounds each
+    head's query to 14-bit integers relative to its largest element, which
+    such heads stress most."""
+    B, Hkv, S = 2, 2, 8 * 700 + 3
+    print(f"case outlier queries {dt} G={G} D={D}", flush=True)
+    ks, vs = build_streams(I8_C3, dt, B, Hkv, S, D, 606 + G + D, oracle)
+    rng = np.random.default_rng(607)
+    qn = (rng.standard_normal((B, Hkv * G, 1, D)) / math.sqrt(D)).astype(np.float32)
+    for b in range(B):
+        for h in range(Hkv * G):
+            qn[b, h, 0, rng.choice(D, 4, replace=False)] *= 100.0
+    qn[0, 0, 0, 3] = 1000.0 / math.sqrt(D)
+    q = torch.from_numpy(qn).to(torch_dtype(dt)).to(DEV)
+    out = fc.codec_decode_attention(q, ks, vs)
+    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), dt)
+
+
+def test_impl_selectors_reference_style(oracle):
+    """The reference's own check (tests/test_attention.py:100-115): impl
+    "torch" and "triton" agree within 2e-3 on bf16 jpeg stores (int8 k=2,
+    and unquantised k=4), "auto" returns the query dtype; here every
+    selector runs the HIP kernels, so they also match the oracle."""
+    torch.manual_seed(0)
+    B, Hk, D, S, g = 1, 8, 128, 4096, 2
+    k = torch.randn(B, Hk, S, D, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, Hk, S, D, device=DEV, dtype=torch.bfloat16)
+    q = torch.randn(B, Hk * g, 1, D, device=DEV, dtype=torch.bfloat16)
+    for cfg in (dict(keep_freqs=2, quant_bits=8), dict(keep_freqs=4)):
+        ks = _CodecStream(fc.make_codec("jpeg", block_size=8, **cfg))
+        vs = _CodecStream(fc.make_codec("jpeg", block_size=8, **cfg))
+        ks.append(k)
+        vs.append(v)
+        ref = fc.codec_decode_attention(q, ks, vs, impl="torch")
+        tri = fc.codec_decode_attention(q, ks, vs, impl="triton")
+        d = (ref.float() - tri.float()).abs().max().item()
+        assert d < 2e-3, f"triton vs torch mismatch: {cfg} maxdiff={d:.2e}"
+        auto = fc.codec_decode_attention(q, ks, vs)
+        assert auto.dtype == q.dtype
+        assert_close(to_values(auto)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "bf16")
+
+
+def test_static_pass_order_is_bitwise_reproducible(oracle, attention_pass):
+    """FC_PASS_STATIC: the matrix-core pass with a fixed pass order gives
+    bitwise-equal outputs call after call, within tolerance of the oracle
+    and of the queue-driven default."""
+    B, Hkv, G, D, S = 2, 4, 4, 128, 8 * 2000 + 5
+    ks, vs = build_streams(I8_C3, "f16", B, Hkv, S, D, 808, oracle)
+    q = queries(B, Hkv * G, D, 809, "f16")
+    auto = fc.codec_decode_attention(q, ks, vs)
+    attention_pass("static")
+    outs = [fc.codec_decode_attention(q, ks, vs) for _ in range(5)]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ref = oracle_out(oracle, q, ks, vs, D ** -0.5)
+    assert_close(to_values(outs[0])[:, :, 0], ref, "f16")
+    assert_close(to_values(auto)[:, :, 0], ref, "f16")
+
+
+def test_merge_give_up_is_reported_and_recovers(oracle):
+    """A fused merge whose bounded wait gives up (forced from the host: a
+    wait limit of 0 polls) sets the workspace status, which
+    check_workspaces() reports as IncompleteMergeError; the counters it
+    leaves behind are zero again, so the next call with the normal limit is
+    correct and reports nothing."""
+    B, Hkv, G, D, S = 2, 4, 4, 128, 8 * 3000 + 5
+    ks, vs = build_streams(I8_C3, "f16", B, Hkv, S, D, 909, oracle)
+    q = queries(B, Hkv * G, D, 910, "f16")
+    fa.check_workspaces()
+    L = N.lib()
+    try:
+        L.fc_set_merge_wait_limit(0)
+        fc.codec_decode_attention(q, ks, vs, _n_splits=8)
+        with pytest.raises(N.IncompleteMergeError):
+            fa.check_workspaces()
+    finally:
+        L.fc_set_merge_wait_limit(1 << 24)
+    for _ in range(3):
+        out = fc.codec_decode_attention(q, ks, vs, _n_splits=8)
+        fa.check_workspaces()
+        assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "f16")
+
+
+STEP_CFGS = [(I8_C3, "bf16", 2), (I8_C3, "f16", 4),
+             (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 4),
+             (dict(mode="png", block_size=8, keep_ratio=0.5), "f16", 2)]
+
+
+def _tokens(g, B, H, D, dt):
+    """(B, H, 1, D) with the strides of an HF projection: (B, 1, H, D) transposed."""
+    return torch.randn((B, 1, H, D), generator=g, device=DEV).to(torch_dtype(dt)).transpose(1, 2)
+
+
+@pytest.mark.parametrize("cfg,dt,G", STEP_CFGS, ids=["i8-bf16", "i8-f16", "fp-f32", "png-f16"])
+def test_fused_decode_step_matches_oracle(cfg, dt, G, oracle):
+    """codec_decode_step (token append + block archive + attention in one
+    library call) against the oracle on the streams' rows after each step,
+    across three block boundaries."""
+    B, Hkv, D, r = 2, 2, 128, cfg["block_size"]
+    print(f"case fused step vs oracle {cfg} {dt}", flush=True)
+    ks, vs = build_streams(cfg, dt, B, Hkv, 5 * r + 3, D, 111, oracle)
+    g = torch.Generator(device=DEV).manual_seed(112)
+    for _ in range(3 * r + 1):
+        q = _tokens(g, B, Hkv * G, D, dt)
+        out = fc.codec_decode_step(q, _tokens(g, B, Hkv, D, dt), _tokens(g, B, Hkv, D, dt), ks, vs)
+        assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), dt)
+    fa.check_workspaces()
+
+
+class _Cache:
+    """The part of an HF cache that graph.prepare reads: a list of codec layers."""
+
+    def __init__(self, layers):
+        self.layers = layers
+
+
+def _codec_layer(cfg, ks, vs):
+    from flashcodec_amd.cache import FlashCodecLayer
+    layer = FlashCodecLayer(**cfg)
+    layer._key_stream, layer._value_stream = ks, vs
+    layer.codec = ks.codec
+    return layer
+
+
+@pytest.mark.parametrize("cfg,dt,G", STEP_CFGS, ids=["i8-bf16", "i8-f16", "fp-f32", "png-f16"])
+def test_graph_replayed_steps_match_oracle(cfg, dt, G, oracle):
+    """One device-state decode step captured as a HIP graph and replayed
+    with new query / key / value tokens copied into its input buffers: every
+    replay's output against the oracle on the streams' rows (host counters
+    advanced after each replay), with eager work between replays."""
+    pytest.importorskip("transformers")
+    from flashcodec_amd import graph
+    B, Hkv, D, r = 2, 2, 128, cfg["block_size"]
+    steps = 3 * r + 2
+    print(f"case graph step vs oracle {cfg} {dt}", flush=True)
+    ks, vs = build_streams(cfg, dt, B, Hkv, 4 * r + 5, D, 222, oracle)
+    cache = _Cache([_codec_layer(cfg, ks, vs)])
+    graph.prepare(cache, steps + 1)
+    g = torch.Generator(device=DEV).manual_seed(223)
+    q_in = torch.zeros((B, 1, Hkv * G, D), device=DEV, dtype=torch_dtype(dt)).transpose(1, 2)
+    k_in = torch.zeros((B, 1, Hkv, D), device=DEV, dtype=torch_dtype(dt)).transpose(1, 2)
+    v_in = torch.zeros_like(k_in)
+    stream = torch.cuda.Stream()
+
+    def fill():
+        q_in.copy_(_tokens(g, B, Hkv * G, D, dt))
+        k_in.copy_(_tokens(g, B, Hkv, D, dt))
+        v_in.copy_(_tokens(g, B, Hkv, D, dt))
+
+    # one eager device-state step on the capture stream creates its workspace
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fill()
+        out = fc.codec_decode_step(q_in, k_in, v_in, ks, vs)
+    torch.cuda.synchronize()
+    graph.advance_host(cache)
+    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q_in, ks, vs, D ** -0.5), dt)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=stream):
+        out = fc.codec_decode_step(q_in, k_in, v_in, ks, vs)
+    for i in range(steps):
+        fill()
+        gr.replay()
+        torch.cuda.synchronize()
+        graph.advance_host(cache)
+        assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q_in, ks, vs, D ** -0.5), dt)
+        _ = (torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)).sum()
+        torch.cuda.synchronize()
+    graph.release(cache)                      # device counters == host counters, no overflow
+
+
+def test_graph_step_past_reserved_capacity_is_reported(oracle):
+    """Device-state steps beyond the room prepare() reserved: the block that
+    does not fit is not archived, and release() reports it."""
+    pytest.importorskip("transformers")
+    from flashcodec_amd import graph
+    B, Hkv, G, D, r = 1, 2, 2, 64, 8
+    ks, vs = build_streams(I8_C3, "f16", B, Hkv, 16 * r, D, 333, oracle)
+    assert ks.n_blocks == 16 and ks._capacity == 16
+    cache = _Cache([_codec_layer(I8_C3, ks, vs)])
+    graph.prepare(cache, 0)                   # room for one more block: 17 -> capacity 32
+    g = torch.Generator(device=DEV).manual_seed(334)
+    for _ in range(16 * r + 2 * r):           # 18 more blocks: two past the 32
+        fc.codec_decode_step(_tokens(g, B, Hkv * G, D, "f16"), _tokens(g, B, Hkv, D, "f16"),
+                             _tokens(g, B, Hkv, D, "f16"), ks, vs)
+        graph.advance_host(cache)
+    with pytest.raises(RuntimeError, match="capacity"):
+        graph.release(cache)
+
+
+def test_graph_decoder_refuses_steps_past_capacity():
+    """GraphDecoder counts its steps and raises before a replay that would
+    need archive room prepare() did not reserve."""
+    pytest.importorskip("transformers")
+    from flashcodec_amd import graph
+    from tests.test_gpu_graph import prefill, tiny_qwen3
+    model = tiny_qwen3(torch.float16, I8_C3)
+    prompt = torch.randint(1, 512, (2, 19), generator=torch.Generator().manual_seed(3)).cuda()
+    cache = prefill(model, prompt)
+    dec = graph.GraphDecoder(model, cache, prompt[:, -1:], position=19, max_new_tokens=4,
+                             warmup=1)
+    toks = dec.generate(5)                    # 1 warm-up step + 4 replays
+    assert toks.shape == (2, 5)
+    with pytest.raises(RuntimeError, match="reserved"):
+        dec.step()
+    dec.close()
+
+
+def test_c5_full_shape_materialization_free_tracks_materialized():
+    """BASELINE C5's model at full shape (Qwen3-0.6B dims: 28 layers, hidden
+    1024, 16 q / 8 kv heads, head_dim 128, bf16, random init), batch 16,
+    4096-token prompt, 16 teacher-forced decode steps, jpeg r=8 k=4 int8:
+    the materialisation-free logits track the materialised codec path (the
+    reference's own semantics) and every layer takes the codec step."""
+    pytest.importorskip("transformers")
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    cfg = Qwen3Config(vocab_size=151936, hidden_size=1024, intermediate_size=3072,
+                      num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8,
+                      head_dim=128, max_position_embeddings=8192, tie_word_embeddings=True)
+    torch.manual_seed(0)
+    with torch.device(DEV):
+        model = Qwen3ForCausalLM(cfg).to(torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(1)
+    B, P, steps = 16, 4096, 16
+    ids = torch.randint(1, cfg.vocab_size, (B, P), generator=g).to(DEV)
+    forced = torch.randint(1, cfg.vocab_size, (B, steps), generator=g).to(DEV)
+    codec = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+
+    def run(materialization_free):
+        print(f"case c5 full shape, materialization_free={materialization_free}", flush=True)
+        fc.apply_flash_codec(model, materialization_free=materialization_free, **codec)
+        logits = []
+        with torch.no_grad():
+            out = model(input_ids=ids, use_cache=True, logits_to_keep=1)
+            pkv = out.past_key_values
+            for i in range(steps):
+                pos = torch.full((B, 1), P + i, dtype=torch.long, device=DEV)
+                out = model(input_ids=forced[:, i:i + 1], position_ids=pos, past_key_values=pkv,
+                            use_cache=True, logits_to_keep=1)
+                logits.append(out.logits[:, -1].float())
+        counts = [getattr(m, "_flashcodec_codec_steps", 0)
+                  for m in fc.find_attention_modules(model)]
+        fc.remove_flash_codec(model)
+        del pkv, out
+        torch.cuda.empty_cache()
+        return logits, counts
+
+    ref, counts_m = run(False)
+    got, counts_f = run(True)
+    assert counts_m == [0] * 28
+    assert counts_f == [steps] * 28, counts_f
+    fa.check_workspaces()
+    for i, (a, b) in enumerate(zip(ref, got)):
+        err = (a - b).abs().max().item()
+        assert err <= 3e-2 * a.abs().max().item(), (i, err)

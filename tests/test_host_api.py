@@ -68,10 +68,17 @@ def test_decode_attention_argument_errors():
     vs = _CodecStream(fc.make_codec("jpeg"))
     with pytest.raises(ValueError):
         fc.codec_decode_attention(torch.randn(1, 2, 4, 8), ks, vs)       # prefill shape
-    with pytest.raises(ValueError):
-        fc.codec_decode_attention(torch.randn(1, 2, 1, 8), ks, vs, impl="torch")
-    # empty cache: zeros, no device work
-    out = fc.codec_decode_attention(torch.randn(1, 2, 1, 8), ks, vs)
+    # the reference's impl="triton" raises when its Triton path cannot run a
+    # jpeg case (here: an empty archive; flashcodec/attention.py:91-99)
+    with pytest.raises(RuntimeError, match="triton"):
+        fc.codec_decode_attention(torch.randn(1, 2, 1, 8), ks, vs, impl="triton")
+    # empty cache: zeros, no device work, whichever implementation is named
+    for impl in ("auto", "torch", "hip"):
+        out = fc.codec_decode_attention(torch.randn(1, 2, 1, 8), ks, vs, impl=impl)
+        assert torch.equal(out, torch.zeros(1, 2, 1, 8))
+    # png stores never take the reference's Triton branch: no error there
+    ps = _CodecStream(fc.make_codec("png")), _CodecStream(fc.make_codec("png"))
+    out = fc.codec_decode_attention(torch.randn(1, 2, 1, 8), *ps, impl="triton")
     assert torch.equal(out, torch.zeros(1, 2, 1, 8))
 
 
