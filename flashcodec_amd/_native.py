@@ -14,7 +14,8 @@ import torch
 from . import _build
 
 F32, F16, BF16, I8 = 0, 1, 2, 3
-OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_INCOMPLETE = 0, -1, -2, -3, -4
+OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_INCOMPLETE, ERR_SCRATCH = 0, -1, -2, -3, -4, -5
+NOALLOC_SCRATCH_BYTES = 16 << 20
 PASS_AUTO, PASS_VECTOR, PASS_STATIC = 0, 1, 2
 STORE_JPEG_I8, STORE_JPEG_FP, STORE_PNG = 0, 1, 2
 MAX_BLOCK = 64
@@ -85,6 +86,7 @@ SIGNATURES = {
     "fc_png_topm_mask_host": (ctypes.c_uint64, [_vp, _int, _int]),
     "fc_decode_step": (_int, [ctypes.POINTER(StepArgs)]),
     "fc_attention_workspace_status": (_int, [_vp, _vp]),
+    "fc_decode_attention_noalloc": (_int, _ATTN_SIG[1][:21] + [_int, _vp]),
     "fc_set_attention_pass": (_int, [_int]),
     "fc_get_attention_pass": (_int, []),
     "fc_set_merge_wait_limit": (None, [_int]),

@@ -1471,8 +1471,12 @@ int fc_decode_attention_merge(FC_ATTN_PARAMS) {
 }
 
 int fc_attention_workspace_status(void* workspace, void* stream) {
-  if (!workspace) return FC_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
+  if (!workspace) {
+    int rc = FC_OK;
+    workspace = noalloc_scratch(st, &rc);  // the static scratch of this device
+    if (!workspace) return rc;
+  }
   unsigned int word = 0;
   int rc = hip_status(hipMemcpyAsync(&word, workspace, sizeof(word), hipMemcpyDeviceToHost, st));
   if (rc == FC_OK) rc = hip_status(hipStreamSynchronize(st));

@@ -92,6 +92,11 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                            float scale, void* out, int64_t o_sb, int64_t o_sh, void* workspace,
                            int n_splits, void* stream, int parts);
 
+// Device address of the static scratch array of fc_decode_attention_noalloc
+// on the current device (looked up, and its counters cleared, on the first
+// call per device), or NULL with *rc set.
+void* noalloc_scratch(hipStream_t stream, int* rc);
+
 // Decode attention over a graph-capturable decode step (fc_decode_step with
 // a device state): one launch with the merge fused (matrix-core pass for
 // int8 jpeg archives it supports, else the vector-ALU pass), block and tail

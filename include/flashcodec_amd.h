@@ -43,8 +43,10 @@ enum {
   FC_ERR_ARG = -1,         /* invalid argument (shape, dtype, pointer)       */
   FC_ERR_UNSUPPORTED = -2, /* valid but outside this build's kernel limits   */
   FC_ERR_HIP = -3,         /* a HIP runtime call failed (see fc_last_hip_error) */
-  FC_ERR_INCOMPLETE = -4   /* a fused decode-attention merge stopped waiting for
+  FC_ERR_INCOMPLETE = -4,  /* a fused decode-attention merge stopped waiting for
                               split partials (fc_attention_workspace_status) */
+  FC_ERR_SCRATCH = -5      /* the call needs more scratch than the static array of
+                              fc_decode_attention_noalloc holds */
 };
 
 /* Limits of the kernels in this library. */
@@ -264,12 +266,42 @@ int fc_decode_attention_merge(const void* q, int q_dtype, int64_t q_sb,
  * workgroup of a head group) stopped waiting for the other splits'
  * partials after its bounded wait and merged without them, so an output
  * may be wrong.  Synchronizes `stream` (the one the calls were enqueued
- * on), reads the workspace's status word and clears it.  Not for use
- * inside a graph capture.  No reference counterpart (the reference's
- * Triton path merges in a second kernel and has nothing to wait for,
- * flashcodec/triton_attention.py:214-221).
+ * on), reads the workspace's status word and clears it.  workspace == NULL
+ * checks the static scratch of fc_decode_attention_noalloc on the current
+ * device.  Not for use inside a graph capture.  No reference counterpart
+ * (the reference's Triton path merges in a second kernel and has nothing
+ * to wait for, flashcodec/triton_attention.py:214-221).
  */
 int fc_attention_workspace_status(void* workspace, void* stream);
+
+/* Bytes of the static scratch array of fc_decode_attention_noalloc (one per
+ * GPU, held until the process ends). */
+#define FC_NOALLOC_SCRATCH_BYTES (16 << 20)
+
+/*
+ * fc_decode_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the workspace is a static device
+ * array of this library, FC_NOALLOC_SCRATCH_BYTES per GPU, looked up on the
+ * first call on a device; nothing is allocated, ever.  Arguments, results
+ * and split count rules as fc_decode_attention (the caller still passes q,
+ * the stores and out).  A call whose fc_attention_workspace_bytes(B, Hq, D,
+ * n_splits) exceeds FC_NOALLOC_SCRATCH_BYTES returns FC_ERR_SCRATCH.  All
+ * calls on one GPU share the array (the last call's contents stay in it;
+ * every call returns its counters to zero): calls that overlap on one GPU
+ * (several streams or threads) race and must not be issued.
+ * No counterpart in the reference; it exists for the callers that cannot
+ * allocate.
+ */
+int fc_decode_attention_noalloc(const void* q, int q_dtype, int64_t q_sb,
+                                int64_t q_sh, int64_t B, int64_t Hq,
+                                int64_t Hkv, int64_t D, int store_kind,
+                                int stream_dtype, int r, int s, int64_t nb,
+                                const fc_stream_view* key,
+                                const fc_stream_view* value, int64_t n_raw,
+                                const float* A, float scale, void* out,
+                                int64_t o_sb, int64_t o_sh, int n_splits,
+                                void* stream);
 
 /* Split pass selection for fc_decode_attention / fc_decode_step. */
 enum {
