@@ -13,15 +13,19 @@ merges the split partials with the raw tail.  `value` is algorithmic GB/s of
 the call:
   K+V int8 codes 2*134,217,728 + fp32 scales 2*4,194,304 + raw tails
   163,840 + q 65,536 + out 65,536 = 277,118,976 bytes per call.
-The roofline object covers that kernel, each launch timed with HIP events on
-the stream it is launched on.  With `--rotating-sets N` (N >= 2) a
-`rotating_sets` object times the same launches cycling over N copies of the
-archives (as a decode step cycles over its layers' caches), so that no launch
-finds data a previous one left in the caches.  `cpu_baseline` times the fp64
-CPU oracle on the same workload's sequences for at least 10 s (one whole
-call or more).
+The timed steps cycle over --sets copies of the archives (default 4, 1.1 GB:
+more than the 256 MB last-level cache can hold, as a decode step cycles over
+its layers' caches), so each call streams its archive from HBM; the same
+launches repeated on one set (largely served by the last-level cache) are
+reported as `single_set`.  The roofline object covers the kernel, each
+launch timed with HIP events on the stream it is launched on.  Every
+sequence of the output is checked against the fp64 CPU oracle (exit status
+3 above the 2e-3 tolerance).  `cpu_baseline` times the reference's torch
+CPU path (this build's restatement of flashcodec/attention.py:101-140,
+oracle/torch_path.py) on all host cores for a bounded sample of the same
+workload.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--sets N]
   python bench.py --mode copy     # plain copy, for PMC byte calibration
 """
 
@@ -89,13 +93,17 @@ def copy_mode(args):
                       "read_plus_write_GBs": 2 * n / ms / 1e6}))
 
 
-def split_kernel_name():
+def split_kernel_name(n_splits):
     """Kernel of this workload's call (int8 codes, fp16 q, D=128, 4 rows per
-    block, groups of 4 q heads): the matrix-core split pass with its merge
-    fused in (one launch)."""
-    if os.environ.get("FLASHCODEC_AMD_ATTN", "").startswith("v"):
-        return "attn_split_kernel + attn_merge_head_kernel"
-    return "attn_split_i8_mfma<4,4,4> (merge fused)"
+    block, groups of 4 q heads): the matrix-core split pass, its merge fused
+    in when the split count allows (one launch)."""
+    from flashcodec_amd import _native as N
+    from flashcodec_amd.attention import launches_per_call
+    if N.lib().fc_get_attention_pass() == N.PASS_VECTOR:
+        return "attn_split_kernel (merge fused)"
+    if launches_per_call(N.STORE_JPEG_I8, n_splits) == 1:
+        return "attn_split_i8_mfma<4,4,4> (merge fused)"
+    return "attn_split_i8_mfma<4,4,4> + attn_merge_head_kernel"
 
 
 def cpu_model():
@@ -499,8 +507,11 @@ def c5_mode(args):
 
 def read_pmc_traffic():
     """HBM bytes per launch of the matrix-core kernel from the committed PMC
-    summary, if any (None for the vector-ALU variant, which it does not cover)."""
-    if os.environ.get("FLASHCODEC_AMD_ATTN", "").startswith("v") or not os.path.exists(PMC_SUMMARY):
+    summary (rocprofv3 FETCH_SIZE / WRITE_SIZE of this workload, scaled by
+    the copy-kernel calibration), or None when the vector-ALU pass runs or
+    no summary exists.  Not measured by this process."""
+    from flashcodec_amd import _native as N
+    if N.lib().fc_get_attention_pass() == N.PASS_VECTOR or not os.path.exists(PMC_SUMMARY):
         return None
     for line in open(PMC_SUMMARY):
         if line.startswith("traffic_bytes_per_launch:"):
@@ -508,44 +519,220 @@ def read_pmc_traffic():
     return None
 
 
-def cpu_baseline(q, ks, vs, min_seconds=10.0):
-    """The CPU restatement of the path (oracle/) on the same workload: per
-    sequence, dequantise the int8 K/V codes to rows and run fp64 decode
-    attention over 32 q heads.  Sequences are taken in turn until at least
-    `min_seconds` have passed and every sequence has run once (one whole
-    call); host copies of the codes are made before the clock starts.
-    Returns (sequence-0 output, baseline record)."""
+def cpu_baseline(ks, vs, q, min_seconds=10.0):
+    """The reference's CPU path on this workload: its torch decode attention
+    (oracle/torch_path.py, the restatement of flashcodec/attention.py:101-140
+    pinned bit-exact against the reference's outputs) on one sequence at a
+    time, dequantising that sequence's int8 rows into the query dtype first
+    as the reference does per call; all host cores; sequences taken in turn
+    until `min_seconds` have passed.  Host copies of the codes are made
+    before the clock starts."""
+    import torch
+    from oracle import torch_path
+    import flashcodec_amd as fc
+    cores = len(os.sched_getaffinity(0))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    codes = [st._coeffs[:, :, :NB].cpu() for st in (ks, vs)]
+    scales = [st._scales[:, :, :NB].cpu() for st in (ks, vs)]
+    raws = [st.raw.cpu() for st in (ks, vs)]
+    A = fc.dct_basis(R, K).t()
+    qc = q.cpu()
+
+    def one(b):
+        sl = slice(b, b + 1)
+        rk = torch_path.jpeg_rows(codes[0][sl], scales[0][sl], qc.dtype)
+        rv = torch_path.jpeg_rows(codes[1][sl], scales[1][sl], qc.dtype)
+        return torch_path.decode_attention(qc[sl], rk, rv, raws[0][sl], raws[1][sl], A,
+                                           D ** -0.5)
+
+    one(0)                                        # warm-up
+    done = 0
+    t0 = time.perf_counter()
+    while done < B or time.perf_counter() - t0 < min_seconds:
+        one(done % B)
+        done += 1
+    dt = time.perf_counter() - t0
+    torch.set_num_threads(prev)
+    seq_bytes = ALG_BYTES_CALL / B
+    return {"value": round(done * seq_bytes / dt / 1e9, 3), "unit": "GB/s",
+            "cores": cores, "kind": "port",
+            "sample": f"{done} sequences of the workload ({done / B:.2f} calls) through the "
+                      "reference's torch CPU decode attention (restated in oracle/torch_path.py): "
+                      "int8 rows dequantised to fp16, fp16 einsums, fp32 softmax, over 32 q "
+                      "heads x (32768 archived + 5 raw tokens)",
+            "seconds": round(dt, 3), "cpu_model": cpu_model(),
+            "torch_threads": cores}
+
+
+def check_against_oracle(q, ks, vs, out):
+    """Max error of every sequence of `out` against the fp64 oracle,
+    relative to max|ref| (the contract's 2e-3 for fp16 outputs)."""
     import numpy as np
     from oracle import oracle as O
     import flashcodec_amd as fc
-    threads = min(len(os.sched_getaffinity(0)), 16)
-    codes = [st._coeffs[:, :, :NB].cpu().numpy() for st in (ks, vs)]
-    scales = [st._scales[:, :, :NB, :, 0].cpu().numpy() for st in (ks, vs)]
+    rows = [O.stored_rows_jpeg(st._coeffs[:, :, :NB].cpu().numpy(),
+                               st._scales[:, :, :NB, :, 0].cpu().numpy()) for st in (ks, vs)]
     raws = [st.raw.float().cpu().numpy() for st in (ks, vs)]
     A = O.synthesis_matrix("jpeg", R, fc.dct_basis(R, K).numpy())
-    qn = q[:, :, 0].float().cpu().numpy()
+    ref = O.attention(q[:, :, 0].float().cpu().numpy(), rows[0], rows[1], raws[0], raws[1], A,
+                      D ** -0.5, n_threads=min(16, len(os.sched_getaffinity(0))))
+    got = out[:, :, 0].float().cpu().numpy()
+    per_seq = np.abs(got - ref).reshape(B, -1).max(-1) / np.abs(ref).max()
+    return float(per_seq.max()), [float(e) for e in per_seq]
 
-    def one(b):
-        rk = O.stored_rows_jpeg(codes[0][b:b + 1], scales[0][b:b + 1])
-        rv = O.stored_rows_jpeg(codes[1][b:b + 1], scales[1][b:b + 1])
-        return O.attention(qn[b:b + 1], rk, rv, raws[0][b:b + 1], raws[1][b:b + 1], A,
-                           D ** -0.5, n_threads=threads)
 
-    ref0, done = None, 0
-    t0 = time.perf_counter()
-    while done < B or time.perf_counter() - t0 < min_seconds:
-        o = one(done % B)
-        if done == 0:
-            ref0 = o
-        done += 1
-    dt = time.perf_counter() - t0
-    seq_bytes = ALG_BYTES_CALL / B
-    return ref0, {"value": round(done * seq_bytes / dt / 1e9, 3), "unit": "GB/s",
-                  "cores": threads, "kind": "port",
-                  "sample": f"{done} sequences of the workload ({done / B:.2f} calls): int8 "
-                            "codes -> fp64 rows (numpy) -> fp64 decode attention over 32 q "
-                            "heads x (32768 archived + 5 raw tokens) (C++ oracle, OpenMP)",
-                  "seconds": round(dt, 3), "cpu_model": cpu_model()}
+def archive_copy(st):
+    """Another stream holding a copy of `st`'s archive and tail (its own
+    buffers): one more set for the rotating measurement."""
+    from flashcodec_amd.cache import _CodecStream
+    c = _CodecStream(st.codec)
+    c._coeffs, c._scales = st._coeffs.clone(), st._scales.clone()
+    c._capacity, c.n_blocks, c.n_archived = st._capacity, st.n_blocks, st.n_archived
+    c.dtype, c.meta = st.dtype, st.meta
+    c._raw_buf, c._n_raw = st._raw_buf.clone(), st._n_raw
+    return c
+
+
+def c3_mode(args):
+    import torch
+    import flashcodec_amd as fc
+    from flashcodec_amd import _native as N
+    from flashcodec_amd.attention import _device_A, _view, check_workspaces, launches_per_call
+    from flashcodec_amd.cache import _CodecStream
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("bench: generating AR(1) K/V and archiving them")
+    S = S_ARCH + TAIL
+    cfg = dict(mode="jpeg", block_size=R, keep_freqs=K, quant_bits=8)
+    ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
+    for st, seed in ((ks, 1), (vs, 2)):
+        x = ar1_device((B, HKV, S, D), 0.95, seed, dev).to(torch.float16)
+        st.append(x)
+        del x
+    torch.cuda.empty_cache()
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = (torch.randn((B, HQ, 1, D), generator=g, device=dev) / math.sqrt(D)).to(torch.float16)
+    assert ks.n_blocks == NB and ks.raw.shape[-2] == TAIL
+    n_sets = max(1, args.sets)
+    sets = [(ks, vs)] + [(archive_copy(ks), archive_copy(vs)) for _ in range(n_sets - 1)]
+
+    L = N.lib()
+    n_splits = args.splits or L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, K, NB, B, HKV,
+                                                    HQ // HKV, D, N.num_cus(dev))
+    keep = []
+    A = _device_A(ks.codec, R, dev)
+    out_c = torch.empty_like(q)
+    # zero-filled once: its counters return to zero after every call
+    ws = torch.zeros(L.fc_attention_workspace_bytes(B, HQ, D, n_splits), dtype=torch.uint8,
+                     device=dev)
+
+    def abi_args(kst, vst):
+        return (q.data_ptr(), N.F16, q.stride(0), q.stride(1), B, HQ, HKV, D, N.STORE_JPEG_I8,
+                N.F16, R, K, NB, _view(kst, keep), _view(vst, keep), TAIL, A.data_ptr(),
+                D ** -0.5, out_c.data_ptr(), out_c.stride(0), out_c.stride(1), ws.data_ptr(),
+                n_splits, N.stream_ptr(dev))
+    set_args = [abi_args(*kv) for kv in sets]
+
+    if args.splits:
+        def call(i):
+            N.check(L.fc_decode_attention(*set_args[i % n_sets]), "fc_decode_attention")
+            return out_c
+    else:
+        def call(i):
+            kst, vst = sets[i % n_sets]
+            return fc.codec_decode_attention(q, kst, vst)
+
+    def events_ms(fn, steps, stream=None):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    log(f"bench: warmup {args.warmup}, steps {args.steps}, splits {n_splits}, sets {n_sets}")
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    ms = events_ms(call, args.steps)
+    log(f"bench: {ms * 1e3:.1f} us per call over {n_sets} archive sets")
+
+    # dominant kernel: the call is one launch of the split kernel (its last
+    # workgroup per head group merges); back-to-back launches through the C
+    # ABI, cycling over the sets, between two events on the stream they are
+    # launched on (the stream N.stream_ptr hands the library)
+    stream = torch.cuda.current_stream(dev)
+
+    def launch(i):
+        N.check(L.fc_decode_attention(*set_args[i % n_sets]), "fc_decode_attention")
+
+    for i in range(2 * n_sets):
+        launch(i)
+    torch.cuda.synchronize()
+    launch_ms = events_ms(launch, args.steps, stream)
+    achieved = ALG_BYTES_CALL / (launch_ms * 1e-3) / 1e9
+    log(f"bench: kernel {launch_ms * 1e3:.1f} us per launch, {achieved:.0f} GB/s")
+    single_ms = events_ms(lambda i: N.check(L.fc_decode_attention(*set_args[0]), "attn"),
+                          args.steps, stream)
+    single = ALG_BYTES_CALL / (single_ms * 1e-3) / 1e9
+    log(f"bench: one repeated set {single_ms * 1e3:.1f} us per launch, {single:.0f} GB/s")
+
+    out = fc.codec_decode_attention(q, ks, vs)
+    check_workspaces(dev)                          # no merge gave up during the run
+    err, per_seq = check_against_oracle(q, ks, vs, out)
+    log(f"bench: max error vs the fp64 oracle over all {B} sequences {err:.2e}")
+    lpc = launches_per_call(N.STORE_JPEG_I8, n_splits)
+    result = {
+        "metric": METRIC,
+        "value": round(ALG_BYTES_CALL / (ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "accumulate": "f32",
+        "data": "synthetic AR(1) rho=0.95 K/V (fp16, archived int8 by the kernels), "
+                "q fp16 N(0,1)/sqrt(D)",
+        "config": {"workload": "C3 coefficient-domain split-K decode attention",
+                   "B": B, "Hq": HQ, "Hkv": HKV, "D": D, "S_archived": S_ARCH, "raw_tail": TAIL,
+                   "block": R, "keep_freqs": K, "coeffs": "int8 + fp32 scales",
+                   "q_dtype": "fp16", "n_splits": n_splits, "archive_sets": n_sets,
+                   "algorithmic_bytes_per_call": ALG_BYTES_CALL},
+        "hbm_frac": round(ALG_BYTES_CALL / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "tokens_per_s": round(B / (ms * 1e-3), 1),
+        "launches_per_call": lpc,
+        "roofline": {"bound": "hbm", "kernel": split_kernel_name(n_splits),
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": read_pmc_traffic(),
+                     "traffic_source": "committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary "
+                                       "(profiles/attn_split_c3_pmc.md), not this run",
+                     "algorithmic_bytes_per_launch": ALG_BYTES_CALL,
+                     "avg_launch_us": round(launch_ms * 1e3, 2),
+                     "archive_sets": n_sets},
+        "single_set": {"avg_launch_us": round(single_ms * 1e3, 2), "achieved": round(single, 2),
+                       "frac": round(single / HBM_PEAK_GBS, 4),
+                       "note": "the same launches repeated on one archive set, which the "
+                               "256 MB last-level cache partly serves"},
+        "check": {"vs_oracle_max_rel_err": err, "per_sequence": per_seq, "tolerance": 2e-3,
+                  "sequences": B},
+    }
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline (the reference's torch CPU path, >= 10 s of the workload)")
+        result["cpu_baseline"] = cpu_baseline(ks, vs, q)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result))
+    if not err <= 2e-3:
+        log(f"bench: output differs from the oracle beyond the tolerance ({err:.2e} > 2e-3)")
+        sys.exit(3)
 
 
 def main():
@@ -557,8 +744,8 @@ def main():
                     default="c3")
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--rotating-sets", type=int, default=0,
-                    help="c3: also time launches cycling over this many archive copies")
+    ap.add_argument("--sets", type=int, default=4,
+                    help="c3: archive copies the timed calls cycle over (1: one repeated set)")
     ap.add_argument("--splits", type=int, default=0, help="override the split count")
     ap.add_argument("--c5-steps", type=int, default=None,
                     help="c5: one run of this many decode steps (0: prefill only)")
@@ -590,158 +777,7 @@ def main():
     if args.mode == "c4":
         return c4_mode(args)
 
-    import numpy as np
-    import flashcodec_amd as fc
-    from flashcodec_amd import _native as N
-    from flashcodec_amd.attention import _device_A, _view
-    from flashcodec_amd.cache import _CodecStream
-
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    log("bench: generating AR(1) K/V and archiving them")
-    S = S_ARCH + TAIL
-    cfg = dict(mode="jpeg", block_size=R, keep_freqs=K, quant_bits=8)
-    ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
-    for st, seed in ((ks, 1), (vs, 2)):
-        x = ar1_device((B, HKV, S, D), 0.95, seed, dev).to(torch.float16)
-        st.append(x)
-        del x
-    torch.cuda.empty_cache()
-    g = torch.Generator(device=dev).manual_seed(3)
-    q = (torch.randn((B, HQ, 1, D), generator=g, device=dev) / math.sqrt(D)).to(torch.float16)
-    assert ks.n_blocks == NB and ks.raw.shape[-2] == TAIL
-
-    L = N.lib()
-    n_splits = args.splits or L.fc_attention_splits(N.STORE_JPEG_I8, N.F16, N.F16, K, NB, B, HKV,
-                                                    HQ // HKV, D, N.num_cus(dev))
-    keep = []
-    kv, vv = _view(ks, keep), _view(vs, keep)
-    A = _device_A(ks.codec, R, dev)
-    out_c = torch.empty_like(q)
-    # zero-filled once: its arrival counters return to zero after every call
-    ws = torch.zeros(L.fc_attention_workspace_bytes(B, HQ, D, n_splits), dtype=torch.uint8,
-                     device=dev)
-    abi_args = (q.data_ptr(), N.F16, q.stride(0), q.stride(1), B, HQ, HKV, D, N.STORE_JPEG_I8,
-                N.F16, R, K, NB, kv, vv, TAIL, A.data_ptr(), D ** -0.5, out_c.data_ptr(),
-                out_c.stride(0), out_c.stride(1), ws.data_ptr(), n_splits, N.stream_ptr(dev))
-
-    if args.splits:
-        def call():
-            N.check(L.fc_decode_attention(*abi_args), "fc_decode_attention")
-            return out_c
-    else:
-        def call():
-            return fc.codec_decode_attention(q, ks, vs)
-
-    log(f"bench: warmup {args.warmup}, steps {args.steps}, splits {n_splits}")
-    for _ in range(args.warmup):
-        out = call()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        out = call()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
-    log(f"bench: {ms * 1e3:.1f} us per call")
-
-    # dominant kernel: the call is one launch of the split kernel (its last
-    # workgroup per head group merges); K back-to-back launches through the
-    # C ABI between two events on the stream they are launched on
-    for _ in range(3):
-        N.check(L.fc_decode_attention(*abi_args), "fc_decode_attention")
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)   # the stream N.stream_ptr hands the library
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record(stream)
-    for _ in range(args.steps):
-        N.check(L.fc_decode_attention(*abi_args), "fc_decode_attention")
-    k1.record(stream)
-    torch.cuda.synchronize()
-    launch_ms = k0.elapsed_time(k1) / args.steps
-    achieved = ALG_BYTES_CALL / (launch_ms * 1e-3) / 1e9
-    log(f"bench: kernel {launch_ms * 1e3:.1f} us per launch, {achieved:.0f} GB/s")
-
-    # optionally the same launches rotating over N copies of the archives
-    # (277 MB each), as a decode step does over its layers: no call finds
-    # its inputs in the caches a previous call left behind
-    rot = None
-    ROT_SETS = args.rotating_sets
-    rot_args = [abi_args]
-    copies = []
-    for _ in range(ROT_SETS - 1 if ROT_SETS >= 2 else 0):
-        views = []
-        for st in (ks, vs):
-            c = _CodecStream(st.codec)
-            c._coeffs, c._scales = st._coeffs.clone(), st._scales.clone()
-            c._capacity, c.n_blocks, c.n_archived = st._capacity, st.n_blocks, st.n_archived
-            c.dtype, c.meta = st.dtype, st.meta
-            c._raw_buf, c._n_raw = st._raw_buf.clone(), st._n_raw
-            copies.append(c)
-            views.append(_view(c, keep))
-        rot_args.append(abi_args[:13] + tuple(views) + abi_args[15:])
-    if copies:
-        for i in range(2 * ROT_SETS):
-            N.check(L.fc_decode_attention(*rot_args[i % ROT_SETS]), "fc_decode_attention")
-        torch.cuda.synchronize()
-        k0.record(stream)
-        for i in range(args.steps):
-            N.check(L.fc_decode_attention(*rot_args[i % ROT_SETS]), "fc_decode_attention")
-        k1.record(stream)
-        torch.cuda.synchronize()
-        rot_ms = k0.elapsed_time(k1) / args.steps
-        rot_achieved = ALG_BYTES_CALL / (rot_ms * 1e-3) / 1e9
-        log(f"bench: kernel over {ROT_SETS} rotating archive sets {rot_ms * 1e3:.1f} us per "
-            f"launch, {rot_achieved:.0f} GB/s")
-        rot = {"sets": ROT_SETS, "avg_launch_us": round(rot_ms * 1e3, 2),
-               "achieved": round(rot_achieved, 2), "frac": round(rot_achieved / HBM_PEAK_GBS, 4)}
-        del copies, rot_args
-        torch.cuda.empty_cache()
-
-    result = {
-        "metric": METRIC,
-        "value": round(ALG_BYTES_CALL / (ms * 1e-3) / 1e9, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16",
-        "accumulate": "f32",
-        "data": "synthetic AR(1) rho=0.95 K/V (fp16, archived int8 by the kernels), "
-                "q fp16 N(0,1)/sqrt(D)",
-        "config": {"workload": "C3 coefficient-domain split-K decode attention",
-                   "B": B, "Hq": HQ, "Hkv": HKV, "D": D, "S_archived": S_ARCH, "raw_tail": TAIL,
-                   "block": R, "keep_freqs": K, "coeffs": "int8 + fp32 scales",
-                   "q_dtype": "fp16", "n_splits": n_splits,
-                   "algorithmic_bytes_per_call": ALG_BYTES_CALL},
-        "hbm_frac": round(ALG_BYTES_CALL / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "tokens_per_s": round(B / (ms * 1e-3), 1),
-        "launches_per_call": 1,
-        "roofline": {"bound": "hbm", "kernel": split_kernel_name(),
-                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_pmc_traffic(),
-                     "algorithmic_bytes_per_launch": ALG_BYTES_CALL,
-                     "avg_launch_us": round(launch_ms * 1e3, 2)},
-    }
-    if rot is not None:
-        result["rotating_sets"] = rot
-    if not args.no_cpu_baseline:
-        log("bench: cpu baseline (fp64 oracle, >= 10 s of the workload)")
-        ref, cpu = cpu_baseline(q, ks, vs)
-        got = out[:1, :, 0].float().cpu().numpy()
-        err = float(np.abs(got - ref).max() / np.abs(ref).max())
-        result["cpu_baseline"] = cpu
-        result["check"] = {"vs_oracle_max_rel_err_seq0": err, "tolerance": 2e-3}
-    else:
-        result["cpu_baseline"] = None
-    print(json.dumps(result))
-
+    return c3_mode(args)
 
 if __name__ == "__main__":
     main()

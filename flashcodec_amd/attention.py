@@ -71,6 +71,19 @@ def workspace(device, nbytes):
     return ws
 
 
+FUSED_MERGE_MAX_SPLITS = 64   # the matrix-core pass merges in-kernel up to this many splits
+
+
+def launches_per_call(store_kind, n_splits):
+    """Kernel launches of one fc_decode_attention call over archived blocks:
+    one when the split pass merges its own partials (the vector-ALU pass
+    always; the matrix-core pass up to FUSED_MERGE_MAX_SPLITS splits), else
+    the split pass plus the merge pass."""
+    if store_kind == N.STORE_JPEG_I8 and N.lib().fc_get_attention_pass() != N.PASS_VECTOR:
+        return 1 if n_splits <= FUSED_MERGE_MAX_SPLITS else 2
+    return 1
+
+
 def _view(stream, keep):
     """fc_stream_view of a stream; tensors it points into are added to `keep`."""
     v = N.StreamView()

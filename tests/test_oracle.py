@@ -15,6 +15,10 @@ Pinning map of oracle/oracle.py:
   stream (append/read)   -> golden _CodecStream archives, read() and crop
   attention              -> golden torch-path outputs; dense attention on
                             the golden reconstructed view
+Pinning map of oracle/torch_path.py (bench.py's CPU baseline):
+  decode_attention       -> the reference's impl="torch" outputs (golden),
+                            bit-exact; fp64 attention within tolerance; a
+                            planted mistake (tail dropped) is caught
 """
 
 import math
@@ -316,3 +320,71 @@ def test_attention_oracle_matches_dense_softmax_on_reconstruction(golden, oracle
     dense = np.einsum("bht,bhtd->bhd", p, vv)
     got = oracle.attention(q, rk, rv, zk, zv, A, D ** -0.5)
     assert np.abs(got - dense).max() < 1e-10
+
+
+def _torch_path_inputs(oracle, golden, c, m):
+    """torch CPU tensors of a golden attention case as the reference's torch
+    path sees them: stored rows in the work dtype, raw tails, A (r x s)."""
+    import torch
+    from tests.conftest import to_torch
+    from oracle import torch_path
+    cfg, dt = m["cfg"], m["dtype"]
+    r = cfg["block_size"]
+    q = to_torch(c["q"], dt, device="cpu")
+    seqs = [oracle.values_of(c[x], dt) for x in ("k", "v")]
+    S = seqs[0].shape[-2]
+    n = S // r
+    rows = []
+    for x in seqs:
+        head = x[..., :n * r, :]
+        if cfg["mode"] == "jpeg":
+            kk = cfg["keep_freqs"]
+            basis = golden("basis").data[f"r{r}"][:kk]
+            if cfg.get("quant_bits"):
+                _, codes, scales = oracle.jpeg_encode(head, r, kk, basis, dt, quant=True)
+                rows.append(torch_path.jpeg_rows(torch.from_numpy(codes),
+                                                 torch.from_numpy(scales)[..., None], q.dtype))
+            else:
+                coef = oracle.jpeg_encode(head, r, kk, basis, dt)
+                rows.append(to_torch(oracle.encode_as(coef, dt), dt, device="cpu"))
+            A = torch.from_numpy(np.ascontiguousarray(basis)).t()
+        else:
+            d, a = oracle.png_encode(head, r, cfg["keep_ratio"])
+            rows.append(torch_path.png_rows(torch.from_numpy(d),
+                                            to_torch(oracle.encode_as(a, dt), dt, device="cpu")))
+            A = torch.tril(torch.ones(r, r))
+    raws = [None if S == n * r else to_torch(c[x], dt, device="cpu")[..., n * r:, :]
+            for x in ("k", "v")]
+    return q, rows[0], rows[1], raws[0], raws[1], A
+
+
+@pytest.mark.parametrize("name", _attn_cases())
+def test_torch_path_restatement_matches_reference(golden, oracle, name):
+    """oracle/torch_path.py (bench.py's CPU baseline) reproduces the
+    reference's impl="torch" outputs bit for bit on the golden cases, and
+    agrees with the fp64 oracle within tolerance."""
+    from oracle import torch_path
+    G = golden("attention")
+    c, m = G.case(name), G.meta[name]
+    q, rk, rv, zk, zv, A = _torch_path_inputs(oracle, golden, c, m)
+    out = torch_path.decode_attention(q, rk, rv, zk, zv, A, m["D"] ** -0.5)
+    ref = c["out"]
+    got = out.numpy() if m["dtype"] != "bf16" else out.view(torch.int16).numpy().view(np.uint16)
+    assert got.dtype == ref.dtype and np.array_equal(got, ref)
+    q64, rk64, rv64, zk64, zv64, A64 = oracle_attention_inputs(oracle, golden, c, m)
+    exact = oracle.attention(q64, rk64, rv64, zk64, zv64, A64, m["D"] ** -0.5)
+    vals = oracle.values_of(got, m["dtype"])[:, :, 0]
+    tol = 1e-5 if m["dtype"] == "f32" else 4e-3 * np.abs(exact).max()
+    assert np.abs(vals - exact).max() <= tol
+
+
+def test_torch_path_restatement_catches_a_dropped_tail(golden, oracle):
+    """A planted mistake (the raw tail left out) moves the restatement's
+    output off the reference's bits."""
+    from oracle import torch_path
+    G = golden("attention")
+    name = "jpeg_i8_f16_g4_t5"
+    c, m = G.case(name), G.meta[name]
+    q, rk, rv, zk, zv, A = _torch_path_inputs(oracle, golden, c, m)
+    out = torch_path.decode_attention(q, rk, rv, None, None, A, m["D"] ** -0.5)
+    assert not np.array_equal(out.numpy(), c["out"])
