@@ -77,13 +77,17 @@ def encode_into(x3, r, k, quant_bits, coeffs, scales, cap, n0, m, s_valid, H=1):
     N.check(rc, "fc_jpeg_encode")
 
 
-def decode_into(store, scales, B, H, cap, a, nblk, D, r, k, out, out_len):
+def decode_into(store, scales, B, H, cap, a, nblk, D, r, k, out, out_len, token0=0):
     """Run the jpeg reconstruction kernel for blocks [a, a+nblk) into `out`
-    (B, H, T, D) (token t = block*r + row; tokens >= out_len skipped)."""
+    (B, H, T, D) whose row 0 holds token `token0` (token t = block*r + row;
+    tokens >= out_len skipped).  The kernel addresses token t at
+    base + t * row stride, so the base handed over sits token0 rows before
+    `out`; only rows of `out` itself are written."""
     basis = device_basis(r, k, store.device)
+    base = out.data_ptr() - token0 * out.stride(2) * out.element_size()
     rc = N.lib().fc_jpeg_decode(
         store.data_ptr(), N.dtype_code(store.dtype), N.ptr(scales), B, H, cap, a, nblk, D, r,
-        k, basis.data_ptr(), out.data_ptr(), N.dtype_code(out.dtype), out.stride(0),
+        k, basis.data_ptr(), base, N.dtype_code(out.dtype), out.stride(0),
         out.stride(1), out.stride(2), out_len, N.stream_ptr(store.device))
     N.check(rc, "fc_jpeg_decode")
 

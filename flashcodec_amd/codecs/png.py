@@ -37,11 +37,13 @@ def encode_into(x, r, keep_m, deltas, anchors, cap, n0, m, s_valid):
     N.check(rc, "fc_png_encode")
 
 
-def decode_into(deltas, anchors, B, H, cap, a, nblk, D, r, out, out_len):
-    """Run the png reconstruction kernel for blocks [a, a+nblk) into `out`."""
+def decode_into(deltas, anchors, B, H, cap, a, nblk, D, r, out, out_len, token0=0):
+    """Run the png reconstruction kernel for blocks [a, a+nblk) into `out`,
+    whose row 0 holds token `token0` (as jpeg.decode_into)."""
+    base = out.data_ptr() - token0 * out.stride(2) * out.element_size()
     rc = N.lib().fc_png_decode(
         deltas.data_ptr(), anchors.data_ptr(), N.dtype_code(anchors.dtype), B, H, cap, a, nblk,
-        D, r, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), out_len,
+        D, r, base, out.stride(0), out.stride(1), out.stride(2), out_len,
         N.stream_ptr(deltas.device))
     N.check(rc, "fc_png_decode")
 

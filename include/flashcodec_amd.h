@@ -261,6 +261,28 @@ int fc_decode_attention_merge(const void* q, int q_dtype, int64_t q_sb,
                               int n_splits, void* stream);
 
 /*
+ * Gather of per-(row, head) byte segments on the device, for batch-major
+ * buffers (every archive buffer, tail buffer and reconstruction of a
+ * stream): for b in [0, B_out) and h in [0, H),
+ *   dst[b*d_sb + h*d_sh + i] = src[idx[b]*s_sb + h*s_sh + i],  i in [0, len)
+ * with strides and len in bytes, idx B_out int64 device indices into src's
+ * B_src rows (NULL: idx[b] = b).  dst == src (same strides, B_out == B_src)
+ * gathers in place: every source segment of a column is read before any
+ * destination in it is written, so any idx (a permutation, repeats) is
+ * valid; other overlaps are not allowed.  Indices outside [0, B_src) leave
+ * their destination segment unwritten.  No allocation, no host
+ * synchronisation: a captured HIP graph can replay it with new indices.
+ * FC_ERR_UNSUPPORTED when an in-place gather has more than 2048 rows.
+ * Replaces the index_select gathers of _CodecStream.select_batch and the
+ * verbatim prefix copy of _CodecStream._grow (flashcodec/cache.py:106-121,
+ * 259-301).
+ */
+int fc_gather_segments(void* dst, int64_t d_sb, int64_t d_sh, const void* src,
+                       int64_t s_sb, int64_t s_sh, const int64_t* idx,
+                       int64_t B_out, int64_t B_src, int64_t H, int64_t len,
+                       void* stream);
+
+/*
  * Status of the decode attentions that used `workspace` since it was last
  * checked: FC_OK, or FC_ERR_INCOMPLETE when a fused merge (the last
  * workgroup of a head group) stopped waiting for the other splits'
