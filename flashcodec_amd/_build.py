@@ -56,6 +56,7 @@ def sources():
 
 FILE_FLAGS = {
     "fc_attn_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "fc_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

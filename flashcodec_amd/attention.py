@@ -209,6 +209,58 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
     return out
 
 
+def prefill_supported(codec, dtype, head_dim):
+    """Whether codec_prefill_attention runs streams of `codec` with queries
+    of `dtype` and head size `head_dim`: int8 jpeg archives with 1 / 2 / 4
+    kept frequencies, fp16 / bf16 queries, head size 64 / 128 / 256."""
+    return (codec.name == "jpeg" and codec.quantized and codec.keep_freqs in (1, 2, 4)
+            and dtype in (torch.float16, torch.bfloat16) and head_dim in (64, 128, 256))
+
+
+def codec_prefill_attention(query, key_stream, value_stream, scale=None):
+    """Causal attention of the newest Sq cached tokens' queries over the
+    whole cache, on the archive's stored rows (no reconstructed view).
+
+    query (B, Hq, Sq, D) holds the queries of the last Sq tokens of the
+    streams (positions seq_len - Sq .. seq_len - 1); token i attends every
+    cached token up to its own position: archived blocks through the codec's
+    synthesis matrix in the coefficient domain, raw-tail tokens at full
+    precision.  Returns (B, Hq, Sq, D) in the query dtype.  This build's
+    replacement for the reference's prefill on the materialised view
+    (flashcodec/attention.py:24-26, flashcodec/patch_attention.py:58-61);
+    int8 jpeg streams only (prefill_supported)."""
+    ks, vs = key_stream, value_stream
+    B, Hq, Sq, D = query.shape
+    if not (prefill_supported(ks.codec, query.dtype, D) and _same_codec(ks.codec, vs.codec)):
+        raise NotImplementedError("codec_prefill_attention runs int8 jpeg archives with "
+                                  "fp16/bf16 queries, D in (64, 128, 256), keep_freqs in (1, 2, 4)")
+    N.require_gpu(query)
+    if ks.seq_len != vs.seq_len or ks.n_blocks != vs.n_blocks or ks.meta is None:
+        raise ValueError("key and value streams hold different token counts")
+    if Sq > ks.seq_len:
+        raise ValueError(f"{Sq} query tokens but {ks.seq_len} cached tokens: the queries are "
+                         "the newest cached tokens' (append their keys and values first)")
+    Hkv = ks.meta[1]
+    assert Hq % Hkv == 0, f"query heads ({Hq}) must be a multiple of kv heads ({Hkv})"
+    c = ks.codec
+    r = c.block_size
+    scale = D ** -0.5 if scale is None else float(scale)
+    q = query if query.stride(-1) == 1 else query.contiguous()
+    if (q.data_ptr() % 16) or any(x % 8 for x in q.stride()[:3]):
+        q = q.contiguous()
+    out = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
+    keep = []
+    kv, vv = _view(ks, keep), _view(vs, keep)
+    A = _device_A(c, r, q.device)
+    rc = N.lib().fc_prefill_attention(
+        q.data_ptr(), N.dtype_code(q.dtype), q.stride(0), q.stride(1), q.stride(2), B, Hq, Hkv,
+        Sq, D, ks.seq_len - Sq, N.dtype_code(ks.dtype), r, c.keep_freqs, ks.n_blocks, kv, vv,
+        ks._n_raw, N.ptr(A), scale, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+        N.stream_ptr(q.device))
+    N.check(rc, "fc_prefill_attention")
+    return out
+
+
 def _step_args(ks, vs, query, tokens):
     """The fc_step_args of a (key, value) stream pair with the fields that do
     not change between decode steps filled in (cached on the key stream)."""

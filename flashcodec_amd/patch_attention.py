@@ -1,34 +1,35 @@
-"""Route decode steps of Llama/Qwen-style attention through the
-coefficient-domain kernels (flashcodec/patch_attention.py:1-151).
+"""Route the attention of Llama/Qwen-style modules on codec layers through
+the coefficient-domain kernels (flashcodec/patch_attention.py:1-151).
 
 ``apply_flash_codec`` swaps the cache, but transformers still attends on the
 reconstructed view.  This patch replaces the forward of standard attention
 modules (q_proj / k_proj / v_proj / o_proj, optional q_norm / k_norm, plain
-or gated query projection) so that a single-token decode step on a codec
-layer runs projection + norm + RoPE as usual, then appends K/V to the codec
-streams and attends on the archive in one library call
-(``codec_decode_step``) — no (S, D) view.
+or gated query projection).  On a codec layer the projections, norms and
+RoPE run as usual; then
+* a decode step (one query token) appends K/V to the codec streams and
+  attends on the archive in one library call (``codec_decode_step``);
+* a prefill (several query tokens) on int8 jpeg archives appends the
+  prompt's K/V and attends causally on the archive's stored rows
+  (``codec_prefill_attention``): no reconstructed view is ever built.  Other
+  archives (png, unquantised jpeg) run the model's own attention on the
+  view the cache returns, released as soon as that forward returns, so a
+  prefill holds one layer's view at a time (the reference keeps every
+  layer's until that layer's first decode step, patch_attention.py:90-94).
+  ``set_prefill_on_archive(False)`` selects that path for every archive.
 
 Guards (anything else calls the original forward): codec cache layer, eval
-mode, one query token, ``position_embeddings`` given, no sliding window, a
-RoPE function in the model's module, and either batch 1 or no attention mask
-(transformers passes no mask to SDPA-style attention when nothing is padded,
-so unpadded batched decoding takes the codec path too; the reference stops
-at batch 1, patch_attention.py:52).
-
-Prefill (several query tokens) runs the original forward, which attends on
-the reconstructed view the cache returns; on a codec layer that decode steps
-can serve from the archive the view is released as soon as that forward
-returns, so a prefill holds one layer's view at a time instead of every
-layer's until the first decode step (the reference drops each view on the
-layer's first decode step, patch_attention.py:90-94).
+mode, ``position_embeddings`` given, no sliding window, a RoPE function in
+the model's module, and either batch 1 or no attention mask (transformers
+passes no mask to SDPA-style attention when nothing is padded, so unpadded
+batches take the codec path too; the reference stops at batch 1 and at
+decode steps, patch_attention.py:52-61).
 """
 
 import importlib
 
 import torch
 
-from .attention import codec_decode_step
+from .attention import codec_decode_step, codec_prefill_attention, prefill_supported
 from .cache import FlashCodecLayer
 
 _ROPE_CACHE = {}
@@ -62,31 +63,17 @@ def _release_view(layer):
     layer.keys = layer.values = None
 
 
-def _attention_forward(module, orig, hidden_states, position_embeddings=None,
-                       attention_mask=None, past_key_values=None, **kwargs):
-    layer = _codec_layer(module, past_key_values)
-    codec_ok = (layer is not None
-                and not module.training
-                and position_embeddings is not None
-                and getattr(module, "sliding_window", None) is None
-                and _rope_fn(module) is not None)
-    usable = (codec_ok
-              and hidden_states.shape[-2] == 1
-              and (hidden_states.shape[0] == 1 or attention_mask is None))
-    if not usable:
-        out = orig(hidden_states, position_embeddings=position_embeddings,
-                   attention_mask=attention_mask, past_key_values=past_key_values, **kwargs)
-        if codec_ok and hidden_states.shape[-2] > 1 and layer.is_initialized:
-            _release_view(layer)  # prefill done: decode attends on the archive
-        return out
-
+def _project(module, hidden_states, position_embeddings):
+    """q (B, Hq, T, D), k, v (B, Hkv, T, D) after the projections, the
+    optional q/k norms and RoPE, plus the output gate of gated (Qwen3.5-
+    style) query projections; the sequence is fixed by the HF attention
+    modules this wraps."""
     lead = hidden_states.shape[:-1]
     hd = module.head_dim
     width = module.o_proj.in_features
-    gated = module.q_proj.out_features == 2 * width      # Qwen3.5-style output gate
     qp = module.q_proj(hidden_states)
     gate = None
-    if gated:
+    if module.q_proj.out_features == 2 * width:
         q, gate = torch.chunk(qp.view(*lead, -1, 2 * hd), 2, dim=-1)
         gate = gate.reshape(*lead, -1)
     else:
@@ -98,10 +85,48 @@ def _attention_forward(module, orig, hidden_states, position_embeddings=None,
         q = module.q_norm(q)
     if hasattr(module, "k_norm"):
         k = module.k_norm(k)
-    q, k = q.transpose(1, 2), k.transpose(1, 2)
     cos, sin = position_embeddings
-    q, k = _rope_fn(module)(q, k, cos, sin)
+    q, k = _rope_fn(module)(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
+    return q, k, v, gate
 
+
+def _finish(module, out, gate, lead):
+    out = out.transpose(1, 2).reshape(*lead, -1).contiguous()
+    if gate is not None:
+        out = out * torch.sigmoid(gate)
+    return module.o_proj(out), None
+
+
+def _attention_forward(module, orig, hidden_states, position_embeddings=None,
+                       attention_mask=None, past_key_values=None, **kwargs):
+    layer = _codec_layer(module, past_key_values)
+    codec_ok = (layer is not None
+                and not module.training
+                and position_embeddings is not None
+                and getattr(module, "sliding_window", None) is None
+                and _rope_fn(module) is not None
+                and (hidden_states.shape[0] == 1 or attention_mask is None))
+    T = hidden_states.shape[-2]
+    if (codec_ok and T > 1 and _PREFILL["on"]
+            and prefill_supported(layer.codec, hidden_states.dtype, module.head_dim)):
+        # prefill on the archive: append the prompt's K/V, attend without a view
+        q, k, v, gate = _project(module, hidden_states, position_embeddings)
+        if not layer.is_initialized:
+            layer.lazy_initialization(k, v)
+        _release_view(layer)
+        layer._pair.append(k, v)
+        out = codec_prefill_attention(q, layer._key_stream, layer._value_stream,
+                                      scale=module.scaling)
+        module._flashcodec_prefills = getattr(module, "_flashcodec_prefills", 0) + 1
+        return _finish(module, out, gate, hidden_states.shape[:-1])
+    if not (codec_ok and T == 1):
+        out = orig(hidden_states, position_embeddings=position_embeddings,
+                   attention_mask=attention_mask, past_key_values=past_key_values, **kwargs)
+        if codec_ok and T > 1 and layer.is_initialized:
+            _release_view(layer)  # prefill done: decode attends on the archive
+        return out
+
+    q, k, v, gate = _project(module, hidden_states, position_embeddings)
     if not layer.is_initialized:
         layer.lazy_initialization(k, v)
     # the prefill view is dead weight once decoding attends on the archive
@@ -110,11 +135,23 @@ def _attention_forward(module, orig, hidden_states, position_embeddings=None,
     # attention call in the reference, patch_attention.py:95-98)
     out = codec_decode_step(q, k, v, layer._key_stream, layer._value_stream,
                             scale=module.scaling)
-    out = out.transpose(1, 2).reshape(*lead, -1).contiguous()
-    if gated:
-        out = out * torch.sigmoid(gate)
     module._flashcodec_codec_steps = getattr(module, "_flashcodec_codec_steps", 0) + 1
-    return module.o_proj(out), None
+    return _finish(module, out, gate, hidden_states.shape[:-1])
+
+
+# Reconstruct-free prefill switch (on by default; off runs the reference's
+# prefill on the materialised view, for comparisons).
+_PREFILL = {"on": True}
+
+
+def set_prefill_on_archive(enabled):
+    """Choose how patched prefills attend: on the archive's stored rows
+    (True, the default: no reconstructed view) or on the reconstructed view
+    through the model's own attention (False, the reference's semantics).
+    Returns the previous setting."""
+    prev = _PREFILL["on"]
+    _PREFILL["on"] = bool(enabled)
+    return prev
 
 
 def _supported(module):

@@ -357,6 +357,32 @@ int fc_get_attention_pass(void);
 void fc_set_merge_wait_limit(int polls);
 
 /*
+ * Causal prefill attention on int8 jpeg archives without the reconstructed
+ * view: the Sq query tokens q (B, Hq, Sq, D) (q_dtype FC_F16 / FC_BF16,
+ * element strides q_sb, q_sh, q_st) sit at positions P0 .. P0+Sq-1 of the
+ * streams (P0 + Sq <= nb * r + n_raw), and query token i attends every
+ * cached token at a position <= P0 + i: archived blocks through their
+ * stored rows (codes x scales, synthesis matrix A r x s) in the coefficient
+ * domain, raw-tail tokens at full precision.  Softmax in fp32; out
+ * (B, Hq, Sq, D) in q_dtype, strides o_sb, o_sh, o_st.  GQA as
+ * fc_decode_attention.  Supports D in {64, 128, 256} and s in {1, 2, 4}
+ * (FC_ERR_UNSUPPORTED otherwise), 16-byte aligned q and stores.  One
+ * launch, no workspace.
+ * Replaces the reference's prefill attention on the materialised view
+ * (the read() view SDPA attends, flashcodec/cache.py:203-220 through
+ * flashcodec/patch_attention.py:58-61; flashcodec/attention.py:24-26 names
+ * the gap).
+ */
+int fc_prefill_attention(const void* q, int q_dtype, int64_t q_sb,
+                         int64_t q_sh, int64_t q_st, int64_t B, int64_t Hq,
+                         int64_t Hkv, int64_t Sq, int64_t D, int64_t P0,
+                         int stream_dtype, int r, int s, int64_t nb,
+                         const fc_stream_view* key, const fc_stream_view* value,
+                         int64_t n_raw, const float* A, float scale, void* out,
+                         int64_t o_sb, int64_t o_sh, int64_t o_st,
+                         void* stream);
+
+/*
  * One stream (key or value) of a layer for fc_decode_step: its archive
  * buffers (as fc_stream_view), its (B, H, r, D) contiguous tail buffer in
  * the stream dtype (the raw tail is its first n_tail token rows), and the

@@ -1,0 +1,179 @@
+"""GPU: reconstruct-free causal prefill attention on int8 jpeg archives
+(fc_prefill_attention) against fp64 causal attention over the codec's exact
+reconstruction, and the patched HF prefill that uses it.
+
+The oracle is the coefficient-domain definition the decode oracle uses:
+stored rows (codes x scales) in fp64 synthesised through the codec's A
+matrix, raw-tail tokens as stored, brute-force fp64 softmax(q K^T * scale +
+causal mask) V.  The reference's prefill attends on the read() view, whose
+tokens are that reconstruction rounded to the stream dtype; in bf16 that
+rounding alone moves the attention by up to ~2.2e-3 of max|out|
+(measured), so the view is not the oracle.  Tolerance: the contract's 2e-3
+of max|ref| plus half an ulp of the output dtype.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import flashcodec_amd as fc
+from flashcodec_amd.attention import codec_prefill_attention
+from flashcodec_amd.cache import _CodecStream
+from tests.conftest import to_values, torch_dtype
+from tests.test_gpu_attention import HALF_ULP
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def view_oracle(oracle, st):
+    """The stream's tokens (B, H, S, D) in fp64: the archive's stored rows
+    (oracle.stored_rows_jpeg) synthesised through A, then the raw tail."""
+    n, r, k = st.n_blocks, st.block_size, st.codec.keep_freqs
+    parts = []
+    if n:
+        rows = oracle.stored_rows_jpeg(st._coeffs[:, :, :n].cpu().numpy(),
+                                       st._scales[:, :, :n, :, 0].cpu().numpy())
+        A = oracle.synthesis_matrix("jpeg", r, fc.dct_basis(r, k).numpy())
+        B, H, _, _, D = rows.shape
+        parts.append(np.einsum("ps,bhnsd->bhnpd", A, rows).reshape(B, H, n * r, D))
+    if st.raw is not None:
+        parts.append(to_values(st.raw).astype(np.float64))
+    return np.concatenate(parts, axis=2)
+
+
+def causal_reference(q, kview, vview, P0, scale, rows=None):
+    """fp64 causal attention of queries at positions P0 + i (q (B, Hq, Sq,
+    D) values) over the views (B, Hkv, S, D); `rows` limits the checked
+    query indices."""
+    B, Hq, Sq, D = q.shape
+    G = Hq // kview.shape[1]
+    rows = range(Sq) if rows is None else rows
+    out = np.zeros((B, Hq, len(rows), D))
+    for n, i in enumerate(rows):
+        L = P0 + i + 1
+        for h in range(Hq):
+            kk, vv = kview[:, h // G, :L], vview[:, h // G, :L]
+            s = np.einsum("bd,btd->bt", q[:, h, i].astype(np.float64), kk) * scale
+            p = np.exp(s - s.max(-1, keepdims=True))
+            p /= p.sum(-1, keepdims=True)
+            out[:, h, n] = np.einsum("bt,btd->bd", p, vv)
+    return out
+
+
+def check(out, ref, dt):
+    err = np.abs(out - ref)
+    tol = 2e-3 * np.abs(ref).max() + HALF_ULP[dt] * np.abs(ref)
+    assert not (err > tol).any(), f"max err {err.max():.3e} vs max|ref| {np.abs(ref).max():.3e}"
+
+
+def streams(dt, B, Hkv, S, D, k, seed, oracle):
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=k, quant_bits=8)
+    x = [torch.from_numpy(oracle.ar1((B, Hkv, S, D), 0.9, seed + i)).to(torch_dtype(dt)).to(DEV)
+         for i in range(2)]
+    ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
+    return ks, vs, x
+
+
+CASES = [
+    # dt, B, Hkv, G, D, k, S (prompt), S0 (tokens cached before it)
+    ("bf16", 2, 2, 2, 128, 4, 8 * 37 + 5, 0),
+    ("f16", 1, 2, 4, 128, 4, 8 * 20 + 3, 0),
+    ("bf16", 1, 1, 1, 64, 2, 8 * 30 + 7, 0),
+    ("f16", 2, 2, 3, 64, 1, 8 * 12 + 1, 0),
+    ("bf16", 1, 2, 8, 256, 4, 8 * 9 + 2, 0),
+    ("f16", 1, 1, 16, 128, 2, 8 * 11, 0),
+    ("bf16", 2, 2, 2, 128, 4, 77, 8 * 25 + 3),       # chunked: 203 cached, 77 more
+    ("f16", 1, 2, 2, 128, 4, 5, 0),                  # shorter than a block: tail only
+    ("bf16", 1, 2, 2, 128, 4, 3, 8 * 10 + 6),         # 3 more tokens completing a block
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-G{c[3]}-D{c[4]}-k{c[5]}-S{c[6]}+{c[7]}"
+                                             for c in CASES])
+def test_prefill_matches_causal_attention_on_the_view(case, oracle):
+    dt, B, Hkv, G, D, k, S, S0 = case
+    print(f"case prefill {case}", flush=True)
+    ks, vs, (kx, vx) = streams(dt, B, Hkv, S0 + S, D, k, 40 + G + D + S, oracle)
+    if S0:
+        ks.append(kx[:, :, :S0])
+        vs.append(vx[:, :, :S0])
+    ks.append(kx[:, :, S0:])
+    vs.append(vx[:, :, S0:])
+    rng = np.random.default_rng(41)
+    qn = (rng.standard_normal((B, Hkv * G, S, D)) / math.sqrt(D)).astype(np.float32)
+    qn[:, :, :, :3] *= 6.0                      # a few larger features, as real queries have
+    q = torch.from_numpy(qn).to(torch_dtype(dt)).to(DEV)
+    out = codec_prefill_attention(q, ks, vs)
+    assert out.shape == q.shape and out.dtype == q.dtype
+    assert ks._rec is None and vs._rec is None
+    ref = causal_reference(to_values(q), view_oracle(oracle, ks), view_oracle(oracle, vs), S0,
+                           D ** -0.5)
+    check(to_values(out), ref, dt)
+
+
+def test_prefill_c5_prompt_shape(oracle):
+    """One sequence of the C5 prefill: 16 q / 8 kv heads, D=128, bf16,
+    4096 + 3 prompt tokens, k=4; checked on every 61st query and the last 9
+    (the raw tail and the block boundary before it)."""
+    dt, B, Hkv, G, D, S = "bf16", 1, 8, 2, 128, 4096 + 3
+    ks, vs, (kx, vx) = streams(dt, B, Hkv, S, D, 4, 77, oracle)
+    ks.append(kx)
+    vs.append(vx)
+    g = torch.Generator(device=DEV).manual_seed(78)
+    q = (torch.randn((B, Hkv * G, S, D), generator=g, device=DEV) / math.sqrt(D)).to(
+        torch.bfloat16)
+    out = codec_prefill_attention(q, ks, vs)
+    rows = list(range(0, S, 61)) + list(range(S - 9, S))
+    ref = causal_reference(to_values(q), view_oracle(oracle, ks), view_oracle(oracle, vs), 0,
+                           D ** -0.5, rows=rows)
+    check(to_values(out)[:, :, rows], ref, dt)
+
+
+def tiny_qwen3(dtype=torch.bfloat16):
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    torch.manual_seed(3)
+    cfg = Qwen3Config(vocab_size=256, hidden_size=256, intermediate_size=512,
+                      num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=4,
+                      head_dim=64, max_position_embeddings=1024, tie_word_embeddings=True)
+    m = Qwen3ForCausalLM(cfg).eval()
+    m.generation_config.eos_token_id = None
+    return m.to(DEV, dtype)
+
+
+def test_patched_prefill_runs_on_the_archive():
+    """With the attention patch, a batched prefill on int8 jpeg layers
+    attends on the archive (no view, counted per module) and its logits and
+    the next decode steps track the model's own attention on the view."""
+    pytest.importorskip("transformers")
+    from flashcodec_amd import patch_attention as pa
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(1, 256, (3, 8 * 21 + 5), generator=g).to(DEV)
+    forced = torch.randint(1, 256, (3, 3), generator=g).to(DEV)
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+    model = tiny_qwen3()
+    fc.apply_flash_codec(model, materialization_free=True, **cfg)
+    results = {}
+    for on_archive in (False, True):
+        prev = pa.set_prefill_on_archive(on_archive)
+        try:
+            with torch.no_grad():
+                out = model(input_ids=ids, use_cache=True)
+                logits = [out.logits[:, -1].float()]
+                pkv = out.past_key_values
+                for layer in pkv.layers:
+                    assert layer._key_stream._rec is None and layer.keys is None
+                for i in range(3):
+                    out = model(input_ids=forced[:, i:i + 1], past_key_values=pkv,
+                                use_cache=True)
+                    logits.append(out.logits[:, -1].float())
+        finally:
+            pa.set_prefill_on_archive(prev)
+        results[on_archive] = (logits, out.logits[:, -1].float())
+    counts = [getattr(m, "_flashcodec_prefills", 0) for m in fc.find_attention_modules(model)]
+    assert counts == [1, 1]
+    for a, b in zip(results[False][0], results[True][0]):
+        assert (a - b).abs().max().item() <= 3e-2 * a.abs().max().item()
+    fc.remove_flash_codec(model)
