@@ -475,9 +475,12 @@ def c5_mode(args):
         # one run of the named setting (for kernel traces: launches per step
         # are the dispatch count of a run minus that of the same run with 0
         # steps, divided by the steps)
-        if args.c5_kv == "codec":
+        if args.c5_kv != "raw":
             fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8,
                                  materialization_free=True)
+        if args.c5_kv == "codec-view-prefill":
+            from flashcodec_amd import patch_attention as pa
+            pa.set_prefill_on_archive(False)
         run(2, 64, 4)                                        # warm-up, same in every run
         one = run(args.c5_batch, args.c5_prompt, args.c5_steps)
         print(json.dumps({"mode": "c5 single run", "kv": args.c5_kv, "batch": args.c5_batch,
@@ -497,6 +500,13 @@ def c5_mode(args):
     run(2, 64, 4)
     res["codec_b16"] = run(16, 4096, 256)
     res["codec_b1"] = run(1, 4096, 32)
+    res["codec_prefill_b16"] = run(16, 4096, 0)
+    # the same prefill attending on the reconstructed view (the reference's
+    # semantics) instead of the archive
+    from flashcodec_amd import patch_attention as pa
+    prev = pa.set_prefill_on_archive(False)
+    res["codec_view_prefill_b16"] = run(16, 4096, 0)
+    pa.set_prefill_on_archive(prev)
     steps = [getattr(m, "_flashcodec_codec_steps", 0) for m in fc.find_attention_modules(model)]
     res["codec_attention_steps_per_layer"] = max(steps) if steps else 0
     res["value"] = res["codec_b16"]["decode_tokens_per_s"]
@@ -751,7 +761,7 @@ def main():
                     help="c5: one run of this many decode steps (0: prefill only)")
     ap.add_argument("--c5-batch", type=int, default=16)
     ap.add_argument("--c5-prompt", type=int, default=4096)
-    ap.add_argument("--c5-kv", choices=["raw", "codec"], default="codec")
+    ap.add_argument("--c5-kv", choices=["raw", "codec", "codec-view-prefill"], default="codec")
     ap.add_argument("--c5-graph", action="store_true",
                     help="c5: codec decode steps replayed from a captured HIP graph")
     args = ap.parse_args()
