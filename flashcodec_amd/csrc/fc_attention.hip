@@ -1101,6 +1101,7 @@ WsLayout ws_layout(void* workspace, int64_t B, int64_t Hq, int n_splits) {
   WsLayout w;
   unsigned int* base = static_cast<unsigned int*>(workspace);
   w.status = base;
+  w.done = base + 32;  // its own line
   w.counters = base + kWsStatusWords;
   const int64_t ws_head = (B * Hq * (int64_t)n_splits + 3) / 4 * 4;
   w.pm = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);

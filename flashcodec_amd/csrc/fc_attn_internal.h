@@ -47,6 +47,7 @@ constexpr int64_t kCounterBytes = kWsCounterRegionWords * 4;
 constexpr int64_t kCounterStride = 32;  // words between counters (no two share a line)
 struct WsLayout {
   unsigned int* status;
+  unsigned int* done;      // fused decode step: workgroups finished (zero between calls)
   unsigned int* counters;  // kCounterWords words
   float* pm;
   float* pl;
@@ -65,7 +66,23 @@ struct MfmaFuse {
   // decode-step state on the device, (n_blocks, n_tail) before the step's
   // token, or NULL: the kernel then takes the block and tail counts from it
   const int64_t* state = nullptr;
+  // fused decode step in the same launch (see fc_decode_step): the step's
+  // tokens, the writable archives, the basis and the host counters (used
+  // when state is NULL); `done` counts finished workgroups for the state
+  // advance
+  bool step = false;
+  const void* ktok = nullptr;
+  const void* vtok = nullptr;
+  int64_t kt_sb = 0, kt_sh = 0, vt_sb = 0, vt_sh = 0;
+  const float* basis = nullptr;
+  int64_t step_t = 0, step_nb = 0;
+  unsigned int* done = nullptr;
 };
+
+// Whether fc_decode_step can run as one launch of the matrix-core pass for
+// this step (int8 jpeg, the matrix-core pass's shapes, fp16 / bf16 stream,
+// the step's rows fit the kernel's LDS scratch, fused merge).
+bool step_i8_mfma_supported(int stream_dtype, int r, int64_t D, int n_splits);
 
 bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
                              int s, const fc_stream_view* key, const fc_stream_view* value);

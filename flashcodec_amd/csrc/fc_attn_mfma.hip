@@ -92,6 +92,25 @@ struct MfmaArgs {
   // takes passes w, w + n_splits * 4, ...; fixed summation order, so the
   // output is bitwise reproducible
   int static_passes;
+  // fused decode step (step != 0): the step's key / value tokens
+  // (B, Hkv, 1, D) join the tails (kraw / vraw: (B, Hkv, r, D) contiguous
+  // buffers) at row t; when they complete a block, split 0 archives it as
+  // block nb (codes at kcodes_w / vcodes_w, scales at kscales_w / vscales_w,
+  // DCT basis `basis`, k = SROWS) and attends it from the fresh codes, and
+  // the passes cover the blocks before it.  t and nb come from `state`
+  // (then the last workgroup of the launch advances it, counting workgroups
+  // on `done`) or from step_t / step_nb.
+  int step;
+  const void* ktok;
+  const void* vtok;
+  int64_t kt_sb, kt_sh, vt_sb, vt_sh;
+  int8_t* kcodes_w;
+  int8_t* vcodes_w;
+  float* kscales_w;
+  float* vscales_w;
+  const float* basis;
+  int64_t step_t, step_nb;
+  unsigned int* done;
 };
 
 constexpr int kMThreads = 256;
@@ -130,7 +149,7 @@ __device__ __forceinline__ void st_elem(void* ptr, int dt, int64_t i, float v) {
 // other workgroups stream the archive, where every serialized load waits
 // several microseconds).
 template <int D, typename QT, typename RT>
-__device__ void raw_tail_partial_t(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
+__device__ __forceinline__ void raw_tail_partial_t(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
                                    int nr, int tid, float* etl, float* acc, float* tm,
                                    float* tl) {
   const int lane = tid & 63, wave = tid >> 6;
@@ -195,7 +214,7 @@ __device__ void raw_tail_partial_t(const MfmaArgs& p, int64_t b, int64_t hkv, in
 }
 
 template <int D>
-__device__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
+__device__ __forceinline__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
                                  int nr, int tid, float* etl, float* acc, float* tm, float* tl) {
   // the matrix-core pass takes fp16 / bf16 queries; tails are in the stream dtype
   auto with_q = [&](auto rt) {
@@ -212,6 +231,133 @@ __device__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int6
   }
 }
 
+// Archive of one stream's completed block inside the fused decode step:
+// rows x (r rows of D fp32 values of the stream dtype TT) -> DCT-II
+// coefficients by the fma chain over the taps rounded to TT, per-frequency
+// absmax scale rounded to TT (1 when not > 0), codes as quant_code — the
+// archive kernels' arithmetic, bit for bit — stored when `write`; then x is
+// replaced by the block's tokens synthesised from the dequantised codes
+// through A (r x SROWS), so the block is attended exactly as an archived
+// one.  kk: SROWS x D, sc: SROWS floats of LDS scratch.
+template <int D, int SROWS, typename TT>
+__device__ __forceinline__ void step_archive(float* x, int r, const float* basis, const float* A,
+                                             bool write, int8_t* codes, float* scales, float* kk,
+                                             float* sc, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < SROWS * D; e += kMThreads) {
+    const int j = e / D, d = e - j * D;
+    float a = 0.f;
+    for (int i = 0; i < r; ++i) a = __builtin_fmaf(x[i * D + d], basis[j * r + i], a);
+    kk[e] = to_f32(from_f32<TT>(a));
+  }
+  __syncthreads();
+  if (wave < SROWS) {
+    float m = 0.f;
+    for (int d = lane; d < D; d += 64) m = fmaxf(m, fabsf(kk[wave * D + d]));
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float sj = to_f32(from_f32<TT>(m / 127.0f));
+    if (!(sj > 0.f)) sj = 1.0f;
+    if (lane == 0) {
+      sc[wave] = sj;
+      if (write) scales[wave] = sj;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < SROWS * D; e += kMThreads) {
+    const float sj = sc[e / D];
+    const float q = quant_code(kk[e], sj, 1.0f / sj);
+    if (write) codes[e] = (int8_t)(int)q;
+    kk[e] = q * sj;
+  }
+  __syncthreads();
+  for (int e = tid; e < r * D; e += kMThreads) {
+    const int i = e / D, d = e - i * D;
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < SROWS; ++j) a = __builtin_fmaf(A[i * SROWS + j], kk[j * D + d], a);
+    x[e] = a;
+  }
+  __syncthreads();
+}
+
+// Fused decode step, split 0: the rows this step adds to the attention, in
+// LDS as fp32 (xk, xv: n rows of D), and the partial of the group's G heads
+// over them (as raw_tail_partial_t: tm, tl, acc).
+//   * t + 1 < r: the tail rows 0..t-1 (buffer) and the new token; the token
+//     is written to tail row t.
+//   * t + 1 == r: the block of tail rows 0..r-2 and the new token is
+//     archived as block nb (step_archive) and attended from its codes.
+// `write`: this workgroup stores the token / the block (one head group per
+// (batch, kv head) does; all compute the partial).  The query rows are
+// q + qb + (h0 + h) * q_sh for the G heads.
+template <int D, int SROWS, typename TT>
+__device__ __forceinline__ void step_partial(
+    int64_t t, int r, TT* ktail, TT* vtail, const TT* ktok, const TT* vtok, bool write,
+    int8_t* kcodes, float* kscales, int8_t* vcodes, float* vscales, const float* basis,
+    const float* A, const void* q, int q_dtype, int64_t qb, int64_t q_sh, int64_t h0, int G,
+    float scale_log2, int tid, float* xk, float* xv, float* kk, float* sc, float* etl, float* acc,
+    float* tm, float* tl) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const bool complete = t + 1 == r;
+  const int n = complete ? r : (int)t + 1;
+  for (int x = tid; x < n * D; x += kMThreads) {
+    const int i = x / D, d = x - i * D;
+    xk[x] = to_f32(i < t ? ktail[i * D + d] : ktok[d]);
+    xv[x] = to_f32(i < t ? vtail[i * D + d] : vtok[d]);
+  }
+  if (write && !complete)
+    for (int d = tid; d < D; d += kMThreads) {
+      ktail[t * D + d] = ktok[d];
+      vtail[t * D + d] = vtok[d];
+    }
+  __syncthreads();
+  if (complete) {
+    step_archive<D, SROWS, TT>(xk, r, basis, A, write, kcodes, kscales, kk, sc, tid);
+    step_archive<D, SROWS, TT>(xv, r, basis, A, write, vcodes, vscales, kk, sc, tid);
+  }
+  // the partial over the n rows, at full precision
+  {
+    const int grp = tid >> 4, gl = tid & 15;
+    for (int u = grp; u < G * n; u += kMThreads / 16) {
+      const int h = u / n, i = u - h * n;
+      const int64_t qr = qb + (h0 + h) * q_sh + gl;
+      float a = 0.f;
+      for (int c = 0; c < D / 16; ++c)
+        a = __builtin_fmaf(load_q(q, q_dtype, qr + 16 * c), xk[i * D + gl + 16 * c], a);
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) a += __shfl_xor(a, m, 16);
+      if (gl == 0) etl[h * FC_MAX_BLOCK + i] = a * scale_log2;
+    }
+  }
+  __syncthreads();
+  for (int h = wave; h < G; h += kWaves) {
+    float mx = -INFINITY;
+    for (int i = lane; i < n; i += 64) mx = fmaxf(mx, etl[h * FC_MAX_BLOCK + i]);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    float l = 0.f;
+    for (int i = lane; i < n; i += 64) {
+      const float e = __builtin_amdgcn_exp2f(etl[h * FC_MAX_BLOCK + i] - mx);
+      etl[h * FC_MAX_BLOCK + i] = e;
+      l += e;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
+    if (lane == 0) {
+      tm[h] = mx;
+      tl[h] = l;
+    }
+  }
+  __syncthreads();
+  for (int x = tid; x < G * D; x += kMThreads) {
+    const int h = x / D, d = x - h * D;
+    float o = 0.f;
+    for (int i = 0; i < n; ++i) o = __builtin_fmaf(etl[h * FC_MAX_BLOCK + i], xv[i * D + d], o);
+    acc[h * D + d] = o;
+  }
+}
+
 // Merge of one (batch, kv head, head group) by the workgroup that arrived
 // last, once every other workgroup of the group has published its partial:
 // out = sum_s w_s acc_s / sum_s w_s l_s over the n_splits partials of its G
@@ -222,7 +368,7 @@ __device__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int6
 // thread owns an output task (head, 4 features) and requests its partials
 // kPre splits at a time.  `lds` holds >= 2 * 16 * kFuseMaxSplits floats.
 template <int D>
-__device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
+__device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
                             int split, int tid, float* lds, const float* own_acc,
                             const float* own_m, const float* own_l) {
   constexpr int C4 = D / 4;  // float4 chunks of a head's output
@@ -307,7 +453,7 @@ __device__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g
   }
 }
 
-template <int SROWS, int DK, int GP>
+template <int SROWS, int DK, int GP, bool STEP>
 __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma(MfmaArgs p) {
   constexpr int D = 32 * DK;
   constexpr int DV = (D + 127) / 128;  // 128-feature groups of the value product
@@ -328,6 +474,7 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   __shared__ float tail_ml[2][16];    // raw-tail (max, sum) per head
   __shared__ float wg_ml[2][16];      // this workgroup's (max, sum) per head
   __shared__ int s_last;
+  __shared__ int s_final;
 
   // 1-D grid, split-major: workgroup L runs split s of group g; the splits of
   // a group are spread over the dispatch order and over the XCDs
@@ -349,7 +496,18 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   // group's n_splits workgroups takes the next untaken pass from the group's
   // queue until none is left, so faster wavefronts take more passes.
   int64_t nb = p.nb, n_raw = p.n_raw;
-  if (p.state) {
+  int64_t step_t = 0, step_nb = 0;  // fused step: tail length and blocks before the token
+  bool step_write = false;
+  if constexpr (STEP) {
+    const int64_t cap = min(p.kcap, p.vcap);
+    step_t = p.state ? min<int64_t>(max<int64_t>(p.state[1], 0), p.r - 1) : p.step_t;
+    step_nb = p.state ? max<int64_t>(p.state[0], 0) : p.step_nb;
+    // one head group per (batch, kv head) stores the token / block; a block
+    // past the capacity is not stored (the state's overflow word says so)
+    step_write = split == 0 && g0 == 0 && (step_t + 1 < p.r || step_nb < cap);
+    nb = min(step_nb, cap);
+    n_raw = 0;
+  } else if (p.state) {
     // counts of the step's view, kept inside the buffers whatever the words hold
     const int64_t t = min<int64_t>(max<int64_t>(p.state[1], 0), p.r - 1) + 1;
     nb = min<int64_t>(max<int64_t>(p.state[0], 0) + (t == p.r ? 1 : 0), min(p.kcap, p.vcap));
@@ -533,12 +691,37 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   };
 
   // raw tail (fused calls): split 0 computes its partial before the passes
-  // and folds it into its own, so the final merge reads partials only
-  const bool fold_tail = p.fused && split == 0 && n_raw > 0;
-  if (fold_tail)
+  // and folds it into its own, so the final merge reads partials only; in a
+  // fused step that partial covers the rows the step adds
+  const bool fold_tail = p.fused && split == 0 && (STEP || n_raw > 0);
+  if constexpr (STEP) {
+    if (split == 0) {
+      __shared__ float step_sc[4];
+      float* xk = &s_lds[0][0][0];  // the pass loop has not started: its scratch is free
+      float* etl = reinterpret_cast<float*>(&w_lds[0][0][0]);
+      const int64_t bh_s = b * p.Hkv + hkv;
+      const int64_t kblk = (bh_s * p.kcap + step_nb) * SROWS, vblk = (bh_s * p.vcap + step_nb) * SROWS;
+      auto go = [&](auto tt) {
+        using TT = decltype(tt);
+        step_partial<D, SROWS, TT>(
+            step_t, p.r, static_cast<TT*>(const_cast<void*>(p.kraw)) + bh_s * p.r * D,
+            static_cast<TT*>(const_cast<void*>(p.vraw)) + bh_s * p.r * D,
+            static_cast<const TT*>(p.ktok) + b * p.kt_sb + hkv * p.kt_sh,
+            static_cast<const TT*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write,
+            p.kcodes_w + kblk * D, p.kscales_w + kblk, p.vcodes_w + vblk * D, p.vscales_w + vblk,
+            p.basis, p.A, p.q, p.q_dtype, b * p.q_sb, p.q_sh, hkv * p.G + g0, G, p.scale_log2,
+            tid, xk, xk + p.r * D, cbuf[0][0], step_sc, etl, part_lds, tail_ml[0], tail_ml[1]);
+      };
+      if (p.raw_dtype == FC_F16)
+        go(f16_t{});
+      else
+        go(bf16_t{});
+    }
+  } else if (fold_tail) {
     raw_tail_partial<D>(p, b, hkv, g0, G, (int)n_raw, tid,
                         reinterpret_cast<float*>(&w_lds[0][0][0]), part_lds, tail_ml[0],
                         tail_ml[1]);
+  }
 
   __syncthreads();  // a_lds; the tail's scratch (w_lds) is free again
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
@@ -732,6 +915,24 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   // and the merge runs as its own kernel.
   // thread x publishes (or merges) the outputs x + 256 k it combined itself;
   // the barrier below orders the combine before the last workgroup's merge
+  // fused step with a device state: the launch's last workgroup to finish
+  // (all others have read the state by then) advances it
+  auto step_done = [&]() {
+    if constexpr (!STEP) return;
+    if (!p.state) return;
+    if (tid == 0) s_final = atomicAdd(p.done, 1u) + 1 == gridDim.x ? 1 : 0;
+    __syncthreads();
+    if (s_final && tid < 64) {  // lane-indexed vector stores
+      const int64_t cap = min(p.kcap, p.vcap);
+      const bool full = step_t + 1 == p.r;
+      const bool over = full && step_nb >= cap;
+      const int64_t word = tid == 0   ? (full ? step_nb + 1 : step_nb)
+                           : tid == 1 ? (full ? 0 : step_t + 1)
+                                      : ((p.state[2] != 0 || over) ? 1 : 0);
+      if (tid < 3) const_cast<int64_t*>(p.state)[tid] = word;
+      if (tid == 0) __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
   unsigned int* arrive = p.arrive + g * p.cstride;
   if (tid == 0) {
     const unsigned int old = atomicAdd(arrive, 1u);
@@ -765,6 +966,7 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     if (tid == 0) atomicAdd(arrive + kPubWord, 1u);
+    step_done();
     return;
   }
   if (tid == 0) {
@@ -795,6 +997,7 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   }
   __syncthreads();
   fused_merge<D>(p, b, hkv, g0, G, split, tid, &s_lds[0][0][0], part_lds, wg_ml[0], wg_ml[1]);
+  step_done();
 }
 
 template <int... Vs, typename F>
@@ -817,6 +1020,12 @@ bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q
 }
 
 bool split_i8_mfma_fusable(int n_splits) { return n_splits <= kFuseMaxSplits; }
+
+bool step_i8_mfma_supported(int stream_dtype, int r, int64_t D, int n_splits) {
+  // the step's rows (2 r D floats) live in the score scratch before the passes
+  return (stream_dtype == FC_F16 || stream_dtype == FC_BF16) && split_i8_mfma_fusable(n_splits) &&
+         2 * (int64_t)r * D <= (int64_t)kWaves * 16 * kSPad;
+}
 
 int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
                          int64_t Hq, int64_t Hkv, int64_t D, int r, int s, int64_t nb,
@@ -863,6 +1072,23 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
     a.o_sb = fuse->o_sb;
     a.o_sh = fuse->o_sh;
     a.state = fuse->state;
+    if (fuse->step) {
+      a.step = 1;
+      a.ktok = fuse->ktok;
+      a.vtok = fuse->vtok;
+      a.kt_sb = fuse->kt_sb;
+      a.kt_sh = fuse->kt_sh;
+      a.vt_sb = fuse->vt_sb;
+      a.vt_sh = fuse->vt_sh;
+      a.kcodes_w = const_cast<int8_t*>(a.kcodes);
+      a.vcodes_w = const_cast<int8_t*>(a.vcodes);
+      a.kscales_w = const_cast<float*>(a.kscales);
+      a.vscales_w = const_cast<float*>(a.vscales);
+      a.basis = fuse->basis;
+      a.step_t = fuse->step_t;
+      a.step_nb = fuse->step_nb;
+      a.done = fuse->done;
+    }
   }
   const int64_t G = Hq / Hkv;
   const int gg = (int)std::min<int64_t>(G, 16);
@@ -883,7 +1109,10 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
       constexpr int DKv = decltype(dc)::value;
       return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
         constexpr int GPv = decltype(gc)::value;
-        attn_split_i8_mfma<SR, DKv, GPv><<<grid, kMThreads, 0, st>>>(a);
+        if (a.step)
+          attn_split_i8_mfma<SR, DKv, GPv, true><<<grid, kMThreads, 0, st>>>(a);
+        else
+          attn_split_i8_mfma<SR, DKv, GPv, false><<<grid, kMThreads, 0, st>>>(a);
         return FC_OK;
       });
     });

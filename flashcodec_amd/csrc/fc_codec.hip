@@ -44,21 +44,6 @@ __device__ __forceinline__ ItemMap item_of_thread(int lpi_log2) {
   return m;
 }
 
-// clamp(rint(fl(c / s)), -127, 127) for a quantizer row with scale s and
-// rs = fl(1 / s), where fl(c / s) is the IEEE single-precision quotient.
-// For |c / s| < 128: x = fl(c * rs) is within |c/s| 2^-23 <= 2^-16 of c / s
-// and fl(c / s) within 2^-17 of it, so they round to the same integer unless
-// a half-integer lies within 2^-15 of x; only then is the quotient computed
-// exactly.  (Scales are fl(amax / 127) rounded to the stream dtype, so
-// |c / s| <= 127 (1 + 2^-8) < 128.)
-// A NaN quotient gets code 0 (the reference's int8 cast of NaN is
-// undefined; 0 is what x86's truncating conversion gives).
-__device__ __forceinline__ float quant_code(float c, float s, float rs) {
-  const float x = c * rs;
-  float q = __builtin_rintf(x);
-  if (!(0.5f - fabsf(x - q) > 0x1p-15f)) q = __builtin_rintf(c / s);
-  return q == q ? fminf(fmaxf(q, -127.f), 127.f) : 0.f;
-}
 
 // ---------------------------------------------------------------- jpeg encode
 

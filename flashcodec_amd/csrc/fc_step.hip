@@ -57,6 +57,66 @@ __global__ void state_advance_kernel(int64_t* state, int64_t r, int64_t cap) {
   state[i] = v[i];
 }
 
+// The whole step as one launch of the matrix-core decode attention: split
+// 0's workgroups append the tokens to the tails (or archive the block they
+// complete, attending it from its fresh codes) before their passes over the
+// blocks already archived; with a device state the launch's last workgroup
+// advances it.  FC_ERR_UNSUPPORTED when the step's shape does not allow it
+// (then the step takes the multi-launch path).
+static int step_single_launch(const fc_step_args* a, const int64_t* state) {
+  if (a->store_kind != FC_STORE_JPEG_I8 || a->quant_bits != 8 || !mfma_split_allowed())
+    return FC_ERR_UNSUPPORTED;
+  const int64_t B = a->B, Hq = a->Hq, Hkv = a->Hkv, D = a->D;
+  const int r = a->r;
+  const int64_t G = Hq / Hkv;
+  const int64_t nb = a->n_blocks;  // host counters: blocks before the step; state: split hint
+  if (nb < 1) return FC_ERR_UNSUPPORTED;
+  const fc_step_stream* st[2] = {&a->key, &a->value};
+  fc_stream_view v[2];
+  for (int i = 0; i < 2; ++i) {
+    v[i].rows = st[i]->rows;
+    v[i].scales = st[i]->scales;
+    v[i].anchors = nullptr;
+    v[i].cap = st[i]->cap;
+    v[i].raw = st[i]->tail;
+    v[i].raw_sb = Hkv * r * D;
+    v[i].raw_sh = (int64_t)r * D;
+    v[i].raw_st = D;
+  }
+  if (!split_i8_mfma_supported(a->q, a->q_dtype, a->q_sb, a->q_sh, D, a->s, &v[0], &v[1]))
+    return FC_ERR_UNSUPPORTED;
+  if (2 * B * Hkv * ((G + 15) / 16) * kCounterStride > kCounterWords) return FC_ERR_UNSUPPORTED;
+  const int n_splits = fc_attention_splits(a->store_kind, a->stream_dtype, a->q_dtype, a->s, nb,
+                                           B, Hkv, G, D, a->n_cu);
+  if (n_splits < 1 || !step_i8_mfma_supported(a->stream_dtype, r, D, n_splits))
+    return FC_ERR_UNSUPPORTED;
+  if (!a->workspace || fc_attention_workspace_bytes(B, Hq, D, n_splits) > a->workspace_bytes)
+    return FC_ERR_ARG;
+  const WsLayout ws = ws_layout(a->workspace, B, Hq, n_splits);
+  MfmaFuse fz{};
+  fz.raw_dtype = a->stream_dtype;
+  fz.n_raw = 0;
+  fz.out = a->out;
+  fz.o_sb = a->o_sb;
+  fz.o_sh = a->o_sh;
+  fz.state = state;
+  fz.step = true;
+  fz.ktok = a->key.token;
+  fz.vtok = a->value.token;
+  fz.kt_sb = a->key.tok_sb;
+  fz.kt_sh = a->key.tok_sh;
+  fz.vt_sb = a->value.tok_sb;
+  fz.vt_sh = a->value.tok_sh;
+  fz.basis = a->basis;
+  fz.step_t = a->n_tail;
+  fz.step_nb = a->n_blocks;
+  fz.done = ws.done;
+  return launch_split_i8_mfma(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, r, a->s, nb,
+                              &v[0], &v[1], a->A, a->scale * 1.4426950408889634f, ws.pm, ws.pl,
+                              ws.pacc, n_splits, ws.counters, kCounterWords, kCounterStride,
+                              ws.status, &fz, (hipStream_t)a->stream);
+}
+
 // The step with its counters on the device (a->state): every launch reads
 // them there, so one captured graph of the step is valid at every step.
 static int decode_step_state(const fc_step_args* a) {
@@ -65,6 +125,8 @@ static int decode_step_state(const fc_step_args* a) {
   if (kind != FC_STORE_JPEG_I8 && kind != FC_STORE_JPEG_FP && kind != FC_STORE_PNG)
     return FC_ERR_ARG;
   if (a->n_blocks < 1) return FC_ERR_ARG;  // the archive holds a block before capture
+  const int one = step_single_launch(a, a->state);
+  if (one != FC_ERR_UNSUPPORTED) return one;
   const int64_t B = a->B, Hkv = a->Hkv, D = a->D;
   const int r = a->r;
   hipStream_t stream = (hipStream_t)a->stream;
@@ -147,6 +209,8 @@ int fc_decode_step(const fc_step_args* a) {
   const bool completes = a->n_tail + 1 == r;
   if (completes && (a->n_blocks + 1 > a->key.cap || a->n_blocks + 1 > a->value.cap))
     return FC_ERR_ARG;  // the caller grows the archives first
+  const int one = step_single_launch(a, nullptr);
+  if (one != FC_ERR_UNSUPPORTED) return one;
   hipStream_t stream = (hipStream_t)a->stream;
 
   // 1. the new tokens into the tails
