@@ -17,7 +17,7 @@ F32, F16, BF16, I8 = 0, 1, 2, 3
 OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_INCOMPLETE, ERR_SCRATCH = 0, -1, -2, -3, -4, -5
 NOALLOC_SCRATCH_BYTES = 16 << 20
 PASS_AUTO, PASS_VECTOR, PASS_STATIC = 0, 1, 2
-STORE_JPEG_I8, STORE_JPEG_FP, STORE_PNG = 0, 1, 2
+STORE_JPEG_I8, STORE_JPEG_FP, STORE_PNG, STORE_JPEG_I8G = 0, 1, 2, 3
 MAX_BLOCK = 64
 MAX_HEAD_DIM = 512
 
@@ -71,6 +71,10 @@ SIGNATURES = {
                               _int, _int, _vp, _vp, _vp, _i64, _i64, _int, _vp]),
     "fc_jpeg_decode": (_int, [_vp, _int, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
                               _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp]),
+    "fc_jpeg_encode_grouped": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                      _int, _int, _vp, _vp, _vp, _i64, _i64, _int, _vp]),
+    "fc_jpeg_decode_grouped": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
+                                      _int, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp]),
     "fc_quantize_rows": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp]),
     "fc_dequantize_rows": (_int, [_vp, _vp, _i64, _i64, _vp, _int, _vp]),
     "fc_png_encode": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,

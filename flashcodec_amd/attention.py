@@ -71,6 +71,13 @@ def workspace(device, nbytes):
     return ws
 
 
+def _jpeg_kind(codec):
+    """Store kind of a jpeg codec's archive for the decode attention."""
+    if not codec.quantized:
+        return N.STORE_JPEG_FP
+    return N.STORE_JPEG_I8G if codec.quant_group else N.STORE_JPEG_I8
+
+
 FUSED_MERGE_MAX_SPLITS = 64   # the matrix-core pass merges in-kernel up to this many splits
 
 
@@ -180,7 +187,7 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
     c = ks.codec
     r = ks.block_size
     if c.name == "jpeg":
-        kind = N.STORE_JPEG_I8 if c.quantized else N.STORE_JPEG_FP
+        kind = _jpeg_kind(c)
         s = c.keep_freqs
     else:
         kind = N.STORE_PNG
@@ -213,7 +220,8 @@ def prefill_supported(codec, dtype, head_dim):
     """Whether codec_prefill_attention runs streams of `codec` with queries
     of `dtype` and head size `head_dim`: int8 jpeg archives with 1 / 2 / 4
     kept frequencies, fp16 / bf16 queries, head size 64 / 128 / 256."""
-    return (codec.name == "jpeg" and codec.quantized and codec.keep_freqs in (1, 2, 4)
+    return (codec.name == "jpeg" and codec.quantized and not codec.quant_group
+            and codec.keep_freqs in (1, 2, 4)
             and dtype in (torch.float16, torch.bfloat16) and head_dim in (64, 128, 256))
 
 
@@ -277,7 +285,7 @@ def _step_args(ks, vs, query, tokens):
     a.q_dtype = N.dtype_code(query.dtype)
     a.B, a.Hq, a.Hkv, a.D = B, Hq, Hkv, D
     if c.name == "jpeg":
-        a.store_kind = N.STORE_JPEG_I8 if c.quantized else N.STORE_JPEG_FP
+        a.store_kind = _jpeg_kind(c)
         a.s = c.keep_freqs
         a.quant_bits = c.quant_bits
         a.basis = dct_basis_device(r, c.keep_freqs, dev).data_ptr()
@@ -305,6 +313,7 @@ def _same_codec(a, b):
     return (a.name == b.name and a.block_size == b.block_size
             and getattr(a, "keep_freqs", None) == getattr(b, "keep_freqs", None)
             and getattr(a, "quant_bits", None) == getattr(b, "quant_bits", None)
+            and getattr(a, "quant_group", None) == getattr(b, "quant_group", None)
             and getattr(a, "keep_ratio", None) == getattr(b, "keep_ratio", None))
 
 

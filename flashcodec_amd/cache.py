@@ -48,16 +48,20 @@ except Exception:  # transformers absent: CodecKVCache still works
 _FIRST_CAPACITY = 16   # archive blocks of a stream's first allocation
 
 
-def make_codec(mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0, quant_bits=0):
+def make_codec(mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0, quant_bits=0,
+               quant_group=0):
     """Codec instance from a mode name (flashcodec/cache.py:39-54); png keeps
-    fp32 deltas on purpose and rejects quant_bits."""
+    fp32 deltas on purpose and rejects quant_bits.  quant_group=32 (jpeg with
+    quant_bits=8; this build's extension) scales every 32 features of a
+    coefficient row separately."""
     if mode == "png":
-        if quant_bits:
+        if quant_bits or quant_group:
             raise ValueError("quant_bits is only supported for mode='jpeg' "
                              "(the png lossless tier must keep fp32 deltas)")
         return PNGCodec(block_size=block_size, keep_ratio=keep_ratio)
     if mode == "jpeg":
-        return JPEGCodec(block_size=block_size, keep_freqs=keep_freqs, quant_bits=quant_bits)
+        return JPEGCodec(block_size=block_size, keep_freqs=keep_freqs, quant_bits=quant_bits,
+                         quant_group=quant_group)
     raise ValueError(f"unknown mode: {mode!r} (expected 'jpeg' | 'png')")
 
 
@@ -180,7 +184,8 @@ class _CodecStream:
         spec = [("_coeffs", (B, H, cap, c.keep_freqs, D),
                  torch.int8 if c.quantized else self.dtype)]
         if c.quantized:
-            spec.append(("_scales", (B, H, cap, c.keep_freqs, 1), torch.float32))
+            groups = D // c.quant_group if c.quant_group else 1
+            spec.append(("_scales", (B, H, cap, c.keep_freqs, groups), torch.float32))
         return spec
 
     def _archive_tensors(self):
@@ -218,8 +223,12 @@ class _CodecStream:
             _png.encode_into(head, r, c.keep_m, self._deltas, self._anchors, self._capacity,
                              self.n_blocks, m, m * r)
         else:
+            if c.quant_group and head.shape[-1] % c.quant_group:
+                raise ValueError(f"quant_group={c.quant_group} needs a head size that is a "
+                                 f"multiple of it (got {head.shape[-1]})")
             _jpeg.encode_into(head, r, c.keep_freqs, c.quant_bits, self._coeffs, self._scales,
-                              self._capacity, self.n_blocks, m, m * r)
+                              self._capacity, self.n_blocks, m, m * r,
+                              group=getattr(c, "quant_group", 0))
         self.n_blocks += m
 
     def _reconstruct(self, first, count, out, out_len, token0=0):
@@ -233,7 +242,7 @@ class _CodecStream:
                              r, out, out_len, token0)
         else:
             _jpeg.decode_into(self._coeffs, self._scales, B, H, self._capacity, first, count, D,
-                              r, c.keep_freqs, out, out_len, token0)
+                              r, c.keep_freqs, out, out_len, token0, group=c.quant_group)
 
     # ------------------------------------------------------------ write
     def append(self, tokens):
@@ -437,9 +446,10 @@ class CodecKVCache:
     """
 
     def __init__(self, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0,
-                 quant_bits=0):
+                 quant_bits=0, quant_group=0):
         self.mode = mode
-        self.codec = make_codec(mode, block_size, keep_freqs, keep_ratio, quant_bits=quant_bits)
+        self.codec = make_codec(mode, block_size, keep_freqs, keep_ratio, quant_bits=quant_bits,
+                                quant_group=quant_group)
         self._pairs = {}     # layer index -> _KVPair
 
     def _pair(self, layer_idx):
@@ -536,10 +546,12 @@ class FlashCodecLayer(_HFDynamicLayer):
     ``update`` returns the reconstructed causal KV
     (flashcodec/cache.py:446-544)."""
 
-    def __init__(self, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0, quant_bits=0):
+    def __init__(self, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0, quant_bits=0,
+                 quant_group=0):
         super().__init__()
         self.mode = mode
-        self.codec = make_codec(mode, block_size, keep_freqs, keep_ratio, quant_bits=quant_bits)
+        self.codec = make_codec(mode, block_size, keep_freqs, keep_ratio, quant_bits=quant_bits,
+                                quant_group=quant_group)
         self._pair = _KVPair(self.codec)
 
     @property
@@ -652,12 +664,15 @@ class FlashCodecCache(_HFCache):
         model.generate(input_ids, past_key_values=cache, use_cache=True)
     """
 
-    def __init__(self, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0, quant_bits=0):
+    def __init__(self, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0, quant_bits=0,
+                 quant_group=0):
         if not HAS_HF_CACHE:
             raise ImportError("FlashCodecCache requires transformers 5.x; use CodecKVCache "
                               "when transformers is unavailable.")
         cfg = dict(mode=mode, block_size=block_size, keep_freqs=keep_freqs,
                    keep_ratio=keep_ratio, quant_bits=quant_bits)
+        if quant_group:
+            cfg["quant_group"] = quant_group
         super().__init__(layers=None, layer_class_to_replicate=partial(FlashCodecLayer, **cfg))
         self._remember(cfg)
 
@@ -672,13 +687,15 @@ class FlashCodecCache(_HFCache):
 
     @classmethod
     def from_config(cls, config, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0,
-                    quant_bits=0, per_layer=None):
+                    quant_bits=0, per_layer=None, quant_group=0):
         """Per-layer cache for a model config: codec layers where the model
         uses full attention (each optionally overridden through
         ``per_layer[index]``), transformers' own layers elsewhere."""
         from transformers.cache_utils import DYNAMIC_LAYER_TYPE_MAPPING
         cfg = dict(mode=mode, block_size=block_size, keep_freqs=keep_freqs,
                    keep_ratio=keep_ratio, quant_bits=quant_bits)
+        if quant_group:
+            cfg["quant_group"] = quant_group
         layers = [FlashCodecLayer(**kw) if kind == "full_attention"
                   else DYNAMIC_LAYER_TYPE_MAPPING[kind](**kw)
                   for kind, kw in _layer_plan(config, per_layer, cfg)]

@@ -59,7 +59,7 @@ def _as_rows(x):
     return x3
 
 
-def encode_into(x3, r, k, quant_bits, coeffs, scales, cap, n0, m, s_valid, H=1):
+def encode_into(x3, r, k, quant_bits, coeffs, scales, cap, n0, m, s_valid, H=1, group=0):
     """Run the jpeg archive kernel: m blocks of every sequence of x3
     (B, H, S, D) or (BH, S, D) into the store at block offset n0."""
     if x3.dim() == 3:
@@ -70,6 +70,13 @@ def encode_into(x3, r, k, quant_bits, coeffs, scales, cap, n0, m, s_valid, H=1):
         sb, sh, ss = x3.stride(0), x3.stride(1), x3.stride(2)
     D = x3.shape[-1]
     basis = device_basis(r, k, x3.device)
+    if group:
+        rc = N.lib().fc_jpeg_encode_grouped(
+            x3.data_ptr(), N.dtype_code(x3.dtype), B, Hh, sb, sh, ss, s_valid, m, D, r, k,
+            basis.data_ptr(), coeffs.data_ptr(), scales.data_ptr(), cap, n0, group,
+            N.stream_ptr(x3.device))
+        N.check(rc, "fc_jpeg_encode_grouped")
+        return
     rc = N.lib().fc_jpeg_encode(
         x3.data_ptr(), N.dtype_code(x3.dtype), B, Hh, sb, sh, ss, s_valid, m, D, r, k,
         basis.data_ptr(), coeffs.data_ptr(), N.ptr(scales), cap, n0, quant_bits,
@@ -77,7 +84,7 @@ def encode_into(x3, r, k, quant_bits, coeffs, scales, cap, n0, m, s_valid, H=1):
     N.check(rc, "fc_jpeg_encode")
 
 
-def decode_into(store, scales, B, H, cap, a, nblk, D, r, k, out, out_len, token0=0):
+def decode_into(store, scales, B, H, cap, a, nblk, D, r, k, out, out_len, token0=0, group=0):
     """Run the jpeg reconstruction kernel for blocks [a, a+nblk) into `out`
     (B, H, T, D) whose row 0 holds token `token0` (token t = block*r + row;
     tokens >= out_len skipped).  The kernel addresses token t at
@@ -85,6 +92,13 @@ def decode_into(store, scales, B, H, cap, a, nblk, D, r, k, out, out_len, token0
     `out`; only rows of `out` itself are written."""
     basis = device_basis(r, k, store.device)
     base = out.data_ptr() - token0 * out.stride(2) * out.element_size()
+    if group:
+        rc = N.lib().fc_jpeg_decode_grouped(
+            store.data_ptr(), scales.data_ptr(), B, H, cap, a, nblk, D, r, k, group,
+            basis.data_ptr(), base, N.dtype_code(out.dtype), out.stride(0), out.stride(1),
+            out.stride(2), out_len, N.stream_ptr(store.device))
+        N.check(rc, "fc_jpeg_decode_grouped")
+        return
     rc = N.lib().fc_jpeg_decode(
         store.data_ptr(), N.dtype_code(store.dtype), N.ptr(scales), B, H, cap, a, nblk, D, r,
         k, basis.data_ptr(), base, N.dtype_code(out.dtype), out.stride(0),
@@ -162,38 +176,55 @@ def dct_decompress(coeffs, r, out_len=None):
     return _decompress(coeffs, r, out_len)
 
 
-def quantize_coeffs(coeffs, bits=8):
+def _row_view(t, width):
+    """(..., D) -> (rows, width) view of a contiguous tensor, D a multiple of width."""
+    D = t.shape[-1]
+    if D % width:
+        raise ValueError(f"the feature width {D} is not a multiple of the quantizer group {width}")
+    return t.contiguous().reshape(-1, width)
+
+
+def quantize_coeffs(coeffs, bits=8, group=0):
     """Symmetric int8 quantisation, one scale per (block, frequency) row:
     (..., n, k, D) -> (int8 codes, fp32 scales (..., n, k, 1))
-    (flashcodec/codecs/jpeg.py:85-100)."""
+    (flashcodec/codecs/jpeg.py:85-100).  group=32 (this build's extension):
+    one scale per 32 features of each row, scales (..., n, k, D/32) — the
+    same rule applied to every 32-feature run."""
     if bits != 8:
         raise ValueError(f"only 8-bit coefficient quantization is supported, got bits={bits}")
+    if group not in (0, 32):
+        raise ValueError(f"quantizer group must be 0 (one scale per row) or 32, got {group}")
     N.require_gpu(coeffs)
     D = coeffs.shape[-1]
-    rows = coeffs.reshape(-1, D)
+    width = group or D
+    rows = coeffs.reshape(-1, D) if not group else _row_view(coeffs, width)
     if rows.stride(-1) != 1:
         rows = rows.contiguous()
     codes = torch.empty(coeffs.shape, dtype=torch.int8, device=coeffs.device)
-    scales = torch.empty(coeffs.shape[:-1] + (1,), dtype=torch.float32, device=coeffs.device)
+    scales = torch.empty(coeffs.shape[:-1] + (D // width,), dtype=torch.float32,
+                         device=coeffs.device)
     if rows.shape[0]:
         rc = N.lib().fc_quantize_rows(rows.data_ptr(), N.dtype_code(rows.dtype), rows.shape[0],
-                                      rows.stride(0), D, codes.data_ptr(), scales.data_ptr(),
+                                      rows.stride(0), width, codes.data_ptr(), scales.data_ptr(),
                                       N.stream_ptr(coeffs.device))
         N.check(rc, "fc_quantize_rows")
     return codes, scales
 
 
 def dequantize_coeffs(q, scale, dtype=torch.float32):
-    """int8 codes + per-row scale -> q.to(dtype) * scale.to(dtype)
-    (flashcodec/codecs/jpeg.py:103-105)."""
+    """int8 codes + scales -> q.to(dtype) * scale.to(dtype)
+    (flashcodec/codecs/jpeg.py:103-105); scales (..., 1) per row or
+    (..., D/32) per 32 features (quantize_coeffs with group=32)."""
     N.require_gpu(q, scale)
     D = q.shape[-1]
+    groups = scale.shape[-1] if scale.dim() == q.dim() else 1
+    width = D // groups if groups else D
     qc = q.contiguous()
-    sc = scale.reshape(q.shape[:-1]).to(torch.float32).contiguous()
+    sc = scale.reshape(q.shape[:-1] + (groups,)).to(torch.float32).contiguous()
     out = torch.empty(q.shape, dtype=dtype, device=q.device)
-    n_rows = qc.numel() // D if D else 0
+    n_rows = qc.numel() // width if width else 0
     if n_rows:
-        rc = N.lib().fc_dequantize_rows(qc.data_ptr(), sc.data_ptr(), n_rows, D,
+        rc = N.lib().fc_dequantize_rows(qc.data_ptr(), sc.data_ptr(), n_rows, width,
                                         out.data_ptr(), N.dtype_code(dtype),
                                         N.stream_ptr(q.device))
         N.check(rc, "fc_dequantize_rows")
@@ -203,17 +234,23 @@ def dequantize_coeffs(q, scale, dtype=torch.float32):
 class JPEGCodec:
     """JPEG-style lossy frequency-domain codec (stateless, shareable).
     ``quant_bits=8`` stores the kept coefficients as int8 with one fp32 scale
-    per (block, frequency) (flashcodec/codecs/jpeg.py:108-158)."""
+    per (block, frequency) (flashcodec/codecs/jpeg.py:108-158);
+    ``quant_group=32`` (this build's extension) gives every 32 features of a
+    row their own scale (the per-32 absmax quantizer of flashcodec
+    README.md:487-494)."""
 
     name = "jpeg"
 
-    def __init__(self, block_size=8, keep_freqs=2, quant_bits=0):
+    def __init__(self, block_size=8, keep_freqs=2, quant_bits=0, quant_group=0):
         assert 1 <= keep_freqs <= block_size, f"keep_freqs must be within [1, {block_size}]"
         assert quant_bits in (0, 8), \
             f"quant_bits must be 0 (store in input dtype) or 8, got {quant_bits}"
+        assert quant_group in (0, 32) and (quant_group == 0 or quant_bits == 8), \
+            f"quant_group must be 0 or 32 (with quant_bits=8), got {quant_group}"
         self.block_size = block_size
         self.keep_freqs = keep_freqs
         self.quant_bits = quant_bits
+        self.quant_group = quant_group
 
     @property
     def quantized(self):
@@ -226,7 +263,7 @@ class JPEGCodec:
         """Coefficients -> (int8, scale) when quantized, else (None, None)."""
         if not self.quantized:
             return None, None
-        return quantize_coeffs(coeffs, self.quant_bits)
+        return quantize_coeffs(coeffs, self.quant_bits, self.quant_group)
 
     def decompress(self, coeffs, out_len=None, scales=None):
         if self.quantized:
@@ -242,4 +279,6 @@ class JPEGCodec:
 
     def __repr__(self):
         q = f", quant_bits={self.quant_bits}" if self.quantized else ""
+        if self.quant_group:
+            q += f", quant_group={self.quant_group}"
         return f"JPEGCodec(block_size={self.block_size}, keep_freqs={self.keep_freqs}{q})"

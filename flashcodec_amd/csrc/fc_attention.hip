@@ -166,6 +166,14 @@ __device__ __forceinline__ float load_row(const void* rows, const float* scales,
     const int64_t row = (bh * cap + n) * s + j;
     load_f32<int8_t, VEC>(static_cast<const int8_t*>(rows) + row * D + d0, x);
     return scales[row];
+  } else if constexpr (KIND == FC_STORE_JPEG_I8G) {
+    // one scale per 32 features: the lane's VEC features share one, applied here
+    const int64_t row = (bh * cap + n) * s + j;
+    load_f32<int8_t, VEC>(static_cast<const int8_t*>(rows) + row * D + d0, x);
+    const float sg = scales[row * (D / 32) + d0 / 32];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v] *= sg;
+    return 1.f;
   } else if constexpr (KIND == FC_STORE_JPEG_FP) {
     const int64_t row = (bh * cap + n) * s + j;
     load_f32<TS, VEC>(static_cast<const TS*>(rows) + row * D + d0, x);
@@ -495,7 +503,7 @@ void attn_split_kernel(AttnArgs p) {
     auto raw_row = [&](const void* base, int64_t off0, int64_t st, int t, bool ok,
                        float (&x)[VEC]) {
       const int64_t off = ok ? off0 + t * st + d0 : off0;
-      const int dt = KIND == FC_STORE_JPEG_I8 ? p.raw_dtype
+      const int dt = (KIND == FC_STORE_JPEG_I8 || KIND == FC_STORE_JPEG_I8G) ? p.raw_dtype
                      : std::is_same_v<TS, f16_t> ? FC_F16
                      : std::is_same_v<TS, bf16_t> ? FC_BF16 : FC_F32;
       switch (dt) {
@@ -579,8 +587,8 @@ void attn_split_kernel(AttnArgs p) {
       const int rho = rho0 + u * nslot;
       const bool ok = rho < nrows;
       const int nl = ok ? rho / s : 0, j = ok ? rho - nl * s : 0;
-      load_row<TS, KIND, VEC>(p.vrows, nullptr, p.vanch, p.vcap, bh, nb0 + nl, j, s, r, p.D, d0,
-                              dact && ok, x[u]);
+      load_row<TS, KIND, VEC>(p.vrows, KIND == FC_STORE_JPEG_I8G ? p.vscales : nullptr,
+                              p.vanch, p.vcap, bh, nb0 + nl, j, s, r, p.D, d0, dact && ok, x[u]);
     }
   };
 
@@ -1071,6 +1079,9 @@ int valu_split_occupancy(int store_kind, int stream_dtype, int s, int gm) {
     if (store_kind == FC_STORE_JPEG_I8)
       return sreg ? valu_occupancy_of<float, FC_STORE_JPEG_I8, true, GM>()
                   : valu_occupancy_of<float, FC_STORE_JPEG_I8, false, GM>();
+    if (store_kind == FC_STORE_JPEG_I8G)
+      return sreg ? valu_occupancy_of<float, FC_STORE_JPEG_I8G, true, GM>()
+                  : valu_occupancy_of<float, FC_STORE_JPEG_I8G, false, GM>();
     if (store_kind == FC_STORE_PNG) return by_dtype(KPNG{}, std::true_type{});
     if (store_kind == FC_STORE_JPEG_FP)
       return sreg ? by_dtype(KFP{}, std::true_type{}) : by_dtype(KFP{}, std::false_type{});
@@ -1274,6 +1285,10 @@ static int launch_split_valu(const void* q, int q_dtype, int64_t q_sb, int64_t q
     // int8 rows do not depend on the stream dtype (the tail's dtype is read
     // at run time)
     rc = sreg ? go(float{}, KI8{}, ST{}) : go(float{}, KI8{}, SF{});
+  } else if (store_kind == FC_STORE_JPEG_I8G) {
+    if (D % 32) return FC_ERR_ARG;
+    using KI8G = std::integral_constant<int, FC_STORE_JPEG_I8G>;
+    rc = sreg ? go(float{}, KI8G{}, ST{}) : go(float{}, KI8G{}, SF{});
   } else if (store_kind == FC_STORE_JPEG_FP || store_kind == FC_STORE_PNG) {
     const bool png = store_kind == FC_STORE_PNG;
     auto pick = [&](auto ts) {
@@ -1311,7 +1326,10 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
   if (nb > 0) {
     if (!A || !key->rows || !value->rows || !workspace) return FC_ERR_ARG;
     if (n_splits < 1 || n_splits > kMaxSplits) return FC_ERR_ARG;
-    if (store_kind == FC_STORE_JPEG_I8 && (!key->scales || !value->scales)) return FC_ERR_ARG;
+    if ((store_kind == FC_STORE_JPEG_I8 || store_kind == FC_STORE_JPEG_I8G) &&
+        (!key->scales || !value->scales))
+      return FC_ERR_ARG;
+    if (store_kind == FC_STORE_JPEG_I8G && D % 32) return FC_ERR_ARG;
     if (store_kind == FC_STORE_PNG && (!key->anchors || !value->anchors)) return FC_ERR_ARG;
     if (nb > key->cap || nb > value->cap) return FC_ERR_ARG;
   } else {
@@ -1408,7 +1426,9 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv) return FC_ERR_ARG;
   if (r < 1 || r > FC_MAX_BLOCK || s < 1 || s > r) return FC_ERR_ARG;
   if (!key->rows || !value->rows || !key->raw || !value->raw) return FC_ERR_ARG;
-  if (store_kind == FC_STORE_JPEG_I8 && (!key->scales || !value->scales)) return FC_ERR_ARG;
+  if ((store_kind == FC_STORE_JPEG_I8 || store_kind == FC_STORE_JPEG_I8G) &&
+      (!key->scales || !value->scales))
+    return FC_ERR_ARG;
   if (store_kind == FC_STORE_PNG && (!key->anchors || !value->anchors || s != r)) return FC_ERR_ARG;
   const int64_t G = Hq / Hkv;
   const int n_splits =

@@ -137,6 +137,6 @@ int png_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x
 int jpeg_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
                       int64_t x_sh, int64_t x_ss, int64_t D, int r, int k, const float* basis,
                       void* coeffs, float* scales, int64_t cap, int quant_bits, void* stream,
-                      const int64_t* gate);
+                      const int64_t* gate, int group = 0);
 
 }  // namespace fc

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kThreads) void jpeg_encode_kernel(
     const T* __restrict__ x, int64_t sb, int64_t sh, int64_t ss, int64_t H, int64_t m,
     int64_t D, int64_t s_valid, int r, int k, const float* __restrict__ basis,
     void* __restrict__ out, float* __restrict__ scales, int64_t cap, int64_t n0,
-    int64_t items, int lpi_log2, const int64_t* __restrict__ gate = nullptr) {
+    int64_t items, int lpi_log2, const int64_t* __restrict__ gate = nullptr, int group = 0) {
   if constexpr (GATED) {
     // gate = device (n_blocks, n_tail) of a decode step: the block is
     // archived only when the tail completes it, at block n_blocks
@@ -122,10 +122,13 @@ __global__ __launch_bounds__(kThreads) void jpeg_encode_kernel(
     if constexpr (!QUANT) {
       if (active) store_from_f32<T, VEC>(static_cast<T*>(out) + (out_row0 + j) * D + d0, c);
     } else {
+      // one scale per row, or per `group` features of the row (the lanes
+      // of a group are aligned runs of group / VEC lanes)
+      const int glanes = group ? group / VEC : 1 << lpi_log2;
       float amax = 0.f;
 #pragma unroll
       for (int v = 0; v < VEC; ++v) amax = fmaxf(amax, fabsf(c[v]));
-      amax = group_max_rt(amax, 1 << lpi_log2);
+      amax = group_max_rt(amax, glanes);
       float s = to_f32(from_f32<T>(amax / 127.0f));
       if (!(s > 0.f)) s = 1.0f;
       const float rs = 1.0f / s;
@@ -135,7 +138,12 @@ __global__ __launch_bounds__(kThreads) void jpeg_encode_kernel(
         for (int v = 0; v < VEC; ++v) qv.v[v] = (int8_t)(int)quant_code(c[v], s, rs);
         *reinterpret_cast<vec_t<int8_t, VEC>*>(static_cast<int8_t*>(out) + (out_row0 + j) * D +
                                                d0) = qv;
-        if (im.lane == 0) scales[out_row0 + j] = s;
+        if ((im.lane & (glanes - 1)) == 0) {
+          if (group)
+            scales[(out_row0 + j) * (D / group) + d0 / group] = s;
+          else
+            scales[out_row0 + j] = s;
+        }
       }
     }
   }
@@ -325,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void jpeg_decode_kernel(
     const TI* __restrict__ store, const float* __restrict__ scales, int64_t H, int64_t cap,
     int64_t a, int64_t nblk, int64_t D, int r, int k, const float* __restrict__ basis,
     TO* __restrict__ out, int64_t osb, int64_t osh, int64_t oss, int64_t out_len,
-    int64_t items, int lpi_log2) {
+    int64_t items, int lpi_log2, int group = 0) {
   const ItemMap im = item_of_thread(lpi_log2);
   if (im.item >= items) return;
   const int64_t bh = im.item / nblk, blk = a + (im.item - bh * nblk);
@@ -346,7 +354,8 @@ __global__ __launch_bounds__(kThreads) void jpeg_decode_kernel(
       float c[VEC];
       load_f32<TI, VEC>(store + (row0 + j) * D + d0, c);
       if constexpr (QUANT) {
-        const float s = scales[row0 + j];
+        const float s =
+            group ? scales[(row0 + j) * (D / group) + d0 / group] : scales[row0 + j];
 #pragma unroll
         for (int v = 0; v < VEC; ++v) c[v] = c[v] * s;
       }
@@ -373,7 +382,8 @@ __global__ __launch_bounds__(kThreads) void jpeg_decode_kernel(
         float c[VEC];
         load_f32<TI, VEC>(store + (row0 + j) * D + d0, c);
         if constexpr (QUANT) {
-          const float s = scales[row0 + j];
+          const float s =
+              group ? scales[(row0 + j) * (D / group) + d0 / group] : scales[row0 + j];
 #pragma unroll
           for (int v = 0; v < VEC; ++v) c[v] = c[v] * s;
         }
@@ -804,9 +814,10 @@ static int jpeg_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, 
                               int64_t x_sh, int64_t x_ss, int64_t s_valid, int64_t m, int64_t D,
                               int r, int k, const float* basis, void* coeffs, float* scales,
                               int64_t cap, int64_t n0, int quant_bits, void* stream,
-                              const int64_t* gate) {
+                              const int64_t* gate, int group = 0) {
   if (B < 0 || H < 0 || m < 0 || D <= 0 || r < 1 || k < 1 || k > r) return FC_ERR_ARG;
   if (quant_bits != 0 && quant_bits != 8) return FC_ERR_ARG;
+  if (group && (group != 32 || quant_bits != 8 || D % group)) return FC_ERR_ARG;
   if (n0 < 0 || n0 + m > cap) return FC_ERR_ARG;
   const int64_t items = B * H * m;
   if (items == 0) return FC_OK;
@@ -821,7 +832,7 @@ static int jpeg_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, 
   const int lg = log2_lanes(D, vec);
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid = grid_for(items, lg);
-  if (quant_bits && r == 8 && vec == 8 && s_valid >= m * r) {
+  if (quant_bits && !group && r == 8 && vec == 8 && s_valid >= m * r) {
     const int rc = with_float_type(x_dtype, [&](auto tv) {
       using T = decltype(tv);
       return with_int<2, 4, 8, 0>(k == 2 || k == 4 || k == 8 ? k : 0, [&](auto kc) {
@@ -843,7 +854,7 @@ static int jpeg_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, 
         if (quant_bits)
           jpeg_encode_kernel<T, VEC, RMAX, true, GATED><<<grid, kThreads, 0, st>>>(
               (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, k, basis, coeffs, scales, cap,
-              n0, items, lg, gate);
+              n0, items, lg, gate, group);
         else
           jpeg_encode_kernel<T, VEC, RMAX, false, GATED><<<grid, kThreads, 0, st>>>(
               (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, k, basis, coeffs, scales, cap,
@@ -858,10 +869,10 @@ static int jpeg_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, 
 int jpeg_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
                       int64_t x_sh, int64_t x_ss, int64_t D, int r, int k, const float* basis,
                       void* coeffs, float* scales, int64_t cap, int quant_bits, void* stream,
-                      const int64_t* gate) {
+                      const int64_t* gate, int group) {
   if (!gate || cap < 1) return FC_ERR_ARG;
   return jpeg_encode_launch<true>(x, x_dtype, B, H, x_sb, x_sh, x_ss, r, 1, D, r, k, basis,
-                                  coeffs, scales, cap, 0, quant_bits, stream, gate);
+                                  coeffs, scales, cap, 0, quant_bits, stream, gate, group);
 }
 
 template <bool GATED>
@@ -927,13 +938,26 @@ int fc_jpeg_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_s
                                    coeffs, scales, cap, n0, quant_bits, stream, nullptr);
 }
 
-int fc_jpeg_decode(const void* store, int store_dtype, const float* scales, int64_t B,
-                   int64_t H, int64_t cap, int64_t a, int64_t nblk, int64_t D, int r, int k,
-                   const float* basis, void* out, int out_dtype, int64_t o_sb, int64_t o_sh,
-                   int64_t o_ss, int64_t out_len, void* stream) {
+int fc_jpeg_encode_grouped(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
+                           int64_t x_sh, int64_t x_ss, int64_t s_valid, int64_t m, int64_t D,
+                           int r, int k, const float* basis, int8_t* codes, float* scales,
+                           int64_t cap, int64_t n0, int group, void* stream) {
+  if (group != 32) return FC_ERR_ARG;
+  return jpeg_encode_launch<false>(x, x_dtype, B, H, x_sb, x_sh, x_ss, s_valid, m, D, r, k, basis,
+                                   codes, scales, cap, n0, 8, stream, nullptr, group);
+}
+
+}  // extern "C"
+
+static int jpeg_decode_launch(const void* store, int store_dtype, const float* scales, int64_t B,
+                              int64_t H, int64_t cap, int64_t a, int64_t nblk, int64_t D, int r,
+                              int k, const float* basis, void* out, int out_dtype, int64_t o_sb,
+                              int64_t o_sh, int64_t o_ss, int64_t out_len, void* stream,
+                              int group) {
   if (B < 0 || H < 0 || a < 0 || nblk < 0 || a + nblk > cap || D <= 0 || r < 1 || k < 1 ||
       k > r)
     return FC_ERR_ARG;
+  if (group && (group != 32 || store_dtype != FC_I8 || D % group)) return FC_ERR_ARG;
   const int64_t items = B * H * nblk;
   if (items == 0) return FC_OK;
   if (!store || !basis || !out) return FC_ERR_ARG;
@@ -958,13 +982,14 @@ int fc_jpeg_decode(const void* store, int store_dtype, const float* scales, int6
         constexpr int RMAX = decltype(rc_)::value;
         jpeg_decode_kernel<TI, TO, VEC, RMAX, std::is_same<TI, int8_t>::value>
             <<<grid, kThreads, 0, st>>>((const TI*)store, scales, H, cap, a, nblk, D, r, k,
-                                        basis, (TO*)out, o_sb, o_sh, o_ss, out_len, items, lg);
+                                        basis, (TO*)out, o_sb, o_sh, o_ss, out_len, items, lg,
+                                        group);
         return FC_OK;
       });
     });
   };
   int rc;
-  if (quant && r == 8 && vec == 8) {
+  if (quant && !group && r == 8 && vec == 8) {
     rc = with_float_type(out_dtype, [&](auto to) {
       using TO = decltype(to);
       return with_int<2, 4, 8, 0>(k == 2 || k == 4 || k == 8 ? k : 0, [&](auto kc) {
@@ -985,6 +1010,25 @@ int fc_jpeg_decode(const void* store, int store_dtype, const float* scales, int6
     return FC_ERR_UNSUPPORTED;
   }
   return rc != FC_OK ? rc : check_launch();
+}
+
+extern "C" {
+
+int fc_jpeg_decode(const void* store, int store_dtype, const float* scales, int64_t B,
+                   int64_t H, int64_t cap, int64_t a, int64_t nblk, int64_t D, int r, int k,
+                   const float* basis, void* out, int out_dtype, int64_t o_sb, int64_t o_sh,
+                   int64_t o_ss, int64_t out_len, void* stream) {
+  return jpeg_decode_launch(store, store_dtype, scales, B, H, cap, a, nblk, D, r, k, basis, out,
+                            out_dtype, o_sb, o_sh, o_ss, out_len, stream, 0);
+}
+
+int fc_jpeg_decode_grouped(const int8_t* codes, const float* scales, int64_t B, int64_t H,
+                           int64_t cap, int64_t a, int64_t nblk, int64_t D, int r, int k,
+                           int group, const float* basis, void* out, int out_dtype, int64_t o_sb,
+                           int64_t o_sh, int64_t o_ss, int64_t out_len, void* stream) {
+  if (group != 32) return FC_ERR_ARG;
+  return jpeg_decode_launch(codes, FC_I8, scales, B, H, cap, a, nblk, D, r, k, basis, out,
+                            out_dtype, o_sb, o_sh, o_ss, out_len, stream, group);
 }
 
 int fc_quantize_rows(const void* c, int c_dtype, int64_t n_rows, int64_t c_rs, int64_t D,

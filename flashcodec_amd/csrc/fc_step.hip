@@ -121,8 +121,10 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
 // them there, so one captured graph of the step is valid at every step.
 static int decode_step_state(const fc_step_args* a) {
   const int kind = a->store_kind;
-  if (kind == FC_STORE_JPEG_I8 && a->quant_bits != 8) return FC_ERR_ARG;
-  if (kind != FC_STORE_JPEG_I8 && kind != FC_STORE_JPEG_FP && kind != FC_STORE_PNG)
+  if ((kind == FC_STORE_JPEG_I8 || kind == FC_STORE_JPEG_I8G) && a->quant_bits != 8)
+    return FC_ERR_ARG;
+  if (kind != FC_STORE_JPEG_I8 && kind != FC_STORE_JPEG_FP && kind != FC_STORE_PNG &&
+      kind != FC_STORE_JPEG_I8G)
     return FC_ERR_ARG;
   if (a->n_blocks < 1) return FC_ERR_ARG;  // the archive holds a block before capture
   const int one = step_single_launch(a, a->state);
@@ -159,7 +161,8 @@ static int decode_step_state(const fc_step_args* a) {
     else
       rc = jpeg_encode_gated(st[i]->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, D, r, a->s,
                              a->basis, st[i]->rows, st[i]->scales, st[i]->cap,
-                             kind == FC_STORE_JPEG_I8 ? 8 : 0, a->stream, a->state);
+                             kind == FC_STORE_JPEG_FP ? 0 : 8, a->stream, a->state,
+                             kind == FC_STORE_JPEG_I8G ? 32 : 0);
     if (rc != FC_OK) return rc;
   }
   fc_stream_view v[2];
@@ -202,7 +205,9 @@ int fc_decode_step(const fc_step_args* a) {
   const fc_step_stream* st[2] = {&a->key, &a->value};
   for (const fc_step_stream* x : st)
     if (!x->token || !x->tail || !x->rows) return FC_ERR_ARG;
-  if (a->store_kind == FC_STORE_JPEG_I8 && (!a->key.scales || !a->value.scales)) return FC_ERR_ARG;
+  if ((a->store_kind == FC_STORE_JPEG_I8 || a->store_kind == FC_STORE_JPEG_I8G) &&
+      (!a->key.scales || !a->value.scales))
+    return FC_ERR_ARG;
   if (a->store_kind == FC_STORE_PNG && (!a->key.anchors || !a->value.anchors)) return FC_ERR_ARG;
   if (a->store_kind != FC_STORE_PNG && !a->basis) return FC_ERR_ARG;
   if (a->state) return decode_step_state(a);
@@ -243,6 +248,10 @@ int fc_decode_step(const fc_step_args* a) {
       if (a->store_kind == FC_STORE_PNG)
         rc = fc_png_encode(x->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, r, 1, D, r, a->keep_m,
                            static_cast<float*>(x->rows), x->anchors, x->cap, nb, a->stream);
+      else if (a->store_kind == FC_STORE_JPEG_I8G)
+        rc = fc_jpeg_encode_grouped(x->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, r, 1, D, r,
+                                    a->s, a->basis, static_cast<int8_t*>(x->rows), x->scales,
+                                    x->cap, nb, 32, a->stream);
       else
         rc = fc_jpeg_encode(x->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, r, 1, D, r, a->s,
                             a->basis, x->rows, x->scales, x->cap, nb, a->quant_bits, a->stream);

@@ -102,6 +102,34 @@ int fc_jpeg_decode(const void* store, int store_dtype, const float* scales,
                    int64_t out_len, void* stream);
 
 /*
+ * JPEG-mode int8 archive with one fp32 scale per `group` features of each
+ * (block, frequency) row instead of one per row: the per-32 absmax
+ * coefficient quantizer (group must be 32, D a multiple of it).  Same
+ * transform, rounding and code rule as fc_jpeg_encode with quant_bits 8;
+ * the scale of features [32 g, 32 g + 32) of row j of block n is
+ * scales[((b*H + h)*cap + n)*k + j][g] of a (B*H, cap, k, D/32) fp32 store.
+ * No reference counterpart as a library format: flashcodec documents it as
+ * the quantizer that makes the coefficient archive competitive
+ * (README.md:487-494) without shipping it.
+ */
+int fc_jpeg_encode_grouped(const void* x, int x_dtype, int64_t B, int64_t H,
+                           int64_t x_sb, int64_t x_sh, int64_t x_ss,
+                           int64_t s_valid, int64_t m, int64_t D, int r, int k,
+                           const float* basis, int8_t* codes, float* scales,
+                           int64_t cap, int64_t n0, int group, void* stream);
+
+/*
+ * Reconstruction of blocks [a, a+nblk) of a per-`group` scaled int8 store
+ * (fc_jpeg_encode_grouped) into out, as fc_jpeg_decode.
+ */
+int fc_jpeg_decode_grouped(const int8_t* codes, const float* scales,
+                           int64_t B, int64_t H, int64_t cap, int64_t a,
+                           int64_t nblk, int64_t D, int r, int k, int group,
+                           const float* basis, void* out, int out_dtype,
+                           int64_t o_sb, int64_t o_sh, int64_t o_ss,
+                           int64_t out_len, void* stream);
+
+/*
  * Symmetric int8 quantisation of coefficient rows: n_rows rows of D values
  * (dtype c_dtype, row stride c_rs elements) -> int8 codes (contiguous
  * rows of D) and one fp32 scale per row.
@@ -156,13 +184,15 @@ uint64_t fc_png_topm_mask_host(const float* delta, int n, int keep_m);
 enum {
   FC_STORE_JPEG_I8 = 0,  /* rows: int8 coeffs x fp32 scale, s = k      */
   FC_STORE_JPEG_FP = 1,  /* rows: coeffs in the stream dtype, s = k    */
-  FC_STORE_PNG = 2       /* rows: anchor (stream dtype) + r-1 fp32 deltas, s = r */
+  FC_STORE_PNG = 2,      /* rows: anchor (stream dtype) + r-1 fp32 deltas, s = r */
+  FC_STORE_JPEG_I8G = 3  /* rows: int8 coeffs x one fp32 scale per 32 features
+                            (scales (B*H, cap, k, D/32)), s = k */
 };
 
 /* One KV stream as seen by the decode attention. */
 typedef struct fc_stream_view {
   const void* rows;      /* jpeg: coeffs (B*H, cap, k, D); png: deltas (B*H, cap, r-1, D) */
-  const float* scales;   /* jpeg int8: (B*H, cap, k); else NULL */
+  const float* scales;   /* jpeg int8: (B*H, cap, k); per-32: (B*H, cap, k, D/32); else NULL */
   const void* anchors;   /* png: (B*H, cap, D); else NULL */
   int64_t cap;           /* capacity of the store in blocks */
   const void* raw;       /* raw tail (B, H, n_raw, D) in the stream dtype, or NULL */

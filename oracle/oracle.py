@@ -12,6 +12,11 @@ Parity status (each function's pinning is listed in tests/test_oracle.py):
   jpeg_encode / quantize / jpeg_decode / dequantize / png_encode /
   png_decode: pinned bit-exactly against the golden vectors written from the
   reference (tests/golden/) plus closed-form checks.
+  jpeg_encode_grouped / grouped_coefficients (the per-32 absmax archive,
+  which the reference has no code for): the pinned quantize applied per
+  group; pinned by the one-group case equalling the row quantizer bit for
+  bit, per-group absmax-to-127 and half-step error bounds, and the k = r
+  round trip bound.
   attention: fp64 by definition (synthesise every block, softmax over all
   tokens), pinned against brute-force dense attention on tiny inputs and the
   reference's torch-path outputs within tolerance.
@@ -167,6 +172,27 @@ def quantize(c, dtype="f32"):
     return codes.reshape(c.shape), scales.reshape(c.shape[:-1])
 
 
+def jpeg_encode_grouped(x, r, k, basis, dtype="f32", group=32):
+    """dct_compress, then the quantize_coeffs rule applied to every `group`
+    features of a coefficient row (each run gets its own absmax scale: the
+    per-32 absmax quantizer of flashcodec README.md:487-494, which the
+    reference describes but does not ship).  Returns coef (..., n, k, D),
+    codes (..., n, k, D), scales (..., n, k, D/group)."""
+    coef = jpeg_encode(x, r, k, basis, dtype)
+    D = coef.shape[-1]
+    assert D % group == 0, "D must be a multiple of the group"
+    codes, scales = quantize(coef.reshape(coef.shape[:-1] + (D // group, group)), dtype)
+    return coef, codes.reshape(coef.shape), scales
+
+
+def grouped_coefficients(codes, scales):
+    """fp32 codes * scale of each feature's group: (..., D) codes with
+    (..., D/g) scales -> (..., D) (the fp32 products the decode takes)."""
+    codes = np.asarray(codes, np.int8)
+    g = codes.shape[-1] // scales.shape[-1]
+    return codes.astype(np.float32) * np.repeat(_f32(scales), g, axis=-1)
+
+
 def dequantize(codes, scales, dtype="f32"):
     codes = np.ascontiguousarray(codes, np.int8)
     D = codes.shape[-1]
@@ -261,9 +287,12 @@ def attention(q, rows_k, rows_v, raw_k, raw_v, A, scale, n_threads=1):
 
 
 def stored_rows_jpeg(codes_or_coef, scales=None):
-    """Dequantised jpeg rows (fp64) from codes * scales or float coefficients."""
+    """Dequantised jpeg rows (fp64) from codes * scales or float coefficients;
+    scales (..., k) per row or (..., k, D/g) per g features."""
     if scales is None:
         return np.asarray(codes_or_coef, np.float64)
+    if np.ndim(scales) == np.ndim(codes_or_coef):
+        return grouped_coefficients(codes_or_coef, scales).astype(np.float64)
     return np.asarray(codes_or_coef, np.float64) * np.asarray(scales, np.float32).astype(
         np.float32)[..., None].astype(np.float64)
 

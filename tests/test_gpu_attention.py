@@ -40,7 +40,8 @@ def stream_rows(oracle, st):
     if st.codec.name == "jpeg":
         c = st._coeffs[:, :, :n].float().cpu().numpy()
         if st.codec.quantized:
-            return oracle.stored_rows_jpeg(c, st._scales[:, :, :n, :, 0].cpu().numpy())
+            sc = st._scales[:, :, :n].cpu().numpy()
+            return oracle.stored_rows_jpeg(c, sc if st.codec.quant_group else sc[..., 0])
         return oracle.stored_rows_jpeg(c)
     return oracle.stored_rows_png(st._deltas[:, :, :n].cpu().numpy(),
                                   st._anchors[:, :, :n].float().cpu().numpy())
@@ -97,6 +98,10 @@ CASES = [
     ("jpeg-i8-f32-no-tail", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f32", 1, 2, 4, 8 * 33, 64),
     ("jpeg-i8-f16-32k", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16", 1, 2, 4, 8 * 4096 + 5, 128),
     ("jpeg-i8-f32-r16-d40", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8), "f32", 1, 2, 2, 16 * 9 + 4, 40),
+    ("jpeg-i8g-f16-g4", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=32), "f16", 2, 4, 4, 8 * 200 + 5, 128),
+    ("jpeg-i8g-bf16-g2-d64", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8, quant_group=32), "bf16", 1, 2, 2, 8 * 90 + 3, 64),
+    ("jpeg-i8g-f32-r16-d96", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8, quant_group=32), "f32", 1, 2, 3, 16 * 30 + 9, 96),
+    ("jpeg-i8g-f16-d256", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=32), "f16", 1, 1, 8, 8 * 64 + 1, 256),
 ]
 
 

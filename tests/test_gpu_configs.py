@@ -177,7 +177,9 @@ def test_merge_give_up_is_reported_and_recovers(oracle):
 
 STEP_CFGS = [(I8_C3, "bf16", 2), (I8_C3, "f16", 4),
              (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 4),
-             (dict(mode="png", block_size=8, keep_ratio=0.5), "f16", 2)]
+             (dict(mode="png", block_size=8, keep_ratio=0.5), "f16", 2),
+             (dict(I8_C3, quant_group=32), "bf16", 2)]
+STEP_IDS = ["i8-bf16", "i8-f16", "fp-f32", "png-f16", "i8g-bf16"]
 
 
 def _tokens(g, B, H, D, dt):
@@ -185,7 +187,7 @@ def _tokens(g, B, H, D, dt):
     return torch.randn((B, 1, H, D), generator=g, device=DEV).to(torch_dtype(dt)).transpose(1, 2)
 
 
-@pytest.mark.parametrize("cfg,dt,G", STEP_CFGS, ids=["i8-bf16", "i8-f16", "fp-f32", "png-f16"])
+@pytest.mark.parametrize("cfg,dt,G", STEP_CFGS, ids=STEP_IDS)
 def test_fused_decode_step_matches_oracle(cfg, dt, G, oracle):
     """codec_decode_step (token append + block archive + attention in one
     library call) against the oracle on the streams' rows after each step,
@@ -216,7 +218,7 @@ def _codec_layer(cfg, ks, vs):
     return layer
 
 
-@pytest.mark.parametrize("cfg,dt,G", STEP_CFGS, ids=["i8-bf16", "i8-f16", "fp-f32", "png-f16"])
+@pytest.mark.parametrize("cfg,dt,G", STEP_CFGS, ids=STEP_IDS)
 def test_graph_replayed_steps_match_oracle(cfg, dt, G, oracle):
     """One device-state decode step captured as a HIP graph and replayed
     with new query / key / value tokens copied into its input buffers: every

@@ -1,7 +1,8 @@
 """GPU: decode steps replayed from a captured HIP graph (device-side stream
 counters) against the same steps run eagerly through the host-driven codec
 path, on a tiny Qwen3 decoder with int8 jpeg (matrix-core attention),
-unquantised jpeg and png archives (vector-ALU attention)."""
+unquantised jpeg, per-32-scaled int8 jpeg and png archives (vector-ALU
+attention)."""
 
 import pytest
 import torch
@@ -34,11 +35,13 @@ def prefill(model, prompt):
 I8 = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
 FP = dict(mode="jpeg", block_size=8, keep_freqs=4)
 PNG = dict(mode="png", block_size=8, keep_ratio=0.5)
+I8G = dict(I8, quant_group=32)
 
 
 @pytest.mark.parametrize("dtype,codec", [(torch.float16, I8), (torch.bfloat16, I8),
-                                         (torch.bfloat16, FP), (torch.float16, PNG)],
-                         ids=["i8-f16", "i8-bf16", "fp-bf16", "png-f16"])
+                                         (torch.bfloat16, FP), (torch.float16, PNG),
+                                         (torch.bfloat16, I8G)],
+                         ids=["i8-f16", "i8-bf16", "fp-bf16", "png-f16", "i8g-bf16"])
 def test_graph_replays_match_eager_steps(dtype, codec):
     model = tiny_qwen3(dtype, codec)
     g = torch.Generator().manual_seed(5)

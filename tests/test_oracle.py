@@ -143,6 +143,61 @@ def test_jpeg_closed_form_properties(golden, oracle):
     assert not np.array_equal(_bits(flipped), _bits(c["coef"]))
 
 
+def _group_bounds_hold(coef, codes, scales, g):
+    """Per-group quantizer invariants: codes within +-127, every group with
+    a nonzero absmax reaches +-127, |code * s - c| <= s / 2."""
+    cg = coef.reshape(coef.shape[:-1] + (-1, g))
+    qg = codes.reshape(cg.shape).astype(np.int32)
+    s = scales[..., None]
+    amax = np.abs(cg).max(-1)
+    hits = np.where(amax > 0, np.abs(qg).max(-1) == 127, True)
+    err_ok = np.abs(qg * s - cg) <= s / 2 * (1 + 1e-6)
+    return np.abs(qg).max() <= 127 and hits.all() and err_ok.all()
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
+def test_grouped_quantizer_oracle(golden, oracle, dt):
+    """The per-32 absmax archive (no reference code; README.md:487-494):
+    a one-group row equals the pinned row quantizer bit for bit; with
+    groups of very different magnitude every group keeps its own absmax at
+    +-127 and a half-step error bound (a planted mistake, one scale per row,
+    breaks both); k = r round trips within the summed half steps."""
+    rng = np.random.default_rng(11)
+    r = 8
+    basis = golden("basis").data["r8"]
+    one = oracle.round_to(rng.standard_normal((2, 3, 40, 32)).astype(np.float32), dt)
+    _, rc, rs = oracle.jpeg_encode(one, r, 4, basis[:4], dt, quant=True)
+    _, gc, gs = oracle.jpeg_encode_grouped(one, r, 4, basis[:4], dt)
+    assert gs.shape == rs.shape + (1,)
+    assert np.array_equal(gc, rc) and np.array_equal(_bits(gs[..., 0]), _bits(rs))
+    x = rng.standard_normal((2, 2, 43, 128)).astype(np.float32)
+    x[..., 32:64] *= 100.0                        # one loud group per row
+    x[..., 96:128] *= 1e-3                        # and one quiet one
+    x = oracle.round_to(x, dt)
+    coef, codes, scales = oracle.jpeg_encode_grouped(x, r, 4, basis[:4], dt)
+    assert scales.shape == coef.shape[:-1] + (4,)
+    assert _group_bounds_hold(coef, codes, scales, 32)
+    _, row_codes, row_scales = oracle.jpeg_encode(x, r, 4, basis[:4], dt, quant=True)
+    planted = np.repeat(row_scales[..., None], 4, axis=-1)
+    assert not _group_bounds_hold(coef, row_codes, planted, 32)
+    # quieter groups quantize finer: the grouped error is never above the row's
+    deq_g = oracle.grouped_coefficients(codes, scales)
+    deq_r = row_codes * row_scales[..., None]
+    assert np.all(np.abs(deq_g - coef) <= np.abs(row_scales)[..., None] / 2 * (1 + 1e-6))
+    assert np.abs(deq_g - coef)[..., 96:].max() < np.abs(deq_r - coef)[..., 96:].max()
+    # k = r: the orthonormal synthesis of the dequantised rows is within
+    # sum_j |basis[j, t]| * s_j / 2 of the (dtype-rounded) coefficients' view
+    if dt == "f32":
+        cf, cc, cs = oracle.jpeg_encode_grouped(x, r, r, basis, dt)
+        rec = oracle.jpeg_decode(oracle.grouped_coefficients(cc, cs), r, basis, "f32")
+        exact = oracle.jpeg_decode(cf, r, basis, "f32")
+        half = np.repeat(cs, 32, axis=-1) / 2               # (..., n, r, D)
+        bound = np.einsum("jt,...njd->...ntd", np.abs(basis), half)
+        bound = bound.reshape(rec.shape) * (1 + 1e-5) + 1e-6
+        assert np.all(np.abs(rec - exact) <= bound)
+        assert np.abs(exact[..., :43, :] - x).max() < 1e-5 * np.abs(x).max()
+
+
 # ---------------------------------------------------------------- png
 
 def test_topk_keep_matches_torch_topk(oracle):
