@@ -366,57 +366,68 @@ __device__ __forceinline__ void step_partial(
 // device-scope loads; the raw tail is part of split 0's partial.  The
 // statistics of all splits come in with one load per thread; then each
 // thread owns an output task (head, 4 features) and requests its partials
-// kPre splits at a time.  `lds` holds >= 2 * 16 * kFuseMaxSplits floats.
+// kPre splits at a time.  The code runs once per call, after the pass loop,
+// when its instructions are not in the instruction cache: it is kept short
+// and free of per-element branches (every load of a batch is issued and
+// splits past n_splits are selected away; one store branch per task).
+// `lds` holds >= 2 * 16 * kFuseMaxSplits floats.
 template <int D>
 __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
                             int split, int tid, float* lds, const float* own_acc,
                             const float* own_m, const float* own_l) {
   constexpr int C4 = D / 4;  // float4 chunks of a head's output
-  constexpr int kPre = 16;   // partials in flight per task
+  constexpr int kPre = 8;    // partials in flight per task
   const int ns = p.n_splits;
   const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;  // slot of head 0 of the group
   float* wsp = lds;                        // [16][kFuseMaxSplits] split maxima
   float* plv = wsp + 16 * kFuseMaxSplits;  // [16][kFuseMaxSplits] split sums
 
-  // device-scope (L2-missing) loads of the group's partials and statistics
+  // device-scope (L2-missing) loads of the group's partials and statistics;
+  // offsets past the group's slots read as zero
   const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, G * ns * D * 4);
   const __amdgpu_buffer_rsrc_t rm = buf_rsrc(p.pm + bq0 * ns, G * ns * 4);
   const __amdgpu_buffer_rsrc_t rl = buf_rsrc(p.pl + bq0 * ns, G * ns * 4);
-  auto part = [&](int h, int sp, int c) {
-    const float4_t v = __builtin_bit_cast(
-        float4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, ((h * ns + sp) * C4 + c) * 16, 0,
-                                                        kCachePolicySc1));
-    return sp == split ? *reinterpret_cast<const float4_t*>(own_acc + h * D + 4 * c) : v;
-  };
-  auto fma4 = [](float w, const float4_t& v, float4_t& o) {
+  auto load_batch = [&](int h, int sp0, int c, float4_t (&pre)[kPre]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(w, v[i], o[i]);
+    for (int j = 0; j < kPre; ++j)
+      pre[j] = __builtin_bit_cast(
+          float4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, ((h * ns + sp0 + j) * C4 + c) * 16, 0,
+                                                          kCachePolicySc1));
   };
-  auto task_out = [&](int h, int c, const float* wh, const float* lh, float4_t (&pre)[kPre],
-                      bool have0) {
+  auto task_out = [&](int h, int c, float4_t (&pre)[kPre], bool have0) {
+    const float* wh = wsp + h * kFuseMaxSplits;
+    const float* lh = plv + h * kFuseMaxSplits;
     float mx = -INFINITY;
     for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, wh[sp]);
+    const float4_t own = *reinterpret_cast<const float4_t*>(own_acc + h * D + 4 * c);
     float l = 0.f;
     float4_t o = {0.f, 0.f, 0.f, 0.f};
     for (int sp0 = 0; sp0 < ns; sp0 += kPre) {
-      if (sp0 > 0 || !have0) {
+      if (sp0 > 0 || !have0) load_batch(h, sp0, c, pre);
 #pragma unroll
-        for (int j = 0; j < kPre; ++j)
-          if (sp0 + j < ns) pre[j] = part(h, sp0 + j, c);
-      }
+      for (int j = 0; j < kPre; ++j) {
+        const int sp = sp0 + j;
+        const bool ok = sp < ns;
+        const int si = ok ? sp : 0;
+        const float pmv = wh[si];
+        const float w = (!ok || pmv == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pmv - mx);
+        l = __builtin_fmaf(w, lh[si], l);
 #pragma unroll
-      for (int j = 0; j < kPre; ++j)
-        if (sp0 + j < ns) {
-          const float pmv = wh[sp0 + j];
-          const float w = pmv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pmv - mx);
-          l = __builtin_fmaf(w, lh[sp0 + j], l);
-          fma4(w, pre[j], o);
+        for (int i = 0; i < 4; ++i) {
+          const float v = sp == split ? own[i] : (ok ? pre[j][i] : 0.f);
+          o[i] = __builtin_fmaf(w, v, o[i]);
         }
+      }
     }
     const float iv = 1.0f / l;
     const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
+    if (p.q_dtype == FC_F16) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) store_any(p.out, p.q_dtype, ob + i, o[i] * iv);
+      for (int i = 0; i < 4; ++i) static_cast<f16_t*>(p.out)[ob + i] = from_f32<f16_t>(o[i] * iv);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) static_cast<bf16_t*>(p.out)[ob + i] = from_f32<bf16_t>(o[i] * iv);
+    }
   };
   auto stats = [&]() {
     for (int u = tid; u < G * ns; u += kMThreads) {
@@ -435,21 +446,17 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
     // one task per thread: its first kPre partials fly with the statistics
     const bool act = tid < G * C4;
     const int h = act ? tid / C4 : 0, c = tid - h * C4;
-    if (act) {
-#pragma unroll
-      for (int j = 0; j < kPre; ++j)
-        if (j < ns) pre[j] = part(h, j, c);
-    }
+    load_batch(h, 0, c, pre);
     stats();
     __syncthreads();
-    if (act) task_out(h, c, wsp + h * kFuseMaxSplits, plv + h * kFuseMaxSplits, pre, true);
+    if (act) task_out(h, c, pre, true);
     return;
   }
   stats();
   __syncthreads();
   for (int task = tid; task < G * C4; task += kMThreads) {
     const int h = task / C4, c = task - h * C4;
-    task_out(h, c, wsp + h * kFuseMaxSplits, plv + h * kFuseMaxSplits, pre, false);
+    task_out(h, c, pre, false);
   }
 }
 
@@ -519,10 +526,14 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   const unsigned int wslot = (unsigned int)(split * kWaves + wave);
   const unsigned int wstride = (unsigned int)(p.n_splits * kWaves);
   unsigned int wtaken = 0;
+  // A wavefront's first pass is fixed (pass wslot: no queue round trip before
+  // the first loads); the queue hands out the others from wstride on, or, in
+  // the static order, wslot + k * wstride.
   auto grab = [&]() -> unsigned int {  // result in lane 0, read when needed
-    if (p.static_passes) return wslot + wstride * wtaken++;
+    if (p.static_passes) return wslot + wstride * ++wtaken;
     unsigned int v = 0;
-    if (lane == 0) v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0)
+      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + wstride;
     return v;
   };
   auto pass_of = [](unsigned int v) { return (int64_t)__builtin_amdgcn_readfirstlane((int)v); };
@@ -725,7 +736,7 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
 
   __syncthreads();  // a_lds; the tail's scratch (w_lds) is free again
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
-  int64_t cur = pass_of(grab());
+  int64_t cur = wslot;
   if (cur < npass) load_k(cur * PR, rows_of(cur));
   while (cur < npass) {
     const int64_t pr0 = cur * PR;
@@ -861,16 +872,18 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
     comb[wave][lane][1] = l_lane;
     comb[wave][lane][2] = ldexpf(1.0f, sig_run);
   }
+  // One predicate per lane, not per element (per-element conditions became a
+  // branch per store): lanes whose registers hold heads < GP (rows of
+  // cbuf; heads in [G, GP) carry zeros and are never read) and features < D.
   constexpr int NI = GP < 4 ? GP : 4;  // accumulator registers that can hold a head
+  if (lq < (GP >= 4 ? GP / 4 : 1) && (D % 128 == 0 || lc < D / 8)) {
 #pragma unroll
-  for (int dv = 0; dv < DV; ++dv)
+    for (int dv = 0; dv < DV; ++dv)
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+      for (int e = 0; e < 8; ++e)
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const int h = 4 * lq + i, d = 128 * dv + 8 * lc + e;
-        if (h < G && d < D) cbuf[wave][h][d] = acc[dv][e][i];
-      }
+        for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][128 * dv + 8 * lc + e] = acc[dv][e][i];
+  }
   __syncthreads();
   {
     for (int x = tid; x < G * D; x += kMThreads) {
