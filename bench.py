@@ -457,15 +457,75 @@ def c5_mode(args):
                 "decode_ms_per_step": round((t2 - t1) / n * 1e3, 3),
                 "decode_tokens_per_s": round(batch * n / (t2 - t1), 1), "graph_steps": n}
 
+    def run_graph_raw(batch, prompt, steps, warmup=2):
+        """The same decode on raw KV in transformers' StaticCache (preallocated
+        for the whole run, written in place) with each step replayed from a
+        captured HIP graph: the baseline on equal footing with run_graph."""
+        from transformers import StaticCache
+        g = torch.Generator().manual_seed(1)
+        ids = torch.randint(1, cfg.vocab_size, (batch, prompt), generator=g).to(dev)
+        cache = StaticCache(config=model.config, max_cache_len=prompt + steps + 1)
+        with torch.no_grad():
+            out = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1,
+                        cache_position=torch.arange(prompt, device=dev))
+            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+            pos = torch.full((batch, 1), prompt, dtype=torch.long, device=dev)
+            cpos = torch.tensor([prompt], dtype=torch.long, device=dev)
+            stream = torch.cuda.Stream(device=dev)
+
+            def fwd():
+                return model(input_ids=tok, position_ids=pos, cache_position=cpos,
+                             past_key_values=cache, use_cache=True, logits_to_keep=1).logits
+
+            def advance(logits):
+                tok.copy_(logits[:, -1].argmax(-1, keepdim=True))
+                pos.add_(1)
+                cpos.add_(1)
+
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            stream.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(stream):
+                for _ in range(warmup):
+                    advance(fwd())
+            torch.cuda.current_stream(dev).wait_stream(stream)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                logits = fwd()
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            with torch.cuda.stream(stream):
+                for _ in range(steps - warmup):
+                    gr.replay()
+                    advance(logits)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+        n = steps - warmup
+        del gr, cache
+        torch.cuda.empty_cache()
+        return {"warmup_and_capture_s": round(t1 - t0, 4),
+                "decode_ms_per_step": round((t2 - t1) / n * 1e3, 3),
+                "decode_tokens_per_s": round(batch * n / (t2 - t1), 1), "graph_steps": n}
+
     if args.c5_graph:
-        # codec decoding with each step replayed from a captured HIP graph
+        # raw KV (StaticCache) and codec decoding, each step replayed from a
+        # captured HIP graph
+        raw = {}
+        for tag, (bt, pr, st) in (("raw_static_graph_b16", (16, 4096, 256)),
+                                  ("raw_static_graph_b1", (1, 4096, 32))):
+            try:
+                raw[tag] = run_graph_raw(bt, pr, st)
+            except Exception as exc:         # a baseline that cannot be captured is reported
+                raw[tag] = {"error": f"{type(exc).__name__}: {exc}"[:300]}
+            log(f"bench c5 graph: {tag} {raw[tag]}")
         fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8,
                              materialization_free=True)
         run(2, 64, 4)
         res = {"metric": "end-to-end decode tokens/s (C5), codec, HIP-graph decode steps",
                "unit": "tokens/s", "n_gpus": 1,
                "codec_graph_b16": run_graph(16, 4096, 256),
-               "codec_graph_b1": run_graph(1, 4096, 32)}
+               "codec_graph_b1": run_graph(1, 4096, 32), **raw}
         res["value"] = res["codec_graph_b16"]["decode_tokens_per_s"]
         log(f"bench c5 graph: {res}")
         print(json.dumps(res))
