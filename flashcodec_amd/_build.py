@@ -54,15 +54,20 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
+# extra flags by source-name prefix (the matrix-core kernels' translation units)
 FILE_FLAGS = {
-    "fc_attn_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-    "fc_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "fc_attn_mfma": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "fc_prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
+
+
+def file_flags(name):
+    return next((flags for prefix, flags in FILE_FLAGS.items() if name.startswith(prefix)), [])
 
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
-    extra = FILE_FLAGS.get(os.path.basename(src), [])
+    extra = file_flags(os.path.basename(src))
     cmd = [hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

@@ -1149,8 +1149,7 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G, i
 int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, int64_t nb,
                         int64_t B, int64_t Hkv, int64_t G, int64_t D, int n_cu) {
   if (nb <= 0) return 0;
-  const bool mfma = store_kind == FC_STORE_JPEG_I8 && (q_dtype == FC_F16 || q_dtype == FC_BF16) &&
-                    (D == 64 || D == 128 || D == 256) && (s == 1 || s == 2 || s == 4) &&
+  const bool mfma = store_kind == FC_STORE_JPEG_I8 && fc::mfma_shape_supported(q_dtype, D, s) &&
                     fc::mfma_split_allowed();
   if (n_cu <= 0) n_cu = 256;
   if (mfma) {

@@ -84,6 +84,8 @@ struct MfmaFuse {
 // the step's rows fit the kernel's LDS scratch, fused merge).
 bool step_i8_mfma_supported(int stream_dtype, int r, int64_t D, int n_splits);
 
+// Query dtype, head size and stored rows per block of the matrix-core pass.
+bool mfma_shape_supported(int q_dtype, int64_t D, int s);
 bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
                              int s, const fc_stream_view* key, const fc_stream_view* value);
 bool split_i8_mfma_fusable(int n_splits);

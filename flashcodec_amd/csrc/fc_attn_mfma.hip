@@ -1,1024 +1,15 @@
-// Split pass of the decode attention for int8 jpeg archives on gfx950 matrix
-// cores, with the merge of the split partials fused in.
-//
-// With G query heads per kv head, a block's work is a skinny GEMM: scores
-// S = K_rows . Q^T (M = rows, N = heads, K-dim = features) and output
-// O = W . V_rows (M = heads, N = features, K-dim = rows).  On the vector ALU
-// that costs ~4 fp32 FMAs per code byte per head group — more VALU time than
-// the HBM time of the bytes — so both products run on the matrix cores and
-// the VALU runs the softmax and the V code conversion.
-//
-// Scores: v_mfma_i32_16x16x64_i8 straight on the K codes.  Each head's query
-// is scaled by a power of two to integers of at most 14 bits and split as
-// q' = 256 hi + lo (int8 hi, lo): 256 (K . hi) + (K . lo) is the exact
-// integer score.
-// Values: v_mfma_f32_16x16x32_f16.  A V code b converts to f16 exactly:
-// u = b ^ 0x80 = b + 128, the f16 with bits 0x6400 | u is 1024 + u, and one
-// packed f16 add of -1152 (exact) leaves b.  Output weights enter as f16
-// scaled by a per-wavefront power of two; products are exact in fp32 and
-// the matrix cores accumulate in fp32.
-//
-// Workgroup = 4 wavefronts = one (batch, kv head, split, group of <= 16 query
-// heads).  Each wavefront owns a contiguous run of 32-row slabs of the split
-// and walks it in passes of 64 rows (32 at D = 256):
-//   scores: per 16-row tile and 64-feature chunk k, lane (q, m) holds row m,
-//      features 64k + 16q .. +15 (one 64-byte run of each row per load; any
-//      relabelling of the feature axis shared by both operands is allowed);
-//      lane (q, c < G) gets the scores of rows 4q..4q+3 for head c and parks
-//      them in LDS.
-//   softmax: (block, head) pairs over all 64 lanes (head = lane % GP): r
-//      logits from the s scores, exponentials against a running reference
-//      maximum, and s output weights w_j = sum_p 2^(logit_p - m) A[p][j] times
-//      the V row scale, stored as f16 in LDS.
-//   values: per 32-row slab, lane (q, c) loads rows 8q..8q+7, bytes
-//      [8c, 8c+8) (16 lanes cover a 128-byte row) and transposes the 8x8
-//      byte tile in registers, so matrix-core instance e of the slab sees
-//      feature 8c + e in column c.
-// The four wavefronts combine their (max, sum, acc) in LDS into one partial
-// per (query head, split); the last workgroup of each head group to finish
-// merges the partials with the raw tail (fused_merge).
-#include <hip/hip_runtime.h>
-
-#include <type_traits>
-
-#include "fc_attn_internal.h"
-#include "fc_common.h"
-#include "fc_mfma_pass.h"
+// Host side of the matrix-core split pass of the decode attention (int8
+// jpeg archives): which configurations it takes, and its launch.  The kernel
+// is fc_attn_mfma_kernel.h.
+#include "fc_attn_mfma_kernel.h"
 
 namespace fc {
 
-struct MfmaArgs {
-  const void* q;
-  int q_dtype;
-  int64_t q_sb, q_sh;
-  const int8_t* kcodes;
-  const float* kscales;
-  const int8_t* vcodes;
-  const float* vscales;
-  int64_t kcap, vcap;
-  const float* A;  // r x s
-  int64_t Hkv, G, nb;
-  int r;
-  float scale_log2;
-  int64_t blocks_per_split;
-  int n_splits;
-  int64_t ngroups;  // B * Hkv * zg (zg = groups of <= 16 query heads per kv head)
-  int zg;
-  unsigned int* arrive;  // per group: workgroups done (zero between calls)
-  unsigned int* passq;   // per group: next pass to take (zero between calls)
-  int64_t cstride;       // words between the counters of consecutive groups
-  float* pm;
-  float* pl;
-  float* pacc;
-  // fused merge (fused != 0): raw tail, output and arrival counters
-  int fused;
-  const void* kraw;
-  const void* vraw;
-  int raw_dtype;
-  int64_t kr_sb, kr_sh, kr_st, vr_sb, vr_sh, vr_st;
-  int64_t n_raw;
-  void* out;
-  int64_t o_sb, o_sh;
-  // decode-step state on the device (or NULL): (n_blocks, n_tail) before
-  // the step's token; nb and n_raw are then taken from it (graph replays)
-  const int64_t* state;
-  // status word of the workspace: set to FC_STATUS_MERGE_INCOMPLETE when a
-  // merging workgroup stops waiting for the other splits' publications
-  unsigned int* status;
-  // polls of the publication counter before the merge gives up (< 0: give
-  // up at once; a test knob that makes the give-up path run)
-  int spin_cap;
-  // static pass order (no queue): wavefront w of the group's n_splits * 4
-  // takes passes w, w + n_splits * 4, ...; fixed summation order, so the
-  // output is bitwise reproducible
-  int static_passes;
-  // fused decode step (step != 0): the step's key / value tokens
-  // (B, Hkv, 1, D) join the tails (kraw / vraw: (B, Hkv, r, D) contiguous
-  // buffers) at row t; when they complete a block, split 0 archives it as
-  // block nb (codes at kcodes_w / vcodes_w, scales at kscales_w / vscales_w,
-  // DCT basis `basis`, k = SROWS) and attends it from the fresh codes, and
-  // the passes cover the blocks before it.  t and nb come from `state`
-  // (then the last workgroup of the launch advances it, counting workgroups
-  // on `done`) or from step_t / step_nb.
-  int step;
-  const void* ktok;
-  const void* vtok;
-  int64_t kt_sb, kt_sh, vt_sb, vt_sh;
-  int8_t* kcodes_w;
-  int8_t* vcodes_w;
-  float* kscales_w;
-  float* vscales_w;
-  const float* basis;
-  int64_t step_t, step_nb;
-  unsigned int* done;
-};
-
-constexpr int kMThreads = 256;
-constexpr int kFuseMaxSplits = 64;  // split count limit of the fused merge
-
-constexpr int kWaves = kMThreads / 64;
-constexpr int kPubWord = 1;            // publication counter: word 1 of a group's arrival line
-
-
-// Element load / store with the dtype fixed at compile time (T = f16_t,
-// bf16_t) or read at run time (T = void).
-template <typename T>
-__device__ __forceinline__ float ld_elem(const void* ptr, int dt, int64_t i) {
-  if constexpr (std::is_void_v<T>) {
-    return load_q(ptr, dt, i);
-  } else {
-    return to_f32(static_cast<const T*>(ptr)[i]);
-  }
-}
-template <typename T>
-__device__ __forceinline__ void st_elem(void* ptr, int dt, int64_t i, float v) {
-  if constexpr (std::is_void_v<T>) {
-    store_any(ptr, dt, i, v);
-  } else {
-    static_cast<T*>(ptr)[i] = from_f32<T>(v);
-  }
-}
-
-// Raw-tail partial of one (batch, kv head, head group): for each of its G
-// query heads the base-2 logits of the n_raw tail tokens at full precision,
-// their maximum tm[h], sum tl[h] = sum_t 2^(logit_t - tm[h]) and
-// acc[h][d] = sum_t 2^(logit_t - tm[h]) v_t[d].  `etl` holds
-// 16 * FC_MAX_BLOCK floats; every thread of the workgroup takes part.  QT /
-// RT are the query and tail element types: with them fixed at compile time
-// each thread issues all its loads before it uses any (this runs while the
-// other workgroups stream the archive, where every serialized load waits
-// several microseconds).
-template <int D, typename QT, typename RT>
-__device__ __forceinline__ void raw_tail_partial_t(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
-                                   int nr, int tid, float* etl, float* acc, float* tm,
-                                   float* tl) {
-  const int lane = tid & 63, wave = tid >> 6;
-  const QT* qb = static_cast<const QT*>(p.q) + b * p.q_sb;
-  const RT* kb = static_cast<const RT*>(p.kraw) + b * p.kr_sb + hkv * p.kr_sh;
-  const RT* vb = static_cast<const RT*>(p.vraw) + b * p.vr_sb + hkv * p.vr_sh;
-  {
-    // logits: 16 lanes per (head, token), features strided by 16
-    const int grp = tid >> 4, gl = tid & 15;
-    for (int u = grp; u < G * nr; u += kMThreads / 16) {
-      const int h = u / nr, t = u - h * nr;
-      const QT* qr = qb + (hkv * p.G + g0 + h) * p.q_sh + gl;
-      const RT* kr = kb + t * p.kr_st + gl;
-      float qv[D / 16], kv[D / 16];
-#pragma unroll
-      for (int i = 0; i < D / 16; ++i) {
-        qv[i] = to_f32(qr[16 * i]);
-        kv[i] = to_f32(kr[16 * i]);
-      }
-      float a = 0.f;
-#pragma unroll
-      for (int i = 0; i < D / 16; ++i) a = __builtin_fmaf(qv[i], kv[i], a);
-#pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) a += __shfl_xor(a, m, 16);
-      if (gl == 0) etl[h * FC_MAX_BLOCK + t] = a * p.scale_log2;
-    }
-  }
-  __syncthreads();
-  for (int h = wave; h < G; h += kWaves) {
-    float mx = -INFINITY;
-    for (int t = lane; t < nr; t += 64) mx = fmaxf(mx, etl[h * FC_MAX_BLOCK + t]);
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-    float l = 0.f;
-    for (int t = lane; t < nr; t += 64) {
-      const float e = __builtin_amdgcn_exp2f(etl[h * FC_MAX_BLOCK + t] - mx);
-      etl[h * FC_MAX_BLOCK + t] = e;
-      l += e;
-    }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
-    if (lane == 0) {
-      tm[h] = mx;
-      tl[h] = l;
-    }
-  }
-  __syncthreads();
-  constexpr int kT = 8;  // tail rows requested together
-  for (int x = tid; x < G * D; x += kMThreads) {
-    const int h = x / D, d = x - h * D;
-    float o = 0.f;
-    for (int t0 = 0; t0 < nr; t0 += kT) {
-      float vv[kT];
-#pragma unroll
-      for (int j = 0; j < kT; ++j) vv[j] = t0 + j < nr ? to_f32(vb[(t0 + j) * p.vr_st + d]) : 0.f;
-#pragma unroll
-      for (int j = 0; j < kT; ++j)
-        if (t0 + j < nr) o = __builtin_fmaf(etl[h * FC_MAX_BLOCK + t0 + j], vv[j], o);
-    }
-    acc[h * D + d] = o;
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
-                                 int nr, int tid, float* etl, float* acc, float* tm, float* tl) {
-  // the matrix-core pass takes fp16 / bf16 queries; tails are in the stream dtype
-  auto with_q = [&](auto rt) {
-    using RT = decltype(rt);
-    if (p.q_dtype == FC_F16)
-      raw_tail_partial_t<D, f16_t, RT>(p, b, hkv, g0, G, nr, tid, etl, acc, tm, tl);
-    else
-      raw_tail_partial_t<D, bf16_t, RT>(p, b, hkv, g0, G, nr, tid, etl, acc, tm, tl);
-  };
-  switch (p.raw_dtype) {
-    case FC_F16: with_q(f16_t{}); break;
-    case FC_BF16: with_q(bf16_t{}); break;
-    default: with_q(float{}); break;
-  }
-}
-
-// Archive of one stream's completed block inside the fused decode step:
-// rows x (r rows of D fp32 values of the stream dtype TT) -> DCT-II
-// coefficients by the fma chain over the taps rounded to TT, per-frequency
-// absmax scale rounded to TT (1 when not > 0), codes as quant_code — the
-// archive kernels' arithmetic, bit for bit — stored when `write`; then x is
-// replaced by the block's tokens synthesised from the dequantised codes
-// through A (r x SROWS), so the block is attended exactly as an archived
-// one.  kk: SROWS x D, sc: SROWS floats of LDS scratch.
-template <int D, int SROWS, typename TT>
-__device__ __forceinline__ void step_archive(float* x, int r, const float* basis, const float* A,
-                                             bool write, int8_t* codes, float* scales, float* kk,
-                                             float* sc, int tid) {
-  const int lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < SROWS * D; e += kMThreads) {
-    const int j = e / D, d = e - j * D;
-    float a = 0.f;
-    for (int i = 0; i < r; ++i) a = __builtin_fmaf(x[i * D + d], basis[j * r + i], a);
-    kk[e] = to_f32(from_f32<TT>(a));
-  }
-  __syncthreads();
-  if (wave < SROWS) {
-    float m = 0.f;
-    for (int d = lane; d < D; d += 64) m = fmaxf(m, fabsf(kk[wave * D + d]));
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    float sj = to_f32(from_f32<TT>(m / 127.0f));
-    if (!(sj > 0.f)) sj = 1.0f;
-    if (lane == 0) {
-      sc[wave] = sj;
-      if (write) scales[wave] = sj;
-    }
-  }
-  __syncthreads();
-  for (int e = tid; e < SROWS * D; e += kMThreads) {
-    const float sj = sc[e / D];
-    const float q = quant_code(kk[e], sj, 1.0f / sj);
-    if (write) codes[e] = (int8_t)(int)q;
-    kk[e] = q * sj;
-  }
-  __syncthreads();
-  for (int e = tid; e < r * D; e += kMThreads) {
-    const int i = e / D, d = e - i * D;
-    float a = 0.f;
-#pragma unroll
-    for (int j = 0; j < SROWS; ++j) a = __builtin_fmaf(A[i * SROWS + j], kk[j * D + d], a);
-    x[e] = a;
-  }
-  __syncthreads();
-}
-
-// Fused decode step, split 0: the rows this step adds to the attention, in
-// LDS as fp32 (xk, xv: n rows of D), and the partial of the group's G heads
-// over them (as raw_tail_partial_t: tm, tl, acc).
-//   * t + 1 < r: the tail rows 0..t-1 (buffer) and the new token; the token
-//     is written to tail row t.
-//   * t + 1 == r: the block of tail rows 0..r-2 and the new token is
-//     archived as block nb (step_archive) and attended from its codes.
-// `write`: this workgroup stores the token / the block (one head group per
-// (batch, kv head) does; all compute the partial).  The query rows are
-// q + qb + (h0 + h) * q_sh for the G heads.
-template <int D, int SROWS, typename TT>
-__device__ __forceinline__ void step_partial(
-    int64_t t, int r, TT* ktail, TT* vtail, const TT* ktok, const TT* vtok, bool write,
-    int8_t* kcodes, float* kscales, int8_t* vcodes, float* vscales, const float* basis,
-    const float* A, const void* q, int q_dtype, int64_t qb, int64_t q_sh, int64_t h0, int G,
-    float scale_log2, int tid, float* xk, float* xv, float* kk, float* sc, float* etl, float* acc,
-    float* tm, float* tl) {
-  const int lane = tid & 63, wave = tid >> 6;
-  const bool complete = t + 1 == r;
-  const int n = complete ? r : (int)t + 1;
-  for (int x = tid; x < n * D; x += kMThreads) {
-    const int i = x / D, d = x - i * D;
-    xk[x] = to_f32(i < t ? ktail[i * D + d] : ktok[d]);
-    xv[x] = to_f32(i < t ? vtail[i * D + d] : vtok[d]);
-  }
-  if (write && !complete)
-    for (int d = tid; d < D; d += kMThreads) {
-      ktail[t * D + d] = ktok[d];
-      vtail[t * D + d] = vtok[d];
-    }
-  __syncthreads();
-  if (complete) {
-    step_archive<D, SROWS, TT>(xk, r, basis, A, write, kcodes, kscales, kk, sc, tid);
-    step_archive<D, SROWS, TT>(xv, r, basis, A, write, vcodes, vscales, kk, sc, tid);
-  }
-  // the partial over the n rows, at full precision
-  {
-    const int grp = tid >> 4, gl = tid & 15;
-    for (int u = grp; u < G * n; u += kMThreads / 16) {
-      const int h = u / n, i = u - h * n;
-      const int64_t qr = qb + (h0 + h) * q_sh + gl;
-      float a = 0.f;
-      for (int c = 0; c < D / 16; ++c)
-        a = __builtin_fmaf(load_q(q, q_dtype, qr + 16 * c), xk[i * D + gl + 16 * c], a);
-#pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) a += __shfl_xor(a, m, 16);
-      if (gl == 0) etl[h * FC_MAX_BLOCK + i] = a * scale_log2;
-    }
-  }
-  __syncthreads();
-  for (int h = wave; h < G; h += kWaves) {
-    float mx = -INFINITY;
-    for (int i = lane; i < n; i += 64) mx = fmaxf(mx, etl[h * FC_MAX_BLOCK + i]);
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-    float l = 0.f;
-    for (int i = lane; i < n; i += 64) {
-      const float e = __builtin_amdgcn_exp2f(etl[h * FC_MAX_BLOCK + i] - mx);
-      etl[h * FC_MAX_BLOCK + i] = e;
-      l += e;
-    }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
-    if (lane == 0) {
-      tm[h] = mx;
-      tl[h] = l;
-    }
-  }
-  __syncthreads();
-  for (int x = tid; x < G * D; x += kMThreads) {
-    const int h = x / D, d = x - h * D;
-    float o = 0.f;
-    for (int i = 0; i < n; ++i) o = __builtin_fmaf(etl[h * FC_MAX_BLOCK + i], xv[i * D + d], o);
-    acc[h * D + d] = o;
-  }
-}
-
-// Merge of one (batch, kv head, head group) by the workgroup that arrived
-// last, once every other workgroup of the group has published its partial:
-// out = sum_s w_s acc_s / sum_s w_s l_s over the n_splits partials of its G
-// query heads, w_s = 2^(m_s - max_s m_s).  This workgroup's own partial is
-// read from LDS (own_acc [16][D], own_m, own_l), the others with
-// device-scope loads; the raw tail is part of split 0's partial.  The
-// statistics of all splits come in with one load per thread; then each
-// thread owns an output task (head, 4 features) and requests its partials
-// kPre splits at a time.  The code runs once per call, after the pass loop,
-// when its instructions are not in the instruction cache: it is kept short
-// and free of per-element branches (every load of a batch is issued and
-// splits past n_splits are selected away; one store branch per task).
-// `lds` holds >= 2 * 16 * kFuseMaxSplits floats.
-template <int D>
-__device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
-                            int split, int tid, float* lds, const float* own_acc,
-                            const float* own_m, const float* own_l) {
-  constexpr int C4 = D / 4;  // float4 chunks of a head's output
-  constexpr int kPre = 8;    // partials in flight per task
-  const int ns = p.n_splits;
-  const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;  // slot of head 0 of the group
-  float* wsp = lds;                        // [16][kFuseMaxSplits] split maxima
-  float* plv = wsp + 16 * kFuseMaxSplits;  // [16][kFuseMaxSplits] split sums
-
-  // device-scope (L2-missing) loads of the group's partials and statistics;
-  // offsets past the group's slots read as zero
-  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, G * ns * D * 4);
-  const __amdgpu_buffer_rsrc_t rm = buf_rsrc(p.pm + bq0 * ns, G * ns * 4);
-  const __amdgpu_buffer_rsrc_t rl = buf_rsrc(p.pl + bq0 * ns, G * ns * 4);
-  auto load_batch = [&](int h, int sp0, int c, float4_t (&pre)[kPre]) {
-#pragma unroll
-    for (int j = 0; j < kPre; ++j)
-      pre[j] = __builtin_bit_cast(
-          float4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, ((h * ns + sp0 + j) * C4 + c) * 16, 0,
-                                                          kCachePolicySc1));
-  };
-  auto task_out = [&](int h, int c, float4_t (&pre)[kPre], bool have0) {
-    const float* wh = wsp + h * kFuseMaxSplits;
-    const float* lh = plv + h * kFuseMaxSplits;
-    float mx = -INFINITY;
-    for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, wh[sp]);
-    const float4_t own = *reinterpret_cast<const float4_t*>(own_acc + h * D + 4 * c);
-    float l = 0.f;
-    float4_t o = {0.f, 0.f, 0.f, 0.f};
-    for (int sp0 = 0; sp0 < ns; sp0 += kPre) {
-      if (sp0 > 0 || !have0) load_batch(h, sp0, c, pre);
-#pragma unroll
-      for (int j = 0; j < kPre; ++j) {
-        const int sp = sp0 + j;
-        const bool ok = sp < ns;
-        const int si = ok ? sp : 0;
-        const float pmv = wh[si];
-        const float w = (!ok || pmv == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pmv - mx);
-        l = __builtin_fmaf(w, lh[si], l);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = sp == split ? own[i] : (ok ? pre[j][i] : 0.f);
-          o[i] = __builtin_fmaf(w, v, o[i]);
-        }
-      }
-    }
-    const float iv = 1.0f / l;
-    const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
-    if (p.q_dtype == FC_F16) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) static_cast<f16_t*>(p.out)[ob + i] = from_f32<f16_t>(o[i] * iv);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) static_cast<bf16_t*>(p.out)[ob + i] = from_f32<bf16_t>(o[i] * iv);
-    }
-  };
-  auto stats = [&]() {
-    for (int u = tid; u < G * ns; u += kMThreads) {
-      const int h = u / ns, sp = u - h * ns;
-      const bool own = sp == split;
-      const float mv = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(rm, u * 4, 0, kCachePolicySc1));
-      const float lv = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(rl, u * 4, 0, kCachePolicySc1));
-      wsp[h * kFuseMaxSplits + sp] = own ? own_m[h] : mv;
-      plv[h * kFuseMaxSplits + sp] = own ? own_l[h] : lv;
-    }
-  };
-  float4_t pre[kPre];
-  if (G * C4 <= kMThreads) {
-    // one task per thread: its first kPre partials fly with the statistics
-    const bool act = tid < G * C4;
-    const int h = act ? tid / C4 : 0, c = tid - h * C4;
-    load_batch(h, 0, c, pre);
-    stats();
-    __syncthreads();
-    if (act) task_out(h, c, pre, true);
-    return;
-  }
-  stats();
-  __syncthreads();
-  for (int task = tid; task < G * C4; task += kMThreads) {
-    const int h = task / C4, c = task - h * C4;
-    task_out(h, c, pre, false);
-  }
-}
-
-template <int SROWS, int DK, int GP, bool STEP>
-__global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma(MfmaArgs p) {
-  constexpr int D = 32 * DK;
-  constexpr int DV = (D + 127) / 128;  // 128-feature groups of the value product
-  // rows per wavefront pass: its K codes (NT tiles) and V codes (NS slabs)
-  // are in flight while the previous stage computes
-  constexpr int PR = D == 256 ? 32 : 64;
-  constexpr int NT = PR / 16;
-  constexpr int NS = PR / 32;
-  constexpr int KDW = 2 * DK;  // K dwords per lane per tile
-  static_assert(DK % 2 == 0 && PR <= kPassRowsW, "feature width");
-  __shared__ float s_lds[kWaves][16][kSPad];
-  __shared__ _Float16 w_lds[kWaves][16][kWPad];
-  __shared__ float sc_lds[kWaves][2][PR];  // K and V row scales of the pass
-  __shared__ float a_lds[FC_MAX_BLOCK * 4];
-  __shared__ float comb[kWaves][16][3];
-  __shared__ float cbuf[kWaves][GP][D];  // the wavefronts' accumulators, for the combine
-  __shared__ __attribute__((aligned(16))) float part_lds[16 * D];  // raw-tail partial, then this workgroup's partial
-  __shared__ float tail_ml[2][16];    // raw-tail (max, sum) per head
-  __shared__ float wg_ml[2][16];      // this workgroup's (max, sum) per head
-  __shared__ int s_last;
-  __shared__ int s_final;
-
-  // 1-D grid, split-major: workgroup L runs split s of group g; the splits of
-  // a group are spread over the dispatch order and over the XCDs
-  const int64_t L = blockIdx.x;
-  const int split = (int)(L / p.ngroups);
-  const int64_t g = ((L % p.ngroups) - split % p.ngroups + p.ngroups) % p.ngroups;
-  const int64_t bh = g / p.zg;
-  const int64_t g0 = (g % p.zg) * 16;
-  const int64_t b = bh / p.Hkv, hkv = bh - b * p.Hkv;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lq = lane >> 4, lc = lane & 15;
-  const int G = (int)min<int64_t>(16, p.G - g0);  // heads of this group (<= GP)
-  const int r = p.r;
-
-  for (int i = tid; i < r * SROWS; i += kMThreads) a_lds[i] = p.A[i];
-
-  // The group's rows are cut into passes of PR rows; every wavefront of the
-  // group's n_splits workgroups takes the next untaken pass from the group's
-  // queue until none is left, so faster wavefronts take more passes.
-  int64_t nb = p.nb, n_raw = p.n_raw;
-  int64_t step_t = 0, step_nb = 0;  // fused step: tail length and blocks before the token
-  bool step_write = false;
-  if constexpr (STEP) {
-    const int64_t cap = min(p.kcap, p.vcap);
-    step_t = p.state ? min<int64_t>(max<int64_t>(p.state[1], 0), p.r - 1) : p.step_t;
-    step_nb = p.state ? max<int64_t>(p.state[0], 0) : p.step_nb;
-    // one head group per (batch, kv head) stores the token / block; a block
-    // past the capacity is not stored (the state's overflow word says so)
-    step_write = split == 0 && g0 == 0 && (step_t + 1 < p.r || step_nb < cap);
-    nb = min(step_nb, cap);
-    n_raw = 0;
-  } else if (p.state) {
-    // counts of the step's view, kept inside the buffers whatever the words hold
-    const int64_t t = min<int64_t>(max<int64_t>(p.state[1], 0), p.r - 1) + 1;
-    nb = min<int64_t>(max<int64_t>(p.state[0], 0) + (t == p.r ? 1 : 0), min(p.kcap, p.vcap));
-    n_raw = t == p.r ? 0 : t;
-  }
-  const int64_t rows_total = nb * SROWS;
-  const int64_t npass = (rows_total + PR - 1) / PR;
-  unsigned int* passq = p.passq + g * p.cstride;
-  const unsigned int wslot = (unsigned int)(split * kWaves + wave);
-  const unsigned int wstride = (unsigned int)(p.n_splits * kWaves);
-  unsigned int wtaken = 0;
-  // A wavefront's first pass is fixed (pass wslot: no queue round trip before
-  // the first loads); the queue hands out the others from wstride on, or, in
-  // the static order, wslot + k * wstride.
-  auto grab = [&]() -> unsigned int {  // result in lane 0, read when needed
-    if (p.static_passes) return wslot + wstride * ++wtaken;
-    unsigned int v = 0;
-    if (lane == 0)
-      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + wstride;
-    return v;
-  };
-  auto pass_of = [](unsigned int v) { return (int64_t)__builtin_amdgcn_readfirstlane((int)v); };
-
-  const int8_t* kbase = p.kcodes + bh * p.kcap * SROWS * D;
-  const int8_t* vbase = p.vcodes + bh * p.vcap * SROWS * D;
-  const float* ksc = p.kscales + bh * p.kcap * SROWS;
-  const float* vsc = p.vscales + bh * p.vcap * SROWS;
-
-  // ---- queries: B operand of the score product.  Lane (q, c): head c,
-  // features q*D/4 + 8*kc + i of product kc, scaled per head by a power of two
-  const bool hq_ok = lc < G;
-  const int64_t hq = hkv * p.G + g0 + (hq_ok ? lc : 0);
-  // lane (q, c) holds features 64 k + 16 q + [0, 16) of chunk k
-  const uint16_t* qrow =
-      static_cast<const uint16_t*>(p.q) + b * p.q_sb + hq * p.q_sh + 16 * lq;
-  const bool q_f16 = p.q_dtype == FC_F16;
-  float qf[DK][8];
-  float qmax = 0.f;
-  // dtype branch outside the loops; fp16 lanes are read through a half8 view
-  // (hipcc 7.2 reused dword 0's conversion for all dwords when each dword was
-  // bit-cast to half2 inside an unrolled loop)
-#pragma unroll
-  for (int kc = 0; kc < DK; ++kc) {
-    const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + 64 * (kc / 2) + 8 * (kc % 2));
-    if (q_f16) {
-      const half8_t h = __builtin_bit_cast(half8_t, raw);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qf[kc][i] = (float)h[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        qf[kc][2 * i] = __uint_as_float(raw[i] << 16);
-        qf[kc][2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      qf[kc][i] = hq_ok ? qf[kc][i] : 0.f;
-      qmax = fmaxf(qmax, fabsf(qf[kc][i]));
-    }
-  }
-  qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
-  qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
-  // 14-bit integer query per head (largest magnitude in [2^13, 2^14)), split
-  // q' = 256 * hi + lo into two int8 operands: scores are exact integers
-  // 256 * (K . hi) + (K . lo) from the int8 matrix cores
-  const int qe = pow2_exp_for(qmax, 14);
-  constexpr int NC = D / 64;  // 64-feature chunks of the score product
-  i32x4_t qhi[NC], qlo[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      uint32_t hw = 0, lw = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = 16 * c + 4 * w + j;  // feature 64c + 16q + 4w + j
-        const int qi = (int)rintf(ldexpf(qf[e / 8][e % 8], -qe));
-        const int lo = (int)(int8_t)(qi & 0xff);
-        const int hi = (qi - lo) >> 8;
-        lw |= (uint32_t)(lo & 0xff) << (8 * j);
-        hw |= (uint32_t)(hi & 0xff) << (8 * j);
-      }
-      qhi[c][w] = (int)hw;
-      qlo[c][w] = (int)lw;
-    }
-  const float head_mul = ldexpf(p.scale_log2, qe);  // integer score -> base-2 logit / K scale
-
-  float4_t acc[DV][8];
-#pragma unroll
-  for (int dv = 0; dv < DV; ++dv)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[dv][e] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  // Head (lane % GP): reference max m_run (identical in all lanes of a head)
-  // and this lane's share of the exponential sum, both relative to m_run.
-  // The accumulators hold acc * 2^-sig_run.  Both references move only when
-  // a logit exceeds m_run + kLazyMax or a V row scale reaches 2^(sig_run+1).
-  const int myh = lane % GP;
-  float m_run = -INFINITY, l_lane = 0.f;
-  int sig_run = -1000;
-  float wmul_run = INFINITY;  // 2^-sig_run
-
-  // loop-invariant lane offsets (bytes) of the pass loads
-  const int k_off = lc * D + 16 * lq;
-  int v_off[DV];
-#pragma unroll
-  for (int dv = 0; dv < DV; ++dv) v_off[dv] = 8 * lq * D + min(128 * dv + 8 * lc, D - 8);
-  const int sc_off = (lane % PR) * 4;
-
-  uint32_t kr[NT][KDW];
-  float ks_r, vs_r;
-  auto load_k = [&](int64_t pr0, int prow) {
-    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kbase + pr0 * D, prow * D);
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int h = 0; h < DK / 2; ++h) {
-        const u32x4_t v = __builtin_bit_cast(
-            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, k_off + 16 * t * D + 64 * h, 0, 0));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kr[t][4 * h + i] = v[i];
-      }
-    ks_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         buf_rsrc(ksc + pr0, prow * 4), sc_off, 0, 0));
-    vs_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         buf_rsrc(vsc + pr0, prow * 4), sc_off, 0, 0));
-  };
-  uint32_t vr[NS][DV][16];
-  auto load_v = [&](int64_t pr0, int prow) {
-    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vbase + pr0 * D, prow * D);
-#pragma unroll
-    for (int sl = 0; sl < NS; ++sl)
-#pragma unroll
-      for (int dv = 0; dv < DV; ++dv)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          // V rows are consumed once per pass: streaming loads (measured
-          // faster than default or device-scope policy; K stays default,
-          // where streaming measured slower)
-          const u32x2_t v = __builtin_bit_cast(
-              u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-                           rv, v_off[dv] + (32 * sl + i) * D, 0, kCachePolicyNt));
-          vr[sl][dv][2 * i] = v[0];
-          vr[sl][dv][2 * i + 1] = v[1];
-        }
-  };
-
-  // Output weights of the pass's (block, head) pairs, exponentials relative
-  // to mref, scaled by the V row scale * wm, into w_lds; returns this lane's
-  // largest logit and exponential sum.
-  auto weights = [&](int prow, float mref, float wm, float& pmax, float& lsum) {
-    pmax = -INFINITY;
-    lsum = 0.f;
-    if (myh >= G) return;
-    const int npair = (prow / SROWS) * GP;
-    for (int u = lane; u < npair; u += 64) {
-      const int row0 = (u / GP) * SROWS;
-      float sv[SROWS], w[SROWS];
-#pragma unroll
-      for (int j = 0; j < SROWS; ++j) {
-        sv[j] = s_lds[wave][myh][row0 + j] * sc_lds[wave][0][row0 + j];
-        w[j] = 0.f;
-      }
-      auto tap = [&](int t) {
-        float lg = 0.f;
-#pragma unroll
-        for (int j = 0; j < SROWS; ++j) lg = __builtin_fmaf(a_lds[t * SROWS + j], sv[j], lg);
-        pmax = fmaxf(pmax, lg);
-        const float e = __builtin_amdgcn_exp2f(lg - mref);
-        lsum += e;
-#pragma unroll
-        for (int j = 0; j < SROWS; ++j) w[j] = __builtin_fmaf(e, a_lds[t * SROWS + j], w[j]);
-      };
-      if (r <= kTapsUnrolled) {
-#pragma unroll
-        for (int t = 0; t < kTapsUnrolled; ++t)
-          if (t < r) tap(t);
-      } else {
-        for (int t = 0; t < r; ++t) tap(t);
-      }
-#pragma unroll
-      for (int j = 0; j < SROWS; ++j)
-        w_lds[wave][myh][row0 + j] = (_Float16)(w[j] * (sc_lds[wave][1][row0 + j] * wm));
-    }
-  };
-
-  // raw tail (fused calls): split 0 computes its partial before the passes
-  // and folds it into its own, so the final merge reads partials only; in a
-  // fused step that partial covers the rows the step adds
-  const bool fold_tail = p.fused && split == 0 && (STEP || n_raw > 0);
-  if constexpr (STEP) {
-    if (split == 0) {
-      __shared__ float step_sc[4];
-      float* xk = &s_lds[0][0][0];  // the pass loop has not started: its scratch is free
-      float* etl = reinterpret_cast<float*>(&w_lds[0][0][0]);
-      const int64_t bh_s = b * p.Hkv + hkv;
-      const int64_t kblk = (bh_s * p.kcap + step_nb) * SROWS, vblk = (bh_s * p.vcap + step_nb) * SROWS;
-      auto go = [&](auto tt) {
-        using TT = decltype(tt);
-        step_partial<D, SROWS, TT>(
-            step_t, p.r, static_cast<TT*>(const_cast<void*>(p.kraw)) + bh_s * p.r * D,
-            static_cast<TT*>(const_cast<void*>(p.vraw)) + bh_s * p.r * D,
-            static_cast<const TT*>(p.ktok) + b * p.kt_sb + hkv * p.kt_sh,
-            static_cast<const TT*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write,
-            p.kcodes_w + kblk * D, p.kscales_w + kblk, p.vcodes_w + vblk * D, p.vscales_w + vblk,
-            p.basis, p.A, p.q, p.q_dtype, b * p.q_sb, p.q_sh, hkv * p.G + g0, G, p.scale_log2,
-            tid, xk, xk + p.r * D, cbuf[0][0], step_sc, etl, part_lds, tail_ml[0], tail_ml[1]);
-      };
-      if (p.raw_dtype == FC_F16)
-        go(f16_t{});
-      else
-        go(bf16_t{});
-    }
-  } else if (fold_tail) {
-    raw_tail_partial<D>(p, b, hkv, g0, G, (int)n_raw, tid,
-                        reinterpret_cast<float*>(&w_lds[0][0][0]), part_lds, tail_ml[0],
-                        tail_ml[1]);
-  }
-
-  __syncthreads();  // a_lds; the tail's scratch (w_lds) is free again
-  auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
-  int64_t cur = wslot;
-  if (cur < npass) load_k(cur * PR, rows_of(cur));
-  while (cur < npass) {
-    const int64_t pr0 = cur * PR;
-    const int prow = rows_of(cur);  // multiple of SROWS
-    load_v(pr0, prow);
-    // the next pass, taken now and read after the score products (a wavefront
-    // holds at most one pass beyond the current one)
-    const unsigned int nxt_v = grab();
-
-    // ------------------------------------------------------------ scores
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      i32x4_t shi = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        // lane (q, m): row m, features 64c + 16q .. +15, straight from the load
-        const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
-                           (int)kr[t][4 * c + 3]};
-        shi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qhi[c], shi, 0, 0, 0);
-        slo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qlo[c], slo, 0, 0, 0);
-      }
-      if (lc < G) {
-        float4_t sv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = (float)(shi[i] * 256 + slo[i]) * head_mul;
-        *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = sv;
-      }
-    }
-    if (lane < PR) {
-      sc_lds[wave][0][lane] = ks_r;
-      sc_lds[wave][1][lane] = vs_r;
-    }
-    // a V row scale past the headroom of the current exponent forces a rescale
-    const bool sig_need = vs_r * wmul_run >= 2.0f;
-    const float vs_pass = vs_r;
-    // next pass's K codes and scales fly during the softmax and value stages
-    const int64_t nxt = pass_of(nxt_v);
-    if (nxt < npass) load_k(nxt * PR, rows_of(nxt));
-    wave_lds_sync();
-
-    // ------------------------------------------------------------ softmax
-    float pmax, lsum;
-    weights(prow, m_run, wmul_run, pmax, lsum);
-    const bool m_need = pmax > m_run + kLazyMax;
-    if (__builtin_amdgcn_ballot_w64(sig_need || m_need) != 0) {
-      // move the references: V exponent from the pass's largest row scale,
-      // head maxima from the pass's logits; recompute the weights
-      float smax = vs_pass;
-#pragma unroll
-      for (int m = 1; m < 64; m <<= 1) smax = fmaxf(smax, __shfl_xor(smax, m, 64));
-      const int sig_new = max(sig_run, pow2_exp_for(smax, 1));
-#pragma unroll
-      for (int m = GP; m < 64; m <<= 1) pmax = fmaxf(pmax, __shfl_xor(pmax, m, 64));
-      const float m_new = fmaxf(m_run, pmax);
-      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      const float wm = ldexpf(1.0f, -sig_new);
-      float pdummy;
-      weights(prow, m_new, wm, pdummy, lsum);
-      l_lane = l_lane * alpha + lsum;
-      // lane (q, c) register i holds head 4q + i
-      const float sfix = ldexpf(1.0f, sig_run - sig_new);
-      float al[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lq + i, 64) * sfix;
-#pragma unroll
-      for (int dv = 0; dv < DV; ++dv)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[dv][e][i] *= al[i];
-      m_run = m_new;
-      sig_run = sig_new;
-      wmul_run = wm;
-    } else {
-      l_lane += lsum;
-    }
-    // rows past the pass end carry zero weight (their codes read as zero)
-    if (prow < PR)
-      for (int i = prow + lane; i < PR; i += 64)
-        for (int h = 0; h < G; ++h) w_lds[wave][h][i] = (_Float16)0.f;
-    wave_lds_sync();
-
-    // ------------------------------------------------------------ values
-#pragma unroll
-    for (int sl = 0; sl < NS; ++sl) {
-      u32x4_t wa = *reinterpret_cast<const u32x4_t*>(&w_lds[wave][lc][32 * sl + 8 * lq]);
-      if (lc >= G) wa = (u32x4_t){0u, 0u, 0u, 0u};
-      const half8_t wop = __builtin_bit_cast(half8_t, wa);
-#pragma unroll
-      for (int dv = 0; dv < DV; ++dv) {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          // row pair (a, b) = (2pp, 2pp+1): t0 = [a0 b0 a1 b1], t1 = [a2 b2 a3 b3]
-          uint32_t t0[4], t1[4];
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t ra = vr[sl][dv][2 * (2 * pp) + hh] ^ 0x80808080u;
-            const uint32_t rb = vr[sl][dv][2 * (2 * pp + 1) + hh] ^ 0x80808080u;
-            t0[pp] = __builtin_amdgcn_perm(rb, ra, 0x05010400u);
-            t1[pp] = __builtin_amdgcn_perm(rb, ra, 0x07030602u);
-          }
-#pragma unroll
-          for (int ee = 0; ee < 4; ++ee) {
-            // the operand is built in place as one 4-dword vector (no copies)
-            half8_t ov;
-#pragma unroll
-            for (int pp = 0; pp < 4; ++pp) {
-              const uint32_t src = ee < 2 ? t0[pp] : t1[pp];
-              const uint32_t sel = (ee & 1) ? 0x04030402u : 0x04010400u;
-              const half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, src, sel)) +
-                                 (half2_t){(_Float16)-1152.0f, (_Float16)-1152.0f};
-              ov[2 * pp] = h2[0];
-              ov[2 * pp + 1] = h2[1];
-            }
-            const int e = 4 * hh + ee;
-            acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, ov, acc[dv][e], 0, 0, 0);
-          }
-        }
-      }
-    }
-    wave_lds_sync();
-    cur = nxt;
-  }
-
-  // ---- combine the wavefronts.  Each wavefront parks its (max, sum,
-  // 2^sig_run) per head and its accumulators in its own LDS region; after one
-  // barrier thread x of the G * D outputs combines them (lane (q, c) of a
-  // wavefront carries head c's statistics; its register i holds head 4q + i).
-#pragma unroll
-  for (int m = GP; m < 64; m <<= 1) l_lane += __shfl_xor(l_lane, m, 64);
-  if (lane < GP) {
-    comb[wave][lane][0] = m_run;
-    comb[wave][lane][1] = l_lane;
-    comb[wave][lane][2] = ldexpf(1.0f, sig_run);
-  }
-  // One predicate per lane, not per element (per-element conditions became a
-  // branch per store): lanes whose registers hold heads < GP (rows of
-  // cbuf; heads in [G, GP) carry zeros and are never read) and features < D.
-  constexpr int NI = GP < 4 ? GP : 4;  // accumulator registers that can hold a head
-  if (lq < (GP >= 4 ? GP / 4 : 1) && (D % 128 == 0 || lc < D / 8)) {
-#pragma unroll
-    for (int dv = 0; dv < DV; ++dv)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-#pragma unroll
-        for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][128 * dv + 8 * lc + e] = acc[dv][e][i];
-  }
-  __syncthreads();
-  {
-    for (int x = tid; x < G * D; x += kMThreads) {
-      const int h = x / D, d = x - h * D;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[w][h][0]);
-      float o = 0.f, l = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float mw = comb[w][h][0];
-        const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-        o = __builtin_fmaf(f * comb[w][h][2], cbuf[w][h][d], o);
-        l = __builtin_fmaf(f, comb[w][h][1], l);
-      }
-      if (fold_tail) {
-        // rescale both sums to the common maximum max(M, mt)
-        const float mt = tail_ml[0][h];
-        const float mm = fmaxf(M, mt);
-        const float fw = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mm);
-        const float ft = __builtin_amdgcn_exp2f(mt - mm);
-        o = __builtin_fmaf(ft, part_lds[h * D + d], o * fw);
-        l = __builtin_fmaf(ft, tail_ml[1][h], l * fw);
-        M = mm;
-      }
-      part_lds[x] = o;
-      if (d == 0) {
-        wg_ml[0][h] = M;
-        wg_ml[1][h] = l;
-      }
-    }
-  }
-  // ---- arrival, then publication.  A workgroup counts its arrival first;
-  // all but the last of the group's n_splits workgroups then publish their
-  // partial (device-scope stores) and, once the stores are complete, count
-  // the publication.  The last one keeps its own partial in LDS, waits for
-  // the other n_splits - 1 publications (they arrived before it and need
-  // nothing more to finish), returns the group's counters to zero for the
-  // next call and merges.  No cache-wide writeback/invalidate is used (each
-  // costs ~0.1 us and they serialize per XCD); partials are read back with
-  // device-scope loads.  Without the fused merge every workgroup publishes
-  // and the merge runs as its own kernel.
-  // thread x publishes (or merges) the outputs x + 256 k it combined itself;
-  // the barrier below orders the combine before the last workgroup's merge
-  // fused step with a device state: the launch's last workgroup to finish
-  // (all others have read the state by then) advances it
-  auto step_done = [&]() {
-    if constexpr (!STEP) return;
-    if (!p.state) return;
-    if (tid == 0) s_final = atomicAdd(p.done, 1u) + 1 == gridDim.x ? 1 : 0;
-    __syncthreads();
-    if (s_final && tid < 64) {  // lane-indexed vector stores
-      const int64_t cap = min(p.kcap, p.vcap);
-      const bool full = step_t + 1 == p.r;
-      const bool over = full && step_nb >= cap;
-      const int64_t word = tid == 0   ? (full ? step_nb + 1 : step_nb)
-                           : tid == 1 ? (full ? 0 : step_t + 1)
-                                      : ((p.state[2] != 0 || over) ? 1 : 0);
-      if (tid < 3) const_cast<int64_t*>(p.state)[tid] = word;
-      if (tid == 0) __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  };
-  unsigned int* arrive = p.arrive + g * p.cstride;
-  if (tid == 0) {
-    const unsigned int old = atomicAdd(arrive, 1u);
-    s_last = old + 1 == (unsigned int)p.n_splits ? 1 : 0;
-  }
-  __syncthreads();
-  const bool last = s_last != 0;
-  if (!last || !p.fused) {
-    const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;
-    for (int x = tid; x < G * D; x += kMThreads) {
-      const int h = x / D, d = x - h * D;
-      const int64_t slot = (bq0 + h) * p.n_splits + split;
-      __hip_atomic_store(p.pacc + slot * D + d, part_lds[x], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-      if (d == 0) {
-        __hip_atomic_store(p.pm + slot, wg_ml[0][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.pl + slot, wg_ml[1][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-  if (!p.fused) {
-    if (last && tid == 0) {
-      __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return;
-  }
-  if (!last) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    if (tid == 0) atomicAdd(arrive + kPubWord, 1u);
-    step_done();
-    return;
-  }
-  if (tid == 0) {
-    // Ordering: every partial word was written by an agent-scope atomic
-    // store, which is performed at the device's coherence point (not held in
-    // the writer XCD's L2), and each publisher waited for its stores to
-    // complete (vmcnt(0)) before counting itself; the merge reads partials
-    // with agent-scope loads issued after it has seen the count, so no load
-    // can be served by a stale L2 line.  No cache-wide writeback or
-    // invalidate is needed (each costs ~0.1 us and they serialize per XCD).
-    const unsigned int want = (unsigned int)p.n_splits - 1u;
-    unsigned int seen = 0;
-    for (int it = 0; it < p.spin_cap; ++it) {
-      seen = __hip_atomic_load(arrive + kPubWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (seen >= want) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (seen < want)  // merged without every partial: the host reads this word
-      __hip_atomic_store(p.status, (unsigned int)FC_STATUS_MERGE_INCOMPLETE, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // publications still in flight after a give-up add to the word later:
-    // subtracting what was expected (not storing 0) leaves it at zero once
-    // every publisher has counted itself, i.e. before the next call starts
-    __hip_atomic_fetch_add(arrive + kPubWord, 0u - want, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  fused_merge<D>(p, b, hkv, g0, G, split, tid, &s_lds[0][0][0], part_lds, wg_ml[0], wg_ml[1]);
-  step_done();
-}
-
-template <int... Vs, typename F>
-int mfma_with_int(int v, F&& f) {
-  int rc = FC_ERR_UNSUPPORTED;
-  bool hit = false;
-  ((v == Vs ? (rc = f(std::integral_constant<int, Vs>{}), hit = true) : false), ...);
-  return hit ? rc : FC_ERR_UNSUPPORTED;
+// Query dtypes, head sizes and stored rows per block the matrix-core split
+// pass is built for.
+bool mfma_shape_supported(int q_dtype, int64_t D, int s) {
+  return (q_dtype == FC_F16 || q_dtype == FC_BF16) && (D == 64 || D == 128 || D == 256) &&
+         (s == 1 || s == 2 || s == 3 || s == 4 || s == 8);
 }
 
 // Whether the matrix-core split pass handles this configuration.
@@ -1027,8 +18,7 @@ int mfma_with_int(int v, F&& f) {
 bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
                              int s, const fc_stream_view* key, const fc_stream_view* value) {
   const auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-  return (q_dtype == FC_F16 || q_dtype == FC_BF16) && (D == 64 || D == 128 || D == 256) &&
-         (s == 1 || s == 2 || s == 4) && al16(q) && q_sb % 8 == 0 && q_sh % 8 == 0 &&
+  return mfma_shape_supported(q_dtype, D, s) && al16(q) && q_sb % 8 == 0 && q_sh % 8 == 0 &&
          al16(key->rows) && al16(value->rows);
 }
 
@@ -1116,19 +106,8 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   a.static_passes = static_pass_order() ? 1 : 0;
   a.cstride = stride;
   const dim3 grid((unsigned)(a.ngroups * n_splits));
-  const int rc = mfma_with_int<1, 2, 4>(s, [&](auto sc) {
-    constexpr int SR = decltype(sc)::value;
-    return mfma_with_int<2, 4, 8>((int)(D / 32), [&](auto dc) {
-      constexpr int DKv = decltype(dc)::value;
-      return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
-        constexpr int GPv = decltype(gc)::value;
-        if (a.step)
-          attn_split_i8_mfma<SR, DKv, GPv, true><<<grid, kMThreads, 0, st>>>(a);
-        else
-          attn_split_i8_mfma<SR, DKv, GPv, false><<<grid, kMThreads, 0, st>>>(a);
-        return FC_OK;
-      });
-    });
+  const int rc = mfma_with_int<FC_MFMA_ROWS_LIST>(s, [&](auto sc) {
+    return launch_mfma_rows<decltype(sc)::value>(a, (int)(D / 32), gp, grid, st);
   });
   if (rc != FC_OK) return rc;
   return check_launch();
