@@ -8,7 +8,8 @@ namespace fc {
 // Query dtypes, head sizes and stored rows per block the matrix-core split
 // pass is built for.
 bool mfma_shape_supported(int q_dtype, int64_t D, int s) {
-  return (q_dtype == FC_F16 || q_dtype == FC_BF16) && (D == 64 || D == 128 || D == 256) &&
+  return (q_dtype == FC_F16 || q_dtype == FC_BF16) &&
+         (D == 64 || D == 80 || D == 96 || D == 128 || D == 256) &&
          (s == 1 || s == 2 || s == 3 || s == 4 || s == 8);
 }
 
@@ -107,7 +108,7 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   a.cstride = stride;
   const dim3 grid((unsigned)(a.ngroups * n_splits));
   const int rc = mfma_with_int<FC_MFMA_ROWS_LIST>(s, [&](auto sc) {
-    return launch_mfma_rows<decltype(sc)::value>(a, (int)(D / 32), gp, grid, st);
+    return launch_mfma_rows<decltype(sc)::value>(a, (int)D, gp, grid, st);
   });
   if (rc != FC_OK) return rc;
   return check_launch();

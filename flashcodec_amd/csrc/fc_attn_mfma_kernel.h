@@ -466,14 +466,25 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
   }
 }
 
-template <int SROWS, int DK, int GP, bool STEP>
-__global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma(MfmaArgs p) {
-  constexpr int D = 32 * DK;
-  constexpr int DV = (D + 127) / 128;  // 128-feature groups of the value product
+// D: head size (64, 80, 96, 128, 256); the products run on DC = D rounded up
+// to 64 features: the query's features past D are zero, so the score
+// product's code bytes past a row's end (the next row's, or zeros past the
+// pass) add nothing, and value-product outputs past D are not kept.
+template <int D>
+constexpr int mfma_width() {
+  return (D + 63) / 64 * 64;
+}
+
+template <int SROWS, int D, int GP, bool STEP>
+__global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void attn_split_i8_mfma(
+    MfmaArgs p) {
+  constexpr int DC = mfma_width<D>();
+  constexpr int DK = DC / 32;
+  constexpr int DV = (DC + 127) / 128;  // 128-feature groups of the value product
   // rows per wavefront pass: its K codes (NT tiles of 16 rows) and V codes
   // (NS slabs of 32) are in flight while the previous stage computes; a pass
   // holds whole blocks (PR rows of the PRT tile rows; the rest read zero)
-  constexpr int PRT = D == 256 ? 32 : 64;
+  constexpr int PRT = DC == 256 ? 32 : 64;
   constexpr int PR = (PRT / SROWS) * SROWS;
   constexpr int NT = PRT / 16;
   constexpr int NS = PRT / 32;
@@ -569,7 +580,11 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   // bit-cast to half2 inside an unrolled loop)
 #pragma unroll
   for (int kc = 0; kc < DK; ++kc) {
-    const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(qrow + 64 * (kc / 2) + 8 * (kc % 2));
+    // features past D (D = 80, 96) are not loaded and stay zero
+    const int f0 = 64 * (kc / 2) + 16 * lq + 8 * (kc % 2);
+    u32x4_t raw = {0u, 0u, 0u, 0u};
+    if (D % 64 == 0 || f0 < D)
+      raw = *reinterpret_cast<const u32x4_t*>(qrow + 64 * (kc / 2) + 8 * (kc % 2));
     if (q_f16) {
       const half8_t h = __builtin_bit_cast(half8_t, raw);
 #pragma unroll
@@ -593,7 +608,7 @@ __global__ __launch_bounds__(kMThreads, DK == 8 ? 1 : 2) void attn_split_i8_mfma
   // q' = 256 * hi + lo into two int8 operands: scores are exact integers
   // 256 * (K . hi) + (K . lo) from the int8 matrix cores
   const int qe = pow2_exp_for(qmax, 14);
-  constexpr int NC = D / 64;  // 64-feature chunks of the score product
+  constexpr int NC = DC / 64;  // 64-feature chunks of the score product
   i32x4_t qhi[NC], qlo[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
@@ -1034,26 +1049,28 @@ int mfma_with_int(int v, F&& f) {
   return hit ? rc : FC_ERR_UNSUPPORTED;
 }
 
+// stored rows per block and head sizes the matrix-core pass is built for
+#define FC_MFMA_ROWS_LIST 1, 2, 3, 4, 8
+#define FC_MFMA_HEAD_DIMS 64, 80, 96, 128, 256
+
 // Launch of the split pass with SR stored rows per block, dispatched on the
-// feature chunks (D / 32) and the head-group size.  Each SR is instantiated
+// head size and the head-group size.  Each SR is instantiated
 // in a translation unit of its own (fc_attn_mfma_s<SR>.hip).
 template <int SR>
-int launch_mfma_rows(const MfmaArgs& a, int dk, int gp, dim3 grid, hipStream_t st) {
-  return mfma_with_int<2, 4, 8>(dk, [&](auto dc) {
-    constexpr int DKv = decltype(dc)::value;
+int launch_mfma_rows(const MfmaArgs& a, int d, int gp, dim3 grid, hipStream_t st) {
+  return mfma_with_int<FC_MFMA_HEAD_DIMS>(d, [&](auto dc) {
+    constexpr int Dv = decltype(dc)::value;
     return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
       constexpr int GPv = decltype(gc)::value;
       if (a.step)
-        attn_split_i8_mfma<SR, DKv, GPv, true><<<grid, kMThreads, 0, st>>>(a);
+        attn_split_i8_mfma<SR, Dv, GPv, true><<<grid, kMThreads, 0, st>>>(a);
       else
-        attn_split_i8_mfma<SR, DKv, GPv, false><<<grid, kMThreads, 0, st>>>(a);
+        attn_split_i8_mfma<SR, Dv, GPv, false><<<grid, kMThreads, 0, st>>>(a);
       return FC_OK;
     });
   });
 }
 
-// stored rows per block the matrix-core pass is built for
-#define FC_MFMA_ROWS_LIST 1, 2, 3, 4, 8
 extern template int launch_mfma_rows<1>(const MfmaArgs&, int, int, dim3, hipStream_t);
 extern template int launch_mfma_rows<2>(const MfmaArgs&, int, int, dim3, hipStream_t);
 extern template int launch_mfma_rows<3>(const MfmaArgs&, int, int, dim3, hipStream_t);

@@ -104,6 +104,10 @@ CASES = [
     ("jpeg-i8-k8-f16-d64-g16", dict(mode="jpeg", block_size=8, keep_freqs=8, quant_bits=8), "f16", 1, 1, 16, 8 * 70 + 1, 64),
     ("jpeg-i8-r16-k3-f16-g4", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8), "f16", 1, 2, 4, 16 * 50 + 9, 128),
     ("jpeg-i8-r16-k8-bf16-g1", dict(mode="jpeg", block_size=16, keep_freqs=8, quant_bits=8), "bf16", 2, 2, 1, 16 * 40 + 2, 128),
+    ("jpeg-i8-f16-d80-g4", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16", 1, 2, 4, 8 * 100 + 3, 80),
+    ("jpeg-i8-bf16-d96-g2", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8), "bf16", 2, 2, 2, 8 * 120 + 5, 96),
+    ("jpeg-i8-k3-f16-d96-g8", dict(mode="jpeg", block_size=8, keep_freqs=3, quant_bits=8), "f16", 1, 1, 8, 8 * 90, 96),
+    ("jpeg-i8-k8-bf16-d80-g16", dict(mode="jpeg", block_size=8, keep_freqs=8, quant_bits=8), "bf16", 1, 2, 16, 8 * 40 + 7, 80),
     ("jpeg-i8g-f16-g4", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=32), "f16", 2, 4, 4, 8 * 200 + 5, 128),
     ("jpeg-i8g-bf16-g2-d64", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8, quant_group=32), "bf16", 1, 2, 2, 8 * 90 + 3, 64),
     ("jpeg-i8g-f32-r16-d96", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8, quant_group=32), "f32", 1, 2, 3, 16 * 30 + 9, 96),

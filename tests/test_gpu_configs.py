@@ -204,6 +204,22 @@ def test_fused_decode_step_matches_oracle(cfg, dt, G, oracle):
     fa.check_workspaces()
 
 
+@pytest.mark.parametrize("D,k,dt", [(80, 4, "bf16"), (96, 8, "f16")])
+def test_fused_decode_step_head_dims_80_96(D, k, dt, oracle):
+    """The one-launch step on the matrix-core pass at head sizes that are not
+    a multiple of 64 (products padded to 128 features) against the oracle."""
+    B, Hkv, G, r = 2, 2, 4, 8
+    cfg = dict(I8_C3, keep_freqs=k)
+    print(f"case fused step D={D} k={k} {dt}", flush=True)
+    ks, vs = build_streams(cfg, dt, B, Hkv, 6 * r + 2, D, 131 + D, oracle)
+    g = torch.Generator(device=DEV).manual_seed(132)
+    for _ in range(2 * r + 1):
+        q = _tokens(g, B, Hkv * G, D, dt)
+        out = fc.codec_decode_step(q, _tokens(g, B, Hkv, D, dt), _tokens(g, B, Hkv, D, dt), ks, vs)
+        assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), dt)
+    fa.check_workspaces()
+
+
 class _Cache:
     """The part of an HF cache that graph.prepare reads: a list of codec layers."""
 
