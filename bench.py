@@ -378,6 +378,46 @@ def refshapes_mode(args):
     print(json.dumps(res))
 
 
+def shapes_mode(args):
+    """Decode attention on int8 archives at C3's geometry (B=8, 32 q / 8 kv
+    heads, 32768 archived + 5 raw tokens, fp16, r=8) for head sizes and
+    keep_freqs besides C3's: each on the matrix-core pass (FC_PASS_AUTO) and
+    on the vector-ALU pass (FC_PASS_VECTOR), one archive set, max error vs
+    the fp64 oracle over all sequences."""
+    import torch
+    import flashcodec_amd as fc
+    from flashcodec_amd import _native as N
+    from flashcodec_amd.cache import _CodecStream
+    dev = torch.device("cuda:0")
+    res = {"metric": "decode attention GB/s by head size and keep_freqs, int8 jpeg, C3 geometry",
+           "unit": "GB/s", "shapes": []}
+    prev = N.lib().fc_get_attention_pass()
+    for D, k in ((128, 3), (128, 8), (80, 4), (96, 4), (128, 4)):
+        cfg = dict(mode="jpeg", block_size=R, keep_freqs=k, quant_bits=8)
+        ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
+        for st, seed in ((ks, 1), (vs, 2)):
+            x = ar1_device((B, HKV, S_ARCH + TAIL, D), 0.95, seed, dev).to(torch.float16)
+            st.append(x)
+            del x
+        g = torch.Generator(device=dev).manual_seed(3)
+        q = (torch.randn((B, HQ, 1, D), generator=g, device=dev) / math.sqrt(D)).to(torch.float16)
+        nbytes = 2 * (B * HKV * NB * k * (D + 4)) + 2 * B * HKV * TAIL * D * 2 + 2 * B * HQ * D * 2
+        row = {"D": D, "keep_freqs": k, "algorithmic_bytes": nbytes}
+        for name, code in (("matrix_core", N.PASS_AUTO), ("vector_alu", N.PASS_VECTOR)):
+            N.lib().fc_set_attention_pass(code)
+            ms = timed(lambda: fc.codec_decode_attention(q, ks, vs), args.steps, args.warmup)
+            out = fc.codec_decode_attention(q, ks, vs)
+            err, _ = check_against_oracle(q, ks, vs, out)
+            row[name] = {"us": round(ms * 1e3, 2), "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "max_rel_err": err}
+        N.lib().fc_set_attention_pass(prev)
+        res["shapes"].append(row)
+        log(f"bench shapes: {row}")
+        del ks, vs
+        torch.cuda.empty_cache()
+    print(json.dumps(res))
+
+
 def c5_mode(args):
     """end-to-end greedy decoding through the attention
     patch on a randomly initialised Qwen3-0.6B-shaped decoder (28 layers,
@@ -641,14 +681,15 @@ def check_against_oracle(q, ks, vs, out):
     import numpy as np
     from oracle import oracle as O
     import flashcodec_amd as fc
-    rows = [O.stored_rows_jpeg(st._coeffs[:, :, :NB].cpu().numpy(),
-                               st._scales[:, :, :NB, :, 0].cpu().numpy()) for st in (ks, vs)]
+    nb, r, k = ks.n_blocks, ks.block_size, ks.codec.keep_freqs
+    rows = [O.stored_rows_jpeg(st._coeffs[:, :, :nb].cpu().numpy(),
+                               st._scales[:, :, :nb, :, 0].cpu().numpy()) for st in (ks, vs)]
     raws = [st.raw.float().cpu().numpy() for st in (ks, vs)]
-    A = O.synthesis_matrix("jpeg", R, fc.dct_basis(R, K).numpy())
+    A = O.synthesis_matrix("jpeg", r, fc.dct_basis(r, k).numpy())
     ref = O.attention(q[:, :, 0].float().cpu().numpy(), rows[0], rows[1], raws[0], raws[1], A,
-                      D ** -0.5, n_threads=min(16, len(os.sched_getaffinity(0))))
+                      q.shape[-1] ** -0.5, n_threads=min(16, len(os.sched_getaffinity(0))))
     got = out[:, :, 0].float().cpu().numpy()
-    per_seq = np.abs(got - ref).reshape(B, -1).max(-1) / np.abs(ref).max()
+    per_seq = np.abs(got - ref).reshape(q.shape[0], -1).max(-1) / np.abs(ref).max()
     return float(per_seq.max()), [float(e) for e in per_seq]
 
 
@@ -810,7 +851,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--mode", choices=["c3", "c1", "c2", "c4", "c5", "refshapes", "copy"],
+    ap.add_argument("--mode", choices=["c3", "c1", "c2", "c4", "c5", "refshapes", "shapes", "copy"],
                     default="c3")
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -842,6 +883,8 @@ def main():
         return c2_mode(args)
     if args.mode == "refshapes":
         return refshapes_mode(args)
+    if args.mode == "shapes":
+        return shapes_mode(args)
     if args.mode == "c5":
         return c5_mode(args)
     if args.mode == "c4":
