@@ -146,6 +146,21 @@ def timed(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def timed_cycle(fn, steps, warmup):
+    """ms per call of fn(i), i = 0, 1, ..., between two events."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
 def c2_mode(args):
     """jpeg int8 archive + read of fp16 KV (B=4, H=32,
     S=8192, D=128), AR(1) rho=0.95 with a per-channel scale log-uniform in
@@ -269,12 +284,21 @@ def c4_mode(args):
         ks.append(x["k"])
         vs.append(x["v"])
         t_attn = timed(lambda: fc.codec_decode_attention(q, ks, vs), args.steps, args.warmup)
+        # the same calls cycling over 4 copies of the archives (1.07 GB, beyond
+        # the 256 MB last-level cache), as a decode step cycles over layers
+        sets = [(ks, vs)] + [(archive_copy(ks), archive_copy(vs)) for _ in range(3)]
+        t_rot = timed_cycle(lambda i: fc.codec_decode_attention(q, *sets[i % 4]), args.steps,
+                            args.warmup)
+        del sets
+        torch.cuda.empty_cache()
         tag = f"keep{keep}"
         res[tag] = {"archive_GBs": round(alg_codec / (t_arch * 1e-3) / 1e9, 1),
                     "read_GBs": round(alg_codec / (t_read * 1e-3) / 1e9, 1),
                     "attention_GBs": round(alg_attn / (t_attn * 1e-3) / 1e9, 1),
+                    "attention_rotating_GBs": round(alg_attn / (t_rot * 1e-3) / 1e9, 1),
                     "archive_us": round(t_arch * 1e3, 2), "read_us": round(t_read * 1e3, 2),
-                    "attention_us": round(t_attn * 1e3, 2), "kept_deltas": m_keep}
+                    "attention_us": round(t_attn * 1e3, 2),
+                    "attention_rotating_us": round(t_rot * 1e3, 2), "kept_deltas": m_keep}
         if keep == 1.0:
             o = fc.codec_decode_attention(q, ks, vs)
             G = hq // h_
@@ -698,7 +722,10 @@ def archive_copy(st):
     buffers): one more set for the rotating measurement."""
     from flashcodec_amd.cache import _CodecStream
     c = _CodecStream(st.codec)
-    c._coeffs, c._scales = st._coeffs.clone(), st._scales.clone()
+    for name in ("_coeffs", "_scales", "_deltas", "_anchors"):
+        t = getattr(st, name, None)
+        if t is not None:
+            setattr(c, name, t.clone())
     c._capacity, c.n_blocks, c.n_archived = st._capacity, st.n_blocks, st.n_archived
     c.dtype, c.meta = st.dtype, st.meta
     c._raw_buf, c._n_raw = st._raw_buf.clone(), st._n_raw

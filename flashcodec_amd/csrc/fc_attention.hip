@@ -205,7 +205,9 @@ __device__ __forceinline__ void wg_reduce(float (&v)[GM], float* red, bool is_ma
     }
     if (lane == 0) red[wave * GM + g] = x;
   }
-  __syncthreads();
+  // LDS-only barriers: the V rows the pass requested before its softmax stay
+  // in flight through the reductions
+  lds_barrier();
 #pragma unroll
   for (int g = 0; g < GM; ++g) {
     float x = red[g];
@@ -214,7 +216,7 @@ __device__ __forceinline__ void wg_reduce(float (&v)[GM], float* red, bool is_ma
       x = is_max ? fmaxf(x, red[w * GM + g]) : x + red[w * GM + g];
     v[g] = x;
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 
@@ -1149,7 +1151,10 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G, i
 int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, int64_t nb,
                         int64_t B, int64_t Hkv, int64_t G, int64_t D, int n_cu) {
   if (nb <= 0) return 0;
-  const bool mfma = store_kind == FC_STORE_JPEG_I8 && fc::mfma_shape_supported(q_dtype, D, s) &&
+  const bool png_mfma =
+      store_kind == FC_STORE_PNG && fc::png_mfma_shape_supported(q_dtype, stream_dtype, D, s);
+  const bool mfma = (png_mfma || (store_kind == FC_STORE_JPEG_I8 &&
+                                  fc::mfma_shape_supported(q_dtype, D, s))) &&
                     fc::mfma_split_allowed();
   if (n_cu <= 0) n_cu = 256;
   if (mfma) {
@@ -1161,8 +1166,9 @@ int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, in
     // S=64K where 64 take 28.6
     const int64_t groups = (G + 15) / 16;
     const int64_t cols = std::max<int64_t>(1, B * Hkv * groups);
-    int64_t want = (2 * (int64_t)n_cu + cols - 1) / cols;
-    const int64_t pr = D == 256 ? 32 : 64;
+    const int64_t per_cu = png_mfma ? fc::kPngWgPerCu : 2;
+    int64_t want = (per_cu * (int64_t)n_cu + cols - 1) / cols;
+    const int64_t pr = png_mfma ? 16 : D == 256 ? 32 : 64;  // rows per pass
     const int64_t npass = (nb * s + pr - 1) / pr;
     want = std::min<int64_t>(want, std::max<int64_t>(1, npass / 4));
     want = std::min<int64_t>(want, std::max<int64_t>(16, npass / 10));
@@ -1365,6 +1371,25 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                                         kCounterWords, kCounterStride, ws.status,
                                         fuse ? &fz : nullptr, st);
     if (rc != FC_OK || fuse) return rc;
+  } else if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_PNG &&
+             split_png_mfma_supported(q, q_dtype, q_sb, q_sh, D, r, stream_dtype, key, value) &&
+             2 * B * Hkv * ((G + 15) / 16) * kCounterStride <= kCounterWords &&
+             mfma_split_allowed()) {
+    if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
+    const bool fuse = (parts & kPartMerge) && split_i8_mfma_fusable(n_splits);
+    MfmaFuse fz{};
+    if (fuse) {
+      fz.raw_dtype = stream_dtype;
+      fz.n_raw = n_raw;
+      fz.out = out;
+      fz.o_sb = o_sb;
+      fz.o_sh = o_sh;
+    }
+    const int rc = launch_split_png_mfma(q, q_sb, q_sh, B, Hq, Hkv, D, r, nb, key, value,
+                                         scale_log2, pm, pl, pacc, n_splits, counters,
+                                         kCounterWords, kCounterStride, ws.status,
+                                         fuse ? &fz : nullptr, nullptr, st);
+    if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit)) {
     // the merge runs inside the split pass when every group has a counter
     if (D % 8) return FC_ERR_UNSUPPORTED;
@@ -1457,6 +1482,20 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     return launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb_hint, key, value,
                                 A, scale * kLog2e, pm, pl, pacc, n_splits, counters,
                                 kCounterWords, kCounterStride, ws.status, &fz, st);
+  }
+  if (store_kind == FC_STORE_PNG &&
+      split_png_mfma_supported(q, q_dtype, q_sb, q_sh, D, r, stream_dtype, key, value) &&
+      mfma_split_allowed() && 2 * B * Hkv * ((G + 15) / 16) * kCounterStride <= kCounterWords) {
+    if (!split_i8_mfma_fusable(n_splits)) return FC_ERR_UNSUPPORTED;
+    MfmaFuse fz{};
+    fz.raw_dtype = stream_dtype;
+    fz.n_raw = 0;  // taken from the state
+    fz.out = out;
+    fz.o_sb = o_sb;
+    fz.o_sh = o_sh;
+    return launch_split_png_mfma(q, q_sb, q_sh, B, Hq, Hkv, D, r, nb_hint, key, value,
+                                 scale * kLog2e, pm, pl, pacc, n_splits, counters, kCounterWords,
+                                 kCounterStride, ws.status, &fz, state, st);
   }
   if (!valu_fusable(B, Hkv, G)) return FC_ERR_UNSUPPORTED;
   return launch_split_valu(q, q_dtype, q_sb, q_sh, B, Hkv, G, D, store_kind, stream_dtype, r, s,

@@ -117,6 +117,12 @@ struct MfmaArgs {
   const float* basis;
   int64_t step_t, step_nb;
   unsigned int* done;
+  // png archives (fc_attn_png.hip): anchors (B, H, cap, D) in the stream
+  // dtype and fp32 deltas (B, H, cap, r - 1, D)
+  const void* kanch;
+  const void* vanch;
+  const float* kdel;
+  const float* vdel;
 };
 
 constexpr int kMThreads = 256;
@@ -219,13 +225,16 @@ __device__ __forceinline__ void raw_tail_partial_t(const MfmaArgs& p, int64_t b,
   }
 }
 
-template <int D>
+// QF32: fp32 queries (the png pass); else fp16 / bf16 (the int8 pass).
+template <int D, bool QF32 = false>
 __device__ __forceinline__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
                                  int nr, int tid, float* etl, float* acc, float* tm, float* tl) {
-  // the matrix-core pass takes fp16 / bf16 queries; tails are in the stream dtype
+  // tails in the stream dtype
   auto with_q = [&](auto rt) {
     using RT = decltype(rt);
-    if (p.q_dtype == FC_F16)
+    if constexpr (QF32)
+      raw_tail_partial_t<D, float, RT>(p, b, hkv, g0, G, nr, tid, etl, acc, tm, tl);
+    else if (p.q_dtype == FC_F16)
       raw_tail_partial_t<D, f16_t, RT>(p, b, hkv, g0, G, nr, tid, etl, acc, tm, tl);
     else
       raw_tail_partial_t<D, bf16_t, RT>(p, b, hkv, g0, G, nr, tid, etl, acc, tm, tl);
@@ -377,7 +386,7 @@ __device__ __forceinline__ void step_partial(
 // and free of per-element branches (every load of a batch is issued and
 // splits past n_splits are selected away; one store branch per task).
 // `lds` holds >= 2 * 16 * kFuseMaxSplits floats.
-template <int D>
+template <int D, bool QF32 = false>
 __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
                             int split, int tid, float* lds, const float* own_acc,
                             const float* own_m, const float* own_l) {
@@ -427,7 +436,10 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
     }
     const float iv = 1.0f / l;
     const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
-    if (p.q_dtype == FC_F16) {
+    if constexpr (QF32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) static_cast<float*>(p.out)[ob + i] = o[i] * iv;
+    } else if (p.q_dtype == FC_F16) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) static_cast<f16_t*>(p.out)[ob + i] = from_f32<f16_t>(o[i] * iv);
     } else {
@@ -464,6 +476,132 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
     const int h = task / C4, c = task - h * C4;
     task_out(h, c, pre, false);
   }
+}
+
+// End of a split-pass workgroup of the matrix-core passes, once its
+// wavefronts have parked their (max, sum, accumulator scale) per head in
+// comb and their accumulators in cbuf (rows = heads):
+//   * combine: thread x of the G * D outputs combines the four wavefronts
+//     (and, in split 0, the raw tail's partial from part_lds / tail_ml)
+//     into this workgroup's partial (part_lds, wg_ml);
+//   * arrival, then publication: a workgroup counts its arrival first; all
+//     but the last of the group's n_splits workgroups then publish their
+//     partial (device-scope stores) and, once the stores are complete, count
+//     the publication.  The last one keeps its own partial in LDS, waits for
+//     the other n_splits - 1 publications (they arrived before it and need
+//     nothing more to finish), returns the group's counters to zero for the
+//     next call and merges (fused_merge).  No cache-wide writeback /
+//     invalidate is used (each costs ~0.1 us and they serialize per XCD);
+//     partials are read back with device-scope loads.  Without the fused
+//     merge every workgroup publishes and the merge runs as its own kernel.
+// step_done() runs when the workgroup is finished (the fused step's state
+// advance); `scratch` holds the merge's statistics (>= 2 * 16 * 64 floats).
+template <int D, int CB, bool QF32, typename Done>
+__device__ __forceinline__ void split_epilogue(
+    const MfmaArgs& p, int64_t g, int64_t b, int64_t hkv, int64_t g0, int G, int split, int tid,
+    bool fold_tail, float (&comb)[kWaves][16][3], float (&cbuf)[kWaves][CB][D], float* part_lds,
+    float (&tail_ml)[2][16], float (&wg_ml)[2][16], float* scratch, int& s_last,
+    unsigned int* passq, Done&& step_done) {
+  __syncthreads();
+  {
+    for (int x = tid; x < G * D; x += kMThreads) {
+      const int h = x / D, d = x - h * D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[w][h][0]);
+      float o = 0.f, l = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float mw = comb[w][h][0];
+        const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+        o = __builtin_fmaf(f * comb[w][h][2], cbuf[w][h][d], o);
+        l = __builtin_fmaf(f, comb[w][h][1], l);
+      }
+      if (fold_tail) {
+        // rescale both sums to the common maximum max(M, mt)
+        const float mt = tail_ml[0][h];
+        const float mm = fmaxf(M, mt);
+        const float fw = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mm);
+        const float ft = __builtin_amdgcn_exp2f(mt - mm);
+        o = __builtin_fmaf(ft, part_lds[h * D + d], o * fw);
+        l = __builtin_fmaf(ft, tail_ml[1][h], l * fw);
+        M = mm;
+      }
+      part_lds[x] = o;
+      if (d == 0) {
+        wg_ml[0][h] = M;
+        wg_ml[1][h] = l;
+      }
+    }
+  }
+  // ---- arrival, then publication (thread x publishes the outputs it
+  // combined; the barrier after the arrival orders the combine before the
+  // last workgroup's merge)
+  unsigned int* arrive = p.arrive + g * p.cstride;
+  if (tid == 0) {
+    const unsigned int old = atomicAdd(arrive, 1u);
+    s_last = old + 1 == (unsigned int)p.n_splits ? 1 : 0;
+  }
+  __syncthreads();
+  const bool last = s_last != 0;
+  if (!last || !p.fused) {
+    const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;
+    for (int x = tid; x < G * D; x += kMThreads) {
+      const int h = x / D, d = x - h * D;
+      const int64_t slot = (bq0 + h) * p.n_splits + split;
+      __hip_atomic_store(p.pacc + slot * D + d, part_lds[x], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      if (d == 0) {
+        __hip_atomic_store(p.pm + slot, wg_ml[0][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.pl + slot, wg_ml[1][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (!p.fused) {
+    if (last && tid == 0) {
+      __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  if (!last) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0) atomicAdd(arrive + kPubWord, 1u);
+    step_done();
+    return;
+  }
+  if (tid == 0) {
+    // Ordering: every partial word was written by an agent-scope atomic
+    // store, which is performed at the device's coherence point (not held in
+    // the writer XCD's L2), and each publisher waited for its stores to
+    // complete (vmcnt(0)) before counting itself; the merge reads partials
+    // with agent-scope loads issued after it has seen the count, so no load
+    // can be served by a stale L2 line.  No cache-wide writeback or
+    // invalidate is needed (each costs ~0.1 us and they serialize per XCD).
+    const unsigned int want = (unsigned int)p.n_splits - 1u;
+    unsigned int seen = 0;
+    for (int it = 0; it < p.spin_cap; ++it) {
+      seen = __hip_atomic_load(arrive + kPubWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (seen >= want) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (seen < want)  // merged without every partial: the host reads this word
+      __hip_atomic_store(p.status, (unsigned int)FC_STATUS_MERGE_INCOMPLETE, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // publications still in flight after a give-up add to the word later:
+    // subtracting what was expected (not storing 0) leaves it at zero once
+    // every publisher has counted itself, i.e. before the next call starts
+    __hip_atomic_fetch_add(arrive + kPubWord, 0u - want, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  fused_merge<D, QF32>(p, b, hkv, g0, G, split, tid, scratch, part_lds, wg_ml[0], wg_ml[1]);
+  step_done();
 }
 
 // D: head size (64, 80, 96, 128, 256); the products run on DC = D rounded up
@@ -912,50 +1050,6 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
 #pragma unroll
         for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][128 * dv + 8 * lc + e] = acc[dv][e][i];
   }
-  __syncthreads();
-  {
-    for (int x = tid; x < G * D; x += kMThreads) {
-      const int h = x / D, d = x - h * D;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[w][h][0]);
-      float o = 0.f, l = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float mw = comb[w][h][0];
-        const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
-        o = __builtin_fmaf(f * comb[w][h][2], cbuf[w][h][d], o);
-        l = __builtin_fmaf(f, comb[w][h][1], l);
-      }
-      if (fold_tail) {
-        // rescale both sums to the common maximum max(M, mt)
-        const float mt = tail_ml[0][h];
-        const float mm = fmaxf(M, mt);
-        const float fw = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mm);
-        const float ft = __builtin_amdgcn_exp2f(mt - mm);
-        o = __builtin_fmaf(ft, part_lds[h * D + d], o * fw);
-        l = __builtin_fmaf(ft, tail_ml[1][h], l * fw);
-        M = mm;
-      }
-      part_lds[x] = o;
-      if (d == 0) {
-        wg_ml[0][h] = M;
-        wg_ml[1][h] = l;
-      }
-    }
-  }
-  // ---- arrival, then publication.  A workgroup counts its arrival first;
-  // all but the last of the group's n_splits workgroups then publish their
-  // partial (device-scope stores) and, once the stores are complete, count
-  // the publication.  The last one keeps its own partial in LDS, waits for
-  // the other n_splits - 1 publications (they arrived before it and need
-  // nothing more to finish), returns the group's counters to zero for the
-  // next call and merges.  No cache-wide writeback/invalidate is used (each
-  // costs ~0.1 us and they serialize per XCD); partials are read back with
-  // device-scope loads.  Without the fused merge every workgroup publishes
-  // and the merge runs as its own kernel.
-  // thread x publishes (or merges) the outputs x + 256 k it combined itself;
-  // the barrier below orders the combine before the last workgroup's merge
   // fused step with a device state: the launch's last workgroup to finish
   // (all others have read the state by then) advances it
   auto step_done = [&]() {
@@ -974,71 +1068,8 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
       if (tid == 0) __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
-  unsigned int* arrive = p.arrive + g * p.cstride;
-  if (tid == 0) {
-    const unsigned int old = atomicAdd(arrive, 1u);
-    s_last = old + 1 == (unsigned int)p.n_splits ? 1 : 0;
-  }
-  __syncthreads();
-  const bool last = s_last != 0;
-  if (!last || !p.fused) {
-    const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;
-    for (int x = tid; x < G * D; x += kMThreads) {
-      const int h = x / D, d = x - h * D;
-      const int64_t slot = (bq0 + h) * p.n_splits + split;
-      __hip_atomic_store(p.pacc + slot * D + d, part_lds[x], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-      if (d == 0) {
-        __hip_atomic_store(p.pm + slot, wg_ml[0][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.pl + slot, wg_ml[1][h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-  if (!p.fused) {
-    if (last && tid == 0) {
-      __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return;
-  }
-  if (!last) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    if (tid == 0) atomicAdd(arrive + kPubWord, 1u);
-    step_done();
-    return;
-  }
-  if (tid == 0) {
-    // Ordering: every partial word was written by an agent-scope atomic
-    // store, which is performed at the device's coherence point (not held in
-    // the writer XCD's L2), and each publisher waited for its stores to
-    // complete (vmcnt(0)) before counting itself; the merge reads partials
-    // with agent-scope loads issued after it has seen the count, so no load
-    // can be served by a stale L2 line.  No cache-wide writeback or
-    // invalidate is needed (each costs ~0.1 us and they serialize per XCD).
-    const unsigned int want = (unsigned int)p.n_splits - 1u;
-    unsigned int seen = 0;
-    for (int it = 0; it < p.spin_cap; ++it) {
-      seen = __hip_atomic_load(arrive + kPubWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (seen >= want) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (seen < want)  // merged without every partial: the host reads this word
-      __hip_atomic_store(p.status, (unsigned int)FC_STATUS_MERGE_INCOMPLETE, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // publications still in flight after a give-up add to the word later:
-    // subtracting what was expected (not storing 0) leaves it at zero once
-    // every publisher has counted itself, i.e. before the next call starts
-    __hip_atomic_fetch_add(arrive + kPubWord, 0u - want, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  fused_merge<D>(p, b, hkv, g0, G, split, tid, &s_lds[0][0][0], part_lds, wg_ml[0], wg_ml[1]);
-  step_done();
+  split_epilogue<D, CB, false>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf, part_lds,
+                               tail_ml, wg_ml, &s_lds[0][0][0], s_last, passq, step_done);
 }
 
 template <int... Vs, typename F>

@@ -1,0 +1,356 @@
+// Split pass of the decode attention for png archives on gfx950 matrix
+// cores, with the merge of the split partials fused in: the pass queue,
+// combine and merge of the int8 pass (fc_attn_mfma_kernel.h) over fp32 rows.
+//
+// A png block of r tokens is stored as its anchor (the first token, in the
+// stream dtype) and r - 1 fp32 first-order deltas, token t = sum_{j <= t}
+// row_j (flashcodec/codecs/png.py:36-74), so for a query q
+// (flashcodec/attention.py:45-61: A is lower-triangular ones for png)
+//   logit_t = scale * sum_{j <= t} (q . row_j)     prefix sums of the scores
+//   out    += sum_j (sum_{t >= j} p_t) row_j        suffix sums of the weights
+// and the token rows are never formed.
+//
+// Scores: v_mfma_f32_16x16x4_f32, 16 rows x 4 features by 4 features x 16
+// heads per instruction.  Lane (q, m) holds features D/4 * q + c of row m
+// (D/4 consecutive floats, read with 16-byte loads) and lane (q, c) the same
+// features of head c's query; instruction c takes feature D/4 * q + c from
+// every lane, so the D/4 instructions cover all features.  Output: lane
+// (q, c) gets the scores of rows 4q .. 4q+3 for head c.
+// Values: the same instruction with the weights (16 heads x 4 rows) by the
+// rows (4 rows x 16 features): lane (q, c) holds rows q, q+4, q+8, q+12 of the
+// pass, features D/16 * c .. D/16 * c + D/16 - 1 (instruction f of a row
+// group takes feature D/16 * c + f in column c).
+// A pass is one 16-row tile (16 / r whole blocks); a wavefront requests the
+// next pass's rows after its score products and the pass's value rows at its
+// start, and takes passes from its group's queue as the int8 pass does.
+// Products and sums are fp32 throughout (the query and the weights are not
+// rounded), so fp32 outputs meet the 1e-5 tolerance.
+#include "fc_attn_mfma_kernel.h"
+
+namespace fc {
+
+namespace {
+
+constexpr int kPngTile = 16;  // rows per pass
+
+
+// kPngWgPerCu (2) workgroups per compute unit: measured at C4, 2 per CU
+// (32 splits) take 59.2 us per call over rotating archive sets where 3 per
+// CU (48 splits, the query operands read from LDS to fit 168 VGPRs) take
+// 64.6 (more partials to merge, more contention on the pass queues)
+template <int R, int D, int GP>
+__global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(MfmaArgs p) {
+  constexpr int FPL = D / 4;   // score-operand features per lane
+  constexpr int FPC = D / 16;  // value-product features per lane column
+  static_assert(kPngTile % R == 0 && FPC % 4 == 0, "block size / head size");
+  __shared__ float s_lds[kWaves][16][kPngTile + 1];  // scaled scores [head][row]
+  __shared__ float w_lds[kWaves][16][kPngTile + 4];  // weights [head][row]
+  __shared__ float comb[kWaves][16][3];
+  __shared__ float cbuf[kWaves][GP][D];
+  __shared__ __attribute__((aligned(16))) float part_lds[16 * D];
+  __shared__ float tail_ml[2][16];
+  __shared__ float wg_ml[2][16];
+  __shared__ float scratch[2 * 16 * kFuseMaxSplits];  // raw-tail logits, then merge statistics
+  __shared__ int s_last;
+
+  // 1-D grid, split-major, as the int8 pass
+  const int64_t L = blockIdx.x;
+  const int split = (int)(L / p.ngroups);
+  const int64_t g = ((L % p.ngroups) - split % p.ngroups + p.ngroups) % p.ngroups;
+  const int64_t bh = g / p.zg;
+  const int64_t g0 = (g % p.zg) * 16;
+  const int64_t b = bh / p.Hkv, hkv = bh - b * p.Hkv;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane >> 4, lc = lane & 15;
+  const int G = (int)min<int64_t>(16, p.G - g0);
+
+  int64_t nb = p.nb, n_raw = p.n_raw;
+  if (p.state) {
+    // counts of a decode step's view on the device (graph replays)
+    const int64_t t = min<int64_t>(max<int64_t>(p.state[1], 0), R - 1) + 1;
+    nb = min<int64_t>(max<int64_t>(p.state[0], 0) + (t == R ? 1 : 0), min(p.kcap, p.vcap));
+    n_raw = t == R ? 0 : t;
+  }
+  const int64_t rows_total = nb * R;
+  const int64_t npass = (rows_total + kPngTile - 1) / kPngTile;
+  unsigned int* passq = p.passq + g * p.cstride;
+  const unsigned int wslot = (unsigned int)(split * kWaves + wave);
+  const unsigned int wstride = (unsigned int)(p.n_splits * kWaves);
+  unsigned int wtaken = 0;
+  // first pass fixed (wslot), the others from the queue (from wstride on) or
+  // in the static order wslot + k * wstride
+  auto grab = [&]() -> unsigned int {
+    if (p.static_passes) return wslot + wstride * ++wtaken;
+    unsigned int v = 0;
+    if (lane == 0)
+      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + wstride;
+    return v;
+  };
+  auto pass_of = [](unsigned int v) { return (int64_t)__builtin_amdgcn_readfirstlane((int)v); };
+
+  const float* kanch = static_cast<const float*>(p.kanch) + bh * p.kcap * D;
+  const float* vanch = static_cast<const float*>(p.vanch) + bh * p.vcap * D;
+  const float* kdel = p.kdel + bh * p.kcap * (R - 1) * D;
+  const float* vdel = p.vdel + bh * p.vcap * (R - 1) * D;
+  // row gr of a stream: the anchor of its block or one of its deltas; rows
+  // past the archive read row 0 and are zeroed by the caller
+  auto row_ptr = [&](const float* anch, const float* del, int64_t gr) {
+    const int64_t blk = gr / R;
+    const int j = (int)(gr - blk * R);
+    return j == 0 ? anch + blk * D : del + (blk * (R - 1) + (j - 1)) * D;
+  };
+
+  // ---- queries: lane (q, c) holds head c's features D/4 * q .. (fp32)
+  const bool hq_ok = lc < G;
+  const int64_t hq = hkv * p.G + g0 + (hq_ok ? lc : 0);
+  const float* qrow = static_cast<const float*>(p.q) + b * p.q_sb + hq * p.q_sh + FPL * lq;
+  float qv[FPL];
+#pragma unroll
+  for (int c = 0; c < FPL; c += 4) {
+    const float4_t v = *reinterpret_cast<const float4_t*>(qrow + c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qv[c + i] = hq_ok ? v[i] : 0.f;
+  }
+
+  float4_t acc[FPC];
+#pragma unroll
+  for (int f = 0; f < FPC; ++f) acc[f] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  const int myh = lane % GP;  // the head of this lane's softmax pairs
+  float m_run = -INFINITY, l_lane = 0.f;
+
+  float kr[FPL];
+  auto load_k = [&](int64_t pass) {
+    const int64_t gr = pass * kPngTile + lc;
+    const bool ok = gr < rows_total;
+    const float* src = row_ptr(kanch, kdel, ok ? gr : 0) + FPL * lq;
+#pragma unroll
+    for (int c = 0; c < FPL; c += 4) {
+      const float4_t v = *reinterpret_cast<const float4_t*>(src + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kr[c + i] = ok ? v[i] : 0.f;
+    }
+  };
+  float vr[4][FPC];
+  auto load_v = [&](int64_t pass) {
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const int64_t gr = pass * kPngTile + 4 * rg + lq;
+      const bool ok = gr < rows_total;
+      const float* src = row_ptr(vanch, vdel, ok ? gr : 0) + FPC * lc;
+#pragma unroll
+      for (int c = 0; c < FPC; c += 4) {
+        const float4_t v = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(src + c));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vr[rg][c + i] = ok ? v[i] : 0.f;
+      }
+    }
+  };
+
+  // weights of the pass's (block, head) pairs: prefix sums of the scaled
+  // scores are the logits, exponentials against mref, suffix sums are the
+  // row weights (into w_lds); this lane's largest logit and exponential sum
+  auto weights = [&](int prow, float mref, float& pmax, float& lsum) {
+    pmax = -INFINITY;
+    lsum = 0.f;
+    if (myh >= G) return;
+    const int npair = (prow / R) * GP;
+    for (int u = lane; u < npair; u += 64) {
+      const int row0 = (u / GP) * R;
+      float e[R];
+      float run = 0.f;
+#pragma unroll
+      for (int t = 0; t < R; ++t) {
+        run += s_lds[wave][myh][row0 + t];
+        pmax = fmaxf(pmax, run);
+        e[t] = __builtin_amdgcn_exp2f(run - mref);
+        lsum += e[t];
+      }
+      float suf = 0.f;
+#pragma unroll
+      for (int t = R - 1; t >= 0; --t) {
+        suf += e[t];
+        w_lds[wave][myh][row0 + t] = suf;
+      }
+    }
+  };
+
+  // raw tail (fused calls): split 0 computes its partial before the passes
+  const bool fold_tail = p.fused && split == 0 && n_raw > 0;
+  if (fold_tail)
+    raw_tail_partial<D, true>(p, b, hkv, g0, G, (int)n_raw, tid, scratch, part_lds, tail_ml[0],
+                              tail_ml[1]);
+  __syncthreads();
+
+  int64_t cur = wslot;
+  if (cur < npass) load_k(cur);
+  while (cur < npass) {
+    const int prow = (int)min<int64_t>(kPngTile, rows_total - cur * kPngTile);  // whole blocks
+    load_v(cur);
+    const unsigned int nxt_v = grab();
+
+    // ------------------------------------------------------------ scores
+    float4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < FPL; ++c) sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[c], qv[c], sacc, 0, 0, 0);
+    if (lc < G) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_lds[wave][lc][4 * lq + i] = sacc[i] * p.scale_log2;
+    }
+    const int64_t nxt = pass_of(nxt_v);
+    if (nxt < npass) load_k(nxt);  // the next pass's rows fly during softmax and values
+    wave_lds_sync();
+
+    // ------------------------------------------------------------ softmax
+    float pmax, lsum;
+    weights(prow, m_run, pmax, lsum);
+    if (__builtin_amdgcn_ballot_w64(pmax > m_run + kLazyMax) != 0) {
+      // move the reference maxima to the pass's logits, recompute the weights
+#pragma unroll
+      for (int m = GP; m < 64; m <<= 1) pmax = fmaxf(pmax, __shfl_xor(pmax, m, 64));
+      const float m_new = fmaxf(m_run, pmax);
+      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      float pdummy;
+      weights(prow, m_new, pdummy, lsum);
+      l_lane = l_lane * alpha + lsum;
+      // lane (q, c) register i holds head 4q + i
+      float al[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lq + i, 64);
+#pragma unroll
+      for (int f = 0; f < FPC; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[f][i] *= al[i];
+      m_run = m_new;
+    } else {
+      l_lane += lsum;
+    }
+    // rows past the pass end carry zero weight (their rows read as zero)
+    if (prow < kPngTile)
+      for (int i = prow + lane; i < kPngTile; i += 64)
+        for (int h = 0; h < G; ++h) w_lds[wave][h][i] = 0.f;
+    wave_lds_sync();
+
+    // ------------------------------------------------------------ values
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const float a = lc < G ? w_lds[wave][lc][4 * rg + lq] : 0.f;
+#pragma unroll
+      for (int f = 0; f < FPC; ++f)
+        acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vr[rg][f], acc[f], 0, 0, 0);
+    }
+    wave_lds_sync();
+    cur = nxt;
+  }
+
+  // ---- combine the wavefronts: (max, sum, 1) per head and the accumulators
+  // (lane (q, c) register i of acc[f]: head 4q + i, feature D/16 * c + f)
+#pragma unroll
+  for (int m = GP; m < 64; m <<= 1) l_lane += __shfl_xor(l_lane, m, 64);
+  if (lane < GP) {
+    comb[wave][lane][0] = m_run;
+    comb[wave][lane][1] = l_lane;
+    comb[wave][lane][2] = 1.f;
+  }
+  constexpr int NI = GP < 4 ? GP : 4;
+  if (lq < (GP >= 4 ? GP / 4 : 1)) {
+#pragma unroll
+    for (int f = 0; f < FPC; ++f)
+#pragma unroll
+      for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][FPC * lc + f] = acc[f][i];
+  }
+  split_epilogue<D, GP, true>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf, part_lds,
+                              tail_ml, wg_ml, scratch, s_last, passq, [] {});
+}
+
+}  // namespace
+
+// Query / stream dtypes, head size and block size of the png matrix-core pass.
+bool png_mfma_shape_supported(int q_dtype, int stream_dtype, int64_t D, int r) {
+  return q_dtype == FC_F32 && stream_dtype == FC_F32 && (D == 64 || D == 128) &&
+         (r == 4 || r == 8 || r == 16);
+}
+
+// Whether the png matrix-core pass handles this call: its shapes, and 16-byte
+// aligned query rows and stores (16-byte row loads).
+bool split_png_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
+                              int r, int stream_dtype, const fc_stream_view* key,
+                              const fc_stream_view* value) {
+  const auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  return png_mfma_shape_supported(q_dtype, stream_dtype, D, r) && al16(q) && q_sb % 4 == 0 &&
+         q_sh % 4 == 0 && al16(key->rows) && al16(value->rows) && al16(key->anchors) &&
+         al16(value->anchors);
+}
+
+int launch_split_png_mfma(const void* q, int64_t q_sb, int64_t q_sh, int64_t B, int64_t Hq,
+                          int64_t Hkv, int64_t D, int r, int64_t nb, const fc_stream_view* key,
+                          const fc_stream_view* value, float scale_log2, float* pm, float* pl,
+                          float* pacc, int n_splits, unsigned int* counters,
+                          int64_t counter_words, int64_t stride, unsigned int* status,
+                          const MfmaFuse* fuse, const int64_t* state, hipStream_t st) {
+  MfmaArgs a{};
+  a.q = q;
+  a.q_dtype = FC_F32;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.kanch = key->anchors;
+  a.vanch = value->anchors;
+  a.kdel = static_cast<const float*>(key->rows);
+  a.vdel = static_cast<const float*>(value->rows);
+  a.kcap = key->cap;
+  a.vcap = value->cap;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.nb = nb;
+  a.r = r;
+  a.scale_log2 = scale_log2;
+  a.n_splits = n_splits;
+  a.pm = pm;
+  a.pl = pl;
+  a.pacc = pacc;
+  a.state = state;
+  if (fuse) {
+    if (n_splits > kFuseMaxSplits) return FC_ERR_ARG;
+    a.fused = 1;
+    a.kraw = key->raw;
+    a.vraw = value->raw;
+    a.raw_dtype = FC_F32;
+    a.kr_sb = key->raw_sb;
+    a.kr_sh = key->raw_sh;
+    a.kr_st = key->raw_st;
+    a.vr_sb = value->raw_sb;
+    a.vr_sh = value->raw_sh;
+    a.vr_st = value->raw_st;
+    a.n_raw = fuse->n_raw;
+    a.out = fuse->out;
+    a.o_sb = fuse->o_sb;
+    a.o_sh = fuse->o_sh;
+  }
+  const int64_t G = Hq / Hkv;
+  const int gg = (int)std::min<int64_t>(G, 16);
+  const int gp = gg <= 1 ? 1 : gg <= 2 ? 2 : gg <= 4 ? 4 : gg <= 8 ? 8 : 16;
+  a.zg = (int)((G + 15) / 16);
+  a.ngroups = B * Hkv * a.zg;
+  if (!counters || 2 * a.ngroups * stride > counter_words) return FC_ERR_ARG;
+  a.arrive = counters;
+  a.passq = counters + counter_words / 2;
+  a.status = status;
+  a.spin_cap = merge_wait_limit();
+  a.static_passes = static_pass_order() ? 1 : 0;
+  a.cstride = stride;
+  const dim3 grid((unsigned)(a.ngroups * n_splits));
+  const int rc = mfma_with_int<4, 8, 16>(r, [&](auto rc_) {
+    constexpr int Rv = decltype(rc_)::value;
+    return mfma_with_int<64, 128>((int)D, [&](auto dc) {
+      constexpr int Dv = decltype(dc)::value;
+      return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
+        attn_split_png_mfma<Rv, Dv, decltype(gc)::value><<<grid, kMThreads, 0, st>>>(a);
+        return FC_OK;
+      });
+    });
+  });
+  if (rc != FC_OK) return rc;
+  return check_launch();
+}
+
+}  // namespace fc

@@ -29,6 +29,15 @@ struct dtype_code<bf16_t> {
   static constexpr int value = FC_BF16;
 };
 
+// Workgroup barrier ordering LDS accesses only: global loads in flight
+// stay in flight, where __syncthreads() first waits for every outstanding
+// load (and store).  For barriers that only hand LDS data between threads.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
 __device__ __forceinline__ float to_f32(bf16_t x) {

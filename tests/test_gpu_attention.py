@@ -108,6 +108,11 @@ CASES = [
     ("jpeg-i8-bf16-d96-g2", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8), "bf16", 2, 2, 2, 8 * 120 + 5, 96),
     ("jpeg-i8-k3-f16-d96-g8", dict(mode="jpeg", block_size=8, keep_freqs=3, quant_bits=8), "f16", 1, 1, 8, 8 * 90, 96),
     ("jpeg-i8-k8-bf16-d80-g16", dict(mode="jpeg", block_size=8, keep_freqs=8, quant_bits=8), "bf16", 1, 2, 16, 8 * 40 + 7, 80),
+    ("png-f32-r16-d128-g4", dict(mode="png", block_size=16, keep_ratio=0.25), "f32", 2, 2, 4, 16 * 100 + 9, 128),
+    ("png-f32-r8-d64-g8", dict(mode="png", block_size=8, keep_ratio=1.0), "f32", 1, 2, 8, 8 * 150 + 3, 64),
+    ("png-f32-r4-d128-g1", dict(mode="png", block_size=4, keep_ratio=1.0), "f32", 2, 2, 1, 4 * 200 + 1, 128),
+    ("png-f32-r16-d64-g16", dict(mode="png", block_size=16, keep_ratio=0.5), "f32", 1, 1, 16, 16 * 40, 64),
+    ("png-f32-r8-d128-g5", dict(mode="png", block_size=8, keep_ratio=1.0), "f32", 1, 2, 5, 8 * 80 + 7, 128),
     ("jpeg-i8g-f16-g4", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=32), "f16", 2, 4, 4, 8 * 200 + 5, 128),
     ("jpeg-i8g-bf16-g2-d64", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8, quant_group=32), "bf16", 1, 2, 2, 8 * 90 + 3, 64),
     ("jpeg-i8g-f32-r16-d96", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8, quant_group=32), "f32", 1, 2, 3, 16 * 30 + 9, 96),

@@ -134,21 +134,24 @@ def test_impl_selectors_reference_style(oracle):
         assert_close(to_values(auto)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "bf16")
 
 
-def test_static_pass_order_is_bitwise_reproducible(oracle, attention_pass):
-    """FC_PASS_STATIC: the matrix-core pass with a fixed pass order gives
-    bitwise-equal outputs call after call, within tolerance of the oracle
-    and of the queue-driven default."""
-    B, Hkv, G, D, S = 2, 4, 4, 128, 8 * 2000 + 5
-    ks, vs = build_streams(I8_C3, "f16", B, Hkv, S, D, 808, oracle)
-    q = queries(B, Hkv * G, D, 809, "f16")
+@pytest.mark.parametrize("cfg,dt,r", [(I8_C3, "f16", 8),
+                                      (dict(mode="png", block_size=16, keep_ratio=1.0), "f32", 16)],
+                         ids=["i8", "png"])
+def test_static_pass_order_is_bitwise_reproducible(cfg, dt, r, oracle, attention_pass):
+    """FC_PASS_STATIC: the matrix-core passes (int8 jpeg, png) with a fixed
+    pass order give bitwise-equal outputs call after call, within tolerance
+    of the oracle and of the queue-driven default."""
+    B, Hkv, G, D, S = 2, 4, 4, 128, r * 2000 + 5
+    ks, vs = build_streams(cfg, dt, B, Hkv, S, D, 808, oracle)
+    q = queries(B, Hkv * G, D, 809, dt)
     auto = fc.codec_decode_attention(q, ks, vs)
     attention_pass("static")
     outs = [fc.codec_decode_attention(q, ks, vs) for _ in range(5)]
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     ref = oracle_out(oracle, q, ks, vs, D ** -0.5)
-    assert_close(to_values(outs[0])[:, :, 0], ref, "f16")
-    assert_close(to_values(auto)[:, :, 0], ref, "f16")
+    assert_close(to_values(outs[0])[:, :, 0], ref, dt)
+    assert_close(to_values(auto)[:, :, 0], ref, dt)
 
 
 def test_merge_give_up_is_reported_and_recovers(oracle):
@@ -179,8 +182,10 @@ STEP_CFGS = [(I8_C3, "bf16", 2), (I8_C3, "f16", 4),
              (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 4),
              (dict(mode="png", block_size=8, keep_ratio=0.5), "f16", 2),
              (dict(I8_C3, quant_group=32), "bf16", 2),
-             (dict(I8_C3, keep_freqs=8), "f16", 4), (dict(I8_C3, keep_freqs=3), "bf16", 2)]
-STEP_IDS = ["i8-bf16", "i8-f16", "fp-f32", "png-f16", "i8g-bf16", "i8k8-f16", "i8k3-bf16"]
+             (dict(I8_C3, keep_freqs=8), "f16", 4), (dict(I8_C3, keep_freqs=3), "bf16", 2),
+             (dict(mode="png", block_size=16, keep_ratio=1.0), "f32", 4)]
+STEP_IDS = ["i8-bf16", "i8-f16", "fp-f32", "png-f16", "i8g-bf16", "i8k8-f16", "i8k3-bf16",
+            "png16-f32"]
 
 
 def _tokens(g, B, H, D, dt):
