@@ -23,8 +23,9 @@
 //
 // Workgroup = 4 wavefronts = one (batch, kv head, split, group of <= 16 query
 // heads).  The wavefronts of a group's workgroups take passes of the group's
-// stored rows from a queue (64 rows of 16-row tiles, 32 at D = 256; with 3
-// rows per block a pass is 63 / 30 rows, the last tile row reading zero):
+// stored rows, three quarters in a fixed order and the rest from a queue (64
+// rows of 16-row tiles, 32 at D = 256; with 3 rows per block a pass is 63 /
+// 30 rows, the last tile row reading zero):
 //   scores: per 16-row tile and 64-feature chunk k, lane (q, m) holds row m,
 //      features 64k + 16q .. +15 (one 64-byte run of each row per load; any
 //      relabelling of the feature axis shared by both operands is allowed);
@@ -659,9 +660,10 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
 
   for (int i = tid; i < r * SROWS; i += kMThreads) a_lds[i] = p.A[i];
 
-  // The group's rows are cut into passes of PR rows; every wavefront of the
-  // group's n_splits workgroups takes the next untaken pass from the group's
-  // queue until none is left, so faster wavefronts take more passes.
+  // The group's rows are cut into passes of PR rows.  Every wavefront of the
+  // group's n_splits workgroups takes its first passes in a fixed order and
+  // then the next untaken pass from the group's queue until none is left, so
+  // faster wavefronts take more passes.
   int64_t nb = p.nb, n_raw = p.n_raw;
   int64_t step_t = 0, step_nb = 0;  // fused step: tail length and blocks before the token
   bool step_write = false;
@@ -686,14 +688,18 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   const unsigned int wslot = (unsigned int)(split * kWaves + wave);
   const unsigned int wstride = (unsigned int)(p.n_splits * kWaves);
   unsigned int wtaken = 0;
-  // A wavefront's first pass is fixed (pass wslot: no queue round trip before
-  // the first loads); the queue hands out the others from wstride on, or, in
-  // the static order, wslot + k * wstride.
+  // Pass k < nfix of a wavefront is fixed, wslot + k * wstride: three
+  // quarters of the group's passes need no queue round trip (per-pass queue
+  // atomics measured 2.2 us slower at C3; the queued quarter still levels
+  // the wavefronts' finishing times).  The queue hands out the rest from
+  // nfix * wstride on; in the static order every pass is fixed.
+  const unsigned int nfix = (unsigned int)max<int64_t>(1, 3 * npass / (4 * (int64_t)wstride));
   auto grab = [&]() -> unsigned int {  // result in lane 0, read when needed
-    if (p.static_passes) return wslot + wstride * ++wtaken;
+    if (p.static_passes || wtaken + 1 < nfix) return wslot + wstride * ++wtaken;
     unsigned int v = 0;
     if (lane == 0)
-      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + wstride;
+      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
+          wstride * nfix;
     return v;
   };
   auto pass_of = [](unsigned int v) { return (int64_t)__builtin_amdgcn_readfirstlane((int)v); };
@@ -711,61 +717,17 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   const uint16_t* qrow =
       static_cast<const uint16_t*>(p.q) + b * p.q_sb + hq * p.q_sh + 16 * lq;
   const bool q_f16 = p.q_dtype == FC_F16;
-  float qf[DK][8];
-  float qmax = 0.f;
-  // dtype branch outside the loops; fp16 lanes are read through a half8 view
-  // (hipcc 7.2 reused dword 0's conversion for all dwords when each dword was
-  // bit-cast to half2 inside an unrolled loop)
+  // the query's loads go out first; it is converted after the first pass's
+  // K loads have been issued behind them
+  u32x4_t qraw[DK];
 #pragma unroll
   for (int kc = 0; kc < DK; ++kc) {
     // features past D (D = 80, 96) are not loaded and stay zero
     const int f0 = 64 * (kc / 2) + 16 * lq + 8 * (kc % 2);
-    u32x4_t raw = {0u, 0u, 0u, 0u};
+    qraw[kc] = (u32x4_t){0u, 0u, 0u, 0u};
     if (D % 64 == 0 || f0 < D)
-      raw = *reinterpret_cast<const u32x4_t*>(qrow + 64 * (kc / 2) + 8 * (kc % 2));
-    if (q_f16) {
-      const half8_t h = __builtin_bit_cast(half8_t, raw);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qf[kc][i] = (float)h[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        qf[kc][2 * i] = __uint_as_float(raw[i] << 16);
-        qf[kc][2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      qf[kc][i] = hq_ok ? qf[kc][i] : 0.f;
-      qmax = fmaxf(qmax, fabsf(qf[kc][i]));
-    }
+      qraw[kc] = *reinterpret_cast<const u32x4_t*>(qrow + 64 * (kc / 2) + 8 * (kc % 2));
   }
-  qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
-  qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
-  // 14-bit integer query per head (largest magnitude in [2^13, 2^14)), split
-  // q' = 256 * hi + lo into two int8 operands: scores are exact integers
-  // 256 * (K . hi) + (K . lo) from the int8 matrix cores
-  const int qe = pow2_exp_for(qmax, 14);
-  constexpr int NC = DC / 64;  // 64-feature chunks of the score product
-  i32x4_t qhi[NC], qlo[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      uint32_t hw = 0, lw = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = 16 * c + 4 * w + j;  // feature 64c + 16q + 4w + j
-        const int qi = (int)rintf(ldexpf(qf[e / 8][e % 8], -qe));
-        const int lo = (int)(int8_t)(qi & 0xff);
-        const int hi = (qi - lo) >> 8;
-        lw |= (uint32_t)(lo & 0xff) << (8 * j);
-        hw |= (uint32_t)(hi & 0xff) << (8 * j);
-      }
-      qhi[c][w] = (int)hw;
-      qlo[c][w] = (int)lw;
-    }
-  const float head_mul = ldexpf(p.scale_log2, qe);  // integer score -> base-2 logit / K scale
 
   float4_t acc[DV][8];
 #pragma unroll
@@ -867,6 +829,67 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
     }
   };
 
+  // The first pass's K loads go out right behind the query's: its prologue
+  // waits for the query only.  (Issuing the first V loads here as well
+  // measured slower: 16 KB per wavefront requested at once at the start.)
+  auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
+  int64_t cur = wslot;
+  if (cur < npass) load_k(cur * PR, rows_of(cur));
+
+  // ---- the query as the B operand: per head a power of two scales it to
+  // integers of at most 14 bits
+  float qf[DK][8];
+  float qmax = 0.f;
+  // dtype branch outside the loops; fp16 lanes are read through a half8 view
+  // (hipcc 7.2 reused dword 0's conversion for all dwords when each dword was
+  // bit-cast to half2 inside an unrolled loop)
+#pragma unroll
+  for (int kc = 0; kc < DK; ++kc) {
+    const u32x4_t raw = qraw[kc];
+    if (q_f16) {
+      const half8_t h = __builtin_bit_cast(half8_t, raw);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[kc][i] = (float)h[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qf[kc][2 * i] = __uint_as_float(raw[i] << 16);
+        qf[kc][2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      qf[kc][i] = hq_ok ? qf[kc][i] : 0.f;
+      qmax = fmaxf(qmax, fabsf(qf[kc][i]));
+    }
+  }
+  qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
+  qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+  // 14-bit integer query per head (largest magnitude in [2^13, 2^14)), split
+  // q' = 256 * hi + lo into two int8 operands: scores are exact integers
+  // 256 * (K . hi) + (K . lo) from the int8 matrix cores
+  const int qe = pow2_exp_for(qmax, 14);
+  constexpr int NC = DC / 64;  // 64-feature chunks of the score product
+  i32x4_t qhi[NC], qlo[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      uint32_t hw = 0, lw = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 16 * c + 4 * w + j;  // feature 64c + 16q + 4w + j
+        const int qi = (int)rintf(ldexpf(qf[e / 8][e % 8], -qe));
+        const int lo = (int)(int8_t)(qi & 0xff);
+        const int hi = (qi - lo) >> 8;
+        lw |= (uint32_t)(lo & 0xff) << (8 * j);
+        hw |= (uint32_t)(hi & 0xff) << (8 * j);
+      }
+      qhi[c][w] = (int)hw;
+      qlo[c][w] = (int)lw;
+    }
+  const float head_mul = ldexpf(p.scale_log2, qe);  // integer score -> base-2 logit / K scale
+
   // raw tail (fused calls): split 0 computes its partial before the passes
   // and folds it into its own, so the final merge reads partials only; in a
   // fused step that partial covers the rows the step adds
@@ -901,9 +924,6 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   }
 
   __syncthreads();  // a_lds; the tail's scratch (w_lds) is free again
-  auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
-  int64_t cur = wslot;
-  if (cur < npass) load_k(cur * PR, rows_of(cur));
   while (cur < npass) {
     const int64_t pr0 = cur * PR;
     const int prow = rows_of(cur);  // multiple of SROWS
