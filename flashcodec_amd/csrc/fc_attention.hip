@@ -1350,10 +1350,12 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
   float* pm = ws.pm;
   float* pl = ws.pl;
   float* pacc = ws.pacc;
+  // counters of the matrix-core passes: arrival and queue per head group
+  const int64_t mstride = counter_stride(2 * B * Hkv * ((G + 15) / 16));
 
   if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_JPEG_I8 &&
       split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) &&
-      2 * B * Hkv * ((G + 15) / 16) * kCounterStride <= kCounterWords && mfma_split_allowed()) {
+      mstride > 0 && mfma_split_allowed()) {
     if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
     // one launch per call when the merge is requested too: the split pass's
     // last workgroup per head group merges
@@ -1368,12 +1370,12 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     }
     const int rc = launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb, key,
                                         value, A, scale_log2, pm, pl, pacc, n_splits, counters,
-                                        kCounterWords, kCounterStride, ws.status,
+                                        kCounterWords, mstride, ws.status,
                                         fuse ? &fz : nullptr, st);
     if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_PNG &&
              split_png_mfma_supported(q, q_dtype, q_sb, q_sh, D, r, stream_dtype, key, value) &&
-             2 * B * Hkv * ((G + 15) / 16) * kCounterStride <= kCounterWords &&
+             mstride > 0 &&
              mfma_split_allowed()) {
     if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
     const bool fuse = (parts & kPartMerge) && split_i8_mfma_fusable(n_splits);
@@ -1387,7 +1389,7 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     }
     const int rc = launch_split_png_mfma(q, q_sb, q_sh, B, Hq, Hkv, D, r, nb, key, value,
                                          scale_log2, pm, pl, pacc, n_splits, counters,
-                                         kCounterWords, kCounterStride, ws.status,
+                                         kCounterWords, mstride, ws.status,
                                          fuse ? &fz : nullptr, nullptr, st);
     if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit)) {
@@ -1464,13 +1466,14 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
   float* pm = ws.pm;
   float* pl = ws.pl;
   float* pacc = ws.pacc;
+  const int64_t mstride = counter_stride(2 * B * Hkv * ((G + 15) / 16));
   hipStream_t st = (hipStream_t)stream;
   // the same pass fc_attention_splits sized: matrix cores for int8 jpeg
   // archives they support, else the vector-ALU pass; both with the merge
   // fused (no second launch depends on the counts)
   if (store_kind == FC_STORE_JPEG_I8 &&
       split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) &&
-      mfma_split_allowed() && 2 * B * Hkv * ((G + 15) / 16) * kCounterStride <= kCounterWords) {
+      mfma_split_allowed() && mstride > 0) {
     if (!split_i8_mfma_fusable(n_splits)) return FC_ERR_UNSUPPORTED;
     MfmaFuse fz{};
     fz.raw_dtype = stream_dtype;
@@ -1481,11 +1484,11 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     fz.state = state;
     return launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb_hint, key, value,
                                 A, scale * kLog2e, pm, pl, pacc, n_splits, counters,
-                                kCounterWords, kCounterStride, ws.status, &fz, st);
+                                kCounterWords, mstride, ws.status, &fz, st);
   }
   if (store_kind == FC_STORE_PNG &&
       split_png_mfma_supported(q, q_dtype, q_sb, q_sh, D, r, stream_dtype, key, value) &&
-      mfma_split_allowed() && 2 * B * Hkv * ((G + 15) / 16) * kCounterStride <= kCounterWords) {
+      mfma_split_allowed() && mstride > 0) {
     if (!split_i8_mfma_fusable(n_splits)) return FC_ERR_UNSUPPORTED;
     MfmaFuse fz{};
     fz.raw_dtype = stream_dtype;
@@ -1495,7 +1498,7 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     fz.o_sh = o_sh;
     return launch_split_png_mfma(q, q_sb, q_sh, B, Hq, Hkv, D, r, nb_hint, key, value,
                                  scale * kLog2e, pm, pl, pacc, n_splits, counters, kCounterWords,
-                                 kCounterStride, ws.status, &fz, state, st);
+                                 mstride, ws.status, &fz, state, st);
   }
   if (!valu_fusable(B, Hkv, G)) return FC_ERR_UNSUPPORTED;
   return launch_split_valu(q, q_dtype, q_sb, q_sh, B, Hkv, G, D, store_kind, stream_dtype, r, s,

@@ -45,6 +45,18 @@ constexpr int64_t kWsStatusWords = 64;              // status word + padding (tw
 constexpr int64_t kCounterWords = kWsCounterRegionWords - kWsStatusWords;
 constexpr int64_t kCounterBytes = kWsCounterRegionWords * 4;
 constexpr int64_t kCounterStride = 32;  // words between counters (no two share a line)
+constexpr int64_t kCounterStrideMax = 256;  // 1 KiB
+// Words between the counters of consecutive groups of the matrix-core
+// passes (`slots` counters: two per group): as far apart as the counter
+// region allows, up to 1 KiB, never closer than one 128-byte line.  Counters
+// packed into a few KiB put every group's atomics on a few memory channels
+// and slowed the streams through those channels (C3: 0.56 us per call).
+// 0 when the region cannot hold the counters.
+inline int64_t counter_stride(int64_t slots) {
+  int64_t st = kCounterStrideMax;
+  while (st > kCounterStride && slots * st > kCounterWords) st >>= 1;
+  return slots * st <= kCounterWords ? st : 0;
+}
 struct WsLayout {
   unsigned int* status;
   unsigned int* done;      // fused decode step: workgroups finished (zero between calls)

@@ -85,7 +85,8 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   }
   if (!split_i8_mfma_supported(a->q, a->q_dtype, a->q_sb, a->q_sh, D, a->s, &v[0], &v[1]))
     return FC_ERR_UNSUPPORTED;
-  if (2 * B * Hkv * ((G + 15) / 16) * kCounterStride > kCounterWords) return FC_ERR_UNSUPPORTED;
+  const int64_t mstride = counter_stride(2 * B * Hkv * ((G + 15) / 16));
+  if (mstride == 0) return FC_ERR_UNSUPPORTED;
   const int n_splits = fc_attention_splits(a->store_kind, a->stream_dtype, a->q_dtype, a->s, nb,
                                            B, Hkv, G, D, a->n_cu);
   if (n_splits < 1 || !step_i8_mfma_supported(a->stream_dtype, r, D, n_splits))
@@ -113,7 +114,7 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   fz.done = ws.done;
   return launch_split_i8_mfma(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, r, a->s, nb,
                               &v[0], &v[1], a->A, a->scale * 1.4426950408889634f, ws.pm, ws.pl,
-                              ws.pacc, n_splits, ws.counters, kCounterWords, kCounterStride,
+                              ws.pacc, n_splits, ws.counters, kCounterWords, mstride,
                               ws.status, &fz, (hipStream_t)a->stream);
 }
 
