@@ -391,7 +391,7 @@ __device__ __forceinline__ void step_partial(
 // stores), run by the workgroups that do not merge, so the merge's code is
 // in their compute units' instruction cache when a merging workgroup there
 // needs it.
-template <int D, bool QF32 = false>
+template <int D, bool QF32 = false, bool COMPACT = true>
 __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
                             int split, int tid, float* lds, const float* own_acc,
                             const float* own_m, const float* own_l, bool dry) {
@@ -465,6 +465,58 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
       plv[h * kFuseMaxSplits + sp] = own ? own_l[h] : lv;
     }
   };
+  if (COMPACT && G * C4 <= kMThreads && ns <= kPre) {
+    // one task per thread and at most kPre splits (the common case): the
+    // statistics and partials of the task's head come in with one batch of
+    // loads, no LDS staging and no barrier (0.33 us shorter than the general
+    // form below at C3); same summation order.  Not in the fused step's
+    // kernels, where its registers would spill.
+    const bool act = tid < G * C4;
+    const int h = act ? tid / C4 : 0, c = tid - h * C4;
+    float4_t pa[kPre];
+    float pmv[kPre], plv[kPre];
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      const int sp = j < ns ? j : 0;
+      pa[j] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rp, ((h * ns + sp) * C4 + c) * 16, 0, kCachePolicySc1));
+      pmv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, (h * ns + sp) * 4, 0,
+                                                                               kCachePolicySc1));
+      plv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, (h * ns + sp) * 4, 0,
+                                                                               kCachePolicySc1));
+    }
+    const float4_t own = *reinterpret_cast<const float4_t*>(own_acc + h * D + 4 * c);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      if (j == split) pmv[j] = own_m[h];
+      if (j == split) plv[j] = own_l[h];
+      if (j < ns) mx = fmaxf(mx, pmv[j]);
+    }
+    float l = 0.f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      const float w = (j >= ns || pmv[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pmv[j] - mx);
+      l = __builtin_fmaf(w, plv[j], l);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(w, j == split ? own[i] : pa[j][i], o[i]);
+    }
+    if (!act || dry) return;
+    const float iv = 1.0f / l;
+    const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
+    if constexpr (QF32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) static_cast<float*>(p.out)[ob + i] = o[i] * iv;
+    } else if (p.q_dtype == FC_F16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) static_cast<f16_t*>(p.out)[ob + i] = from_f32<f16_t>(o[i] * iv);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) static_cast<bf16_t*>(p.out)[ob + i] = from_f32<bf16_t>(o[i] * iv);
+    }
+    return;
+  }
   float4_t pre[kPre];
   if (G * C4 <= kMThreads) {
     // one task per thread: its first kPre partials fly with the statistics
@@ -502,7 +554,7 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
 //     merge every workgroup publishes and the merge runs as its own kernel.
 // step_done() runs when the workgroup is finished (the fused step's state
 // advance); `scratch` holds the merge's statistics (>= 2 * 16 * 64 floats).
-template <int D, int CB, bool QF32, typename Done>
+template <int D, int CB, bool QF32, bool COMPACT, typename Done>
 __device__ __forceinline__ void split_epilogue(
     const MfmaArgs& p, int64_t g, int64_t b, int64_t hkv, int64_t g0, int G, int split, int tid,
     bool fold_tail, float (&comb)[kWaves][16][3], float (&cbuf)[kWaves][CB][D], float* part_lds,
@@ -577,6 +629,7 @@ __device__ __forceinline__ void split_epilogue(
     __syncthreads();
     if (tid == 0) atomicAdd(arrive + kPubWord, 1u);
     step_done();
+    if constexpr (!COMPACT) return;  // the fused step's kernels: no dry merge (its registers spill)
   }
   if (last && tid == 0) {
     // Ordering: every partial word was written by an agent-scope atomic
@@ -606,7 +659,8 @@ __device__ __forceinline__ void split_epilogue(
   }
   __syncthreads();
   // one call site for both: the workgroups that do not merge run it dry
-  fused_merge<D, QF32>(p, b, hkv, g0, G, split, tid, scratch, part_lds, wg_ml[0], wg_ml[1], !last);
+  fused_merge<D, QF32, COMPACT>(p, b, hkv, g0, G, split, tid, scratch, part_lds, wg_ml[0], wg_ml[1],
+                               !last);
   if (last) step_done();
 }
 
@@ -692,19 +746,23 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   unsigned int* passq = p.passq + g * p.cstride;
   const unsigned int wslot = (unsigned int)(split * kWaves + wave);
   const unsigned int wstride = (unsigned int)(p.n_splits * kWaves);
-  unsigned int wtaken = 0;
   // Pass k < nfix of a wavefront is fixed, wslot + k * wstride: three
-  // quarters of the group's passes need no queue round trip (per-pass queue
-  // atomics measured 2.2 us slower at C3; the queued quarter still levels
-  // the wavefronts' finishing times).  The queue hands out the rest from
-  // nfix * wstride on; in the static order every pass is fixed.
+  // quarters of the group's passes need no queue round trip (each queue
+  // atomic costs HBM time: one per pass measured 2.2 us slower at C3; the
+  // queued quarter still levels the wavefronts' finishing times).  The queue
+  // hands out the rest from qbase = nfix * wstride on; in the static order
+  // every pass is fixed.  The fused step's kernels keep the queue for every
+  // pass after the first (the fixed order's registers spilled there).
   const unsigned int nfix = (unsigned int)max<int64_t>(1, 3 * npass / (4 * (int64_t)wstride));
+  const unsigned int qbase = STEP ? wstride : wstride * nfix;  // first queued pass
+  unsigned int next_fixed = wslot + wstride;
   auto grab = [&]() -> unsigned int {  // result in lane 0, read when needed
-    if (p.static_passes || wtaken + 1 < nfix) return wslot + wstride * ++wtaken;
+    const unsigned int f = next_fixed;
+    next_fixed += wstride;
+    if (p.static_passes || f < qbase) return f;
     unsigned int v = 0;
     if (lane == 0)
-      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
-          wstride * nfix;
+      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + qbase;
     return v;
   };
   auto pass_of = [](unsigned int v) { return (int64_t)__builtin_amdgcn_readfirstlane((int)v); };
@@ -839,9 +897,11 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   // The first pass's K loads go out right behind the query's: its prologue
   // waits for the query only.  (Issuing the first V loads here as well
   // measured slower: 16 KB per wavefront requested at once at the start.)
+  // A fused step issues them after its step partial, whose registers they
+  // would otherwise share.
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
   int64_t cur = wslot;
-  if (cur < npass) load_k(cur * PR, rows_of(cur));
+  if (!STEP && cur < npass) load_k(cur * PR, rows_of(cur));
 
   // ---- the query as the B operand: per head a power of two scales it to
   // integers of at most 14 bits
@@ -931,6 +991,7 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   }
 
   __syncthreads();  // a_lds; the tail's scratch (w_lds) is free again
+  if (STEP && cur < npass) load_k(cur * PR, rows_of(cur));
   while (cur < npass) {
     const int64_t pr0 = cur * PR;
     const int prow = rows_of(cur);  // multiple of SROWS
@@ -1095,7 +1156,8 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
       if (tid == 0) __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
-  split_epilogue<D, CB, false>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf, part_lds,
+  split_epilogue<D, CB, false, !STEP>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf,
+                                      part_lds,
                                tail_ml, wg_ml, &s_lds[0][0][0], s_last, passq, step_done);
 }
 

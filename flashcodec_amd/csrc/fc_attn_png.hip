@@ -259,7 +259,8 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
 #pragma unroll
       for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][FPC * lc + f] = acc[f][i];
   }
-  split_epilogue<D, GP, true>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf, part_lds,
+  split_epilogue<D, GP, true, false>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf,
+                                    part_lds,
                               tail_ml, wg_ml, scratch, s_last, passq, [] {});
 }
 
