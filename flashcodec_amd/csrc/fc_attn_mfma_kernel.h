@@ -536,6 +536,66 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
   }
 }
 
+
+// Merge of up to NMAX split partials with two outputs per thread (G * D / 2
+// <= the workgroup's threads): every statistic and partial of a thread's two
+// outputs is requested in one batch (no LDS staging, no barrier), for the
+// png pass's 32 splits per group.  Same summation order as fused_merge.
+template <int D, int NMAX, bool QF32>
+__device__ __forceinline__ void wide_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0,
+                                           int G, int split, int tid, const float* own_acc,
+                                           const float* own_m, const float* own_l) {
+  constexpr int C2 = D / 2;
+  const int ns = p.n_splits;
+  const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;
+  const bool act = tid < G * C2;
+  const int h = act ? tid / C2 : 0, c = tid - h * C2;
+  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, G * ns * D * 4);
+  const __amdgpu_buffer_rsrc_t rm = buf_rsrc(p.pm + bq0 * ns, G * ns * 4);
+  const __amdgpu_buffer_rsrc_t rl = buf_rsrc(p.pl + bq0 * ns, G * ns * 4);
+  u32x2_t pa[NMAX];
+  float pmv[NMAX], plv[NMAX];
+#pragma unroll
+  for (int j = 0; j < NMAX; ++j) {
+    const int sp = j < ns ? j : 0;
+    pa[j] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                            rp, ((h * ns + sp) * C2 + c) * 8, 0, kCachePolicySc1));
+    pmv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, (h * ns + sp) * 4, 0,
+                                                                             kCachePolicySc1));
+    plv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, (h * ns + sp) * 4, 0,
+                                                                             kCachePolicySc1));
+  }
+  const float o0 = own_acc[h * D + 2 * c], o1 = own_acc[h * D + 2 * c + 1];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NMAX; ++j) {
+    if (j == split) pmv[j] = own_m[h];
+    if (j == split) plv[j] = own_l[h];
+    if (j < ns) mx = fmaxf(mx, pmv[j]);
+  }
+  float l = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < NMAX; ++j) {
+    const float w = (j >= ns || pmv[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pmv[j] - mx);
+    l = __builtin_fmaf(w, plv[j], l);
+    a0 = __builtin_fmaf(w, j == split ? o0 : __uint_as_float(pa[j][0]), a0);
+    a1 = __builtin_fmaf(w, j == split ? o1 : __uint_as_float(pa[j][1]), a1);
+  }
+  if (!act) return;
+  const float iv = 1.0f / l;
+  const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 2 * c;
+  if constexpr (QF32) {
+    static_cast<float*>(p.out)[ob] = a0 * iv;
+    static_cast<float*>(p.out)[ob + 1] = a1 * iv;
+  } else if (p.q_dtype == FC_F16) {
+    static_cast<f16_t*>(p.out)[ob] = from_f32<f16_t>(a0 * iv);
+    static_cast<f16_t*>(p.out)[ob + 1] = from_f32<f16_t>(a1 * iv);
+  } else {
+    static_cast<bf16_t*>(p.out)[ob] = from_f32<bf16_t>(a0 * iv);
+    static_cast<bf16_t*>(p.out)[ob + 1] = from_f32<bf16_t>(a1 * iv);
+  }
+}
+
 // End of a split-pass workgroup of the matrix-core passes, once its
 // wavefronts have parked their (max, sum, accumulator scale) per head in
 // comb and their accumulators in cbuf (rows = heads):
@@ -554,7 +614,7 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
 //     merge every workgroup publishes and the merge runs as its own kernel.
 // step_done() runs when the workgroup is finished (the fused step's state
 // advance); `scratch` holds the merge's statistics (>= 2 * 16 * 64 floats).
-template <int D, int CB, bool QF32, bool COMPACT, typename Done>
+template <int D, int CB, bool QF32, bool COMPACT, typename Done, int WIDE = 0>
 __device__ __forceinline__ void split_epilogue(
     const MfmaArgs& p, int64_t g, int64_t b, int64_t hkv, int64_t g0, int G, int split, int tid,
     bool fold_tail, float (&comb)[kWaves][16][3], float (&cbuf)[kWaves][CB][D], float* part_lds,
@@ -658,6 +718,12 @@ __device__ __forceinline__ void split_epilogue(
     __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
+  if constexpr (WIDE > 0) {
+    if (G * (D / 2) <= kMThreads && p.n_splits <= WIDE) {
+      wide_merge<D, WIDE, QF32>(p, b, hkv, g0, G, split, tid, part_lds, wg_ml[0], wg_ml[1]);
+      return;
+    }
+  }
   // one call site for both: the workgroups that do not merge run it dry
   fused_merge<D, QF32, COMPACT>(p, b, hkv, g0, G, split, tid, scratch, part_lds, wg_ml[0], wg_ml[1],
                                !last);

@@ -11,15 +11,19 @@
 // and the token rows are never formed.
 //
 // Scores: v_mfma_f32_16x16x4_f32, 16 rows x 4 features by 4 features x 16
-// heads per instruction.  Lane (q, m) holds features D/4 * q + c of row m
-// (D/4 consecutive floats, read with 16-byte loads) and lane (q, c) the same
-// features of head c's query; instruction c takes feature D/4 * q + c from
-// every lane, so the D/4 instructions cover all features.  Output: lane
-// (q, c) gets the scores of rows 4q .. 4q+3 for head c.
+// heads per instruction.  Lane (q, m) holds features 16 j + 4 q + i (j < D/16,
+// i < 4) of row m and lane (q, c) the same features of head c's query;
+// instruction 4 j + i takes feature 16 j + 4 q + i from every lane, so the
+// D/4 instructions cover all features, and each 16-byte load instruction
+// reads 64 contiguous bytes of every row.  Output: lane (q, c) gets the
+// scores of rows 4q .. 4q+3 for head c.
 // Values: the same instruction with the weights (16 heads x 4 rows) by the
 // rows (4 rows x 16 features): lane (q, c) holds rows q, q+4, q+8, q+12 of the
-// pass, features D/16 * c .. D/16 * c + D/16 - 1 (instruction f of a row
-// group takes feature D/16 * c + f in column c).
+// pass, features 64 k + 4 c + i (k < D/64, i < 4; instruction f = 4 k + i of a
+// row group takes feature 64 k + 4 c + i in column c), so a load instruction
+// reads 256 contiguous bytes of a row.  (With D/4 consecutive features per
+// lane, a load instruction touched 16-byte pieces 128 bytes apart in every
+// row: C4 59.7 us per call over rotating sets, 52.5 us with this mapping.)
 // A pass is one 16-row tile (16 / r whole blocks); a wavefront requests the
 // next pass's rows after its score products and the pass's value rows at its
 // start, and takes passes from its group's queue as the int8 pass does.
@@ -77,14 +81,18 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   unsigned int* passq = p.passq + g * p.cstride;
   const unsigned int wslot = (unsigned int)(split * kWaves + wave);
   const unsigned int wstride = (unsigned int)(p.n_splits * kWaves);
-  unsigned int wtaken = 0;
-  // first pass fixed (wslot), the others from the queue (from wstride on) or
-  // in the static order wslot + k * wstride
+  // fixed order for three quarters of the passes, the rest from the queue,
+  // as the int8 pass (C4: 0.5 us shorter than a queue for every pass)
+  const unsigned int nfix = (unsigned int)max<int64_t>(1, 3 * npass / (4 * (int64_t)wstride));
+  const unsigned int qbase = wstride * nfix;
+  unsigned int next_fixed = wslot + wstride;
   auto grab = [&]() -> unsigned int {
-    if (p.static_passes) return wslot + wstride * ++wtaken;
+    const unsigned int f = next_fixed;
+    next_fixed += wstride;
+    if (p.static_passes || f < qbase) return f;
     unsigned int v = 0;
     if (lane == 0)
-      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + wstride;
+      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + qbase;
     return v;
   };
   auto pass_of = [](unsigned int v) { return (int64_t)__builtin_amdgcn_readfirstlane((int)v); };
@@ -104,13 +112,13 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   // ---- queries: lane (q, c) holds head c's features D/4 * q .. (fp32)
   const bool hq_ok = lc < G;
   const int64_t hq = hkv * p.G + g0 + (hq_ok ? lc : 0);
-  const float* qrow = static_cast<const float*>(p.q) + b * p.q_sb + hq * p.q_sh + FPL * lq;
+  const float* qrow = static_cast<const float*>(p.q) + b * p.q_sb + hq * p.q_sh + 4 * lq;
   float qv[FPL];
 #pragma unroll
-  for (int c = 0; c < FPL; c += 4) {
-    const float4_t v = *reinterpret_cast<const float4_t*>(qrow + c);
+  for (int j = 0; j < FPL / 4; ++j) {
+    const float4_t v = *reinterpret_cast<const float4_t*>(qrow + 16 * j);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qv[c + i] = hq_ok ? v[i] : 0.f;
+    for (int i = 0; i < 4; ++i) qv[4 * j + i] = hq_ok ? v[i] : 0.f;
   }
 
   float4_t acc[FPC];
@@ -123,12 +131,12 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   auto load_k = [&](int64_t pass) {
     const int64_t gr = pass * kPngTile + lc;
     const bool ok = gr < rows_total;
-    const float* src = row_ptr(kanch, kdel, ok ? gr : 0) + FPL * lq;
+    const float* src = row_ptr(kanch, kdel, ok ? gr : 0) + 4 * lq;
 #pragma unroll
-    for (int c = 0; c < FPL; c += 4) {
-      const float4_t v = *reinterpret_cast<const float4_t*>(src + c);
+    for (int j = 0; j < FPL / 4; ++j) {
+      const float4_t v = *reinterpret_cast<const float4_t*>(src + 16 * j);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[c + i] = ok ? v[i] : 0.f;
+      for (int i = 0; i < 4; ++i) kr[4 * j + i] = ok ? v[i] : 0.f;
     }
   };
   float vr[4][FPC];
@@ -137,12 +145,12 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     for (int rg = 0; rg < 4; ++rg) {
       const int64_t gr = pass * kPngTile + 4 * rg + lq;
       const bool ok = gr < rows_total;
-      const float* src = row_ptr(vanch, vdel, ok ? gr : 0) + FPC * lc;
+      const float* src = row_ptr(vanch, vdel, ok ? gr : 0) + 4 * lc;
 #pragma unroll
-      for (int c = 0; c < FPC; c += 4) {
-        const float4_t v = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(src + c));
+      for (int k = 0; k < FPC / 4; ++k) {
+        const float4_t v = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(src + 64 * k));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vr[rg][c + i] = ok ? v[i] : 0.f;
+        for (int i = 0; i < 4; ++i) vr[rg][4 * k + i] = ok ? v[i] : 0.f;
       }
     }
   };
@@ -257,11 +265,14 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
 #pragma unroll
     for (int f = 0; f < FPC; ++f)
 #pragma unroll
-      for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][FPC * lc + f] = acc[f][i];
+      for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][64 * (f / 4) + 4 * lc + (f % 4)] = acc[f][i];
   }
-  split_epilogue<D, GP, true, false>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf,
-                                    part_lds,
-                              tail_ml, wg_ml, scratch, s_last, passq, [] {});
+  // the merge of up to 32 splits reads every partial in one batch (C4: 32
+  // splits per group; 0.4 us shorter than batches of 8)
+  auto no_step = [] {};
+  split_epilogue<D, GP, true, false, decltype(no_step)&, 32>(
+      p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf, part_lds, tail_ml, wg_ml, scratch,
+      s_last, passq, no_step);
 }
 
 }  // namespace
