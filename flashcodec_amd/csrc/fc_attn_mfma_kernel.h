@@ -537,62 +537,84 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
 }
 
 
-// Merge of up to NMAX split partials with two outputs per thread (G * D / 2
-// <= the workgroup's threads): every statistic and partial of a thread's two
-// outputs is requested in one batch (no LDS staging, no barrier), for the
-// png pass's 32 splits per group.  Same summation order as fused_merge.
+// Merge of up to NMAX split partials (NMAX / 2 per thread) for one output
+// task of 4 features per pair of adjacent threads (G * D / 4 * 2 <= the
+// workgroup's threads): each thread requests its half of the splits'
+// partials and statistics in one batch (16-byte loads: at most NMAX / 2 + NMAX
+// / 4 loads in flight, within the wavefront's load counter), then the pair
+// exchanges its maximum and its sums through a lane shuffle (half 0 + half
+// 1, a fixed order).  For the png pass's 32 splits per group.
 template <int D, int NMAX, bool QF32>
 __device__ __forceinline__ void wide_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0,
                                            int G, int split, int tid, const float* own_acc,
                                            const float* own_m, const float* own_l) {
-  constexpr int C2 = D / 2;
+  constexpr int C4 = D / 4;
+  constexpr int NH = NMAX / 2;  // splits per thread
   const int ns = p.n_splits;
   const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;
-  const bool act = tid < G * C2;
-  const int h = act ? tid / C2 : 0, c = tid - h * C2;
+  const int task = tid >> 1, half = tid & 1;
+  const bool act = task < G * C4;
+  const int h = act ? task / C4 : 0, c = task - h * C4;
   const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, G * ns * D * 4);
   const __amdgpu_buffer_rsrc_t rm = buf_rsrc(p.pm + bq0 * ns, G * ns * 4);
   const __amdgpu_buffer_rsrc_t rl = buf_rsrc(p.pl + bq0 * ns, G * ns * 4);
-  u32x2_t pa[NMAX];
-  float pmv[NMAX], plv[NMAX];
+  const int s0 = half * NH;
+  float4_t pa[NH];
 #pragma unroll
-  for (int j = 0; j < NMAX; ++j) {
-    const int sp = j < ns ? j : 0;
-    pa[j] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-                                            rp, ((h * ns + sp) * C2 + c) * 8, 0, kCachePolicySc1));
-    pmv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, (h * ns + sp) * 4, 0,
-                                                                             kCachePolicySc1));
-    plv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, (h * ns + sp) * 4, 0,
-                                                                             kCachePolicySc1));
+  for (int j = 0; j < NH; ++j) {
+    const int sp = s0 + j < ns ? s0 + j : 0;
+    pa[j] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rp, ((h * ns + sp) * C4 + c) * 16, 0, kCachePolicySc1));
   }
-  const float o0 = own_acc[h * D + 2 * c], o1 = own_acc[h * D + 2 * c + 1];
+  // statistics of splits s0 .. s0 + NH - 1 of head h: contiguous (ns % 4 == 0)
+  float pmv[NH], plv[NH];
+#pragma unroll
+  for (int j = 0; j < NH; j += 4) {
+    const float4_t m4 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       rm, (h * ns + s0 + j) * 4, 0, kCachePolicySc1));
+    const float4_t l4 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       rl, (h * ns + s0 + j) * 4, 0, kCachePolicySc1));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pmv[j + i] = m4[i];
+      plv[j + i] = l4[i];
+    }
+  }
+  const float4_t own = *reinterpret_cast<const float4_t*>(own_acc + h * D + 4 * c);
   float mx = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < NMAX; ++j) {
-    if (j == split) pmv[j] = own_m[h];
-    if (j == split) plv[j] = own_l[h];
-    if (j < ns) mx = fmaxf(mx, pmv[j]);
+  for (int j = 0; j < NH; ++j) {
+    if (s0 + j == split) pmv[j] = own_m[h];
+    if (s0 + j == split) plv[j] = own_l[h];
+    if (s0 + j < ns) mx = fmaxf(mx, pmv[j]);
   }
-  float l = 0.f, a0 = 0.f, a1 = 0.f;
+  mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+  float l = 0.f;
+  float4_t o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < NMAX; ++j) {
-    const float w = (j >= ns || pmv[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pmv[j] - mx);
+  for (int j = 0; j < NH; ++j) {
+    const float w = (s0 + j >= ns || pmv[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pmv[j] - mx);
     l = __builtin_fmaf(w, plv[j], l);
-    a0 = __builtin_fmaf(w, j == split ? o0 : __uint_as_float(pa[j][0]), a0);
-    a1 = __builtin_fmaf(w, j == split ? o1 : __uint_as_float(pa[j][1]), a1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(w, s0 + j == split ? own[i] : pa[j][i], o[i]);
   }
-  if (!act) return;
-  const float iv = 1.0f / l;
-  const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 2 * c;
+  // half 0's sums plus half 1's
+  const float l1 = __shfl_xor(l, 1, 64);
+  float4_t o1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o1[i] = __shfl_xor(o[i], 1, 64);
+  if (!act || half != 0) return;
+  const float iv = 1.0f / (l + l1);
+  const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
   if constexpr (QF32) {
-    static_cast<float*>(p.out)[ob] = a0 * iv;
-    static_cast<float*>(p.out)[ob + 1] = a1 * iv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) static_cast<float*>(p.out)[ob + i] = (o[i] + o1[i]) * iv;
   } else if (p.q_dtype == FC_F16) {
-    static_cast<f16_t*>(p.out)[ob] = from_f32<f16_t>(a0 * iv);
-    static_cast<f16_t*>(p.out)[ob + 1] = from_f32<f16_t>(a1 * iv);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) static_cast<f16_t*>(p.out)[ob + i] = from_f32<f16_t>((o[i] + o1[i]) * iv);
   } else {
-    static_cast<bf16_t*>(p.out)[ob] = from_f32<bf16_t>(a0 * iv);
-    static_cast<bf16_t*>(p.out)[ob + 1] = from_f32<bf16_t>(a1 * iv);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) static_cast<bf16_t*>(p.out)[ob + i] = from_f32<bf16_t>((o[i] + o1[i]) * iv);
   }
 }
 
@@ -719,7 +741,7 @@ __device__ __forceinline__ void split_epilogue(
   }
   __syncthreads();
   if constexpr (WIDE > 0) {
-    if (G * (D / 2) <= kMThreads && p.n_splits <= WIDE) {
+    if (last && G * (D / 4) * 2 <= kMThreads && p.n_splits <= WIDE && p.n_splits % 4 == 0) {
       wide_merge<D, WIDE, QF32>(p, b, hkv, g0, G, split, tid, part_lds, wg_ml[0], wg_ml[1]);
       return;
     }
