@@ -6,16 +6,17 @@
 namespace fc {
 
 // Query dtypes, head sizes and stored rows per block the matrix-core split
-// pass is built for.
+// pass is built for (fp32 queries: not in the fused step's kernels).
 bool mfma_shape_supported(int q_dtype, int64_t D, int s) {
-  return (q_dtype == FC_F16 || q_dtype == FC_BF16) &&
+  return (q_dtype == FC_F16 || q_dtype == FC_BF16 || q_dtype == FC_F32) &&
          (D == 64 || D == 80 || D == 96 || D == 128 || D == 256) &&
          (s == 1 || s == 2 || s == 3 || s == 4 || s == 8);
 }
 
 // Whether the matrix-core split pass handles this configuration.
 // The pass reads 16 query bytes and 16 code bytes per load: the query rows
-// and both code stores must be 16-byte aligned.
+// and both code stores must be 16-byte aligned (query strides: multiples of
+// 8 elements).
 bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
                              int s, const fc_stream_view* key, const fc_stream_view* value) {
   const auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };

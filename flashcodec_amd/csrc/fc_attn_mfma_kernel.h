@@ -226,7 +226,7 @@ __device__ __forceinline__ void raw_tail_partial_t(const MfmaArgs& p, int64_t b,
   }
 }
 
-// QF32: fp32 queries (the png pass); else fp16 / bf16 (the int8 pass).
+// QF32: fp32 queries (the png pass, fp32 queries of the int8 pass); else fp16 / bf16.
 template <int D, bool QF32 = false>
 __device__ __forceinline__ void raw_tail_partial(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
                                  int nr, int tid, float* etl, float* acc, float* tm, float* tl) {
@@ -761,9 +761,17 @@ constexpr int mfma_width() {
   return (D + 63) / 64 * 64;
 }
 
-template <int SROWS, int D, int GP, bool STEP>
+// QF: fp32 queries (else fp16 / bf16): the query is split into four int8
+// digits (30 bits relative to its head's largest element: the fp32 value
+// itself but for elements 2^-7 below the largest), the stored rows' logits
+// and their taps are formed in fp64, and each output weight is kept in fp32
+// and split into two f16 halves (w = hi + lo / 2^12, 22 bits), so fp32
+// outputs keep fp32 accuracy; two more score products and one more value
+// product per tile.
+template <int SROWS, int D, int GP, bool STEP, bool QF = false>
 __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void attn_split_i8_mfma(
     MfmaArgs p) {
+  static_assert(!(STEP && QF), "the fused step takes fp16 / bf16 queries");
   constexpr int DC = mfma_width<D>();
   constexpr int DK = DC / 32;
   constexpr int DV = (DC + 127) / 128;  // 128-feature groups of the value product
@@ -777,7 +785,15 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   constexpr int KDW = 2 * DK;  // K dwords per lane per tile
   static_assert(DK % 2 == 0 && PRT <= kPassRowsW, "feature width");
   __shared__ float s_lds[kWaves][16][kSPad];
-  __shared__ _Float16 w_lds[kWaves][16][kWPad];
+  // weights of the pass: fp16 operands, or (QF) fp32 values split into two
+  // fp16 operands as they are read
+  union WeightLds {
+    _Float16 h[kWaves][16][kWPad];
+    float f[QF ? kWaves : 1][16][QF ? kSPad : 4];
+  };
+  __shared__ __attribute__((aligned(16))) WeightLds w_buf;
+  auto& w_lds = w_buf.h;
+  auto& w_lds_f = w_buf.f;
   __shared__ float sc_lds[kWaves][2][PRT];  // K and V row scales of the pass
   __shared__ float a_lds[FC_MAX_BLOCK * SROWS];
   __shared__ float comb[kWaves][16][3];
@@ -865,19 +881,28 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   const bool hq_ok = lc < G;
   const int64_t hq = hkv * p.G + g0 + (hq_ok ? lc : 0);
   // lane (q, c) holds features 64 k + 16 q + [0, 16) of chunk k
-  const uint16_t* qrow =
-      static_cast<const uint16_t*>(p.q) + b * p.q_sb + hq * p.q_sh + 16 * lq;
+  const int64_t qoff = b * p.q_sb + hq * p.q_sh + 16 * lq;
   const bool q_f16 = p.q_dtype == FC_F16;
   // the query's loads go out first; it is converted after the first pass's
-  // K loads have been issued behind them
-  u32x4_t qraw[DK];
+  // K loads have been issued behind them.  8 features per kc: one 16-byte
+  // load of fp16 / bf16, two of fp32.
+  constexpr int QW = QF ? 2 : 1;
+  u32x4_t qraw[DK][QW];
 #pragma unroll
   for (int kc = 0; kc < DK; ++kc) {
     // features past D (D = 80, 96) are not loaded and stay zero
     const int f0 = 64 * (kc / 2) + 16 * lq + 8 * (kc % 2);
-    qraw[kc] = (u32x4_t){0u, 0u, 0u, 0u};
-    if (D % 64 == 0 || f0 < D)
-      qraw[kc] = *reinterpret_cast<const u32x4_t*>(qrow + 64 * (kc / 2) + 8 * (kc % 2));
+    const int64_t e0 = qoff + 64 * (kc / 2) + 8 * (kc % 2);
+#pragma unroll
+    for (int u = 0; u < QW; ++u) {
+      qraw[kc][u] = (u32x4_t){0u, 0u, 0u, 0u};
+      if (D % 64 == 0 || f0 < D) {
+        if constexpr (QF)
+          qraw[kc][u] = *reinterpret_cast<const u32x4_t*>(static_cast<const float*>(p.q) + e0 + 4 * u);
+        else
+          qraw[kc][u] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p.q) + e0);
+      }
+    }
   }
 
   float4_t acc[DV][8];
@@ -951,25 +976,43 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
     const int npair = (prow / SROWS) * GP;
     for (int u = lane; u < npair; u += 64) {
       const int row0 = (u / GP) * SROWS;
-      float sv[SROWS], w[SROWS];
+      // QF: the stored rows' logits and their taps in fp64 (the logits of
+      // stored rows reach hundreds; fp32 roundings there are 1e-5 absolute)
+      using sv_t = std::conditional_t<QF, double, float>;
+      sv_t sv[SROWS];
+      float w[SROWS];
 #pragma unroll
       for (int j = 0; j < SROWS; ++j) {
-        sv[j] = s_lds[wave][myh][row0 + j] * sc_lds[wave][0][row0 + j];
+        if constexpr (QF)
+          sv[j] = (double)s_lds[wave][myh][row0 + j] *
+                  ((double)sc_lds[wave][0][row0 + j] * (double)p.scale_log2);
+        else
+          sv[j] = s_lds[wave][myh][row0 + j] * sc_lds[wave][0][row0 + j];
         w[j] = 0.f;
       }
       auto tap = [&](int t) {
-        float lg = 0.f;
+        float lg, d;
+        if constexpr (QF) {
+          double lgd = 0.0;
 #pragma unroll
-        for (int j = 0; j < SROWS; ++j) lg = __builtin_fmaf(a_lds[t * SROWS + j], sv[j], lg);
+          for (int j = 0; j < SROWS; ++j) lgd = __builtin_fma((double)a_lds[t * SROWS + j], sv[j], lgd);
+          lg = (float)lgd;
+          d = (float)(lgd - (double)mref);
+        } else {
+          lg = 0.f;
+#pragma unroll
+          for (int j = 0; j < SROWS; ++j) lg = __builtin_fmaf(a_lds[t * SROWS + j], sv[j], lg);
+          d = lg - mref;
+        }
         pmax = fmaxf(pmax, lg);
-        const float e = __builtin_amdgcn_exp2f(lg - mref);
+        const float e = __builtin_amdgcn_exp2f(d);
         lsum += e;
 #pragma unroll
         for (int j = 0; j < SROWS; ++j) w[j] = __builtin_fmaf(e, a_lds[t * SROWS + j], w[j]);
       };
-      // taps unrolled up to 4 stored rows (with 8 the unrolled taps' A
-      // coefficients no longer fit the registers)
-      if (SROWS <= 4 && r <= kTapsUnrolled) {
+      // taps unrolled up to 4 stored rows (with 8, or the fp64 taps of fp32
+      // queries, the unrolled taps' A coefficients no longer fit the registers)
+      if (!QF && SROWS <= 4 && r <= kTapsUnrolled) {
 #pragma unroll
         for (int t = 0; t < kTapsUnrolled; ++t)
           if (t < r) tap(t);
@@ -978,7 +1021,13 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
       }
 #pragma unroll
       for (int j = 0; j < SROWS; ++j)
-        w_lds[wave][myh][row0 + j] = (_Float16)(w[j] * (sc_lds[wave][1][row0 + j] * wm));
+      {
+        const float wv = w[j] * (sc_lds[wave][1][row0 + j] * wm);
+        if constexpr (QF)
+          w_lds_f[wave][myh][row0 + j] = wv;
+        else
+          w_lds[wave][myh][row0 + j] = (_Float16)wv;
+      }
     }
   };
 
@@ -992,7 +1041,7 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   if (!STEP && cur < npass) load_k(cur * PR, rows_of(cur));
 
   // ---- the query as the B operand: per head a power of two scales it to
-  // integers of at most 14 bits
+  // integers of at most 14 bits (QF: 30 bits)
   float qf[DK][8];
   float qmax = 0.f;
   // dtype branch outside the loops; fp16 lanes are read through a half8 view
@@ -1000,8 +1049,11 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   // bit-cast to half2 inside an unrolled loop)
 #pragma unroll
   for (int kc = 0; kc < DK; ++kc) {
-    const u32x4_t raw = qraw[kc];
-    if (q_f16) {
+    const u32x4_t raw = qraw[kc][0];
+    if constexpr (QF) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[kc][i] = __uint_as_float(qraw[kc][i / 4][i % 4]);
+    } else if (q_f16) {
       const half8_t h = __builtin_bit_cast(half8_t, raw);
 #pragma unroll
       for (int i = 0; i < 8; ++i) qf[kc][i] = (float)h[i];
@@ -1023,25 +1075,32 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   // 14-bit integer query per head (largest magnitude in [2^13, 2^14)), split
   // q' = 256 * hi + lo into two int8 operands: scores are exact integers
   // 256 * (K . hi) + (K . lo) from the int8 matrix cores
-  const int qe = pow2_exp_for(qmax, 14);
+  // (QF: 30-bit integers, q' = sum_i 256^i d_i over four int8 digits d_i)
+  constexpr int ND = QF ? 4 : 2;  // digits
+  const int qe = pow2_exp_for(qmax, QF ? 30 : 14);
   constexpr int NC = DC / 64;  // 64-feature chunks of the score product
-  i32x4_t qhi[NC], qlo[NC];
+  i32x4_t qdig[ND][NC];        // qdig[0]: the lowest digit
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      uint32_t hw = 0, lw = 0;
+      uint32_t dw[ND];
+#pragma unroll
+      for (int i = 0; i < ND; ++i) dw[i] = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int e = 16 * c + 4 * w + j;  // feature 64c + 16q + 4w + j
-        const int qi = (int)rintf(ldexpf(qf[e / 8][e % 8], -qe));
-        const int lo = (int)(int8_t)(qi & 0xff);
-        const int hi = (qi - lo) >> 8;
-        lw |= (uint32_t)(lo & 0xff) << (8 * j);
-        hw |= (uint32_t)(hi & 0xff) << (8 * j);
+        int qi = (int)rintf(ldexpf(qf[e / 8][e % 8], -qe));
+#pragma unroll
+        for (int i = 0; i < ND - 1; ++i) {  // balanced digits: each in [-128, 127]
+          const int d = (int)(int8_t)(qi & 0xff);
+          dw[i] |= (uint32_t)(d & 0xff) << (8 * j);
+          qi = (qi - d) >> 8;
+        }
+        dw[ND - 1] |= (uint32_t)(qi & 0xff) << (8 * j);
       }
-      qhi[c][w] = (int)hw;
-      qlo[c][w] = (int)lw;
+#pragma unroll
+      for (int i = 0; i < ND; ++i) qdig[i][c][w] = (int)dw[i];
     }
   const float head_mul = ldexpf(p.scale_log2, qe);  // integer score -> base-2 logit / K scale
 
@@ -1073,7 +1132,7 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
         go(bf16_t{});
     }
   } else if (fold_tail) {
-    raw_tail_partial<D>(p, b, hkv, g0, G, (int)n_raw, tid,
+    raw_tail_partial<D, QF>(p, b, hkv, g0, G, (int)n_raw, tid,
                         reinterpret_cast<float*>(&w_lds[0][0][0]), part_lds, tail_ml[0],
                         tail_ml[1]);
   }
@@ -1091,19 +1150,31 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
     // ------------------------------------------------------------ scores
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      i32x4_t shi = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
+      i32x4_t sd[ND];
+#pragma unroll
+      for (int i = 0; i < ND; ++i) sd[i] = (i32x4_t){0, 0, 0, 0};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         // lane (q, m): row m, features 64c + 16q .. +15, straight from the load
         const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
                            (int)kr[t][4 * c + 3]};
-        shi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qhi[c], shi, 0, 0, 0);
-        slo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qlo[c], slo, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < ND; ++i)
+          sd[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qdig[i][c], sd[i], 0, 0, 0);
       }
       if (lc < G) {
         float4_t sv;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = (float)(shi[i] * 256 + slo[i]) * head_mul;
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (QF) {  // the digits' sums are exact; their weighted sum in fp32
+            float acc_s = (float)sd[ND - 1][i];
+#pragma unroll
+            for (int k = ND - 2; k >= 0; --k) acc_s = __builtin_fmaf(acc_s, 256.f, (float)sd[k][i]);
+            sv[i] = ldexpf(acc_s, qe);  // exact; the scales follow in fp64
+          } else {
+            sv[i] = (float)(sd[1][i] * 256 + sd[0][i]) * head_mul;
+          }
+        }
         *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = sv;
       }
     }
@@ -1158,15 +1229,36 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
     // rows past the pass end carry zero weight (their codes read as zero)
     if (prow < PRT)
       for (int i = prow + lane; i < PRT; i += 64)
-        for (int h = 0; h < G; ++h) w_lds[wave][h][i] = (_Float16)0.f;
+        for (int h = 0; h < G; ++h) {
+          if constexpr (QF)
+            w_lds_f[wave][h][i] = 0.f;
+          else
+            w_lds[wave][h][i] = (_Float16)0.f;
+        }
     wave_lds_sync();
 
     // ------------------------------------------------------------ values
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl) {
-      u32x4_t wa = *reinterpret_cast<const u32x4_t*>(&w_lds[wave][lc][32 * sl + 8 * lq]);
-      if (lc >= G) wa = (u32x4_t){0u, 0u, 0u, 0u};
-      const half8_t wop = __builtin_bit_cast(half8_t, wa);
+      half8_t wop, wop_lo = {};
+      if constexpr (QF) {
+        // w = hi + lo / 2^12: the low half scaled by 2^12 stays a normal
+        // f16 down to |w| ~ 2^-14 (its value operand carries the 2^-12)
+        float4_t f0 = *reinterpret_cast<const float4_t*>(&w_lds_f[wave][lc][32 * sl + 8 * lq]);
+        float4_t f1 = *reinterpret_cast<const float4_t*>(&w_lds_f[wave][lc][32 * sl + 8 * lq + 4]);
+        if (lc >= G) f0 = f1 = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float x = k < 4 ? f0[k] : f1[k - 4];
+          const _Float16 hi = (_Float16)x;
+          wop[k] = hi;
+          wop_lo[k] = (_Float16)((x - (float)hi) * kLoScale);
+        }
+      } else {
+        u32x4_t wa = *reinterpret_cast<const u32x4_t*>(&w_lds[wave][lc][32 * sl + 8 * lq]);
+        if (lc >= G) wa = (u32x4_t){0u, 0u, 0u, 0u};
+        wop = __builtin_bit_cast(half8_t, wa);
+      }
 #pragma unroll
       for (int dv = 0; dv < DV; ++dv) {
 #pragma unroll
@@ -1194,6 +1286,10 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
               ov[2 * pp + 1] = h2[1];
             }
             const int e = 4 * hh + ee;
+            if constexpr (QF) {  // codes times 2^-12: exact in f16
+              const half8_t ovl = ov * (_Float16)(1.0f / kLoScale);
+              acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop_lo, ovl, acc[dv][e], 0, 0, 0);
+            }
             acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, ov, acc[dv][e], 0, 0, 0);
           }
         }
@@ -1244,7 +1340,7 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
       if (tid == 0) __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
-  split_epilogue<D, CB, false, !STEP>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf,
+  split_epilogue<D, CB, QF, !STEP>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf,
                                       part_lds,
                                tail_ml, wg_ml, &s_lds[0][0][0], s_last, passq, step_done);
 }
@@ -1270,10 +1366,14 @@ int launch_mfma_rows(const MfmaArgs& a, int d, int gp, dim3 grid, hipStream_t st
     constexpr int Dv = decltype(dc)::value;
     return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
       constexpr int GPv = decltype(gc)::value;
-      if (a.step)
+      if (a.step) {
+        if (a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
         attn_split_i8_mfma<SR, Dv, GPv, true><<<grid, kMThreads, 0, st>>>(a);
-      else
+      } else if (a.q_dtype == FC_F32) {
+        attn_split_i8_mfma<SR, Dv, GPv, false, true><<<grid, kMThreads, 0, st>>>(a);
+      } else {
         attn_split_i8_mfma<SR, Dv, GPv, false><<<grid, kMThreads, 0, st>>>(a);
+      }
       return FC_OK;
     });
   });

@@ -17,6 +17,9 @@ constexpr int kPassRowsW = 64;         // max rows per wavefront pass
 constexpr int kSPad = kPassRowsW + 4;  // float stride of a score row in LDS
 constexpr int kWPad = kPassRowsW + 8;  // half stride of a weight row in LDS
 constexpr float kLazyMax = 8.f;        // exponentials may reach 2^8 before a rescale
+// fp32-weight split w = hi + lo / kLoScale into two f16 operands: |w| stays
+// below 2^13 (16 taps of 2^8 times a V headroom of 2), so |lo| <= 2 |w| fits
+constexpr float kLoScale = 4096.f;
 constexpr int kTapsUnrolled = 16;      // softmax taps unrolled (block sizes up to 16)
 constexpr int kCachePolicyNt = 2;      // buffer load cache policy: nontemporal (streaming)
 

@@ -64,7 +64,8 @@ __global__ void state_advance_kernel(int64_t* state, int64_t r, int64_t cap) {
 // advances it.  FC_ERR_UNSUPPORTED when the step's shape does not allow it
 // (then the step takes the multi-launch path).
 static int step_single_launch(const fc_step_args* a, const int64_t* state) {
-  if (a->store_kind != FC_STORE_JPEG_I8 || a->quant_bits != 8 || !mfma_split_allowed())
+  if (a->store_kind != FC_STORE_JPEG_I8 || a->quant_bits != 8 || !mfma_split_allowed() ||
+      a->q_dtype == FC_F32)
     return FC_ERR_UNSUPPORTED;
   const int64_t B = a->B, Hq = a->Hq, Hkv = a->Hkv, D = a->D;
   const int r = a->r;

@@ -130,6 +130,15 @@ CASES += [
     ("i8-bf16-s2-r16", dict(mode="jpeg", block_size=16, keep_freqs=2, quant_bits=8), "bf16", 1, 2, 8, 16 * 70 + 9, 64),
     ("i8-f16-d256-g2", I8, "f16", 1, 2, 2, 8 * 128 + 7, 256),
     ("i8-f16-d64-g4", I8, "f16", 2, 4, 4, 8 * 123 + 4, 64),
+    # fp32 queries on the matrix-core pass (four query digits, fp64 logits,
+    # two weight halves): head groups, rows per block, widths, tails
+    ("i8-f32-c3", I8, "f32", 2, 4, 4, 8 * 400 + 5, 128),
+    ("i8-f32-d256-g2", I8, "f32", 1, 2, 2, 8 * 128 + 7, 256),
+    ("i8-f32-d64-g8", I8, "f32", 1, 2, 8, 8 * 200 + 3, 64),
+    ("i8-f32-s2-r16-g16", dict(mode="jpeg", block_size=16, keep_freqs=2, quant_bits=8), "f32", 1, 1, 16, 16 * 70 + 9, 64),
+    ("i8-f32-k8-g1", dict(mode="jpeg", block_size=8, keep_freqs=8, quant_bits=8), "f32", 2, 2, 1, 8 * 150, 128),
+    ("i8-f32-k3-d96-g3", dict(mode="jpeg", block_size=8, keep_freqs=3, quant_bits=8), "f32", 1, 2, 3, 8 * 99 + 2, 96),
+    ("i8-f32-s1-d80", dict(mode="jpeg", block_size=8, keep_freqs=1, quant_bits=8), "f32", 1, 3, 2, 8 * 180 + 7, 80),
 ]
 
 P16 = dict(mode="png", block_size=16, keep_ratio=0.25)

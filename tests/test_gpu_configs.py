@@ -90,12 +90,13 @@ def test_c4_png_full_shape(keep, oracle):
 
 
 @pytest.mark.parametrize("dt,G,D", [("f16", 4, 128), ("bf16", 2, 128), ("f16", 8, 64),
-                                    ("bf16", 4, 256)])
+                                    ("bf16", 4, 256), ("f32", 4, 128), ("f32", 2, 256)])
 def test_outlier_queries_on_matrix_cores(dt, G, D, oracle):
     """Queries with a few features 100x (and one head with a 1000x
     feature), the shape of real LLM queries: the matrix-core pass rounds each
     head's query to 14-bit integers relative to its largest element, which
-    such heads stress most."""
+    such heads stress most (fp32 queries: 30-bit integers, within the fp32
+    contract's 1e-5)."""
     B, Hkv, S = 2, 2, 8 * 700 + 3
     print(f"case outlier queries {dt} G={G} D={D}", flush=True)
     ks, vs = build_streams(I8_C3, dt, B, Hkv, S, D, 606 + G + D, oracle)
