@@ -130,10 +130,31 @@ def cpu_rate(fn, nbytes, min_seconds=1.0):
             return round(nbytes * n / dt / 1e9, 3)
 
 
+SETTLE_S = 0.25  # untimed calls before the warm-up steps of each measurement
+
+
+def settle(fn, seconds=SETTLE_S):
+    """Calls fn(i), i = 0, 1, ..., untimed for at least `seconds` of device
+    time.  The MI355X runs a new load below its steady rate for its first
+    milliseconds: C3 calls measured 52.2 us each after 40 warm-up calls
+    straight after setup and 49.9 us after 2000, the kernel alone 49.8 us
+    in both runs.  Returns the number of calls."""
+    import torch
+    n = 0
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(32):
+            fn(n)
+            n += 1
+        torch.cuda.synchronize()
+    return n
+
+
 def timed(fn, steps, warmup):
     """Average ms of fn() over `steps` calls between events on the current
-    stream, after `warmup` calls."""
+    stream, after `warmup` calls (and the untimed settle() period)."""
     import torch
+    settle(lambda i: fn())
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -147,8 +168,10 @@ def timed(fn, steps, warmup):
 
 
 def timed_cycle(fn, steps, warmup):
-    """ms per call of fn(i), i = 0, 1, ..., between two events."""
+    """ms per call of fn(i), i = 0, 1, ..., between two events (after
+    settle() and `warmup` calls)."""
     import torch
+    settle(fn)
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -791,7 +814,9 @@ def c3_mode(args):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps
 
-    log(f"bench: warmup {args.warmup}, steps {args.steps}, splits {n_splits}, sets {n_sets}")
+    n_settle = settle(call)
+    log(f"bench: settle {n_settle} calls, warmup {args.warmup}, steps {args.steps}, "
+        f"splits {n_splits}, sets {n_sets}")
     for i in range(args.warmup):
         call(i)
     torch.cuda.synchronize()
@@ -830,6 +855,9 @@ def c3_mode(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"calls": n_settle, "min_seconds": SETTLE_S,
+                   "note": "untimed calls before the warm-up steps: the device runs a new "
+                           "load below its steady rate for its first milliseconds"},
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
