@@ -759,7 +759,7 @@ def c3_mode(args):
     import torch
     import flashcodec_amd as fc
     from flashcodec_amd import _native as N
-    from flashcodec_amd.attention import _device_A, _view, check_workspaces, launches_per_call
+    from flashcodec_amd.attention import _device_A, _view, launches_per_call
     from flashcodec_amd.cache import _CodecStream
 
     dev = torch.device("cuda:0")
@@ -844,7 +844,6 @@ def c3_mode(args):
     log(f"bench: one repeated set {single_ms * 1e3:.1f} us per launch, {single:.0f} GB/s")
 
     out = fc.codec_decode_attention(q, ks, vs)
-    check_workspaces(dev)                          # no merge gave up during the run
     err, per_seq = check_against_oracle(q, ks, vs, out)
     log(f"bench: max error vs the fp64 oracle over all {B} sequences {err:.2e}")
     lpc = launches_per_call(N.STORE_JPEG_I8, n_splits)

@@ -14,7 +14,7 @@ import torch
 from . import _build
 
 F32, F16, BF16, I8 = 0, 1, 2, 3
-OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_INCOMPLETE, ERR_SCRATCH = 0, -1, -2, -3, -4, -5
+OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_SCRATCH = 0, -1, -2, -3, -5
 NOALLOC_SCRATCH_BYTES = 16 << 20
 PASS_AUTO, PASS_VECTOR, PASS_STATIC = 0, 1, 2
 STORE_JPEG_I8, STORE_JPEG_FP, STORE_PNG, STORE_JPEG_I8G = 0, 1, 2, 3
@@ -89,7 +89,6 @@ SIGNATURES = {
     "fc_decode_attention_merge": _ATTN_SIG,
     "fc_png_topm_mask_host": (ctypes.c_uint64, [_vp, _int, _int]),
     "fc_decode_step": (_int, [ctypes.POINTER(StepArgs)]),
-    "fc_attention_workspace_status": (_int, [_vp, _vp]),
     "fc_prefill_attention": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                     _i64, _int, _int, _int, _i64, ctypes.POINTER(StreamView),
                                     ctypes.POINTER(StreamView), _i64, _vp, _fp, _vp, _i64, _i64,
@@ -99,7 +98,6 @@ SIGNATURES = {
     "fc_decode_attention_noalloc": (_int, _ATTN_SIG[1][:21] + [_int, _vp]),
     "fc_set_attention_pass": (_int, [_int]),
     "fc_get_attention_pass": (_int, []),
-    "fc_set_merge_wait_limit": (None, [_int]),
 }
 
 _LIB = None
@@ -131,11 +129,6 @@ class KernelError(RuntimeError):
     """A flashcodec_amd kernel entry point returned an error status."""
 
 
-class IncompleteMergeError(KernelError):
-    """A fused decode-attention merge gave up waiting for split partials:
-    outputs written since the workspace was last checked may be wrong."""
-
-
 def check(rc, what):
     if rc == OK:
         return
@@ -145,8 +138,6 @@ def check(rc, what):
         msg += f" (hipError {L.fc_last_hip_error()})"
     if rc == ERR_UNSUPPORTED:
         raise NotImplementedError(f"{what}: {msg}")
-    if rc == ERR_INCOMPLETE:
-        raise IncompleteMergeError(f"{what}: {msg}")
     raise KernelError(f"{what}: {msg}")
 
 

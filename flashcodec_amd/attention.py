@@ -44,18 +44,6 @@ def _device_A(codec, r, device):
     return A
 
 
-def check_workspaces(device=None):
-    """Raise IncompleteMergeError if a decode attention since the last check
-    merged without every split partial (its bounded wait for the other
-    workgroups gave up; the output of that call may be wrong).  Synchronizes
-    the device's streams that own a workspace; clears the status."""
-    for (index, stream), ws in list(_WORKSPACES.items()):
-        if device is not None and torch.device(device).index not in (None, index):
-            continue
-        N.check(N.lib().fc_attention_workspace_status(ws.data_ptr(), stream),
-                "decode attention")
-
-
 def workspace(device, nbytes):
     """Workspace of the decode attention for the current stream of `device`,
     at least `nbytes` long.  Zero-filled when created: its arrival counters

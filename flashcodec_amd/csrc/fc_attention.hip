@@ -40,19 +40,16 @@
 
 namespace fc {
 
-// Split pass selection and merge wait limit: read from the environment once,
-// when the library is loaded (FLASHCODEC_AMD_ATTN=valu forces the vector-ALU
-// split pass, for A/B measurements), never on the call path.
-constexpr int kDefaultMergeWait = 1 << 24;  // polls of a publication counter
+// Split pass selection: read from the environment once, when the library is
+// loaded (FLASHCODEC_AMD_ATTN=valu forces the vector-ALU split pass, for A/B
+// measurements), never on the call path.
 static int g_attention_pass = [] {
   const char* v = getenv("FLASHCODEC_AMD_ATTN");
   return (v && v[0] == 'v') ? FC_PASS_VECTOR : FC_PASS_AUTO;
 }();
-static int g_merge_wait = kDefaultMergeWait;
 
 bool mfma_split_allowed() { return g_attention_pass != FC_PASS_VECTOR; }
 bool static_pass_order() { return g_attention_pass == FC_PASS_STATIC; }
-int merge_wait_limit() { return g_merge_wait; }
 
 constexpr int kAttnThreads = 256;
 constexpr int kPassRows = 512;
@@ -1105,7 +1102,7 @@ static int64_t ws_partial_bytes(int64_t B, int64_t Hq, int64_t D, int n_splits) 
   return (bytes + 255) / 256 * 256;
 }
 
-// Workspace of one call: the status line, kCounterWords 32-bit counters of
+// Workspace of one call: the header line, kCounterWords 32-bit counters of
 // the split passes (a fixed region, so calls of any shape find their
 // counters at the same place), then pm | pl | pacc (fp32, sections 16-byte
 // aligned).  The counters must be zero before a workspace's first use;
@@ -1113,9 +1110,8 @@ static int64_t ws_partial_bytes(int64_t B, int64_t Hq, int64_t D, int n_splits) 
 WsLayout ws_layout(void* workspace, int64_t B, int64_t Hq, int n_splits) {
   WsLayout w;
   unsigned int* base = static_cast<unsigned int*>(workspace);
-  w.status = base;
-  w.done = base + 32;  // its own line
-  w.counters = base + kWsStatusWords;
+  w.done = base;
+  w.counters = base + kWsHeadWords;
   const int64_t ws_head = (B * Hq * (int64_t)n_splits + 3) / 4 * 4;
   w.pm = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   w.pl = w.pm + ws_head;
@@ -1370,7 +1366,7 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     }
     const int rc = launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb, key,
                                         value, A, scale_log2, pm, pl, pacc, n_splits, counters,
-                                        kCounterWords, mstride, ws.status,
+                                        kCounterWords, mstride,
                                         fuse ? &fz : nullptr, st);
     if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_PNG &&
@@ -1389,7 +1385,7 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     }
     const int rc = launch_split_png_mfma(q, q_sb, q_sh, B, Hq, Hkv, D, r, nb, key, value,
                                          scale_log2, pm, pl, pacc, n_splits, counters,
-                                         kCounterWords, mstride, ws.status,
+                                         kCounterWords, mstride,
                                          fuse ? &fz : nullptr, nullptr, st);
     if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit)) {
@@ -1484,7 +1480,7 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     fz.state = state;
     return launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb_hint, key, value,
                                 A, scale * kLog2e, pm, pl, pacc, n_splits, counters,
-                                kCounterWords, mstride, ws.status, &fz, st);
+                                kCounterWords, mstride, &fz, st);
   }
   if (store_kind == FC_STORE_PNG &&
       split_png_mfma_supported(q, q_dtype, q_sb, q_sh, D, r, stream_dtype, key, value) &&
@@ -1498,7 +1494,7 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     fz.o_sh = o_sh;
     return launch_split_png_mfma(q, q_sb, q_sh, B, Hq, Hkv, D, r, nb_hint, key, value,
                                  scale * kLog2e, pm, pl, pacc, n_splits, counters, kCounterWords,
-                                 mstride, ws.status, &fz, state, st);
+                                 mstride, &fz, state, st);
   }
   if (!valu_fusable(B, Hkv, G)) return FC_ERR_UNSUPPORTED;
   return launch_split_valu(q, q_dtype, q_sb, q_sh, B, Hkv, G, D, store_kind, stream_dtype, r, s,
@@ -1532,24 +1528,6 @@ int fc_decode_attention_merge(FC_ATTN_PARAMS) {
   return decode_attention_parts(FC_ATTN_ARGS, kPartMerge);
 }
 
-int fc_attention_workspace_status(void* workspace, void* stream) {
-  hipStream_t st = (hipStream_t)stream;
-  if (!workspace) {
-    int rc = FC_OK;
-    workspace = noalloc_scratch(st, &rc);  // the static scratch of this device
-    if (!workspace) return rc;
-  }
-  unsigned int word = 0;
-  int rc = hip_status(hipMemcpyAsync(&word, workspace, sizeof(word), hipMemcpyDeviceToHost, st));
-  if (rc == FC_OK) rc = hip_status(hipStreamSynchronize(st));
-  if (rc != FC_OK) return rc;
-  if (word == 0) return FC_OK;
-  const unsigned int zero = 0;
-  rc = hip_status(hipMemcpyAsync(workspace, &zero, sizeof(zero), hipMemcpyHostToDevice, st));
-  if (rc == FC_OK) rc = hip_status(hipStreamSynchronize(st));
-  return rc != FC_OK ? rc : FC_ERR_INCOMPLETE;
-}
-
 int fc_set_attention_pass(int pass) {
   if (pass != FC_PASS_AUTO && pass != FC_PASS_VECTOR && pass != FC_PASS_STATIC) return FC_ERR_ARG;
   g_attention_pass = pass;
@@ -1557,7 +1535,5 @@ int fc_set_attention_pass(int pass) {
 }
 
 int fc_get_attention_pass(void) { return g_attention_pass; }
-
-void fc_set_merge_wait_limit(int polls) { g_merge_wait = polls; }
 
 }  // extern "C"

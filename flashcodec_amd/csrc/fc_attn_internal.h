@@ -26,23 +26,18 @@ int check_launch();
 int hip_status(hipError_t e);  // FC_OK, or FC_ERR_HIP with the error recorded
 int esize_of(int dt);
 
-// Value of a workspace's status word after a fused merge merged without
-// every split partial (the bounded publication wait gave up).
-constexpr unsigned int FC_STATUS_MERGE_INCOMPLETE = 1;
-
 // Process-wide settings, read once when the library loads
 // (FLASHCODEC_AMD_ATTN=valu selects the vector-ALU split pass) and
-// changeable through fc_set_attention_pass / fc_set_merge_wait_limit.
+// changeable through fc_set_attention_pass.
 bool mfma_split_allowed();
 bool static_pass_order();  // matrix-core pass without its dynamic pass queue
-int merge_wait_limit();
 
-// Decode-attention workspace: a status line, the counter region (pass
-// queues, arrival and publication counts; zero between calls), then the
-// split partials pm | pl | pacc.
+// Decode-attention workspace: a header line (the fused step's count of
+// finished workgroups), the counter region (pass queues and arrival counts;
+// zero between calls), then the split partials pm | pl | pacc.
 constexpr int64_t kWsCounterRegionWords = 262144;  // 1 MiB
-constexpr int64_t kWsStatusWords = 64;              // status word + padding (two lines)
-constexpr int64_t kCounterWords = kWsCounterRegionWords - kWsStatusWords;
+constexpr int64_t kWsHeadWords = 64;                // done count + padding (two lines)
+constexpr int64_t kCounterWords = kWsCounterRegionWords - kWsHeadWords;
 constexpr int64_t kCounterBytes = kWsCounterRegionWords * 4;
 constexpr int64_t kCounterStride = 32;  // words between counters (no two share a line)
 constexpr int64_t kCounterStrideMax = 256;  // 1 KiB
@@ -58,7 +53,6 @@ inline int64_t counter_stride(int64_t slots) {
   return slots * st <= kCounterWords ? st : 0;
 }
 struct WsLayout {
-  unsigned int* status;
   unsigned int* done;      // fused decode step: workgroups finished (zero between calls)
   unsigned int* counters;  // kCounterWords words
   float* pm;
@@ -109,7 +103,7 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
                          unsigned int* counters, int64_t counter_words, int64_t stride,
-                         unsigned int* status, const MfmaFuse* fuse, hipStream_t st);
+                         const MfmaFuse* fuse, hipStream_t st);
 
 // The png matrix-core split pass (fc_attn_png.hip): fp32 queries and
 // anchors, D in {64, 128}, r in {4, 8, 16}; `state` as the fused decode
@@ -123,8 +117,8 @@ int launch_split_png_mfma(const void* q, int64_t q_sb, int64_t q_sh, int64_t B, 
                           int64_t Hkv, int64_t D, int r, int64_t nb, const fc_stream_view* key,
                           const fc_stream_view* value, float scale_log2, float* pm, float* pl,
                           float* pacc, int n_splits, unsigned int* counters,
-                          int64_t counter_words, int64_t stride, unsigned int* status,
-                          const MfmaFuse* fuse, const int64_t* state, hipStream_t st);
+                          int64_t counter_words, int64_t stride, const MfmaFuse* fuse,
+                          const int64_t* state, hipStream_t st);
 
 // fc_decode_attention's body: validates the arguments and enqueues the
 // requested parts (kPartSplit: the split pass over the archived blocks;
@@ -137,11 +131,6 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                            const fc_stream_view* value, int64_t n_raw, const float* A,
                            float scale, void* out, int64_t o_sb, int64_t o_sh, void* workspace,
                            int n_splits, void* stream, int parts);
-
-// Device address of the static scratch array of fc_decode_attention_noalloc
-// on the current device (looked up, and its counters cleared, on the first
-// call per device), or NULL with *rc set.
-void* noalloc_scratch(hipStream_t stream, int* rc);
 
 // Decode attention over a graph-capturable decode step (fc_decode_step with
 // a device state): one launch with the merge fused (matrix-core pass for

@@ -37,7 +37,7 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
                          unsigned int* counters, int64_t counter_words, int64_t stride,
-                         unsigned int* status, const MfmaFuse* fuse, hipStream_t st) {
+                         const MfmaFuse* fuse, hipStream_t st) {
   MfmaArgs a{};
   a.q = q;
   a.q_dtype = q_dtype;
@@ -103,8 +103,6 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   if (!counters || 2 * a.ngroups * stride > counter_words) return FC_ERR_ARG;
   a.arrive = counters;
   a.passq = counters + counter_words / 2;
-  a.status = status;
-  a.spin_cap = merge_wait_limit();
   a.static_passes = static_pass_order() ? 1 : 0;
   a.cstride = stride;
   const dim3 grid((unsigned)(a.ngroups * n_splits));

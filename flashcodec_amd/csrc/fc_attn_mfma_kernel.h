@@ -89,12 +89,6 @@ struct MfmaArgs {
   // decode-step state on the device (or NULL): (n_blocks, n_tail) before
   // the step's token; nb and n_raw are then taken from it (graph replays)
   const int64_t* state;
-  // status word of the workspace: set to FC_STATUS_MERGE_INCOMPLETE when a
-  // merging workgroup stops waiting for the other splits' publications
-  unsigned int* status;
-  // polls of the publication counter before the merge gives up (< 0: give
-  // up at once; a test knob that makes the give-up path run)
-  int spin_cap;
   // static pass order (no queue): wavefront w of the group's n_splits * 4
   // takes passes w, w + n_splits * 4, ...; fixed summation order, so the
   // output is bitwise reproducible
@@ -130,7 +124,6 @@ constexpr int kMThreads = 256;
 constexpr int kFuseMaxSplits = 64;  // split count limit of the fused merge
 
 constexpr int kWaves = kMThreads / 64;
-constexpr int kPubWord = 1;            // publication counter: word 1 of a group's arrival line
 
 
 // Element load / store with the dtype fixed at compile time (T = f16_t,
@@ -624,16 +617,21 @@ __device__ __forceinline__ void wide_merge(const MfmaArgs& p, int64_t b, int64_t
 //   * combine: thread x of the G * D outputs combines the four wavefronts
 //     (and, in split 0, the raw tail's partial from part_lds / tail_ml)
 //     into this workgroup's partial (part_lds, wg_ml);
-//   * arrival, then publication: a workgroup counts its arrival first; all
-//     but the last of the group's n_splits workgroups then publish their
-//     partial (device-scope stores) and, once the stores are complete, count
-//     the publication.  The last one keeps its own partial in LDS, waits for
-//     the other n_splits - 1 publications (they arrived before it and need
-//     nothing more to finish), returns the group's counters to zero for the
-//     next call and merges (fused_merge).  No cache-wide writeback /
-//     invalidate is used (each costs ~0.1 us and they serialize per XCD);
-//     partials are read back with device-scope loads.  Without the fused
-//     merge every workgroup publishes and the merge runs as its own kernel.
+//   * publication, then arrival: every workgroup publishes its partial
+//     (device-scope stores), waits until the stores are complete and then
+//     counts its arrival on the group's counter.  The one that counts last
+//     knows every other partial is complete: it returns the group's
+//     counters to zero for the next call and merges (fused_merge), using its
+//     own partial from LDS, with no wait.  Ordering: each partial word is
+//     written by an agent-scope store, performed at the device's coherence
+//     point (not held in the writer XCD's L2), and complete (vmcnt(0))
+//     before its writer counts itself; the merge reads partials with
+//     agent-scope loads issued after the count has returned, so no load is
+//     served by a stale line.  No cache-wide writeback / invalidate is used
+//     (each costs ~0.1 us and they serialize per XCD).  Counting first and
+//     publishing only from the workgroups that are not last took one more
+//     round trip at the end (C3 49.65 -> 49.27 us, C4 50.41 -> 50.05 us with
+//     this order).  Without the fused merge the merge runs as its own kernel.
 // step_done() runs when the workgroup is finished (the fused step's state
 // advance); `scratch` holds the merge's statistics (>= 2 * 16 * 64 floats).
 template <int D, int CB, bool QF32, bool COMPACT, typename Done, int WIDE = 0>
@@ -674,17 +672,13 @@ __device__ __forceinline__ void split_epilogue(
       }
     }
   }
-  // ---- arrival, then publication (thread x publishes the outputs it
-  // combined; the barrier after the arrival orders the combine before the
-  // last workgroup's merge)
+  // ---- publication, then arrival: every workgroup publishes its partial
+  // (with p.fused the last to arrive keeps its own in LDS, but does not know
+  // it is last yet), waits for its stores to complete and then counts
+  // itself; the workgroup that counts last finds every other partial
+  // complete and merges, with no wait
   unsigned int* arrive = p.arrive + g * p.cstride;
-  if (tid == 0) {
-    const unsigned int old = atomicAdd(arrive, 1u);
-    s_last = old + 1 == (unsigned int)p.n_splits ? 1 : 0;
-  }
-  __syncthreads();
-  const bool last = s_last != 0;
-  if (!last || !p.fused) {
+  {
     const int64_t bq0 = b * (p.Hkv * p.G) + hkv * p.G + g0;
     for (int x = tid; x < G * D; x += kMThreads) {
       const int h = x / D, d = x - h * D;
@@ -698,48 +692,33 @@ __device__ __forceinline__ void split_epilogue(
     }
   }
   if (!p.fused) {
-    if (last && tid == 0) {
-      __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+      const unsigned int old = atomicAdd(arrive, 1u);
+      if (old + 1 == (unsigned int)p.n_splits) {
+        __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     return;
   }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned int old = atomicAdd(arrive, 1u);
+    s_last = old + 1 == (unsigned int)p.n_splits ? 1 : 0;
+    if (s_last) {
+      __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  const bool last = s_last != 0;
   if (!last) {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    if (tid == 0) atomicAdd(arrive + kPubWord, 1u);
     step_done();
     if constexpr (!COMPACT) return;  // the fused step's kernels: no dry merge (its registers spill)
   }
-  if (last && tid == 0) {
-    // Ordering: every partial word was written by an agent-scope atomic
-    // store, which is performed at the device's coherence point (not held in
-    // the writer XCD's L2), and each publisher waited for its stores to
-    // complete (vmcnt(0)) before counting itself; the merge reads partials
-    // with agent-scope loads issued after it has seen the count, so no load
-    // can be served by a stale L2 line.  No cache-wide writeback or
-    // invalidate is needed (each costs ~0.1 us and they serialize per XCD).
-    const unsigned int want = (unsigned int)p.n_splits - 1u;
-    unsigned int seen = 0;
-    for (int it = 0; it < p.spin_cap; ++it) {
-      seen = __hip_atomic_load(arrive + kPubWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (seen >= want) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (seen < want)  // merged without every partial: the host reads this word
-      __hip_atomic_store(p.status, (unsigned int)FC_STATUS_MERGE_INCOMPLETE, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // publications still in flight after a give-up add to the word later:
-    // subtracting what was expected (not storing 0) leaves it at zero once
-    // every publisher has counted itself, i.e. before the next call starts
-    __hip_atomic_fetch_add(arrive + kPubWord, 0u - want, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(passq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
   if constexpr (WIDE > 0) {
     if (last && G * (D / 4) * 2 <= kMThreads && p.n_splits <= WIDE && p.n_splits % 4 == 0) {
       wide_merge<D, WIDE, QF32>(p, b, hkv, g0, G, split, tid, part_lds, wg_ml[0], wg_ml[1]);

@@ -299,8 +299,8 @@ int launch_split_png_mfma(const void* q, int64_t q_sb, int64_t q_sh, int64_t B, 
                           int64_t Hkv, int64_t D, int r, int64_t nb, const fc_stream_view* key,
                           const fc_stream_view* value, float scale_log2, float* pm, float* pl,
                           float* pacc, int n_splits, unsigned int* counters,
-                          int64_t counter_words, int64_t stride, unsigned int* status,
-                          const MfmaFuse* fuse, const int64_t* state, hipStream_t st) {
+                          int64_t counter_words, int64_t stride, const MfmaFuse* fuse,
+                          const int64_t* state, hipStream_t st) {
   MfmaArgs a{};
   a.q = q;
   a.q_dtype = FC_F32;
@@ -347,8 +347,6 @@ int launch_split_png_mfma(const void* q, int64_t q_sb, int64_t q_sh, int64_t B, 
   if (!counters || 2 * a.ngroups * stride > counter_words) return FC_ERR_ARG;
   a.arrive = counters;
   a.passq = counters + counter_words / 2;
-  a.status = status;
-  a.spin_cap = merge_wait_limit();
   a.static_passes = static_pass_order() ? 1 : 0;
   a.cstride = stride;
   const dim3 grid((unsigned)(a.ngroups * n_splits));

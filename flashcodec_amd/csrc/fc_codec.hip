@@ -796,9 +796,6 @@ const char* fc_status_string(int status) {
     case FC_ERR_SCRATCH:
       return "the call needs more scratch than fc_decode_attention_noalloc's static array "
              "holds (FC_NOALLOC_SCRATCH_BYTES)";
-    case FC_ERR_INCOMPLETE:
-      return "a decode-attention merge stopped waiting for split partials; outputs written "
-             "since the workspace was last checked may be wrong";
     default: return "unknown status";
   }
 }

@@ -11,8 +11,8 @@
 // current) and kept per device; kernels receive that pointer exactly as they
 // receive a caller's workspace.
 //
-// What must start at zero (the status word and the pass / arrival /
-// publication counters at the head of the array) is zero when the code
+// What must start at zero (the fused step's done count and the pass-queue /
+// arrival counters at the head of the array) is zero when the code
 // object is loaded, is cleared once more by a fill kernel at set-up, and is
 // returned to zero by every call.  Every call on a GPU shares that GPU's
 // array: calls that overlap on one GPU (other streams, other threads) race
@@ -33,7 +33,7 @@ static __device__ __align__(256) unsigned char scratch[FC_NOALLOC_SCRATCH_BYTES]
 static void* g_scratch_ptr[kMaxDevices] = {};
 static std::mutex g_scratch_mutex;
 
-// zero words [0, n) of the scratch (the status line and the counters)
+// zero words [0, n) of the scratch (the header line and the counters)
 __global__ void scratch_clear_kernel(unsigned int* words, int64_t n) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -42,7 +42,7 @@ __global__ void scratch_clear_kernel(unsigned int* words, int64_t n) {
 
 // Device address of the current device's scratch array (set up on the first
 // call on that device), or NULL with *rc set.
-void* noalloc_scratch(hipStream_t stream, int* rc) {
+static void* noalloc_scratch(hipStream_t stream, int* rc) {
   int dev = -1;
   *rc = hip_status(hipGetDevice(&dev));
   if (*rc != FC_OK) return nullptr;

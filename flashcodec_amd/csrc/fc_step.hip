@@ -116,7 +116,7 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   return launch_split_i8_mfma(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, r, a->s, nb,
                               &v[0], &v[1], a->A, a->scale * 1.4426950408889634f, ws.pm, ws.pl,
                               ws.pacc, n_splits, ws.counters, kCounterWords, mstride,
-                              ws.status, &fz, (hipStream_t)a->stream);
+                              &fz, (hipStream_t)a->stream);
 }
 
 // The step with its counters on the device (a->state): every launch reads

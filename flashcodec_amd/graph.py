@@ -90,9 +90,6 @@ def release(cache, check=True):
             if (nb, nt) != (ks.n_blocks, ks._n_raw):
                 raise RuntimeError(f"device counters ({nb}, {nt}) differ from the host's "
                                    f"({ks.n_blocks}, {ks._n_raw})")
-    if check:
-        from .attention import check_workspaces
-        check_workspaces()
 
 
 class GraphDecoder:

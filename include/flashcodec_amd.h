@@ -6,8 +6,7 @@
  * sizes, enqueues its kernels on the given HIP stream (`stream` is a
  * hipStream_t; NULL = the default stream) and returns an int status:
  * FC_OK (0) or one of the negative FC_ERR_* codes below.  Nothing here
- * allocates device memory or throws, and only fc_attention_workspace_status
- * (which reads a result back) synchronises a stream.
+ * allocates device memory, throws or synchronises a stream.
  *
  * Layout conventions (all element strides, innermost dimension D is
  * contiguous, i.e. stride 1):
@@ -43,8 +42,6 @@ enum {
   FC_ERR_ARG = -1,         /* invalid argument (shape, dtype, pointer)       */
   FC_ERR_UNSUPPORTED = -2, /* valid but outside this build's kernel limits   */
   FC_ERR_HIP = -3,         /* a HIP runtime call failed (see fc_last_hip_error) */
-  FC_ERR_INCOMPLETE = -4,  /* a fused decode-attention merge stopped waiting for
-                              split partials (fc_attention_workspace_status) */
   FC_ERR_SCRATCH = -5      /* the call needs more scratch than the static array of
                               fc_decode_attention_noalloc holds */
 };
@@ -312,20 +309,6 @@ int fc_gather_segments(void* dst, int64_t d_sb, int64_t d_sh, const void* src,
                        int64_t B_out, int64_t B_src, int64_t H, int64_t len,
                        void* stream);
 
-/*
- * Status of the decode attentions that used `workspace` since it was last
- * checked: FC_OK, or FC_ERR_INCOMPLETE when a fused merge (the last
- * workgroup of a head group) stopped waiting for the other splits'
- * partials after its bounded wait and merged without them, so an output
- * may be wrong.  Synchronizes `stream` (the one the calls were enqueued
- * on), reads the workspace's status word and clears it.  workspace == NULL
- * checks the static scratch of fc_decode_attention_noalloc on the current
- * device.  Not for use inside a graph capture.  No reference counterpart
- * (the reference's Triton path merges in a second kernel and has nothing
- * to wait for, flashcodec/triton_attention.py:214-221).
- */
-int fc_attention_workspace_status(void* workspace, void* stream);
-
 /* Bytes of the static scratch array of fc_decode_attention_noalloc (one per
  * GPU, held until the process ends). */
 #define FC_NOALLOC_SCRATCH_BYTES (16 << 20)
@@ -375,16 +358,6 @@ enum {
  */
 int fc_set_attention_pass(int pass);
 int fc_get_attention_pass(void);
-
-/*
- * Polls of a publication counter before a fused merge gives up (default
- * 2^24, several seconds; the other workgroups of the head group have
- * arrived and need nothing more to finish).  A value <= 0 makes the merge
- * give up at once: a test knob that runs the give-up path (status word,
- * counter reset) with every kernel still exiting normally.  Process-wide;
- * no reference counterpart.
- */
-void fc_set_merge_wait_limit(int polls);
 
 /*
  * Causal prefill attention on int8 jpeg archives without the reconstructed
