@@ -1149,8 +1149,10 @@ int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, in
   if (nb <= 0) return 0;
   const bool png_mfma =
       store_kind == FC_STORE_PNG && fc::png_mfma_shape_supported(q_dtype, stream_dtype, D, s);
-  const bool mfma = (png_mfma || (store_kind == FC_STORE_JPEG_I8 &&
-                                  fc::mfma_shape_supported(q_dtype, D, s))) &&
+  const bool mfma = (png_mfma ||
+                     (store_kind == FC_STORE_JPEG_I8 && fc::mfma_shape_supported(q_dtype, D, s)) ||
+                     (store_kind == FC_STORE_JPEG_I8G &&
+                      fc::mfma_group_shape_supported(q_dtype, D, s))) &&
                     fc::mfma_split_allowed();
   if (n_cu <= 0) n_cu = 256;
   if (mfma) {
@@ -1349,9 +1351,10 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
   // counters of the matrix-core passes: arrival and queue per head group
   const int64_t mstride = counter_stride(2 * B * Hkv * ((G + 15) / 16));
 
-  if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_JPEG_I8 &&
-      split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) &&
-      mstride > 0 && mfma_split_allowed()) {
+  const bool grouped = store_kind == FC_STORE_JPEG_I8G;
+  if (nb > 0 && (parts & kPartSplit) &&
+      i8_mfma_takes(store_kind, q, q_dtype, q_sb, q_sh, D, s, key, value) && mstride > 0 &&
+      mfma_split_allowed()) {
     if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
     // one launch per call when the merge is requested too: the split pass's
     // last workgroup per head group merges
@@ -1367,7 +1370,7 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     const int rc = launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb, key,
                                         value, A, scale_log2, pm, pl, pacc, n_splits, counters,
                                         kCounterWords, mstride,
-                                        fuse ? &fz : nullptr, st);
+                                        fuse ? &fz : nullptr, st, grouped);
     if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_PNG &&
              split_png_mfma_supported(q, q_dtype, q_sb, q_sh, D, r, stream_dtype, key, value) &&
@@ -1467,8 +1470,7 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
   // the same pass fc_attention_splits sized: matrix cores for int8 jpeg
   // archives they support, else the vector-ALU pass; both with the merge
   // fused (no second launch depends on the counts)
-  if (store_kind == FC_STORE_JPEG_I8 &&
-      split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value) &&
+  if (i8_mfma_takes(store_kind, q, q_dtype, q_sb, q_sh, D, s, key, value) &&
       mfma_split_allowed() && mstride > 0) {
     if (!split_i8_mfma_fusable(n_splits)) return FC_ERR_UNSUPPORTED;
     MfmaFuse fz{};
@@ -1480,7 +1482,8 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     fz.state = state;
     return launch_split_i8_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb_hint, key, value,
                                 A, scale * kLog2e, pm, pl, pacc, n_splits, counters,
-                                kCounterWords, mstride, &fz, st);
+                                kCounterWords, mstride, &fz, st,
+                                store_kind == FC_STORE_JPEG_I8G);
   }
   if (store_kind == FC_STORE_PNG &&
       split_png_mfma_supported(q, q_dtype, q_sb, q_sh, D, r, stream_dtype, key, value) &&

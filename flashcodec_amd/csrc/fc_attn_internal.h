@@ -95,6 +95,9 @@ bool mfma_shape_supported(int q_dtype, int64_t D, int s);
 bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
                              int s, const fc_stream_view* key, const fc_stream_view* value);
 bool split_i8_mfma_fusable(int n_splits);
+bool mfma_group_shape_supported(int q_dtype, int64_t D, int s);
+bool i8_mfma_takes(int store_kind, const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                   int64_t D, int s, const fc_stream_view* key, const fc_stream_view* value);
 // counters: counter_words zero words (zero again when the work is done): two
 // per (batch, kv head, group of <= 16 query heads), `stride` words apart.
 // fuse == nullptr: write the split partials only (pm, pl, pacc).
@@ -103,7 +106,7 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
                          unsigned int* counters, int64_t counter_words, int64_t stride,
-                         const MfmaFuse* fuse, hipStream_t st);
+                         const MfmaFuse* fuse, hipStream_t st, bool grouped = false);
 
 // The png matrix-core split pass (fc_attn_png.hip): fp32 queries and
 // anchors, D in {64, 128}, r in {4, 8, 16}; `state` as the fused decode

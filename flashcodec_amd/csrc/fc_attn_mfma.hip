@@ -26,6 +26,29 @@ bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q
 
 bool split_i8_mfma_fusable(int n_splits) { return n_splits <= kFuseMaxSplits; }
 
+// Per-32 scales (FC_STORE_JPEG_I8G) on the matrix-core pass: fp16 / bf16
+// queries, head sizes 64 / 128 / 256 (whole 64-feature chunks of groups).
+bool mfma_group_shape_supported(int q_dtype, int64_t D, int s) {
+  return (q_dtype == FC_F16 || q_dtype == FC_BF16) && (D == 64 || D == 128 || D == 256) &&
+         mfma_shape_supported(q_dtype, D, s);
+}
+
+// Whether the int8 matrix-core split pass takes this call's stores: int8
+// jpeg archives with one scale per row, or per-32 scales (16-byte aligned:
+// a row's scales are read in 8- / 16-byte pieces).
+bool i8_mfma_takes(int store_kind, const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                   int64_t D, int s, const fc_stream_view* key, const fc_stream_view* value) {
+  const auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  if (store_kind == FC_STORE_JPEG_I8G) {
+    if (!mfma_group_shape_supported(q_dtype, D, s) || !al16(key->scales) ||
+        !al16(value->scales))
+      return false;
+  } else if (store_kind != FC_STORE_JPEG_I8) {
+    return false;
+  }
+  return split_i8_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, key, value);
+}
+
 bool step_i8_mfma_supported(int stream_dtype, int r, int64_t D, int n_splits) {
   // the step's rows (2 r D floats) live in the score scratch before the passes
   return (stream_dtype == FC_F16 || stream_dtype == FC_BF16) && split_i8_mfma_fusable(n_splits) &&
@@ -37,8 +60,9 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
                          unsigned int* counters, int64_t counter_words, int64_t stride,
-                         const MfmaFuse* fuse, hipStream_t st) {
+                         const MfmaFuse* fuse, hipStream_t st, bool grouped) {
   MfmaArgs a{};
+  a.qgroup = grouped ? 1 : 0;
   a.q = q;
   a.q_dtype = q_dtype;
   a.q_sb = q_sb;

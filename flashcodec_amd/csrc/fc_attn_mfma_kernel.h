@@ -89,6 +89,8 @@ struct MfmaArgs {
   // decode-step state on the device (or NULL): (n_blocks, n_tail) before
   // the step's token; nb and n_raw are then taken from it (graph replays)
   const int64_t* state;
+  // per-32 scales (FC_STORE_JPEG_I8G): D / 32 fp32 scales per stored row
+  int qgroup;
   // static pass order (no queue): wavefront w of the group's n_splits * 4
   // takes passes w, w + n_splits * 4, ...; fixed summation order, so the
   // output is bitwise reproducible
@@ -747,10 +749,12 @@ constexpr int mfma_width() {
 // and split into two f16 halves (w = hi + lo / 2^12, 22 bits), so fp32
 // outputs keep fp32 accuracy; two more score products and one more value
 // product per tile.
-template <int SROWS, int D, int GP, bool STEP, bool QF = false>
+template <int SROWS, int D, int GP, bool STEP, bool QF = false, bool QG = false>
 __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void attn_split_i8_mfma(
     MfmaArgs p) {
   static_assert(!(STEP && QF), "the fused step takes fp16 / bf16 queries");
+  static_assert(!QG || (!STEP && !QF && D % 32 == 0 && D == mfma_width<D>()),
+                "per-32 scales: plain calls, fp16 / bf16 queries, D = 64 / 128 / 256");
   constexpr int DC = mfma_width<D>();
   constexpr int DK = DC / 32;
   constexpr int DV = (DC + 127) / 128;  // 128-feature groups of the value product
@@ -774,6 +778,11 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   auto& w_lds = w_buf.h;
   auto& w_lds_f = w_buf.f;
   __shared__ float sc_lds[kWaves][2][PRT];  // K and V row scales of the pass
+  // QG (one scale per 32 features): the pass's K group scales and the V
+  // group scales relative to their row's largest, by group then row
+  constexpr int NGR = QG ? D / 32 : 1;
+  __shared__ __attribute__((aligned(16))) float kg_lds[QG ? kWaves : 1][NGR][PRT];
+  __shared__ __attribute__((aligned(16))) _Float16 vg_lds[QG ? kWaves : 1][NGR][PRT];
   __shared__ float a_lds[FC_MAX_BLOCK * SROWS];
   __shared__ float comb[kWaves][16][3];
   // the wavefronts' accumulators, for the combine (and the fused step's
@@ -852,8 +861,8 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
 
   const int8_t* kbase = p.kcodes + bh * p.kcap * SROWS * D;
   const int8_t* vbase = p.vcodes + bh * p.vcap * SROWS * D;
-  const float* ksc = p.kscales + bh * p.kcap * SROWS;
-  const float* vsc = p.vscales + bh * p.vcap * SROWS;
+  const float* ksc = p.kscales + bh * p.kcap * SROWS * NGR;
+  const float* vsc = p.vscales + bh * p.vcap * SROWS * NGR;
 
   // ---- queries: B operand of the score product.  Lane (q, c): head c,
   // features q*D/4 + 8*kc + i of product kc, scaled per head by a power of two
@@ -907,11 +916,30 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
 
   uint32_t kr[NT][KDW];
   float ks_r, vs_r;
+  float kgr[NGR], vgr[NGR];  // QG: the group scales of row lane % PRT
+  const int sg_off = (lane % PRT) * NGR * 4;
   // Code rows are read once per call: streaming (nontemporal) loads for K and
   // V, so the archive does not displace what the end phase needs from the
   // caches (C3 over rotating archive sets: 50.6 -> 49.9 us; the row scales
   // stay on the default policy, streaming them measured slower)
   auto load_k = [&](int64_t pr0, int prow) {
+    if constexpr (QG) {
+      // group scales ahead of the codes: the score stage needs them first
+      const __amdgpu_buffer_rsrc_t rks = buf_rsrc(ksc + pr0 * NGR, prow * NGR * 4);
+      if constexpr (NGR == 2) {
+        const u32x2_t a = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rks, sg_off, 0, 0));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) kgr[i] = __uint_as_float(a[i]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < NGR / 4; ++u) {
+          const u32x4_t a = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rks, sg_off + 16 * u, 0, 0));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) kgr[4 * u + i] = __uint_as_float(a[i]);
+        }
+      }
+    }
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kbase + pr0 * D, prow * D);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -923,13 +951,31 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
 #pragma unroll
         for (int i = 0; i < 4; ++i) kr[t][4 * h + i] = v[i];
       }
-    ks_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         buf_rsrc(ksc + pr0, prow * 4), sc_off, 0, 0));
-    vs_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         buf_rsrc(vsc + pr0, prow * 4), sc_off, 0, 0));
+    if constexpr (!QG) {
+      ks_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           buf_rsrc(ksc + pr0, prow * 4), sc_off, 0, 0));
+      vs_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           buf_rsrc(vsc + pr0, prow * 4), sc_off, 0, 0));
+    }
   };
   uint32_t vr[NS][DV][16];
   auto load_v = [&](int64_t pr0, int prow) {
+    if constexpr (QG) {
+      const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(vsc + pr0 * NGR, prow * NGR * 4);
+      if constexpr (NGR == 2) {
+        const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rvs, sg_off, 0, 0));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) vgr[i] = __uint_as_float(v[i]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < NGR / 4; ++u) {
+          const u32x4_t v = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rvs, sg_off + 16 * u, 0, 0));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vgr[4 * u + i] = __uint_as_float(v[i]);
+        }
+      }
+    }
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vbase + pr0 * D, prow * D);
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl)
@@ -1127,8 +1173,43 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
     const unsigned int nxt_v = grab();
 
     // ------------------------------------------------------------ scores
+    if constexpr (QG) {
+      if (lane < PRT) {
+#pragma unroll
+        for (int i = 0; i < NGR; ++i) kg_lds[wave][i][lane] = kgr[i];
+      }
+      wave_lds_sync();
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
+      if constexpr (QG) {
+        // per 32-feature group: the score product with the query's features
+        // of the other group zeroed (lanes q < 2 hold group 2c of chunk c,
+        // q >= 2 group 2c + 1), scaled by the rows' group scales
+        float4_t accg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
+                             (int)kr[t][4 * c + 3]};
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const bool mine = (lq >> 1) == hf;
+            i32x4_t sd[ND];
+#pragma unroll
+            for (int i = 0; i < ND; ++i) {
+              const i32x4_t bq = mine ? qdig[i][c] : (i32x4_t){0, 0, 0, 0};
+              sd[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bq, (i32x4_t){0, 0, 0, 0}, 0, 0, 0);
+            }
+            const float4_t kgv =
+                *reinterpret_cast<const float4_t*>(&kg_lds[wave][2 * c + hf][16 * t + 4 * lq]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              accg[i] = __builtin_fmaf(kgv[i], (float)(sd[1][i] * 256 + sd[0][i]), accg[i]);
+          }
+        }
+        if (lc < G) *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = accg * head_mul;
+        continue;
+      }
       i32x4_t sd[ND];
 #pragma unroll
       for (int i = 0; i < ND; ++i) sd[i] = (i32x4_t){0, 0, 0, 0};
@@ -1156,6 +1237,20 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
         }
         *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = sv;
       }
+    }
+    if constexpr (QG) {
+      // V group scales relative to the row's largest (that one joins the
+      // output weights as the row scale)
+      float vmax = 0.f;
+#pragma unroll
+      for (int i = 0; i < NGR; ++i) vmax = fmaxf(vmax, vgr[i]);
+      const float rv = vmax > 0.f ? __builtin_amdgcn_rcpf(vmax) : 0.f;
+      if (lane < PRT) {
+#pragma unroll
+        for (int i = 0; i < NGR; ++i) vg_lds[wave][i][lane] = (_Float16)(vgr[i] * rv);
+      }
+      ks_r = 1.f;
+      vs_r = vmax;
     }
     if (lane < PRT) {
       sc_lds[wave][0][lane] = ks_r;
@@ -1240,6 +1335,13 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
       }
 #pragma unroll
       for (int dv = 0; dv < DV; ++dv) {
+        // QG: column c holds features 128 dv + 8 c + e, group 4 dv + c / 4
+        // (clamped: columns past D are dropped); the codes of rows 8q .. 8q+7
+        // times their group scale relative to the row's largest
+        half8_t rat = {};
+        if constexpr (QG)
+          rat = *reinterpret_cast<const half8_t*>(
+              &vg_lds[wave][min(4 * dv + lc / 4, NGR - 1)][32 * sl + 8 * lq]);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           // row pair (a, b) = (2pp, 2pp+1): t0 = [a0 b0 a1 b1], t1 = [a2 b2 a3 b3]
@@ -1265,6 +1367,7 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
               ov[2 * pp + 1] = h2[1];
             }
             const int e = 4 * hh + ee;
+            if constexpr (QG) ov *= rat;
             if constexpr (QF) {  // codes times 2^-12: exact in f16
               const half8_t ovl = ov * (_Float16)(1.0f / kLoScale);
               acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop_lo, ovl, acc[dv][e], 0, 0, 0);
@@ -1345,7 +1448,14 @@ int launch_mfma_rows(const MfmaArgs& a, int d, int gp, dim3 grid, hipStream_t st
     constexpr int Dv = decltype(dc)::value;
     return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
       constexpr int GPv = decltype(gc)::value;
-      if (a.step) {
+      if (a.qgroup) {
+        if constexpr (Dv == 64 || Dv == 128 || Dv == 256) {
+          if (a.step || a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
+          attn_split_i8_mfma<SR, Dv, GPv, false, false, true><<<grid, kMThreads, 0, st>>>(a);
+        } else {
+          return FC_ERR_UNSUPPORTED;
+        }
+      } else if (a.step) {
         if (a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
         attn_split_i8_mfma<SR, Dv, GPv, true><<<grid, kMThreads, 0, st>>>(a);
       } else if (a.q_dtype == FC_F32) {

@@ -117,6 +117,12 @@ CASES = [
     ("jpeg-i8g-bf16-g2-d64", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8, quant_group=32), "bf16", 1, 2, 2, 8 * 90 + 3, 64),
     ("jpeg-i8g-f32-r16-d96", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8, quant_group=32), "f32", 1, 2, 3, 16 * 30 + 9, 96),
     ("jpeg-i8g-f16-d256", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=32), "f16", 1, 1, 8, 8 * 64 + 1, 256),
+    # per-32 scales on the matrix-core pass: rows per block, head groups, widths
+    ("i8g-f16-c3", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=32), "f16", 2, 4, 4, 8 * 400 + 5, 128),
+    ("i8g-f16-k8-g16", dict(mode="jpeg", block_size=8, keep_freqs=8, quant_bits=8, quant_group=32), "f16", 1, 1, 16, 8 * 150 + 2, 128),
+    ("i8g-bf16-k1-d64-g1", dict(mode="jpeg", block_size=8, keep_freqs=1, quant_bits=8, quant_group=32), "bf16", 2, 2, 1, 8 * 100 + 7, 64),
+    ("i8g-bf16-k3-r16-g4", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8, quant_group=32), "bf16", 1, 2, 4, 16 * 60 + 5, 128),
+    ("i8g-bf16-k2-d256-g2", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8, quant_group=32), "bf16", 1, 2, 2, 8 * 100 + 3, 256),
 ]
 
 
