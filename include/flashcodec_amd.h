@@ -219,7 +219,8 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G,
  * Split count for a fc_decode_attention call over stores of `store_kind`
  * (stream dtype, query dtype, s stored rows per block, head size D): one
  * round of workgroups of the split pass that will run — the matrix-core
- * pass for int8 jpeg archives with fp16/bf16/fp32 queries (two workgroups per
+ * pass for int8 jpeg archives with fp16/bf16/fp32 queries and per-32 int8
+ * archives with fp16/bf16 queries at D = 64/128/256 (two workgroups per
  * compute unit, but at least one 64-row pass per wavefront and at most
  * max(16, passes / 10) splits), otherwise the vector-ALU pass at the
  * occupancy it reaches on the current device.  0 when nb == 0.
