@@ -427,10 +427,11 @@ def refshapes_mode(args):
 
 def shapes_mode(args):
     """Decode attention on int8 archives at C3's geometry (B=8, 32 q / 8 kv
-    heads, 32768 archived + 5 raw tokens, fp16, r=8) for head sizes and
-    keep_freqs besides C3's: each on the matrix-core pass (FC_PASS_AUTO) and
-    on the vector-ALU pass (FC_PASS_VECTOR), one archive set, max error vs
-    the fp64 oracle over all sequences."""
+    heads, 32768 archived + 5 raw tokens, fp16, r=8) for head sizes,
+    keep_freqs, per-32 scales and fp32 queries besides C3's: each on the
+    matrix-core pass (FC_PASS_AUTO) and on the vector-ALU pass
+    (FC_PASS_VECTOR), one archive set, max error vs the fp64 oracle over all
+    sequences."""
     import torch
     import flashcodec_amd as fc
     from flashcodec_amd import _native as N
@@ -439,17 +440,25 @@ def shapes_mode(args):
     res = {"metric": "decode attention GB/s by head size and keep_freqs, int8 jpeg, C3 geometry",
            "unit": "GB/s", "shapes": []}
     prev = N.lib().fc_get_attention_pass()
-    for D, k in ((128, 3), (128, 8), (80, 4), (96, 4), (128, 4)):
+    for D, k, grp, qdt in ((128, 3, 0, "f16"), (128, 8, 0, "f16"), (80, 4, 0, "f16"),
+                           (96, 4, 0, "f16"), (128, 4, 32, "f16"), (128, 4, 0, "f32"),
+                           (128, 4, 0, "f16")):
         cfg = dict(mode="jpeg", block_size=R, keep_freqs=k, quant_bits=8)
+        if grp:
+            cfg["quant_group"] = grp
         ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
         for st, seed in ((ks, 1), (vs, 2)):
             x = ar1_device((B, HKV, S_ARCH + TAIL, D), 0.95, seed, dev).to(torch.float16)
             st.append(x)
             del x
         g = torch.Generator(device=dev).manual_seed(3)
-        q = (torch.randn((B, HQ, 1, D), generator=g, device=dev) / math.sqrt(D)).to(torch.float16)
-        nbytes = 2 * (B * HKV * NB * k * (D + 4)) + 2 * B * HKV * TAIL * D * 2 + 2 * B * HQ * D * 2
-        row = {"D": D, "keep_freqs": k, "algorithmic_bytes": nbytes}
+        qt = torch.float32 if qdt == "f32" else torch.float16
+        q = (torch.randn((B, HQ, 1, D), generator=g, device=dev) / math.sqrt(D)).to(qt)
+        scale_bytes = 4 * (D // grp if grp else 1)
+        qo_bytes = 2 * B * HQ * D * q.element_size()
+        nbytes = 2 * (B * HKV * NB * k * (D + scale_bytes)) + 2 * B * HKV * TAIL * D * 2 + qo_bytes
+        row = {"D": D, "keep_freqs": k, "quant_group": grp, "q_dtype": qdt,
+               "algorithmic_bytes": nbytes}
         for name, code in (("matrix_core", N.PASS_AUTO), ("vector_alu", N.PASS_VECTOR)):
             N.lib().fc_set_attention_pass(code)
             ms = timed(lambda: fc.codec_decode_attention(q, ks, vs), args.steps, args.warmup)
@@ -729,8 +738,11 @@ def check_against_oracle(q, ks, vs, out):
     from oracle import oracle as O
     import flashcodec_amd as fc
     nb, r, k = ks.n_blocks, ks.block_size, ks.codec.keep_freqs
-    rows = [O.stored_rows_jpeg(st._coeffs[:, :, :nb].cpu().numpy(),
-                               st._scales[:, :, :nb, :, 0].cpu().numpy()) for st in (ks, vs)]
+    # per-row scales (..., k) or, with quant_group, per-32 scales (..., k, D/32)
+    sc = (lambda st: st._scales[:, :, :nb]) if ks.codec.quant_group else \
+        (lambda st: st._scales[:, :, :nb, :, 0])
+    rows = [O.stored_rows_jpeg(st._coeffs[:, :, :nb].cpu().numpy(), sc(st).cpu().numpy())
+            for st in (ks, vs)]
     raws = [st.raw.float().cpu().numpy() for st in (ks, vs)]
     A = O.synthesis_matrix("jpeg", r, fc.dct_basis(r, k).numpy())
     ref = O.attention(q[:, :, 0].float().cpu().numpy(), rows[0], rows[1], raws[0], raws[1], A,
