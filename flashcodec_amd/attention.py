@@ -206,9 +206,10 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
 
 def prefill_supported(codec, dtype, head_dim):
     """Whether codec_prefill_attention runs streams of `codec` with queries
-    of `dtype` and head size `head_dim`: int8 jpeg archives with 1 / 2 / 4
-    kept frequencies, fp16 / bf16 queries, head size 64 / 128 / 256."""
-    return (codec.name == "jpeg" and codec.quantized and not codec.quant_group
+    of `dtype` and head size `head_dim`: int8 jpeg archives (one scale per
+    row or per 32 features) with 1 / 2 / 4 kept frequencies, fp16 / bf16
+    queries, head size 64 / 128 / 256."""
+    return (codec.name == "jpeg" and codec.quantized
             and codec.keep_freqs in (1, 2, 4)
             and dtype in (torch.float16, torch.bfloat16) and head_dim in (64, 128, 256))
 
@@ -250,7 +251,8 @@ def codec_prefill_attention(query, key_stream, value_stream, scale=None):
     A = _device_A(c, r, q.device)
     rc = N.lib().fc_prefill_attention(
         q.data_ptr(), N.dtype_code(q.dtype), q.stride(0), q.stride(1), q.stride(2), B, Hq, Hkv,
-        Sq, D, ks.seq_len - Sq, N.dtype_code(ks.dtype), r, c.keep_freqs, ks.n_blocks, kv, vv,
+        Sq, D, ks.seq_len - Sq, N.dtype_code(ks.dtype), _jpeg_kind(c), r, c.keep_freqs,
+        ks.n_blocks, kv, vv,
         ks._n_raw, N.ptr(A), scale, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
         N.stream_ptr(q.device))
     N.check(rc, "fc_prefill_attention")

@@ -67,7 +67,11 @@ struct PrefillArgs {
 constexpr int kPThreads = 256;
 constexpr int kPWaves = kPThreads / 64;
 
-template <int SROWS, int DK, typename QT, typename RT>
+// QG: per-32 scales (D / 32 per stored row), as the decode pass takes them:
+// one score product per 32-feature group (the query's other group zeroed)
+// scaled by the rows' group scales, V codes times their group scale
+// relative to the row's largest as the value operand.
+template <int SROWS, int DK, typename QT, typename RT, bool QG = false>
 __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(PrefillArgs p) {
   constexpr int D = 32 * DK;
   constexpr int DV = (D + 127) / 128;
@@ -80,6 +84,9 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
   __shared__ float s_lds[kPWaves][16][kSPad];
   __shared__ _Float16 w_lds[kPWaves][16][kWPad];
   __shared__ float sc_lds[kPWaves][2][PR];
+  constexpr int NGR = QG ? D / 32 : 1;
+  __shared__ __attribute__((aligned(16))) float kg_lds[QG ? kPWaves : 1][NGR][PR];
+  __shared__ __attribute__((aligned(16))) _Float16 vg_lds[QG ? kPWaves : 1][NGR][PR];
   __shared__ float a_lds[FC_MAX_BLOCK * 4];
   __shared__ float fin[kPWaves][2][16];  // per query: rescale factor and final sum
 
@@ -120,8 +127,8 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
 
   const int8_t* kbase = p.kcodes + bh * p.kcap * SROWS * D;
   const int8_t* vbase = p.vcodes + bh * p.vcap * SROWS * D;
-  const float* ksc = p.kscales + bh * p.kcap * SROWS;
-  const float* vsc = p.vscales + bh * p.vcap * SROWS;
+  const float* ksc = p.kscales + bh * p.kcap * SROWS * NGR;
+  const float* vsc = p.vscales + bh * p.vcap * SROWS * NGR;
 
   // ---- queries: B operand of the score product.  Lane (q, c): query c,
   // features 64 k + 16 q + [0, 16) of chunk k
@@ -188,7 +195,27 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
 
   uint32_t kr[NT][KDW];
   float ks_r, vs_r;
+  float kgr[NGR], vgr[NGR];  // QG: the group scales of row lane % PR
+  const int sg_off = (lane % PR) * NGR * 4;
+  // QG: a row's NGR group scales (8 or 16-byte pieces) into x
+  auto load_groups = [&](const float* base, int64_t pr0, int prow, float (&x)[NGR]) {
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(base + pr0 * NGR, prow * NGR * 4);
+    if constexpr (NGR == 2) {
+      const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs, sg_off, 0, 0));
+      x[0] = __uint_as_float(v[0]);
+      x[1] = __uint_as_float(v[1]);
+    } else {
+#pragma unroll
+      for (int u = 0; u < NGR / 4; ++u) {
+        const u32x4_t v = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, sg_off + 16 * u, 0, 0));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * u + i] = __uint_as_float(v[i]);
+      }
+    }
+  };
   auto load_k = [&](int64_t pr0, int prow) {
+    if constexpr (QG) load_groups(ksc, pr0, prow, kgr);  // ahead of the codes
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kbase + pr0 * D, prow * D);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -199,13 +226,16 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
 #pragma unroll
         for (int i = 0; i < 4; ++i) kr[t][4 * h + i] = v[i];
       }
-    ks_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         buf_rsrc(ksc + pr0, prow * 4), sc_off, 0, 0));
-    vs_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         buf_rsrc(vsc + pr0, prow * 4), sc_off, 0, 0));
+    if constexpr (!QG) {
+      ks_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           buf_rsrc(ksc + pr0, prow * 4), sc_off, 0, 0));
+      vs_r = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           buf_rsrc(vsc + pr0, prow * 4), sc_off, 0, 0));
+    }
   };
   uint32_t vr[NS][DV][16];
   auto load_v = [&](int64_t pr0, int prow) {
+    if constexpr (QG) load_groups(vsc, pr0, prow, vgr);  // ahead of the codes
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vbase + pr0 * D, prow * D);
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl)
@@ -271,8 +301,38 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
     load_v(pr0, prow);
 
     // ------------------------------------------------------------ scores
+    if constexpr (QG) {
+      if (lane < PR) {
+#pragma unroll
+        for (int i = 0; i < NGR; ++i) kg_lds[wave][i][lane] = kgr[i];
+      }
+      wave_lds_sync();
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
+      if constexpr (QG) {
+        // lanes q < 2 hold group 2c of chunk c, q >= 2 group 2c + 1
+        float4_t accg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
+                             (int)kr[t][4 * c + 3]};
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const bool mine = (lq >> 1) == hf;
+            const i32x4_t zero = {0, 0, 0, 0};
+            const i32x4_t ghi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, mine ? qhi[c] : zero, zero, 0, 0, 0);
+            const i32x4_t glo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, mine ? qlo[c] : zero, zero, 0, 0, 0);
+            const float4_t kgv =
+                *reinterpret_cast<const float4_t*>(&kg_lds[wave][2 * c + hf][16 * t + 4 * lq]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              accg[i] = __builtin_fmaf(kgv[i], (float)(ghi[i] * 256 + glo[i]), accg[i]);
+          }
+        }
+        *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = accg * head_mul;
+        continue;
+      }
       i32x4_t shi = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
@@ -285,6 +345,20 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
 #pragma unroll
       for (int i = 0; i < 4; ++i) sv[i] = (float)(shi[i] * 256 + slo[i]) * head_mul;
       *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = sv;
+    }
+    if constexpr (QG) {
+      // V group scales relative to the row's largest (that one joins the
+      // output weights as the row scale)
+      float vmax = 0.f;
+#pragma unroll
+      for (int i = 0; i < NGR; ++i) vmax = fmaxf(vmax, vgr[i]);
+      const float rv = vmax > 0.f ? __builtin_amdgcn_rcpf(vmax) : 0.f;
+      if (lane < PR) {
+#pragma unroll
+        for (int i = 0; i < NGR; ++i) vg_lds[wave][i][lane] = (_Float16)(vgr[i] * rv);
+      }
+      ks_r = 1.f;
+      vs_r = vmax;
     }
     if (lane < PR) {
       sc_lds[wave][0][lane] = ks_r;
@@ -342,6 +416,12 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
       const half8_t wop = __builtin_bit_cast(half8_t, wa);
 #pragma unroll
       for (int dv = 0; dv < DV; ++dv) {
+        // QG: column c holds features 128 dv + 8 c + e, group 4 dv + c / 4
+        // (clamped: columns past D are dropped), rows 8q .. 8q+7
+        half8_t rat = {};
+        if constexpr (QG)
+          rat = *reinterpret_cast<const half8_t*>(
+              &vg_lds[wave][min(4 * dv + lc / 4, NGR - 1)][32 * sl + 8 * lq]);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           uint32_t t0[4], t1[4];
@@ -366,6 +446,7 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
               ov[2 * pp + 1] = h2[1];
             }
             const int e = 4 * hh + ee;
+            if constexpr (QG) ov *= rat;
             acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, ov, acc[dv][e], 0, 0, 0);
           }
         }
@@ -460,9 +541,10 @@ extern "C" {
 
 int fc_prefill_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
                          int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D, int64_t P0,
-                         int stream_dtype, int r, int s, int64_t nb, const fc_stream_view* key,
-                         const fc_stream_view* value, int64_t n_raw, const float* A, float scale,
-                         void* out, int64_t o_sb, int64_t o_sh, int64_t o_st, void* stream) {
+                         int stream_dtype, int store_kind, int r, int s, int64_t nb,
+                         const fc_stream_view* key, const fc_stream_view* value, int64_t n_raw,
+                         const float* A, float scale, void* out, int64_t o_sb, int64_t o_sh,
+                         int64_t o_st, void* stream) {
   if (!q || !out || !key || !value || B <= 0 || Hq <= 0 || Hkv <= 0 || Sq <= 0 || Hq % Hkv)
     return FC_ERR_ARG;
   if (nb < 0 || n_raw < 0 || P0 < 0 || r < 1 || r > FC_MAX_BLOCK || s < 1 || s > r)
@@ -473,6 +555,8 @@ int fc_prefill_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
     return FC_ERR_UNSUPPORTED;
   if (stream_dtype != FC_F16 && stream_dtype != FC_BF16 && stream_dtype != FC_F32)
     return FC_ERR_ARG;
+  if (store_kind != FC_STORE_JPEG_I8 && store_kind != FC_STORE_JPEG_I8G) return FC_ERR_ARG;
+  const bool grouped = store_kind == FC_STORE_JPEG_I8G;
   if (nb > 0 && (!A || !key->rows || !value->rows || !key->scales || !value->scales ||
                  nb > key->cap || nb > value->cap))
     return FC_ERR_ARG;
@@ -480,6 +564,8 @@ int fc_prefill_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   const auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   if (!al16(q) || q_sb % 8 || q_sh % 8 || q_st % 8 || !al16(key->rows) || !al16(value->rows))
     return FC_ERR_UNSUPPORTED;
+  // per-32 scales are read in 8 / 16-byte pieces per row
+  if (grouped && nb > 0 && (!al16(key->scales) || !al16(value->scales))) return FC_ERR_UNSUPPORTED;
   const int64_t G = Hq / Hkv;
   PrefillArgs a{};
   a.q = q;
@@ -532,7 +618,10 @@ int fc_prefill_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
       auto go = [&](auto qt, auto rt) {
         using QT = decltype(qt);
         using RT = decltype(rt);
-        prefill_i8_mfma<SR, DKv, QT, RT><<<dim3((unsigned)blocks), kPThreads, 0, st>>>(a);
+        if (grouped)
+          prefill_i8_mfma<SR, DKv, QT, RT, true><<<dim3((unsigned)blocks), kPThreads, 0, st>>>(a);
+        else
+          prefill_i8_mfma<SR, DKv, QT, RT><<<dim3((unsigned)blocks), kPThreads, 0, st>>>(a);
         return FC_OK;
       };
       auto with_rt = [&](auto qt) {

@@ -366,7 +366,9 @@ int fc_get_attention_pass(void);
  * element strides q_sb, q_sh, q_st) sit at positions P0 .. P0+Sq-1 of the
  * streams (P0 + Sq <= nb * r + n_raw), and query token i attends every
  * cached token at a position <= P0 + i: archived blocks through their
- * stored rows (codes x scales, synthesis matrix A r x s) in the coefficient
+ * stored rows (codes x scales: store_kind FC_STORE_JPEG_I8, one scale per
+ * row, or FC_STORE_JPEG_I8G, one per 32 features, whose scale stores must
+ * be 16-byte aligned; synthesis matrix A r x s) in the coefficient
  * domain, raw-tail tokens at full precision.  Softmax in fp32; out
  * (B, Hq, Sq, D) in q_dtype, strides o_sb, o_sh, o_st.  GQA as
  * fc_decode_attention.  Supports D in {64, 128, 256} and s in {1, 2, 4}
@@ -380,9 +382,10 @@ int fc_get_attention_pass(void);
 int fc_prefill_attention(const void* q, int q_dtype, int64_t q_sb,
                          int64_t q_sh, int64_t q_st, int64_t B, int64_t Hq,
                          int64_t Hkv, int64_t Sq, int64_t D, int64_t P0,
-                         int stream_dtype, int r, int s, int64_t nb,
-                         const fc_stream_view* key, const fc_stream_view* value,
-                         int64_t n_raw, const float* A, float scale, void* out,
+                         int stream_dtype, int store_kind, int r, int s,
+                         int64_t nb, const fc_stream_view* key,
+                         const fc_stream_view* value, int64_t n_raw,
+                         const float* A, float scale, void* out,
                          int64_t o_sb, int64_t o_sh, int64_t o_st,
                          void* stream);
 

@@ -34,8 +34,8 @@ def view_oracle(oracle, st):
     n, r, k = st.n_blocks, st.block_size, st.codec.keep_freqs
     parts = []
     if n:
-        rows = oracle.stored_rows_jpeg(st._coeffs[:, :, :n].cpu().numpy(),
-                                       st._scales[:, :, :n, :, 0].cpu().numpy())
+        sc = st._scales[:, :, :n] if st.codec.quant_group else st._scales[:, :, :n, :, 0]
+        rows = oracle.stored_rows_jpeg(st._coeffs[:, :, :n].cpu().numpy(), sc.cpu().numpy())
         A = oracle.synthesis_matrix("jpeg", r, fc.dct_basis(r, k).numpy())
         B, H, _, _, D = rows.shape
         parts.append(np.einsum("ps,bhnsd->bhnpd", A, rows).reshape(B, H, n * r, D))
@@ -69,8 +69,10 @@ def check(out, ref, dt):
     assert not (err > tol).any(), f"max err {err.max():.3e} vs max|ref| {np.abs(ref).max():.3e}"
 
 
-def streams(dt, B, Hkv, S, D, k, seed, oracle):
+def streams(dt, B, Hkv, S, D, k, seed, oracle, group=0):
     cfg = dict(mode="jpeg", block_size=8, keep_freqs=k, quant_bits=8)
+    if group:
+        cfg["quant_group"] = group
     x = [torch.from_numpy(oracle.ar1((B, Hkv, S, D), 0.9, seed + i)).to(torch_dtype(dt)).to(DEV)
          for i in range(2)]
     ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
@@ -88,15 +90,23 @@ CASES = [
     ("bf16", 2, 2, 2, 128, 4, 77, 8 * 25 + 3),       # chunked: 203 cached, 77 more
     ("f16", 1, 2, 2, 128, 4, 5, 0),                  # shorter than a block: tail only
     ("bf16", 1, 2, 2, 128, 4, 3, 8 * 10 + 6),         # 3 more tokens completing a block
+    # per-32 scales (quant_group=32)
+    ("bf16", 2, 2, 2, 128, 4, 8 * 37 + 5, 0, 32),
+    ("f16", 1, 1, 16, 128, 2, 8 * 11, 0, 32),
+    ("f16", 2, 2, 3, 64, 1, 8 * 12 + 1, 0, 32),
+    ("bf16", 1, 2, 8, 256, 4, 8 * 9 + 2, 0, 32),
+    ("bf16", 2, 2, 2, 128, 4, 77, 8 * 25 + 3, 32),
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-G{c[3]}-D{c[4]}-k{c[5]}-S{c[6]}+{c[7]}"
+                                             + (f"-g{c[8]}" if len(c) > 8 else "")
                                              for c in CASES])
 def test_prefill_matches_causal_attention_on_the_view(case, oracle):
-    dt, B, Hkv, G, D, k, S, S0 = case
+    dt, B, Hkv, G, D, k, S, S0 = case[:8]
+    group = case[8] if len(case) > 8 else 0
     print(f"case prefill {case}", flush=True)
-    ks, vs, (kx, vx) = streams(dt, B, Hkv, S0 + S, D, k, 40 + G + D + S, oracle)
+    ks, vs, (kx, vx) = streams(dt, B, Hkv, S0 + S, D, k, 40 + G + D + S, oracle, group)
     if S0:
         ks.append(kx[:, :, :S0])
         vs.append(vx[:, :, :S0])
