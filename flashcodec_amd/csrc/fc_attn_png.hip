@@ -113,13 +113,9 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   const bool hq_ok = lc < G;
   const int64_t hq = hkv * p.G + g0 + (hq_ok ? lc : 0);
   const float* qrow = static_cast<const float*>(p.q) + b * p.q_sb + hq * p.q_sh + 4 * lq;
-  float qv[FPL];
+  float4_t qraw[FPL / 4];
 #pragma unroll
-  for (int j = 0; j < FPL / 4; ++j) {
-    const float4_t v = *reinterpret_cast<const float4_t*>(qrow + 16 * j);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qv[4 * j + i] = hq_ok ? v[i] : 0.f;
-  }
+  for (int j = 0; j < FPL / 4; ++j) qraw[j] = *reinterpret_cast<const float4_t*>(qrow + 16 * j);
 
   float4_t acc[FPC];
 #pragma unroll
@@ -128,6 +124,7 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   float m_run = -INFINITY, l_lane = 0.f;
 
   float kr[FPL];
+  float qv[FPL];
   auto load_k = [&](int64_t pass) {
     const int64_t gr = pass * kPngTile + lc;
     const bool ok = gr < rows_total;
@@ -183,6 +180,14 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     }
   };
 
+  // the first pass's rows go out right behind the query, before the query
+  // is read
+  int64_t cur = wslot;
+  if (cur < npass) load_k(cur);
+#pragma unroll
+  for (int j = 0; j < FPL / 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qv[4 * j + i] = hq_ok ? qraw[j][i] : 0.f;
   // raw tail (fused calls): split 0 computes its partial before the passes
   const bool fold_tail = p.fused && split == 0 && n_raw > 0;
   if (fold_tail)
@@ -190,8 +195,6 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
                               tail_ml[1]);
   __syncthreads();
 
-  int64_t cur = wslot;
-  if (cur < npass) load_k(cur);
   while (cur < npass) {
     const int prow = (int)min<int64_t>(kPngTile, rows_total - cur * kPngTile);  // whole blocks
     load_v(cur);
