@@ -1193,13 +1193,14 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
                              (int)kr[t][4 * c + 3]};
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf) {
+            // the codes of the other group's lanes zeroed (the query stays
+            // whole: a masked copy of it would be hoisted out of the loop)
             const bool mine = (lq >> 1) == hf;
+            const i32x4_t am = mine ? a : (i32x4_t){0, 0, 0, 0};
             i32x4_t sd[ND];
 #pragma unroll
-            for (int i = 0; i < ND; ++i) {
-              const i32x4_t bq = mine ? qdig[i][c] : (i32x4_t){0, 0, 0, 0};
-              sd[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bq, (i32x4_t){0, 0, 0, 0}, 0, 0, 0);
-            }
+            for (int i = 0; i < ND; ++i)
+              sd[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qdig[i][c], (i32x4_t){0, 0, 0, 0}, 0, 0, 0);
             const float4_t kgv =
                 *reinterpret_cast<const float4_t*>(&kg_lds[wave][2 * c + hf][16 * t + 4 * lq]);
 #pragma unroll

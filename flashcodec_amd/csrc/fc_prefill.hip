@@ -319,10 +319,13 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
                              (int)kr[t][4 * c + 3]};
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf) {
+            // the codes of the other group's lanes zeroed (the query stays
+            // whole: a masked copy of it would be hoisted out of the loop)
             const bool mine = (lq >> 1) == hf;
             const i32x4_t zero = {0, 0, 0, 0};
-            const i32x4_t ghi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, mine ? qhi[c] : zero, zero, 0, 0, 0);
-            const i32x4_t glo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, mine ? qlo[c] : zero, zero, 0, 0, 0);
+            const i32x4_t am = mine ? a : zero;
+            const i32x4_t ghi = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qhi[c], zero, 0, 0, 0);
+            const i32x4_t glo = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qlo[c], zero, 0, 0, 0);
             const float4_t kgv =
                 *reinterpret_cast<const float4_t*>(&kg_lds[wave][2 * c + hf][16 * t + 4 * lq]);
 #pragma unroll
