@@ -961,6 +961,8 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   uint32_t vr[NS][DV][16];
   auto load_v = [&](int64_t pr0, int prow) {
     if constexpr (QG) {
+      // group scales ahead of the codes, with this pass's V (held one pass
+      // ahead with the K loads they cost registers that spilled)
       const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(vsc + pr0 * NGR, prow * NGR * 4);
       if constexpr (NGR == 2) {
         const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rvs, sg_off, 0, 0));
@@ -1183,9 +1185,8 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       if constexpr (QG) {
-        // per 32-feature group: the score product with the query's features
-        // of the other group zeroed (lanes q < 2 hold group 2c of chunk c,
-        // q >= 2 group 2c + 1), scaled by the rows' group scales
+        // per 32-feature group: one score product (lanes q < 2 hold group 2c
+        // of chunk c, q >= 2 group 2c + 1), scaled by the rows' group scales
         float4_t accg = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
