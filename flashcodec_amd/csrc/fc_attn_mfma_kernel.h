@@ -381,15 +381,11 @@ __device__ __forceinline__ void step_partial(
 // when its instructions are not in the instruction cache: it is kept short
 // and free of per-element branches (every load of a batch is issued and
 // splits past n_splits are selected away; one store branch per task).
-// `lds` holds >= 2 * 16 * kFuseMaxSplits floats.  dry: the same instructions
-// without memory traffic (loads through empty buffer ranges read zero, no
-// stores), run by the workgroups that do not merge, so the merge's code is
-// in their compute units' instruction cache when a merging workgroup there
-// needs it.
+// `lds` holds >= 2 * 16 * kFuseMaxSplits floats.
 template <int D, bool QF32 = false, bool COMPACT = true>
 __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_t hkv, int64_t g0, int G,
                             int split, int tid, float* lds, const float* own_acc,
-                            const float* own_m, const float* own_l, bool dry) {
+                            const float* own_m, const float* own_l) {
   constexpr int C4 = D / 4;  // float4 chunks of a head's output
   constexpr int kPre = 8;    // partials in flight per task
   const int ns = p.n_splits;
@@ -399,9 +395,9 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
 
   // device-scope (L2-missing) loads of the group's partials and statistics;
   // offsets past the group's slots read as zero
-  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, dry ? 0 : G * ns * D * 4);
-  const __amdgpu_buffer_rsrc_t rm = buf_rsrc(p.pm + bq0 * ns, dry ? 0 : G * ns * 4);
-  const __amdgpu_buffer_rsrc_t rl = buf_rsrc(p.pl + bq0 * ns, dry ? 0 : G * ns * 4);
+  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p.pacc + bq0 * ns * D, G * ns * D * 4);
+  const __amdgpu_buffer_rsrc_t rm = buf_rsrc(p.pm + bq0 * ns, G * ns * 4);
+  const __amdgpu_buffer_rsrc_t rl = buf_rsrc(p.pl + bq0 * ns, G * ns * 4);
   auto load_batch = [&](int h, int sp0, int c, float4_t (&pre)[kPre]) {
 #pragma unroll
     for (int j = 0; j < kPre; ++j)
@@ -436,7 +432,6 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
     }
     const float iv = 1.0f / l;
     const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
-    if (dry) return;
     if constexpr (QF32) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) static_cast<float*>(p.out)[ob + i] = o[i] * iv;
@@ -497,7 +492,7 @@ __device__ __forceinline__ void fused_merge(const MfmaArgs& p, int64_t b, int64_
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = __builtin_fmaf(w, j == split ? own[i] : pa[j][i], o[i]);
     }
-    if (!act || dry) return;
+    if (!act) return;
     const float iv = 1.0f / l;
     const int64_t ob = b * p.o_sb + (hkv * p.G + g0 + h) * p.o_sh + 4 * c;
     if constexpr (QF32) {
@@ -719,18 +714,16 @@ __device__ __forceinline__ void split_epilogue(
   const bool last = s_last != 0;
   if (!last) {
     step_done();
-    if constexpr (!COMPACT) return;  // the fused step's kernels: no dry merge (its registers spill)
+    return;
   }
   if constexpr (WIDE > 0) {
-    if (last && G * (D / 4) * 2 <= kMThreads && p.n_splits <= WIDE && p.n_splits % 4 == 0) {
+    if (G * (D / 4) * 2 <= kMThreads && p.n_splits <= WIDE && p.n_splits % 4 == 0) {
       wide_merge<D, WIDE, QF32>(p, b, hkv, g0, G, split, tid, part_lds, wg_ml[0], wg_ml[1]);
       return;
     }
   }
-  // one call site for both: the workgroups that do not merge run it dry
-  fused_merge<D, QF32, COMPACT>(p, b, hkv, g0, G, split, tid, scratch, part_lds, wg_ml[0], wg_ml[1],
-                               !last);
-  if (last) step_done();
+  fused_merge<D, QF32, COMPACT>(p, b, hkv, g0, G, split, tid, scratch, part_lds, wg_ml[0], wg_ml[1]);
+  step_done();
 }
 
 // D: head size (64, 80, 96, 128, 256); the products run on DC = D rounded up
