@@ -95,15 +95,16 @@ def copy_mode(args):
 
 def split_kernel_name(n_splits):
     """Kernel of this workload's call (int8 codes, 4 rows per block, D=128,
-    groups of 4 q heads, no step, fp16 q): the matrix-core split pass, its
-    merge fused in when the split count allows (one launch)."""
+    groups of 4 q heads, no step, fp16 q, per-row scales): the matrix-core
+    split pass, its merge fused in when the split count allows (one
+    launch)."""
     from flashcodec_amd import _native as N
     from flashcodec_amd.attention import launches_per_call
     if N.lib().fc_get_attention_pass() == N.PASS_VECTOR:
         return "attn_split_kernel (merge fused)"
     if launches_per_call(N.STORE_JPEG_I8, n_splits) == 1:
-        return "attn_split_i8_mfma<4,128,4,false,false> (merge fused)"
-    return "attn_split_i8_mfma<4,128,4,false,false> + attn_merge_head_kernel"
+        return "attn_split_i8_mfma<4,128,4,false,false,false> (merge fused)"
+    return "attn_split_i8_mfma<4,128,4,false,false,false> + attn_merge_head_kernel"
 
 
 def cpu_model():
