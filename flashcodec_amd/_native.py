@@ -89,6 +89,7 @@ SIGNATURES = {
     "fc_decode_attention_merge": _ATTN_SIG,
     "fc_png_topm_mask_host": (ctypes.c_uint64, [_vp, _int, _int]),
     "fc_decode_step": (_int, [ctypes.POINTER(StepArgs)]),
+    "fc_last_step_single_launch": (_int, []),
     "fc_prefill_attention": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                     _i64, _int, _int, _int, _int, _i64, ctypes.POINTER(StreamView),
                                     ctypes.POINTER(StreamView), _i64, _vp, _fp, _vp, _i64, _i64,

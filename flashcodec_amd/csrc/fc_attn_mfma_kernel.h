@@ -719,6 +719,7 @@ __device__ __forceinline__ void split_epilogue(
   if constexpr (WIDE > 0) {
     if (G * (D / 4) * 2 <= kMThreads && p.n_splits <= WIDE && p.n_splits % 4 == 0) {
       wide_merge<D, WIDE, QF32>(p, b, hkv, g0, G, split, tid, part_lds, wg_ml[0], wg_ml[1]);
+      step_done();  // every exit counts itself for a state-advancing step
       return;
     }
   }

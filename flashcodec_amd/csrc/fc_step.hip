@@ -19,6 +19,9 @@ namespace fc {
 
 constexpr int kTailThreads = 64;
 
+// fc_last_step_single_launch: how the calling thread's last step ran
+thread_local int g_last_step_single = -1;
+
 struct TailArgs {
   const void* tok[2];  // new token of the key / value stream, (B, H, 1, D)
   int64_t tsb[2], tsh[2];
@@ -130,7 +133,10 @@ static int decode_step_state(const fc_step_args* a) {
     return FC_ERR_ARG;
   if (a->n_blocks < 1) return FC_ERR_ARG;  // the archive holds a block before capture
   const int one = step_single_launch(a, a->state);
-  if (one != FC_ERR_UNSUPPORTED) return one;
+  if (one != FC_ERR_UNSUPPORTED) {
+    if (one == FC_OK) g_last_step_single = 1;
+    return one;
+  }
   const int64_t B = a->B, Hkv = a->Hkv, D = a->D;
   const int r = a->r;
   hipStream_t stream = (hipStream_t)a->stream;
@@ -186,7 +192,9 @@ static int decode_step_state(const fc_step_args* a) {
   state_advance_kernel<<<1, 64, 0, stream>>>(const_cast<int64_t*>(a->state), r,
                                              a->key.cap < a->value.cap ? a->key.cap
                                                                        : a->value.cap);
-  return check_launch();
+  rc = check_launch();
+  if (rc == FC_OK) g_last_step_single = 0;
+  return rc;
 }
 
 }  // namespace fc
@@ -217,7 +225,10 @@ int fc_decode_step(const fc_step_args* a) {
   if (completes && (a->n_blocks + 1 > a->key.cap || a->n_blocks + 1 > a->value.cap))
     return FC_ERR_ARG;  // the caller grows the archives first
   const int one = step_single_launch(a, nullptr);
-  if (one != FC_ERR_UNSUPPORTED) return one;
+  if (one != FC_ERR_UNSUPPORTED) {
+    if (one == FC_OK) g_last_step_single = 1;
+    return one;
+  }
   hipStream_t stream = (hipStream_t)a->stream;
 
   // 1. the new tokens into the tails
@@ -282,9 +293,13 @@ int fc_decode_step(const fc_step_args* a) {
     if (!a->workspace || fc_attention_workspace_bytes(B, Hq, D, n_splits) > a->workspace_bytes)
       return FC_ERR_ARG;
   }
-  return fc_decode_attention(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, a->store_kind,
-                             a->stream_dtype, r, a->s, nb, &v[0], &v[1], nt, a->A, a->scale,
-                             a->out, a->o_sb, a->o_sh, a->workspace, n_splits, a->stream);
+  rc = fc_decode_attention(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, a->store_kind,
+                           a->stream_dtype, r, a->s, nb, &v[0], &v[1], nt, a->A, a->scale,
+                           a->out, a->o_sb, a->o_sh, a->workspace, n_splits, a->stream);
+  if (rc == FC_OK) g_last_step_single = 0;
+  return rc;
 }
+
+int fc_last_step_single_launch(void) { return g_last_step_single; }
 
 }  // extern "C"

@@ -19,10 +19,14 @@ RoPE run as usual; then
 
 Guards (anything else calls the original forward): codec cache layer, eval
 mode, ``position_embeddings`` given, no sliding window, a RoPE function in
-the model's module, and either batch 1 or no attention mask (transformers
-passes no mask to SDPA-style attention when nothing is padded, so unpadded
-batches take the codec path too; the reference stops at batch 1 and at
-decode steps, patch_attention.py:52-61).
+the model's module, and a mask the kernels honour.  Decode steps take the
+codec path at batch 1 whatever the mask (as the reference does,
+patch_attention.py:52-61) or with no mask at all (transformers passes none
+to SDPA-style attention when nothing is padded, so unpadded batches take it
+too).  A prefill on the archive applies the plain causal mask only, so it
+runs there when the mask is absent or is exactly that mask (no padded key
+columns: eager-attention models pass it explicitly); a padded prompt runs
+the original forward with its mask.
 """
 
 import importlib
@@ -97,18 +101,44 @@ def _finish(module, out, gate, lead):
     return module.o_proj(out), None
 
 
+def _plain_causal(mask, T, total):
+    """Whether `mask` lets query i of a T-token prefill (position
+    total - T + i) see exactly the keys 0 .. its own position: None, a 2-D
+    (batch, key) padding mask with every one of the `total` keys kept, or a
+    4-D (batch, 1 or heads, T, keys) mask (bool: True attends; additive
+    float: 0 attends) equal to the causal pattern over the first `total`
+    keys.  Reads the mask back to the host (prefill only: decode steps never
+    call it, so they stay capturable)."""
+    if mask is None:
+        return True
+    if not torch.is_tensor(mask):
+        return False                      # e.g. a flex-attention block mask
+    if mask.dim() == 2:
+        return mask.shape[-1] >= total and bool(mask[:, :total].bool().all())
+    if mask.dim() != 4 or mask.shape[-2] != T or mask.shape[-1] < total:
+        return False
+    m = mask[..., :total]
+    seen = m if m.dtype == torch.bool else m == 0
+    keys = torch.arange(total, device=mask.device)
+    last = torch.arange(total - T, total, device=mask.device)
+    allowed = keys[None, :] <= last[:, None]
+    return bool(torch.equal(seen, allowed.expand_as(seen)))
+
+
 def _attention_forward(module, orig, hidden_states, position_embeddings=None,
                        attention_mask=None, past_key_values=None, **kwargs):
     layer = _codec_layer(module, past_key_values)
+    T = hidden_states.shape[-2]
     codec_ok = (layer is not None
                 and not module.training
                 and position_embeddings is not None
                 and getattr(module, "sliding_window", None) is None
-                and _rope_fn(module) is not None
-                and (hidden_states.shape[0] == 1 or attention_mask is None))
-    T = hidden_states.shape[-2]
+                and _rope_fn(module) is not None)
+    if codec_ok and T == 1:
+        codec_ok = hidden_states.shape[0] == 1 or attention_mask is None
     if (codec_ok and T > 1 and _PREFILL["on"]
-            and prefill_supported(layer.codec, hidden_states.dtype, module.head_dim)):
+            and prefill_supported(layer.codec, hidden_states.dtype, module.head_dim)
+            and _plain_causal(attention_mask, T, layer.get_seq_length() + T)):
         # prefill on the archive: append the prompt's K/V, attend without a view
         q, k, v, gate = _project(module, hidden_states, position_embeddings)
         if not layer.is_initialized:

@@ -459,6 +459,17 @@ int fc_decode_step(const fc_step_args* args);
  * reads at most `cap` blocks, and the third word (overflow, zero when the
  * caller sets up the state) becomes 1 and stays 1, for the caller to check.
  */
+
+/*
+ * How the calling thread's last successful fc_decode_step call ran: 1 when
+ * the whole step was one kernel launch (int8 jpeg archives with one scale
+ * per row, fp16 / bf16 queries and stream, the matrix-core pass), 0 when it
+ * took the multi-launch form (token append, archive, attention, state
+ * advance), -1 before any such call.  No counterpart in the reference (its
+ * step is always two appends and an attention call); for callers and tests
+ * that report or check launches per decode step.
+ */
+int fc_last_step_single_launch(void);
 #ifdef __cplusplus
 }
 #endif

@@ -34,6 +34,21 @@ def assert_close(out, ref, dt):
         assert not bad.any(), f"{bad.sum()} elements out of tolerance; max err {err.max():.3e}"
 
 
+def assert_close_pair(a, b, dt):
+    """Two outputs of the same attention that were each rounded to the
+    output dtype once: the contract's 2e-3 of max|b| plus a whole ulp (half
+    an ulp per rounding) at each element."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    err = np.abs(a - b)
+    if dt == "f32":
+        assert err.max() <= 2e-5, f"max abs err {err.max():.3e}"
+    else:
+        tol = 2e-3 * np.abs(b).max() + 2 * HALF_ULP[dt] * np.abs(b)
+        bad = err > tol
+        assert not bad.any(), f"{bad.sum()} elements out of tolerance; max err {err.max():.3e}"
+
+
 def stream_rows(oracle, st):
     """fp64 stored rows of a stream, read from its device buffers."""
     n = st.n_blocks
@@ -327,19 +342,39 @@ def _archive_of(st):
     return [t[:, :, :st.n_blocks] for t in st._archive_tensors()] if st.n_blocks else []
 
 
-@pytest.mark.parametrize("cfg,dt", [
-    (dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16"),
-    (dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8), "bf16"),
-    (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32"),
-    (dict(mode="png", block_size=8, keep_ratio=0.5), "f32"),
-    (dict(mode="png", block_size=4, keep_ratio=1.0), "bf16"),
-])
-def test_fused_decode_step_matches_append_then_attend(cfg, dt):
+I8 = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+# cfg, dtype, D, G, whether the step is one launch (the in-kernel archive)
+STEP_PAIRS = [
+    (I8, "f16", 64, 4, True),
+    (dict(I8, keep_freqs=2), "bf16", 64, 4, True),
+    (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 64, 4, False),
+    (dict(mode="png", block_size=8, keep_ratio=0.5), "f32", 64, 4, False),
+    (dict(mode="png", block_size=4, keep_ratio=1.0), "bf16", 64, 4, False),
+    # the C5 instantiation (D=128, bf16, k=4, G=2), other row counts and widths
+    (I8, "bf16", 128, 2, True),
+    (dict(I8, keep_freqs=3), "f16", 128, 4, True),
+    (dict(I8, keep_freqs=8), "bf16", 128, 2, True),
+    (I8, "bf16", 80, 4, True),
+    (dict(I8, keep_freqs=8), "f16", 96, 4, True),
+    (dict(I8, keep_freqs=1), "f16", 256, 8, True),
+    (dict(I8, block_size=16, keep_freqs=4), "bf16", 128, 2, True),
+    (dict(I8, quant_group=32), "bf16", 128, 2, False),
+]
+
+
+@pytest.mark.parametrize("cfg,dt,D,G,single", STEP_PAIRS,
+                         ids=[f"{c['mode']}-k{c.get('keep_freqs', 0)}-r{c['block_size']}"
+                              f"{'-g32' if c.get('quant_group') else ''}-{dt}-D{D}"
+                              for c, dt, D, _, _ in STEP_PAIRS])
+def test_fused_decode_step_matches_append_then_attend(cfg, dt, D, G, single, oracle):
     """codec_decode_step (one library call per layer step) leaves the same
-    archives, tails and counters as two appends, and its output matches
-    codec_decode_attention on them, across block boundaries; the first call
-    on uninitialised streams takes the two-call path."""
-    B, Hkv, G, D = 2, 2, 4, 64
+    archives (codes and scale bits), tails and counters as two appends, and
+    its output matches the oracle on them and codec_decode_attention's
+    output (two roundings apart), across block boundaries; int8 steps run as
+    one launch that archives in-kernel; the first call on uninitialised
+    streams takes the two-call path."""
+    from flashcodec_amd import _native as N
+    B, Hkv = 2, 2
     Hq, r = Hkv * G, cfg["block_size"]
     tdt = torch_dtype(dt)
     print(f"case fused step {cfg} {dt}", flush=True)
@@ -358,6 +393,7 @@ def test_fused_decode_step_matches_append_then_attend(cfg, dt):
         k = torch.randn((B, 1, Hkv, D), generator=g, device=DEV).to(tdt).transpose(1, 2)
         v = torch.randn((B, 1, Hkv, D), generator=g, device=DEV).to(tdt).transpose(1, 2)
         out_f = fc.codec_decode_step(q, k, v, ks_f, vs_f)
+        assert N.lib().fc_last_step_single_launch() == int(single)
         ks_r.append(k)
         vs_r.append(v)
         out_r = fc.codec_decode_attention(q, ks_r, vs_r)
@@ -368,7 +404,8 @@ def test_fused_decode_step_matches_append_then_attend(cfg, dt):
             assert (a.raw is None) == (b.raw is None)
             if a.raw is not None:
                 assert torch.equal(a.raw, b.raw)
-        assert_close(to_values(out_f), to_values(out_r), dt)
+        assert_close(to_values(out_f)[:, :, 0], oracle_out(oracle, q, ks_f, vs_f, D ** -0.5), dt)
+        assert_close_pair(to_values(out_f), to_values(out_r), dt)
         if step == 0:
             out0 = fc.codec_decode_step(q, k, v, fresh_k, fresh_v)   # two-call path
             assert fresh_k.seq_len == 1 and torch.equal(fresh_k.raw, k)

@@ -211,6 +211,53 @@ def test_fused_decode_step_matches_oracle(cfg, dt, G, oracle):
         assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), dt)
 
 
+def _archives_equal(a, b):
+    """Archive codes / scales / rows, tails and counters of two streams agree
+    bit for bit."""
+    assert a.n_blocks == b.n_blocks and a.seq_len == b.seq_len
+    for x, y in zip(a._archive_tensors(), b._archive_tensors()):
+        assert torch.equal(x[:, :, :a.n_blocks], y[:, :, :b.n_blocks])
+    assert (a.raw is None) == (b.raw is None)
+    if a.raw is not None:
+        assert torch.equal(a.raw, b.raw)
+
+
+C5 = dict(B=16, Hkv=8, G=2, D=128, dt="bf16")
+
+
+def test_fused_step_c5_scale_multi_split(oracle):
+    """The C5 model's per-layer decode step as it runs there: the one-launch
+    step kernel (attn_split_i8_mfma<4, 128, 2, STEP>) at C5's geometry (batch
+    16, 16 q / 8 kv heads, D=128, bf16, k=4 int8) over 512 archived blocks +
+    a 5-token tail, so the split count is the model's (4 > 1: the cross-split
+    arrival and merge, the queued passes after the first and split 0's
+    in-kernel append / archive beside streaming splits all run).  12 steps
+    cross two block boundaries; after every step all 16 sequences are
+    checked against the fp64 oracle on the streams' rows, and the archives
+    the kernel wrote against the two-append path's, bit for bit."""
+    B, Hkv, G, D, dt = C5["B"], C5["Hkv"], C5["G"], C5["D"], C5["dt"]
+    r = 8
+    S0 = 512 * r + 5
+    print("case fused step at C5 scale", flush=True)
+    ks, vs = build_streams(I8_C3, dt, B, Hkv, S0, D, 141, oracle)
+    ks_r, vs_r = build_streams(I8_C3, dt, B, Hkv, S0, D, 141, oracle)
+    L = N.lib()
+    g = torch.Generator(device=DEV).manual_seed(142)
+    for step in range(r + 4):
+        ns = L.fc_attention_splits(N.STORE_JPEG_I8, N.BF16, N.BF16, 4, ks.n_blocks, B, Hkv, G, D,
+                                   N.num_cus(torch.device(DEV)))
+        assert 1 < ns <= 64, ns
+        q = _tokens(g, B, Hkv * G, D, dt)
+        k, v = _tokens(g, B, Hkv, D, dt), _tokens(g, B, Hkv, D, dt)
+        out = fc.codec_decode_step(q, k, v, ks, vs)
+        assert L.fc_last_step_single_launch() == 1
+        ks_r.append(k)
+        vs_r.append(v)
+        _archives_equal(ks, ks_r)
+        _archives_equal(vs, vs_r)
+        assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), dt)
+
+
 @pytest.mark.parametrize("D,k,dt", [(80, 4, "bf16"), (96, 8, "f16")])
 def test_fused_decode_step_head_dims_80_96(D, k, dt, oracle):
     """The one-launch step on the matrix-core pass at head sizes that are not
@@ -247,15 +294,32 @@ def test_graph_replayed_steps_match_oracle(cfg, dt, G, oracle):
     with new query / key / value tokens copied into its input buffers: every
     replay's output against the oracle on the streams' rows (host counters
     advanced after each replay), with eager work between replays."""
+    r = cfg["block_size"]
+    print(f"case graph step vs oracle {cfg} {dt}", flush=True)
+    _graph_steps(cfg, dt, 2, 2, G, 128, 4 * r + 5, 3 * r + 2, 222, oracle)
+
+
+def test_graph_replayed_steps_c5_scale(oracle):
+    """Graph-replayed one-launch steps at C5's geometry (batch 16, 16 q / 8
+    kv heads, D=128, bf16, k=4 int8, 512 archived blocks + 5 tail tokens: 4
+    splits, the model's): 12 replays across two block boundaries, every
+    sequence of every replay against the fp64 oracle, and the archives the
+    replays wrote against the two-append path's, bit for bit."""
+    print("case graph step at C5 scale", flush=True)
+    _graph_steps(I8_C3, C5["dt"], C5["B"], C5["Hkv"], C5["G"], C5["D"], 512 * 8 + 5, 12, 151,
+                 oracle, check_archive=True, single_launch=True)
+
+
+def _graph_steps(cfg, dt, B, Hkv, G, D, S0, steps, seed, oracle, check_archive=False,
+                 single_launch=False):
     pytest.importorskip("transformers")
     from flashcodec_amd import graph
-    B, Hkv, D, r = 2, 2, 128, cfg["block_size"]
-    steps = 3 * r + 2
-    print(f"case graph step vs oracle {cfg} {dt}", flush=True)
-    ks, vs = build_streams(cfg, dt, B, Hkv, 4 * r + 5, D, 222, oracle)
+    ks, vs = build_streams(cfg, dt, B, Hkv, S0, D, seed, oracle)
+    if check_archive:
+        ks_r, vs_r = build_streams(cfg, dt, B, Hkv, S0, D, seed, oracle)
     cache = _Cache([_codec_layer(cfg, ks, vs)])
     graph.prepare(cache, steps + 1)
-    g = torch.Generator(device=DEV).manual_seed(223)
+    g = torch.Generator(device=DEV).manual_seed(seed + 1)
     q_in = torch.zeros((B, 1, Hkv * G, D), device=DEV, dtype=torch_dtype(dt)).transpose(1, 2)
     k_in = torch.zeros((B, 1, Hkv, D), device=DEV, dtype=torch_dtype(dt)).transpose(1, 2)
     v_in = torch.zeros_like(k_in)
@@ -266,14 +330,24 @@ def test_graph_replayed_steps_match_oracle(cfg, dt, G, oracle):
         k_in.copy_(_tokens(g, B, Hkv, D, dt))
         v_in.copy_(_tokens(g, B, Hkv, D, dt))
 
+    def check():
+        if check_archive:
+            ks_r.append(k_in.clone())
+            vs_r.append(v_in.clone())
+            _archives_equal(ks, ks_r)
+            _archives_equal(vs, vs_r)
+        assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q_in, ks, vs, D ** -0.5), dt)
+
     # one eager device-state step on the capture stream creates its workspace
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         fill()
         out = fc.codec_decode_step(q_in, k_in, v_in, ks, vs)
     torch.cuda.synchronize()
+    if single_launch:
+        assert N.lib().fc_last_step_single_launch() == 1
     graph.advance_host(cache)
-    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q_in, ks, vs, D ** -0.5), dt)
+    check()
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr, stream=stream):
         out = fc.codec_decode_step(q_in, k_in, v_in, ks, vs)
@@ -282,7 +356,7 @@ def test_graph_replayed_steps_match_oracle(cfg, dt, G, oracle):
         gr.replay()
         torch.cuda.synchronize()
         graph.advance_host(cache)
-        assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q_in, ks, vs, D ** -0.5), dt)
+        check()
         _ = (torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)).sum()
         torch.cuda.synchronize()
     graph.release(cache)                      # device counters == host counters, no overflow

@@ -69,8 +69,8 @@ def check(out, ref, dt):
     assert not (err > tol).any(), f"max err {err.max():.3e} vs max|ref| {np.abs(ref).max():.3e}"
 
 
-def streams(dt, B, Hkv, S, D, k, seed, oracle, group=0):
-    cfg = dict(mode="jpeg", block_size=8, keep_freqs=k, quant_bits=8)
+def streams(dt, B, Hkv, S, D, k, seed, oracle, group=0, r=8):
+    cfg = dict(mode="jpeg", block_size=r, keep_freqs=k, quant_bits=8)
     if group:
         cfg["quant_group"] = group
     x = [torch.from_numpy(oracle.ar1((B, Hkv, S, D), 0.9, seed + i)).to(torch_dtype(dt)).to(DEV)
@@ -96,17 +96,34 @@ CASES = [
     ("f16", 2, 2, 3, 64, 1, 8 * 12 + 1, 0, 32),
     ("bf16", 1, 2, 8, 256, 4, 8 * 9 + 2, 0, 32),
     ("bf16", 2, 2, 2, 128, 4, 77, 8 * 25 + 3, 32),
+    # other block sizes (the last field): r = 4 (s == r), 16 (the unrolled
+    # tap loop's limit) and 32 (the tap loop that is not unrolled), with
+    # chunked and tail-only prefills
+    ("bf16", 1, 2, 2, 128, 4, 4 * 50 + 3, 0, 0, 4),
+    ("f16", 2, 1, 4, 64, 2, 4 * 9 + 1, 4 * 30 + 2, 0, 4),
+    ("f16", 2, 2, 4, 128, 2, 16 * 20 + 9, 0, 0, 16),
+    ("bf16", 1, 2, 2, 128, 4, 45, 16 * 12 + 5, 0, 16),
+    ("bf16", 1, 2, 8, 256, 1, 16 * 6 + 15, 0, 32, 16),
+    ("bf16", 1, 2, 2, 64, 4, 32 * 10 + 17, 0, 0, 32),
+    ("f16", 1, 2, 2, 128, 4, 20, 0, 0, 32),
+    ("f16", 1, 1, 4, 128, 1, 50, 32 * 6 + 30, 0, 32),
+    ("bf16", 2, 2, 2, 128, 2, 32 * 5 + 31, 0, 32, 32),
 ]
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-G{c[3]}-D{c[4]}-k{c[5]}-S{c[6]}+{c[7]}"
-                                             + (f"-g{c[8]}" if len(c) > 8 else "")
-                                             for c in CASES])
+def _case_id(c):
+    return (f"{c[0]}-G{c[3]}-D{c[4]}-k{c[5]}-S{c[6]}+{c[7]}"
+            + (f"-g{c[8]}" if len(c) > 8 and c[8] else "")
+            + (f"-r{c[9]}" if len(c) > 9 else ""))
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_case_id(c) for c in CASES])
 def test_prefill_matches_causal_attention_on_the_view(case, oracle):
     dt, B, Hkv, G, D, k, S, S0 = case[:8]
     group = case[8] if len(case) > 8 else 0
+    r = case[9] if len(case) > 9 else 8
     print(f"case prefill {case}", flush=True)
-    ks, vs, (kx, vx) = streams(dt, B, Hkv, S0 + S, D, k, 40 + G + D + S, oracle, group)
+    ks, vs, (kx, vx) = streams(dt, B, Hkv, S0 + S, D, k, 40 + G + D + S, oracle, group, r)
     if S0:
         ks.append(kx[:, :, :S0])
         vs.append(vx[:, :, :S0])
@@ -142,12 +159,48 @@ def test_prefill_c5_prompt_shape(oracle):
     check(to_values(out)[:, :, rows], ref, dt)
 
 
-def tiny_qwen3(dtype=torch.bfloat16):
+def test_prefill_distance_from_the_reference_prefill(oracle):
+    """How far the default prefill (causal attention on the archive's stored
+    rows) sits from the reference's prefill (SDPA on the read() view, the
+    reconstruction rounded to bf16) at the C5 prompt's geometry: both within
+    the contract of the exact (fp64) reconstruction's attention, and from
+    each other within the sum of their distances to it.  Prints the three
+    distances (relative to max|out|)."""
+    dt, B, Hkv, G, D, S = "bf16", 1, 8, 2, 128, 1024 + 3
+    ks, vs, (kx, vx) = streams(dt, B, Hkv, S, D, 4, 91, oracle)
+    ks.append(kx)
+    vs.append(vx)
+    g = torch.Generator(device=DEV).manual_seed(92)
+    q = (torch.randn((B, Hkv * G, S, D), generator=g, device=DEV) / math.sqrt(D)).to(
+        torch.bfloat16)
+    arch = codec_prefill_attention(q, ks, vs)
+    kview, vview = ks.read(), vs.read()
+    ref_view = torch.nn.functional.scaled_dot_product_attention(
+        q, kview.repeat_interleave(G, dim=1), vview.repeat_interleave(G, dim=1), is_causal=True)
+    ks.discard_view()
+    vs.discard_view()
+    rows = list(range(0, S, 17)) + list(range(S - 9, S))
+    exact = causal_reference(to_values(q), view_oracle(oracle, ks), view_oracle(oracle, vs), 0,
+                             D ** -0.5, rows=rows)
+    a, v = to_values(arch)[:, :, rows], to_values(ref_view)[:, :, rows]
+    m = np.abs(exact).max()
+    d_arch, d_view = np.abs(a - exact).max() / m, np.abs(v - exact).max() / m
+    d_between = np.abs(a - v).max() / m
+    print(f"prefill distances / max|out|: archive-exact {d_arch:.2e}, view-exact {d_view:.2e}, "
+          f"archive-view {d_between:.2e}", flush=True)
+    check(to_values(arch)[:, :, rows], exact, dt)
+    assert d_view <= 4e-3
+    assert d_between <= d_arch + d_view + 1e-6
+
+
+def tiny_qwen3(dtype=torch.bfloat16, attn=None):
     from transformers import Qwen3Config, Qwen3ForCausalLM
     torch.manual_seed(3)
     cfg = Qwen3Config(vocab_size=256, hidden_size=256, intermediate_size=512,
                       num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=4,
                       head_dim=64, max_position_embeddings=1024, tie_word_embeddings=True)
+    if attn is not None:
+        cfg._attn_implementation = attn
     m = Qwen3ForCausalLM(cfg).eval()
     m.generation_config.eos_token_id = None
     return m.to(DEV, dtype)
@@ -187,3 +240,75 @@ def test_patched_prefill_runs_on_the_archive():
     for a, b in zip(results[False][0], results[True][0]):
         assert (a - b).abs().max().item() <= 3e-2 * a.abs().max().item()
     fc.remove_flash_codec(model)
+
+
+CFG_I8 = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+
+
+def _prefill_logits(model, ids, mask=None, on_archive=True):
+    from flashcodec_amd import patch_attention as pa
+    prev = pa.set_prefill_on_archive(on_archive)
+    try:
+        with torch.no_grad():
+            out = model(input_ids=ids, attention_mask=mask, use_cache=True)
+    finally:
+        pa.set_prefill_on_archive(prev)
+    return out.logits.float()
+
+
+def test_prefill_switch_off_is_the_reference_prefill():
+    """set_prefill_on_archive(False): the patched prefill is the reference's
+    own (the model's attention on the reconstructed view), so its logits equal
+    those of the codec cache without the attention patch, bit for bit."""
+    pytest.importorskip("transformers")
+    ids = torch.randint(1, 256, (2, 8 * 13 + 3), generator=torch.Generator().manual_seed(4)).to(DEV)
+    ref_model, model = tiny_qwen3(), tiny_qwen3()
+    fc.apply_flash_codec(ref_model, **CFG_I8)
+    fc.apply_flash_codec(model, materialization_free=True, **CFG_I8)
+    with torch.no_grad():
+        ref = ref_model(input_ids=ids, use_cache=True).logits.float()
+    got = _prefill_logits(model, ids, on_archive=False)
+    assert torch.equal(ref, got)
+    assert [getattr(m, "_flashcodec_prefills", 0) for m in fc.find_attention_modules(model)] \
+        == [0, 0]
+
+
+def test_padded_prompt_prefill_keeps_its_mask():
+    """A batch-1 prompt with padded (masked) key columns: the archive prefill
+    applies only the plain causal mask, so the patch runs the model's own
+    attention with the mask; the logits equal those with the archive prefill
+    switched off, and no module counts an archive prefill."""
+    pytest.importorskip("transformers")
+    ids = torch.randint(1, 256, (1, 8 * 9 + 5), generator=torch.Generator().manual_seed(6)).to(DEV)
+    mask = torch.ones_like(ids)
+    mask[:, :3] = 0                               # left padding
+    model = tiny_qwen3()
+    fc.apply_flash_codec(model, materialization_free=True, **CFG_I8)
+    off = _prefill_logits(model, ids, mask, on_archive=False)
+    on = _prefill_logits(model, ids, mask, on_archive=True)
+    assert torch.equal(on, off)
+    assert [getattr(m, "_flashcodec_prefills", 0) for m in fc.find_attention_modules(model)] \
+        == [0, 0]
+
+
+def test_explicit_causal_mask_prefill_on_the_archive():
+    """Eager-attention models pass the plain causal mask explicitly (an
+    additive float mask) even when nothing is padded: the patch recognises it
+    and runs the prefill on the archive (batch 2), whose logits track the
+    model's own attention on the view; a padded batch keeps the masked
+    path."""
+    pytest.importorskip("transformers")
+    ids = torch.randint(1, 256, (2, 8 * 11 + 6), generator=torch.Generator().manual_seed(8)).to(DEV)
+    model = tiny_qwen3(attn="eager")
+    fc.apply_flash_codec(model, materialization_free=True, **CFG_I8)
+    off = _prefill_logits(model, ids, on_archive=False)
+    on = _prefill_logits(model, ids, on_archive=True)
+    counts = [getattr(m, "_flashcodec_prefills", 0) for m in fc.find_attention_modules(model)]
+    assert counts == [1, 1]
+    assert (on - off).abs().max().item() <= 3e-2 * off.abs().max().item()
+    mask = torch.ones_like(ids)
+    mask[1, :4] = 0
+    assert torch.equal(_prefill_logits(model, ids, mask, on_archive=True),
+                       _prefill_logits(model, ids, mask, on_archive=False))
+    counts = [getattr(m, "_flashcodec_prefills", 0) for m in fc.find_attention_modules(model)]
+    assert counts == [1, 1]

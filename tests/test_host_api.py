@@ -166,3 +166,35 @@ def test_fused_step_codec_equality():
     assert not _same_codec(mk(mode="png", block_size=16, keep_ratio=0.25),
                            mk(mode="png", block_size=16, keep_ratio=0.5))
     assert not _same_codec(mk(mode="png", block_size=8), mk(mode="jpeg", block_size=8))
+
+
+def test_plain_causal_mask_recognition():
+    """The attention patch runs a prefill on the archive only under a mask
+    the kernel applies (the plain causal one): None, an all-kept 2-D padding
+    mask, or the exact causal pattern as a bool or additive float 4-D mask
+    (also over a longer key axis); padded or shifted masks are refused."""
+    import torch
+    from flashcodec_amd.patch_attention import _plain_causal
+    T, P0 = 5, 3
+    total = P0 + T
+    keys = torch.arange(total)
+    allowed = keys[None, :] <= torch.arange(P0, total)[:, None]
+    bmask = allowed[None, None].expand(2, 1, T, total).clone()
+    fmask = torch.where(bmask, 0.0, torch.finfo(torch.float32).min)
+    assert _plain_causal(None, T, total)
+    assert _plain_causal(torch.ones(2, total, dtype=torch.long), T, total)
+    assert _plain_causal(bmask, T, total)
+    assert _plain_causal(fmask, T, total)
+    longer = torch.cat([fmask, torch.full((2, 1, T, 4), torch.finfo(torch.float32).min)], -1)
+    assert _plain_causal(longer, T, total)
+    pad2d = torch.ones(2, total, dtype=torch.long)
+    pad2d[1, 0] = 0
+    assert not _plain_causal(pad2d, T, total)
+    padded = bmask.clone()
+    padded[1, :, :, :2] = False                   # left padding of sequence 1
+    assert not _plain_causal(padded, T, total)
+    assert not _plain_causal(torch.where(padded, 0.0, -1e9), T, total)
+    full = torch.ones_like(bmask)                 # bidirectional
+    assert not _plain_causal(full, T, total)
+    assert not _plain_causal(bmask[..., 1:], T, total)   # fewer keys than cached
+    assert not _plain_causal(object(), T, total)
