@@ -119,16 +119,25 @@ def cpu_model():
     return None
 
 
-def cpu_rate(fn, nbytes, min_seconds=1.0):
-    """GB/s of `fn` (a CPU oracle call over `nbytes` algorithmic bytes),
-    repeated until min_seconds have passed (one host thread)."""
-    n, t0 = 0, time.perf_counter()
-    while True:
+def torch_cpu_rate(fn, nbytes, reps=5, min_seconds=2.0):
+    """(GB/s, cores) of fn() — the reference's torch CPU path restated in
+    oracle/torch_path.py — on every affinity core of this host: the median
+    of at least `reps` timed calls (more while under `min_seconds`) after
+    one untimed call."""
+    import statistics
+    import torch
+    cores = len(os.sched_getaffinity(0))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < reps or (time.perf_counter() - t_start < min_seconds and len(times) < 100):
+        t0 = time.perf_counter()
         fn()
-        n += 1
-        dt = time.perf_counter() - t0
-        if dt >= min_seconds:
-            return round(nbytes * n / dt / 1e9, 3)
+        times.append(time.perf_counter() - t0)
+    torch.set_num_threads(prev)
+    return round(nbytes / statistics.median(times) / 1e9, 3), cores
 
 
 SETTLE_S = 0.25  # untimed calls before the warm-up steps of each measurement
@@ -235,18 +244,21 @@ def c2_mode(args):
     same = bool(torch.equal(st._coeffs[:, :, :n_tok // r], coeffs[:, :, :n_tok // r]) and
                 torch.equal(st._scales[:, :, :n_tok // r], scales[:, :, :n_tok // r]))
 
-    # the CPU oracle (the reference's algorithm restated in C++) on the whole
-    # workload, one host thread
-    from oracle import oracle as O
-    basis = fc.dct_basis(r, k).numpy()
-    xs = x.float().cpu().numpy()
-    _, cs, ss = O.jpeg_encode(xs, r, k, basis, "f16", quant=True)
-    alg_s = alg
-    cpu = {"unit": "GB/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
-           "sample": "the whole workload (128 sequences of 8192 tokens), C++ oracle",
-           "archive": cpu_rate(lambda: O.jpeg_encode(xs, r, k, basis, "f16", quant=True), alg_s),
-           "read": cpu_rate(lambda: O.jpeg_decode(None, r, basis, "f16", codes=cs, scales=ss),
-                            alg_s)}
+    # the reference's torch CPU path (oracle/torch_path.py: dct_compress +
+    # quantize, dequantize + dct_decompress + cast) on the whole workload,
+    # every host core
+    from oracle import torch_path as T
+    basis = fc.dct_basis(r, k)
+    xs = x.cpu()
+    cq, sq = T.quantize(T.dct_compress(xs, r, basis))
+    arch_gbs, cores = torch_cpu_rate(lambda: T.quantize(T.dct_compress(xs, r, basis)), alg)
+    read_gbs, _ = torch_cpu_rate(
+        lambda: T.dct_decompress(T.dequantize(cq, sq), r, basis).to(torch.float16), alg)
+    cpu = {"unit": "GB/s", "cores": cores, "kind": "port", "cpu_model": cpu_model(),
+           "sample": "the whole workload (128 sequences of 8192 tokens) through the "
+                     "reference's torch CPU codec (restated in oracle/torch_path.py), median "
+                     "of >= 5 calls",
+           "archive": arch_gbs, "read": read_gbs}
     print(json.dumps({
         "metric": "jpeg int8 archive / read GB/s (C2)", "unit": "GB/s", "n_gpus": 1,
         "archive_GBs": round(alg / (t_arch * 1e-3) / 1e9, 1),
@@ -331,30 +343,74 @@ def c4_mode(args):
             p_ = torch.softmax((q @ kk.transpose(-1, -2).contiguous()) * d_ ** -0.5, dim=-1)
             ref = p_ @ vv
             res[tag]["vs_dense_max_abs_err"] = float((o - ref).abs().max())
-        # the CPU oracle on the whole stream (one host thread); attention on
-        # one of the 16 (batch, kv head) sequences
-        from oracle import oracle as O
-        xs = x["k"].cpu().numpy()
-        dl, an = O.png_encode(xs, r, keep)
-        alg_s = alg_codec
-        cpu = {"unit": "GB/s", "cores": 1, "kind": "port", "cpu_model": cpu_model(),
-               "sample": "archive / read: the whole stream; attention: 1 of the 16 (batch, kv "
-                         "head) sequences (16384 tokens, 4 query heads); C++ oracle",
-               "archive": cpu_rate(lambda: O.png_encode(xs, r, keep), alg_s),
-               "read": cpu_rate(lambda: O.png_decode(dl, an, "f32"), alg_s)}
-        if keep == 1.0:
-            # fp64 decode attention of the sample's 4 query heads over its
-            # stored rows (png rows -> fp64 as the oracle defines them)
-            rk = O.stored_rows_png(ks._deltas[:1, :1, :nb].cpu().numpy(),
-                                   ks._anchors[:1, :1, :nb].cpu().numpy())
-            rv = O.stored_rows_png(vs._deltas[:1, :1, :nb].cpu().numpy(),
-                                   vs._anchors[:1, :1, :nb].cpu().numpy())
-            qs = q[:1, :hq // h_, 0].cpu().numpy()
-            A = O.synthesis_matrix("png", r)
-            cpu["attention"] = cpu_rate(
-                lambda: O.attention(qs, rk, rv, None, None, A, d_ ** -0.5), alg_attn // (b_ * h_))
-        res[tag]["cpu_baseline"] = cpu
+        # the reference's torch CPU path (oracle/torch_path.py) on every host
+        # core: png_filter / png_reconstruct of the whole stream; decode
+        # attention (png rows, fp32) on one of the 16 (batch, kv head)
+        # sequences with its 4 query heads
+        from oracle import torch_path as T
+        xs = x["k"].cpu()
+        dl, an = T.png_filter(xs, r, keep)
+        arch_gbs, cores = torch_cpu_rate(lambda: T.png_filter(xs, r, keep), alg_codec)
+        read_gbs, _ = torch_cpu_rate(lambda: T.png_reconstruct(dl, an), alg_codec)
+        rk = T.png_rows(ks._deltas[:1, :1, :nb].cpu(), ks._anchors[:1, :1, :nb].cpu())
+        rv = T.png_rows(vs._deltas[:1, :1, :nb].cpu(), vs._anchors[:1, :1, :nb].cpu())
+        qs = q[:1, :hq // h_].cpu()
+        A = torch.tril(torch.ones(r, r))
+        attn_gbs, _ = torch_cpu_rate(
+            lambda: T.decode_attention(qs, rk, rv, None, None, A, d_ ** -0.5),
+            alg_attn // (b_ * h_))
+        res[tag]["cpu_baseline"] = {
+            "unit": "GB/s", "cores": cores, "kind": "port", "cpu_model": cpu_model(),
+            "sample": "archive / read: the whole stream; attention: 1 of the 16 (batch, kv "
+                      "head) sequences (16384 tokens, 4 query heads); the reference's torch CPU "
+                      "path (restated in oracle/torch_path.py), median of >= 5 calls",
+            "archive": arch_gbs, "read": read_gbs, "attention": attn_gbs}
         log(f"bench c4 keep {keep}: {res[tag]}")
+
+    # packed Top-M archives (this build's fixed-rate format; the reference
+    # stores the same deltas dense): archive, read and decode attention
+    for keep in (0.25, 0.5):
+        codec = fc.make_codec(mode="png", block_size=r, keep_ratio=keep, packed=True)
+        m_keep = codec.keep_m
+        vals = torch.empty((b_, h_, nb, m_keep, d_), dtype=torch.float32, device=dev)
+        masks = torch.empty((b_, h_, nb, d_), dtype=torch.int32, device=dev)
+        anchors = torch.empty((b_, h_, nb, d_), dtype=torch.float32, device=dev)
+        out = torch.empty_like(x["k"])
+        store = b_ * h_ * nb * d_ * 4 * (m_keep + 2)          # values + mask words + anchors
+        alg_pk_codec = b_ * h_ * s_ * d_ * 4 + store
+        alg_pk_attn = 2 * store + 2 * b_ * hq * d_ * 4
+
+        def archive_pk():
+            P.encode_packed_into(x["k"], r, m_keep, vals, masks, anchors, nb, 0, nb, s_)
+
+        def read_pk():
+            P.decode_packed_into(vals, masks, anchors, b_, h_, nb, 0, nb, d_, r, m_keep, out, s_)
+
+        t_arch = timed(archive_pk, args.steps, args.warmup)
+        t_read = timed(read_pk, args.steps, args.warmup)
+        ks, vs = _CodecStream(codec), _CodecStream(codec)
+        ks.append(x["k"])
+        vs.append(x["v"])
+        t_attn = timed(lambda: fc.codec_decode_attention(q, ks, vs), args.steps, args.warmup)
+        sets = [(ks, vs)] + [(archive_copy(ks), archive_copy(vs)) for _ in range(7)]
+        t_rot = timed_cycle(lambda i: fc.codec_decode_attention(q, *sets[i % 8]), args.steps,
+                            args.warmup)
+        del sets
+        torch.cuda.empty_cache()
+        res[f"packed_keep{keep}"] = {
+            "kept_deltas": m_keep, "store_bytes_per_stream": store,
+            "dense_store_bytes_per_stream": b_ * h_ * nb * d_ * 4 * r,
+            "archive_GBs": round(alg_pk_codec / (t_arch * 1e-3) / 1e9, 1),
+            "read_GBs": round(alg_pk_codec / (t_read * 1e-3) / 1e9, 1),
+            "attention_GBs": round(alg_pk_attn / (t_attn * 1e-3) / 1e9, 1),
+            "attention_rotating_GBs": round(alg_pk_attn / (t_rot * 1e-3) / 1e9, 1),
+            "attention_rotating_hbm_frac": round(alg_pk_attn / (t_rot * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                                 4),
+            "archive_us": round(t_arch * 1e3, 2), "read_us": round(t_read * 1e3, 2),
+            "attention_us": round(t_attn * 1e3, 2), "attention_rotating_us": round(t_rot * 1e3, 2),
+            "algorithmic_bytes_attention": alg_pk_attn,
+            "cpu_baseline": "the reference stores these deltas dense: see keep0.25 (same rows)"}
+        log(f"bench c4 packed keep {keep}: {res[f'packed_keep{keep}']}")
     print(json.dumps(res))
 
 
@@ -382,12 +438,18 @@ def c1_mode(args):
     xn = x.cpu().numpy()
     coef = O.jpeg_encode(xn, r, k, basis, "f32")
     ref = O.jpeg_decode(coef, r, basis, "f32")
-    cpu = {"unit": "GB/s", "cores": 1, "kind": "port", "sample": "the whole C1 stream, C++ oracle",
-           "cpu_model": cpu_model(),
-           "archive": cpu_rate(lambda: O.jpeg_encode(xn, r, k, basis, "f32"),
-                               b_ * h_ * s_ * d_ * 4 + b_ * h_ * (s_ // r) * k * d_ * 4),
-           "read": cpu_rate(lambda: O.jpeg_decode(coef, r, basis, "f32"),
-                            b_ * h_ * s_ * d_ * 4 + b_ * h_ * (s_ // r) * k * d_ * 4)}
+    # the reference's torch CPU path (oracle/torch_path.py), every host core
+    from oracle import torch_path as T
+    bt = fc.dct_basis(r, k)
+    xc = x.cpu()
+    ct = T.dct_compress(xc, r, bt)
+    alg_c = b_ * h_ * s_ * d_ * 4 + b_ * h_ * (s_ // r) * k * d_ * 4
+    arch_gbs, cores = torch_cpu_rate(lambda: T.dct_compress(xc, r, bt), alg_c)
+    read_gbs, _ = torch_cpu_rate(lambda: T.dct_decompress(ct, r, bt), alg_c)
+    cpu = {"unit": "GB/s", "cores": cores, "kind": "port", "cpu_model": cpu_model(),
+           "sample": "the whole C1 stream through the reference's torch CPU codec (restated in "
+                     "oracle/torch_path.py), median of >= 5 calls",
+           "archive": arch_gbs, "read": read_gbs}
     bit_exact = bool(np.array_equal(rec.cpu().numpy().view(np.uint32), np.asarray(ref, np.float32).view(np.uint32)))
     alg = b_ * h_ * s_ * d_ * 4 + b_ * h_ * (s_ // r) * k * d_ * 4
     t_arch = timed(lambda: _CodecStream(st.codec).append(x), args.steps, args.warmup)
@@ -758,7 +820,7 @@ def archive_copy(st):
     buffers): one more set for the rotating measurement."""
     from flashcodec_amd.cache import _CodecStream
     c = _CodecStream(st.codec)
-    for name in ("_coeffs", "_scales", "_deltas", "_anchors"):
+    for name in ("_coeffs", "_scales", "_deltas", "_anchors", "_packed", "_packed_mask"):
         t = getattr(st, name, None)
         if t is not None:
             setattr(c, name, t.clone())

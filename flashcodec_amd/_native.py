@@ -17,7 +17,7 @@ F32, F16, BF16, I8 = 0, 1, 2, 3
 OK, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_SCRATCH = 0, -1, -2, -3, -5
 NOALLOC_SCRATCH_BYTES = 16 << 20
 PASS_AUTO, PASS_VECTOR, PASS_STATIC = 0, 1, 2
-STORE_JPEG_I8, STORE_JPEG_FP, STORE_PNG, STORE_JPEG_I8G = 0, 1, 2, 3
+STORE_JPEG_I8, STORE_JPEG_FP, STORE_PNG, STORE_JPEG_I8G, STORE_PNG_PACKED = 0, 1, 2, 3, 4
 MAX_BLOCK = 64
 MAX_HEAD_DIM = 512
 
@@ -33,7 +33,7 @@ class StreamView(ctypes.Structure):
     """fc_stream_view: one KV stream as seen by the decode attention."""
     _fields_ = [
         ("rows", _vp), ("scales", _vp), ("anchors", _vp), ("cap", _i64),
-        ("raw", _vp), ("raw_sb", _i64), ("raw_sh", _i64), ("raw_st", _i64),
+        ("raw", _vp), ("raw_sb", _i64), ("raw_sh", _i64), ("raw_st", _i64), ("masks", _vp),
     ]
 
 
@@ -41,7 +41,7 @@ class StepStream(ctypes.Structure):
     """fc_step_stream: one stream of a layer for fc_decode_step."""
     _fields_ = [
         ("rows", _vp), ("scales", _vp), ("anchors", _vp), ("cap", _i64), ("tail", _vp),
-        ("token", _vp), ("tok_sb", _i64), ("tok_sh", _i64),
+        ("token", _vp), ("tok_sb", _i64), ("tok_sh", _i64), ("masks", _vp),
     ]
 
 
@@ -81,6 +81,12 @@ SIGNATURES = {
                              _int, _vp, _vp, _i64, _i64, _vp]),
     "fc_png_decode": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp,
                              _i64, _i64, _i64, _i64, _vp]),
+    "fc_png_encode_packed": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                    _int, _int, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "fc_png_decode_packed": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+                                    _int, _int, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "fc_png_unpack": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp,
+                             _i64, _vp]),
     "fc_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _int]),
     "fc_attention_default_splits": (_int, [_i64, _i64, _i64, _i64, _int]),
     "fc_attention_splits": (_int, [_int, _int, _int, _int, _i64, _i64, _i64, _i64, _i64, _int]),

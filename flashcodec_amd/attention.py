@@ -66,6 +66,17 @@ def _jpeg_kind(codec):
     return N.STORE_JPEG_I8G if codec.quant_group else N.STORE_JPEG_I8
 
 
+def _store_kind(codec):
+    """(store kind, stored rows per block) of a codec's archive for the
+    decode attention: jpeg k rows; png r rows (anchor + deltas), packed png
+    keep_m value slots."""
+    if codec.name == "jpeg":
+        return _jpeg_kind(codec), codec.keep_freqs
+    if codec.packed:
+        return N.STORE_PNG_PACKED, codec.keep_m
+    return N.STORE_PNG, codec.block_size
+
+
 FUSED_MERGE_MAX_SPLITS = 64   # the matrix-core pass merges in-kernel up to this many splits
 
 
@@ -87,6 +98,10 @@ def _view(stream, keep):
         if c.name == "jpeg":
             v.rows = stream._coeffs.data_ptr()
             v.scales = stream._scales.data_ptr() if c.quantized else None
+        elif c.packed:
+            v.rows = stream._packed.data_ptr()
+            v.anchors = stream._anchors.data_ptr()
+            v.masks = stream._packed_mask.data_ptr()
         else:
             v.rows = stream._deltas.data_ptr()
             v.anchors = stream._anchors.data_ptr()
@@ -174,12 +189,7 @@ def codec_decode_attention(query, key_stream, value_stream, scale=None, impl="au
 
     c = ks.codec
     r = ks.block_size
-    if c.name == "jpeg":
-        kind = _jpeg_kind(c)
-        s = c.keep_freqs
-    else:
-        kind = N.STORE_PNG
-        s = r
+    kind, s = _store_kind(c)
     q = query if query.stride(-1) == 1 else query.contiguous()
     out = torch.empty_like(q)
     dev = q.device
@@ -274,14 +284,11 @@ def _step_args(ks, vs, query, tokens):
     a = N.StepArgs()
     a.q_dtype = N.dtype_code(query.dtype)
     a.B, a.Hq, a.Hkv, a.D = B, Hq, Hkv, D
+    a.store_kind, a.s = _store_kind(c)
     if c.name == "jpeg":
-        a.store_kind = _jpeg_kind(c)
-        a.s = c.keep_freqs
         a.quant_bits = c.quant_bits
         a.basis = dct_basis_device(r, c.keep_freqs, dev).data_ptr()
     else:
-        a.store_kind = N.STORE_PNG
-        a.s = r
         a.keep_m = c.keep_m
     a.stream_dtype = N.dtype_code(ks.dtype)
     a.r = r
@@ -304,7 +311,8 @@ def _same_codec(a, b):
             and getattr(a, "keep_freqs", None) == getattr(b, "keep_freqs", None)
             and getattr(a, "quant_bits", None) == getattr(b, "quant_bits", None)
             and getattr(a, "quant_group", None) == getattr(b, "quant_group", None)
-            and getattr(a, "keep_ratio", None) == getattr(b, "keep_ratio", None))
+            and getattr(a, "keep_ratio", None) == getattr(b, "keep_ratio", None)
+            and getattr(a, "packed", None) == getattr(b, "packed", None))
 
 
 def codec_decode_step(query, key_tokens, value_tokens, key_stream, value_stream, scale=None):
@@ -358,6 +366,7 @@ def codec_decode_step(query, key_tokens, value_tokens, key_stream, value_stream,
         sv.rows = arch[0].data_ptr()
         sv.scales = arch[1].data_ptr() if (jpeg and len(arch) > 1) else None
         sv.anchors = None if jpeg else arch[1].data_ptr()
+        sv.masks = arch[2].data_ptr() if (not jpeg and len(arch) > 2) else None
         sv.cap = st._capacity
         sv.tail = st._raw_buf.data_ptr()
         sv.token, sv.tok_sb, sv.tok_sh = tok.data_ptr(), tok.stride(0), tok.stride(1)
@@ -400,6 +409,7 @@ def _decode_step_device_state(query, key_tokens, value_tokens, ks, vs, scale, st
         sv.rows = arch[0].data_ptr()
         sv.scales = arch[1].data_ptr() if (jpeg and len(arch) > 1) else None
         sv.anchors = None if jpeg else arch[1].data_ptr()
+        sv.masks = arch[2].data_ptr() if (not jpeg and len(arch) > 2) else None
         sv.cap = st._capacity
         sv.tail = st._raw_buf.data_ptr()
         sv.token, sv.tok_sb, sv.tok_sh = tok.data_ptr(), tok.stride(0), tok.stride(1)

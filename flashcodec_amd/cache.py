@@ -49,16 +49,20 @@ _FIRST_CAPACITY = 16   # archive blocks of a stream's first allocation
 
 
 def make_codec(mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0, quant_bits=0,
-               quant_group=0):
+               quant_group=0, packed=False):
     """Codec instance from a mode name (flashcodec/cache.py:39-54); png keeps
-    fp32 deltas on purpose and rejects quant_bits.  quant_group=32 (jpeg with
-    quant_bits=8; this build's extension) scales every 32 features of a
-    coefficient row separately."""
+    fp32 deltas on purpose and rejects quant_bits.  This build's extensions:
+    quant_group=32 (jpeg with quant_bits=8) scales every 32 features of a
+    coefficient row separately; packed=True (png with keep_ratio < 1) stores
+    only the Top-M surviving deltas of each (block, feature) plus a mask
+    word."""
     if mode == "png":
         if quant_bits or quant_group:
             raise ValueError("quant_bits is only supported for mode='jpeg' "
                              "(the png lossless tier must keep fp32 deltas)")
-        return PNGCodec(block_size=block_size, keep_ratio=keep_ratio)
+        return PNGCodec(block_size=block_size, keep_ratio=keep_ratio, packed=packed)
+    if packed:
+        raise ValueError("packed=True is a png option (Top-M delta packing)")
     if mode == "jpeg":
         return JPEGCodec(block_size=block_size, keep_freqs=keep_freqs, quant_bits=quant_bits,
                          quant_group=quant_group)
@@ -117,6 +121,7 @@ class _CodecStream:
         self._capacity = 0       # allocated archive blocks
         self._coeffs = self._scales = None     # jpeg archive
         self._deltas = self._anchors = None    # png archive
+        self._packed = self._packed_mask = None  # packed png archive
         self._raw_buf = None     # (B, H, r, D) tail buffer in the stream dtype
         self._n_raw = 0          # tokens in the tail (t < r)
         self._tail_rows = None   # per-row (B, H, 1, D) views of the tail buffer
@@ -178,6 +183,12 @@ class _CodecStream:
         """(attribute, shape, dtype) of every archive buffer at capacity cap
         (the reference layout, flashcodec/cache.py:94-104)."""
         c = self.codec
+        if c.name == "png" and c.packed:
+            # packed Top-M deltas: slot values, mask words (kept steps and the
+            # signs of the pruned ones), anchors
+            return [("_packed", (B, H, cap, c.keep_m, D), torch.float32),
+                    ("_anchors", (B, H, cap, D), self.dtype),
+                    ("_packed_mask", (B, H, cap, D), torch.int32)]
         if c.name == "png":
             return [("_deltas", (B, H, cap, c.block_size - 1, D), torch.float32),
                     ("_anchors", (B, H, cap, D), self.dtype)]
@@ -189,6 +200,8 @@ class _CodecStream:
         return spec
 
     def _archive_tensors(self):
+        if self.codec.name == "png" and self.codec.packed:
+            return (self._packed, self._anchors, self._packed_mask)
         if self.codec.name == "png":
             return (self._deltas, self._anchors)
         return (self._coeffs, self._scales) if self.codec.quantized else (self._coeffs,)
@@ -219,7 +232,10 @@ class _CodecStream:
         if head.stride(-1) != 1:
             head = head.contiguous()
         c = self.codec
-        if c.name == "png":
+        if c.name == "png" and c.packed:
+            _png.encode_packed_into(head, r, c.keep_m, self._packed, self._packed_mask,
+                                    self._anchors, self._capacity, self.n_blocks, m, m * r)
+        elif c.name == "png":
             _png.encode_into(head, r, c.keep_m, self._deltas, self._anchors, self._capacity,
                              self.n_blocks, m, m * r)
         else:
@@ -237,7 +253,11 @@ class _CodecStream:
         c, r = self.codec, self.block_size
         like = self._archive_tensors()[0]
         B, H, D = like.shape[0], like.shape[1], like.shape[-1]
-        if c.name == "png":
+        if c.name == "png" and c.packed:
+            _png.decode_packed_into(self._packed, self._packed_mask, self._anchors, B, H,
+                                    self._capacity, first, count, D, r, c.keep_m, out, out_len,
+                                    token0)
+        elif c.name == "png":
             _png.decode_into(self._deltas, self._anchors, B, H, self._capacity, first, count, D,
                              r, out, out_len, token0)
         else:
@@ -446,10 +466,10 @@ class CodecKVCache:
     """
 
     def __init__(self, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0,
-                 quant_bits=0, quant_group=0):
+                 quant_bits=0, quant_group=0, packed=False):
         self.mode = mode
         self.codec = make_codec(mode, block_size, keep_freqs, keep_ratio, quant_bits=quant_bits,
-                                quant_group=quant_group)
+                                quant_group=quant_group, packed=packed)
         self._pairs = {}     # layer index -> _KVPair
 
     def _pair(self, layer_idx):
@@ -547,11 +567,11 @@ class FlashCodecLayer(_HFDynamicLayer):
     (flashcodec/cache.py:446-544)."""
 
     def __init__(self, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0, quant_bits=0,
-                 quant_group=0):
+                 quant_group=0, packed=False):
         super().__init__()
         self.mode = mode
         self.codec = make_codec(mode, block_size, keep_freqs, keep_ratio, quant_bits=quant_bits,
-                                quant_group=quant_group)
+                                quant_group=quant_group, packed=packed)
         self._pair = _KVPair(self.codec)
 
     @property
@@ -665,7 +685,7 @@ class FlashCodecCache(_HFCache):
     """
 
     def __init__(self, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0, quant_bits=0,
-                 quant_group=0):
+                 quant_group=0, packed=False):
         if not HAS_HF_CACHE:
             raise ImportError("FlashCodecCache requires transformers 5.x; use CodecKVCache "
                               "when transformers is unavailable.")
@@ -673,6 +693,8 @@ class FlashCodecCache(_HFCache):
                    keep_ratio=keep_ratio, quant_bits=quant_bits)
         if quant_group:
             cfg["quant_group"] = quant_group
+        if packed:
+            cfg["packed"] = True
         super().__init__(layers=None, layer_class_to_replicate=partial(FlashCodecLayer, **cfg))
         self._remember(cfg)
 
@@ -687,7 +709,7 @@ class FlashCodecCache(_HFCache):
 
     @classmethod
     def from_config(cls, config, mode="jpeg", block_size=8, keep_freqs=2, keep_ratio=1.0,
-                    quant_bits=0, per_layer=None, quant_group=0):
+                    quant_bits=0, per_layer=None, quant_group=0, packed=False):
         """Per-layer cache for a model config: codec layers where the model
         uses full attention (each optionally overridden through
         ``per_layer[index]``), transformers' own layers elsewhere."""
@@ -696,6 +718,8 @@ class FlashCodecCache(_HFCache):
                    keep_ratio=keep_ratio, quant_bits=quant_bits)
         if quant_group:
             cfg["quant_group"] = quant_group
+        if packed:
+            cfg["packed"] = True
         layers = [FlashCodecLayer(**kw) if kind == "full_attention"
                   else DYNAMIC_LAYER_TYPE_MAPPING[kind](**kw)
                   for kind, kw in _layer_plan(config, per_layer, cfg)]

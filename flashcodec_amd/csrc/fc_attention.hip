@@ -1147,6 +1147,22 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G, i
 int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, int64_t nb,
                         int64_t B, int64_t Hkv, int64_t G, int64_t D, int n_cu) {
   if (nb <= 0) return 0;
+  if (n_cu <= 0) n_cu = 256;
+  if (store_kind == FC_STORE_PNG_PACKED) {
+    // one round of the packed png pass's workgroups (two per compute unit),
+    // at least one iteration (256 / D blocks) per wavefront and at most
+    // max(16, iterations / 10) splits, within the fused merge's limit
+    const int64_t groups = (G + 15) / 16;
+    const int64_t cols = std::max<int64_t>(1, B * Hkv * groups);
+    int64_t want = (2 * (int64_t)n_cu + cols - 1) / cols;
+    const int64_t per_it = D > 0 && D <= 256 ? std::max<int64_t>(1, 256 / D) : 1;
+    const int64_t nit = (nb + per_it - 1) / per_it;
+    want = std::min<int64_t>(want, std::max<int64_t>(1, nit / 4));
+    want = std::min<int64_t>(want, std::max<int64_t>(16, nit / 10));
+    want = std::max<int64_t>(1, std::min<int64_t>(want, fc::kFuseMaxSplitsPk));
+    const int64_t bps = (nb + want - 1) / want;
+    return (int)((nb + bps - 1) / bps);
+  }
   const bool png_mfma =
       store_kind == FC_STORE_PNG && fc::png_mfma_shape_supported(q_dtype, stream_dtype, D, s);
   const bool mfma = (png_mfma ||
@@ -1326,6 +1342,7 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
   if (D > FC_MAX_HEAD_DIM || r > FC_MAX_BLOCK || n_raw > FC_MAX_BLOCK) return FC_ERR_UNSUPPORTED;
   if (r < 1 || s < 1 || s > FC_MAX_BLOCK) return FC_ERR_ARG;
   if (store_kind == FC_STORE_PNG && s != r) return FC_ERR_ARG;
+  if (store_kind == FC_STORE_PNG_PACKED && (s >= r || r > 16)) return FC_ERR_ARG;
   if (nb > 0) {
     if (!A || !key->rows || !value->rows || !workspace) return FC_ERR_ARG;
     if (n_splits < 1 || n_splits > kMaxSplits) return FC_ERR_ARG;
@@ -1333,7 +1350,10 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
         (!key->scales || !value->scales))
       return FC_ERR_ARG;
     if (store_kind == FC_STORE_JPEG_I8G && D % 32) return FC_ERR_ARG;
-    if (store_kind == FC_STORE_PNG && (!key->anchors || !value->anchors)) return FC_ERR_ARG;
+    if ((store_kind == FC_STORE_PNG || store_kind == FC_STORE_PNG_PACKED) &&
+        (!key->anchors || !value->anchors))
+      return FC_ERR_ARG;
+    if (store_kind == FC_STORE_PNG_PACKED && (!key->masks || !value->masks)) return FC_ERR_ARG;
     if (nb > key->cap || nb > value->cap) return FC_ERR_ARG;
   } else {
     n_splits = 0;
@@ -1352,7 +1372,27 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
   const int64_t mstride = counter_stride(2 * B * Hkv * ((G + 15) / 16));
 
   const bool grouped = store_kind == FC_STORE_JPEG_I8G;
-  if (nb > 0 && (parts & kPartSplit) &&
+  if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_PNG_PACKED) {
+    // packed png archives have one pass (no vector-ALU form)
+    if (!split_pngpk_supported(q, q_dtype, q_sb, q_sh, D, r, s, stream_dtype, key, value) ||
+        mstride == 0)
+      return FC_ERR_UNSUPPORTED;
+    if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
+    const bool fuse = (parts & kPartMerge) && n_splits <= kFuseMaxSplitsPk;
+    MfmaFuse fz{};
+    if (fuse) {
+      fz.raw_dtype = stream_dtype;
+      fz.n_raw = n_raw;
+      fz.out = out;
+      fz.o_sb = o_sb;
+      fz.o_sh = o_sh;
+    }
+    const int rc = launch_split_pngpk(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, stream_dtype,
+                                      nb, key, value, scale_log2, pm, pl, pacc, n_splits,
+                                      counters, kCounterWords, mstride, fuse ? &fz : nullptr,
+                                      nullptr, st);
+    if (rc != FC_OK || fuse) return rc;
+  } else if (nb > 0 && (parts & kPartSplit) &&
       i8_mfma_takes(store_kind, q, q_dtype, q_sb, q_sh, D, s, key, value) && mstride > 0 &&
       mfma_split_allowed()) {
     if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
@@ -1401,7 +1441,7 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                                      o_sb, o_sh, pm, pl, pacc, n_splits,
                                      fuse ? counters : nullptr, nullptr, st);
     if (rc != FC_OK || fuse) return rc;
-  } else if (nb > 0) {
+  } else if (nb > 0 && store_kind != FC_STORE_PNG_PACKED) {
     // merge only: the split geometry must still be consistent
     if (D % 8) return FC_ERR_UNSUPPORTED;
   }
@@ -1455,6 +1495,9 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
       (!key->scales || !value->scales))
     return FC_ERR_ARG;
   if (store_kind == FC_STORE_PNG && (!key->anchors || !value->anchors || s != r)) return FC_ERR_ARG;
+  if (store_kind == FC_STORE_PNG_PACKED &&
+      (!key->anchors || !value->anchors || !key->masks || !value->masks || s >= r))
+    return FC_ERR_ARG;
   const int64_t G = Hq / Hkv;
   const int n_splits =
       fc_attention_splits(store_kind, stream_dtype, q_dtype, s, nb_hint, B, Hkv, G, D, n_cu);
@@ -1484,6 +1527,20 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                                 A, scale * kLog2e, pm, pl, pacc, n_splits, counters,
                                 kCounterWords, mstride, &fz, st,
                                 store_kind == FC_STORE_JPEG_I8G);
+  }
+  if (store_kind == FC_STORE_PNG_PACKED) {
+    if (!split_pngpk_supported(q, q_dtype, q_sb, q_sh, D, r, s, stream_dtype, key, value) ||
+        mstride == 0 || n_splits > kFuseMaxSplitsPk)
+      return FC_ERR_UNSUPPORTED;
+    MfmaFuse fz{};
+    fz.raw_dtype = stream_dtype;
+    fz.n_raw = 0;  // taken from the state
+    fz.out = out;
+    fz.o_sb = o_sb;
+    fz.o_sh = o_sh;
+    return launch_split_pngpk(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, stream_dtype, nb_hint,
+                              key, value, scale * kLog2e, pm, pl, pacc, n_splits, counters,
+                              kCounterWords, mstride, &fz, state, st);
   }
   if (store_kind == FC_STORE_PNG &&
       split_png_mfma_supported(q, q_dtype, q_sb, q_sh, D, r, stream_dtype, key, value) &&

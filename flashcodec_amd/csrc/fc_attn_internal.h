@@ -123,6 +123,21 @@ int launch_split_png_mfma(const void* q, int64_t q_sb, int64_t q_sh, int64_t B, 
                           int64_t counter_words, int64_t stride, const MfmaFuse* fuse,
                           const int64_t* state, hipStream_t st);
 
+// The packed png split pass (fc_attn_pngpk.hip): fp32 / fp16 / bf16
+// queries and anchors, D in {64, 128, 256}, r <= 16, keep_m <= 8; `state`
+// as the fused decode step's device counters (or NULL).
+constexpr int kFuseMaxSplitsPk = 64;  // the fused merge's split limit (kFuseMaxSplits)
+bool pngpk_shape_supported(int q_dtype, int stream_dtype, int64_t D, int r, int keep_m);
+bool split_pngpk_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
+                           int r, int keep_m, int stream_dtype, const fc_stream_view* key,
+                           const fc_stream_view* value);
+int launch_split_pngpk(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
+                       int64_t Hq, int64_t Hkv, int64_t D, int r, int keep_m, int stream_dtype,
+                       int64_t nb, const fc_stream_view* key, const fc_stream_view* value,
+                       float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
+                       unsigned int* counters, int64_t counter_words, int64_t stride,
+                       const MfmaFuse* fuse, const int64_t* state, hipStream_t st);
+
 // fc_decode_attention's body: validates the arguments and enqueues the
 // requested parts (kPartSplit: the split pass over the archived blocks;
 // kPartMerge: the merge of the split partials with the raw tail, fused into
@@ -149,9 +164,11 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
 
 // png archive of one block of a decode step's tail, gated like
 // jpeg_encode_gated.
+// masks != NULL: the packed layout (deltas = the value store).
 int png_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
                      int64_t x_sh, int64_t x_ss, int64_t D, int r, int keep_m, float* deltas,
-                     void* anchors, int64_t cap, void* stream, const int64_t* gate);
+                     void* anchors, int64_t cap, void* stream, const int64_t* gate,
+                     uint32_t* masks = nullptr);
 
 // jpeg archive of one block of a decode step's tail, gated on the device:
 // runs only when gate[1] == r - 1 and writes block gate[0] (< cap).

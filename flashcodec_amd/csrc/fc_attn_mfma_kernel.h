@@ -120,6 +120,11 @@ struct MfmaArgs {
   const void* vanch;
   const float* kdel;
   const float* vdel;
+  // packed png archives (fc_attn_pngpk.hip): kdel / vdel are the value
+  // stores (B, H, cap, keep_m, D), kmask / vmask the mask words (B, H, cap, D)
+  const uint32_t* kmask;
+  const uint32_t* vmask;
+  int keep_m;
 };
 
 constexpr int kMThreads = 256;

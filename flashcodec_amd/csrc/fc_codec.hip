@@ -580,12 +580,15 @@ __device__ __forceinline__ uint64_t topm_mask(const uint32_t (&key)[RMAX], int n
 
 typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
 
-template <typename T, int VEC, int RMAX, bool GATED = false>
+// PACK: the packed Top-M layout (fc_png_encode_packed) instead of dense
+// deltas: `deltas` is the value store (B*H, cap, keep_m, D), `masks` the
+// mask words (B*H, cap, D); 2 <= r <= 16, 1 <= keep_m <= r - 1.
+template <typename T, int VEC, int RMAX, bool GATED = false, bool PACK = false>
 __global__ __launch_bounds__(kThreads) void png_encode_kernel(
     const T* __restrict__ x, int64_t sb, int64_t sh, int64_t ss, int64_t H, int64_t m,
     int64_t D, int64_t s_valid, int r, int keep_m, float* __restrict__ deltas,
     T* __restrict__ anchors, int64_t cap, int64_t n0, int64_t items, int lpi_log2,
-    const int64_t* __restrict__ gate = nullptr) {
+    const int64_t* __restrict__ gate = nullptr, uint32_t* __restrict__ masks = nullptr) {
   if constexpr (GATED) {
     // gate = device (n_blocks, n_tail): archive only a completed tail, as
     // block n_blocks
@@ -632,6 +635,57 @@ __global__ __launch_bounds__(kThreads) void png_encode_kernel(
     for (int v = 0; v < VEC; ++v) xd[i][v] = xd[i + 1][v] - xd[i][v];
 
   const int n = r - 1;
+  if constexpr (PACK) {
+    // kept steps: the Top-M survivors that are not +-0, then the
+    // lowest-index +-0 steps until keep_m; the signs of the others (their
+    // png_filter value is delta * 0) go to bits 16 + i of the mask word
+    uint32_t kept[VEC], word[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      uint32_t key[RMAX];
+      uint32_t nzm = 0;
+#pragma unroll
+      for (int i = 0; i < RMAX; ++i) {
+        key[i] = i < n ? topm_key(__float_as_uint(xd[i][v])) : 0u;
+        if (key[i] != 0u) nzm |= 1u << i;
+      }
+      uint32_t km = (uint32_t)topm_mask<RMAX>(key, n, keep_m) & nzm;
+      int cnt = __builtin_popcount(km);
+      uint32_t sg = 0;
+#pragma unroll
+      for (int i = 0; i < RMAX; ++i) {
+        if (i < n && !((nzm >> i) & 1u) && cnt < keep_m) {
+          km |= 1u << i;
+          ++cnt;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < RMAX; ++i)
+        if (i < n && !((km >> i) & 1u)) sg |= (__float_as_uint(xd[i][v]) >> 31) << i;
+      kept[v] = km;
+      word[v] = km | (sg << 16);
+    }
+    uint32_t* mdst = masks + slot * D + d0;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) mdst[v] = word[v];
+    // slot j of a feature: its j-th kept step, in step order (popcount of
+    // every kept word is keep_m, so the lowest remaining bit always exists)
+    float* vdst = deltas + slot * (int64_t)keep_m * D + d0;
+    for (int j = 0; j < keep_m; ++j) {
+      float o[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const int i = __builtin_ctz(kept[v]);
+        kept[v] &= kept[v] - 1u;
+        float val = xd[0][v];
+#pragma unroll
+        for (int t = 1; t + 1 < RMAX; ++t) val = i == t ? xd[t][v] : val;
+        o[v] = val;
+      }
+      store_from_f32<float, VEC>(vdst + (int64_t)j * D, o);
+    }
+    return;
+  }
   if (keep_m > 0 && keep_m < n) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
@@ -693,6 +747,73 @@ __global__ __launch_bounds__(kThreads) void png_decode_kernel(
       o[v] = base[v] + (float)run[v];
     }
     store_from_f32<T, VEC>(dst + (tok0 + i) * oss, o);
+  }
+}
+
+// Reconstruction from a packed archive: the dense decoder's fp64 running sum
+// over the unpacked deltas (step i: the feature's next slot value when bit i
+// of its mask word is set, else a zero with sign bit 16 + i).
+template <typename T, int VEC>
+__global__ __launch_bounds__(kThreads) void png_decode_packed_kernel(
+    const float* __restrict__ vals, const uint32_t* __restrict__ masks,
+    const T* __restrict__ anchors, int64_t H, int64_t cap, int64_t a, int64_t nblk, int64_t D,
+    int r, int keep_m, T* __restrict__ out, int64_t osb, int64_t osh, int64_t oss,
+    int64_t out_len, int64_t items, int lpi_log2) {
+  const ItemMap im = item_of_thread(lpi_log2);
+  if (im.item >= items) return;
+  const int64_t bh = im.item / nblk, blk = a + (im.item - bh * nblk);
+  const int64_t b = bh / H, h = bh - b * H;
+  const int64_t d0 = (int64_t)im.lane * VEC;
+  if (d0 >= D) return;
+  const int64_t slot = bh * cap + blk;
+  T* dst = out + b * osb + h * osh + d0;
+  const int64_t tok0 = blk * r;
+  float base[VEC];
+  load_f32<T, VEC>(anchors + slot * D + d0, base);
+  if (tok0 < out_len) store_from_f32<T, VEC>(dst + tok0 * oss, base);
+  uint32_t w[VEC];
+  int cur[VEC];
+  double run[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    w[v] = masks[slot * D + d0 + v];
+    cur[v] = 0;
+    run[v] = 0.0;
+  }
+  const float* src = vals + slot * (int64_t)keep_m * D + d0;
+  for (int i = 1; i < r; ++i) {
+    if (tok0 + i >= out_len) break;
+    float o[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      float dv = __uint_as_float(((w[v] >> (15 + i)) & 1u) << 31);
+      if ((w[v] >> (i - 1)) & 1u) dv = src[(int64_t)min(cur[v]++, keep_m - 1) * D + v];
+      run[v] += (double)dv;
+      o[v] = base[v] + (float)run[v];
+    }
+    store_from_f32<T, VEC>(dst + (tok0 + i) * oss, o);
+  }
+}
+
+// Dense deltas (png_filter's layout) from a packed archive, one thread per
+// (block, feature).
+__global__ __launch_bounds__(kThreads) void png_unpack_kernel(
+    const float* __restrict__ vals, const uint32_t* __restrict__ masks, int64_t cap, int64_t a,
+    int64_t nblk, int64_t D, int r, int keep_m, float* __restrict__ deltas, int64_t d_cap,
+    int64_t total) {
+  const int64_t x = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (x >= total) return;
+  const int64_t d = x % D, it = x / D;
+  const int64_t bh = it / nblk, blk = a + (it - bh * nblk);
+  const int64_t slot = bh * cap + blk;
+  const uint32_t w = masks[slot * D + d];
+  const float* src = vals + slot * (int64_t)keep_m * D + d;
+  float* dst = deltas + (bh * d_cap + blk) * (int64_t)(r - 1) * D + d;
+  int cur = 0;
+  for (int i = 0; i + 1 < r; ++i) {
+    float dv = __uint_as_float(((w >> (16 + i)) & 1u) << 31);
+    if ((w >> i) & 1u) dv = src[(int64_t)min(cur++, keep_m - 1) * D];
+    dst[(int64_t)i * D] = dv;
   }
 }
 
@@ -872,12 +993,15 @@ int jpeg_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t 
                                   coeffs, scales, cap, 0, quant_bits, stream, gate, group);
 }
 
+// masks != NULL: the packed layout (deltas = the value store)
 template <bool GATED>
 static int png_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
                              int64_t x_sh, int64_t x_ss, int64_t s_valid, int64_t m, int64_t D,
                              int r, int keep_m, float* deltas, void* anchors, int64_t cap,
-                             int64_t n0, void* stream, const int64_t* gate) {
+                             int64_t n0, void* stream, const int64_t* gate,
+                             uint32_t* masks = nullptr) {
   if (B < 0 || H < 0 || m < 0 || D <= 0 || r < 2 || keep_m < 0) return FC_ERR_ARG;
+  if (masks && (r > 16 || keep_m < 1 || keep_m > r - 1)) return FC_ERR_ARG;
   if (n0 < 0 || n0 + m > cap) return FC_ERR_ARG;
   const int64_t items = B * H * m;
   if (items == 0) return FC_OK;
@@ -888,8 +1012,8 @@ static int png_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, i
   // register-resident block bucket; rmax*vec <= 64 floats per lane
   const int rmax = r <= 8 ? 8 : (r <= 16 ? 16 : (r <= 32 ? 32 : 64));
   const int max_vec = rmax == 8 ? 8 : (rmax == 16 ? 4 : 1);
-  const int vec =
-      pick_vec(D, max_vec, {x_sb, x_sh, x_ss}, {{x, es}, {anchors, es}, {deltas, 4}});
+  const int vec = pick_vec(D, max_vec, {x_sb, x_sh, x_ss},
+                           {{x, es}, {anchors, es}, {deltas, 4}, {masks, 4}});
   if (!vec) return FC_ERR_UNSUPPORTED;
   const int lg = log2_lanes(D, vec);
   hipStream_t st = (hipStream_t)stream;
@@ -901,6 +1025,16 @@ static int png_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, i
       return with_int<8, 16, 32, 64>(rmax, [&](auto rc_) {
         constexpr int RMAX = decltype(rc_)::value;
         if constexpr (RMAX * VEC <= 64) {
+          if (masks) {
+            if constexpr (RMAX <= 16) {
+              png_encode_kernel<T, VEC, RMAX, GATED, true><<<grid, kThreads, 0, st>>>(
+                  (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, keep_m, deltas,
+                  (T*)anchors, cap, n0, items, lg, gate, masks);
+              return FC_OK;
+            } else {
+              return FC_ERR_ARG;
+            }
+          }
           png_encode_kernel<T, VEC, RMAX, GATED><<<grid, kThreads, 0, st>>>(
               (const T*)x, x_sb, x_sh, x_ss, H, m, D, s_valid, r, keep_m, deltas, (T*)anchors,
               cap, n0, items, lg, gate);
@@ -917,10 +1051,11 @@ static int png_encode_launch(const void* x, int x_dtype, int64_t B, int64_t H, i
 
 int png_encode_gated(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
                      int64_t x_sh, int64_t x_ss, int64_t D, int r, int keep_m, float* deltas,
-                     void* anchors, int64_t cap, void* stream, const int64_t* gate) {
+                     void* anchors, int64_t cap, void* stream, const int64_t* gate,
+                     uint32_t* masks) {
   if (!gate || cap < 1) return FC_ERR_ARG;
   return png_encode_launch<true>(x, x_dtype, B, H, x_sb, x_sh, x_ss, r, 1, D, r, keep_m, deltas,
-                                 anchors, cap, 0, stream, gate);
+                                 anchors, cap, 0, stream, gate, masks);
 }
 
 }  // namespace fc
@@ -1074,6 +1209,61 @@ int fc_png_encode(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb
                   float* deltas, void* anchors, int64_t cap, int64_t n0, void* stream) {
   return png_encode_launch<false>(x, x_dtype, B, H, x_sb, x_sh, x_ss, s_valid, m, D, r, keep_m,
                                   deltas, anchors, cap, n0, stream, nullptr);
+}
+
+int fc_png_encode_packed(const void* x, int x_dtype, int64_t B, int64_t H, int64_t x_sb,
+                         int64_t x_sh, int64_t x_ss, int64_t s_valid, int64_t m, int64_t D, int r,
+                         int keep_m, float* vals, uint32_t* masks, void* anchors, int64_t cap,
+                         int64_t n0, void* stream) {
+  if (!masks && B * H * m > 0) return FC_ERR_ARG;
+  return png_encode_launch<false>(x, x_dtype, B, H, x_sb, x_sh, x_ss, s_valid, m, D, r, keep_m,
+                                  vals, anchors, cap, n0, stream, nullptr, masks);
+}
+
+int fc_png_decode_packed(const float* vals, const uint32_t* masks, const void* anchors,
+                         int anchor_dtype, int64_t B, int64_t H, int64_t cap, int64_t a,
+                         int64_t nblk, int64_t D, int r, int keep_m, void* out, int64_t o_sb,
+                         int64_t o_sh, int64_t o_ss, int64_t out_len, void* stream) {
+  if (B < 0 || H < 0 || a < 0 || nblk < 0 || a + nblk > cap || D <= 0 || r < 2 || r > 16 ||
+      keep_m < 1 || keep_m > r - 1)
+    return FC_ERR_ARG;
+  const int64_t items = B * H * nblk;
+  if (items == 0) return FC_OK;
+  if (!vals || !masks || !anchors || !out) return FC_ERR_ARG;
+  if (D > FC_MAX_HEAD_DIM) return FC_ERR_UNSUPPORTED;
+  const int es = esize_of(anchor_dtype);
+  if (!es || anchor_dtype == FC_I8) return FC_ERR_ARG;
+  const int vec = pick_vec(D, 4, {o_sb, o_sh, o_ss}, {{anchors, es}, {out, es}});
+  if (!vec) return FC_ERR_UNSUPPORTED;
+  const int lg = log2_lanes(D, vec);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = grid_for(items, lg);
+  const int rc = with_float_type(anchor_dtype, [&](auto tv) {
+    using T = decltype(tv);
+    return with_int<1, 4>(vec, [&](auto vc) {
+      constexpr int VEC = decltype(vc)::value;
+      png_decode_packed_kernel<T, VEC><<<grid, kThreads, 0, st>>>(
+          vals, masks, (const T*)anchors, H, cap, a, nblk, D, r, keep_m, (T*)out, o_sb, o_sh,
+          o_ss, out_len, items, lg);
+      return FC_OK;
+    });
+  });
+  return rc != FC_OK ? rc : check_launch();
+}
+
+int fc_png_unpack(const float* vals, const uint32_t* masks, int64_t B, int64_t H, int64_t cap,
+                  int64_t a, int64_t nblk, int64_t D, int r, int keep_m, float* deltas,
+                  int64_t d_cap, void* stream) {
+  if (B < 0 || H < 0 || a < 0 || nblk < 0 || a + nblk > cap || a + nblk > d_cap || D <= 0 ||
+      r < 2 || r > 16 || keep_m < 1 || keep_m > r - 1)
+    return FC_ERR_ARG;
+  const int64_t total = B * H * nblk * D;
+  if (total == 0) return FC_OK;
+  if (!vals || !masks || !deltas) return FC_ERR_ARG;
+  const dim3 grid((unsigned)((total + kThreads - 1) / kThreads));
+  png_unpack_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(vals, masks, cap, a, nblk, D, r,
+                                                                 keep_m, deltas, d_cap, total);
+  return check_launch();
 }
 
 int fc_png_decode(const float* deltas, const void* anchors, int anchor_dtype, int64_t B,

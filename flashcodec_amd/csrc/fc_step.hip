@@ -76,7 +76,7 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   const int64_t nb = a->n_blocks;  // host counters: blocks before the step; state: split hint
   if (nb < 1) return FC_ERR_UNSUPPORTED;
   const fc_step_stream* st[2] = {&a->key, &a->value};
-  fc_stream_view v[2];
+  fc_stream_view v[2]{};
   for (int i = 0; i < 2; ++i) {
     v[i].rows = st[i]->rows;
     v[i].scales = st[i]->scales;
@@ -129,7 +129,7 @@ static int decode_step_state(const fc_step_args* a) {
   if ((kind == FC_STORE_JPEG_I8 || kind == FC_STORE_JPEG_I8G) && a->quant_bits != 8)
     return FC_ERR_ARG;
   if (kind != FC_STORE_JPEG_I8 && kind != FC_STORE_JPEG_FP && kind != FC_STORE_PNG &&
-      kind != FC_STORE_JPEG_I8G)
+      kind != FC_STORE_JPEG_I8G && kind != FC_STORE_PNG_PACKED)
     return FC_ERR_ARG;
   if (a->n_blocks < 1) return FC_ERR_ARG;  // the archive holds a block before capture
   const int one = step_single_launch(a, a->state);
@@ -162,10 +162,11 @@ static int decode_step_state(const fc_step_args* a) {
   if (rc != FC_OK) return rc;
   const int64_t tsb = Hkv * r * D, tsh = (int64_t)r * D;
   for (int i = 0; i < 2; ++i) {
-    if (kind == FC_STORE_PNG)
+    if (kind == FC_STORE_PNG || kind == FC_STORE_PNG_PACKED)
       rc = png_encode_gated(st[i]->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, D, r, a->keep_m,
                             static_cast<float*>(st[i]->rows), st[i]->anchors, st[i]->cap,
-                            a->stream, a->state);
+                            a->stream, a->state,
+                            kind == FC_STORE_PNG_PACKED ? st[i]->masks : nullptr);
     else
       rc = jpeg_encode_gated(st[i]->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, D, r, a->s,
                              a->basis, st[i]->rows, st[i]->scales, st[i]->cap,
@@ -173,7 +174,7 @@ static int decode_step_state(const fc_step_args* a) {
                              kind == FC_STORE_JPEG_I8G ? 32 : 0);
     if (rc != FC_OK) return rc;
   }
-  fc_stream_view v[2];
+  fc_stream_view v[2]{};
   for (int i = 0; i < 2; ++i) {
     v[i].rows = st[i]->rows;
     v[i].scales = st[i]->scales;
@@ -183,6 +184,7 @@ static int decode_step_state(const fc_step_args* a) {
     v[i].raw_sb = tsb;
     v[i].raw_sh = tsh;
     v[i].raw_st = D;
+    v[i].masks = st[i]->masks;
   }
   rc = decode_attention_state(a->q, a->q_dtype, a->q_sb, a->q_sh, B, a->Hq, Hkv, D, kind,
                               a->stream_dtype, r, a->s, a->n_blocks, &v[0], &v[1], a->A, a->scale,
@@ -218,8 +220,11 @@ int fc_decode_step(const fc_step_args* a) {
   if ((a->store_kind == FC_STORE_JPEG_I8 || a->store_kind == FC_STORE_JPEG_I8G) &&
       (!a->key.scales || !a->value.scales))
     return FC_ERR_ARG;
-  if (a->store_kind == FC_STORE_PNG && (!a->key.anchors || !a->value.anchors)) return FC_ERR_ARG;
-  if (a->store_kind != FC_STORE_PNG && !a->basis) return FC_ERR_ARG;
+  const bool png = a->store_kind == FC_STORE_PNG || a->store_kind == FC_STORE_PNG_PACKED;
+  if (png && (!a->key.anchors || !a->value.anchors)) return FC_ERR_ARG;
+  if (a->store_kind == FC_STORE_PNG_PACKED && (!a->key.masks || !a->value.masks))
+    return FC_ERR_ARG;
+  if (!png && !a->basis) return FC_ERR_ARG;
   if (a->state) return decode_step_state(a);
   const bool completes = a->n_tail + 1 == r;
   if (completes && (a->n_blocks + 1 > a->key.cap || a->n_blocks + 1 > a->value.cap))
@@ -258,7 +263,11 @@ int fc_decode_step(const fc_step_args* a) {
   if (completes) {
     for (int i = 0; i < 2; ++i) {
       const fc_step_stream* x = st[i];
-      if (a->store_kind == FC_STORE_PNG)
+      if (a->store_kind == FC_STORE_PNG_PACKED)
+        rc = fc_png_encode_packed(x->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, r, 1, D, r,
+                                  a->keep_m, static_cast<float*>(x->rows), x->masks, x->anchors,
+                                  x->cap, nb, a->stream);
+      else if (a->store_kind == FC_STORE_PNG)
         rc = fc_png_encode(x->tail, a->stream_dtype, B, Hkv, tsb, tsh, D, r, 1, D, r, a->keep_m,
                            static_cast<float*>(x->rows), x->anchors, x->cap, nb, a->stream);
       else if (a->store_kind == FC_STORE_JPEG_I8G)
@@ -275,7 +284,7 @@ int fc_decode_step(const fc_step_args* a) {
   }
 
   // 3. attention over the archive and the tail
-  fc_stream_view v[2];
+  fc_stream_view v[2]{};
   for (int i = 0; i < 2; ++i) {
     v[i].rows = st[i]->rows;
     v[i].scales = st[i]->scales;
@@ -285,6 +294,7 @@ int fc_decode_step(const fc_step_args* a) {
     v[i].raw_sb = tsb;
     v[i].raw_sh = tsh;
     v[i].raw_st = D;
+    v[i].masks = st[i]->masks;
   }
   int n_splits = 0;
   if (nb > 0) {

@@ -24,7 +24,7 @@ __all__ = ["apply_flash_codec", "remove_flash_codec", "undo_flash_codec",
            "find_attention_modules"]
 
 _CODEC_DEFAULTS = (("keep_freqs", 2), ("keep_ratio", 1.0), ("quant_bits", 0),
-                   ("quant_group", 0))
+                   ("quant_group", 0), ("packed", False))
 
 
 def find_attention_modules(model):

@@ -177,13 +177,64 @@ int fc_png_decode(const float* deltas, const void* anchors, int anchor_dtype,
  */
 uint64_t fc_png_topm_mask_host(const float* delta, int n, int keep_m);
 
+/*
+ * Packed png archive (no reference code: the fixed-rate, block-addressable
+ * form of png_filter's Top-M output that the reference leaves to a future
+ * entropy coder, flashcodec/README.md:580-583).  Per (block, feature) the
+ * keep_m deltas png_filter keeps (flashcodec/codecs/png.py:36-60), in step
+ * order, as fp32 values `vals` (B*H, cap, keep_m, D), and one mask word
+ * (B*H, cap, D): bit i set = step i (delta i, token i + 1) kept; bit 16 + i
+ * = the sign bit of step i when it is not kept (png_filter stores a pruned
+ * delta as delta * 0, a signed zero).  Kept steps are the non-zero deltas
+ * of the Top-M selection, then the lowest-index zero steps until keep_m
+ * (a kept and a pruned zero unpack to the same bits).  Unpacking gives
+ * png_filter's dense deltas bit for bit (finite inputs: a pruned delta that
+ * is not finite, which png_filter turns into NaN, unpacks as a signed
+ * zero).  Anchors as the dense archive.  2 <= r <= 16, 1 <= keep_m <= r - 1.
+ * Same arguments as fc_png_encode with the packed stores in place of the
+ * delta store.
+ */
+int fc_png_encode_packed(const void* x, int x_dtype, int64_t B, int64_t H,
+                         int64_t x_sb, int64_t x_sh, int64_t x_ss,
+                         int64_t s_valid, int64_t m, int64_t D, int r,
+                         int keep_m, float* vals, uint32_t* masks,
+                         void* anchors, int64_t cap, int64_t n0,
+                         void* stream);
+
+/*
+ * png_reconstruct of blocks [a, a + nblk) of a packed archive, as
+ * fc_png_decode (fp64 running sum of the unpacked deltas, bit for bit the
+ * dense archive's reconstruction).  Replaces png_reconstruct
+ * (flashcodec/codecs/png.py:63-74) for packed stores.
+ */
+int fc_png_decode_packed(const float* vals, const uint32_t* masks,
+                         const void* anchors, int anchor_dtype, int64_t B,
+                         int64_t H, int64_t cap, int64_t a, int64_t nblk,
+                         int64_t D, int r, int keep_m, void* out, int64_t o_sb,
+                         int64_t o_sh, int64_t o_ss, int64_t out_len,
+                         void* stream);
+
+/*
+ * Dense deltas (B*H, d_cap, r-1, D) fp32 at blocks [a, a + nblk) from a
+ * packed archive: png_filter's delta output bit for bit (the layout of
+ * fc_png_encode's delta store).  No reference counterpart (the reference
+ * stores only the dense form); for callers converting packed archives.
+ */
+int fc_png_unpack(const float* vals, const uint32_t* masks, int64_t B, int64_t H,
+                  int64_t cap, int64_t a, int64_t nblk, int64_t D, int r,
+                  int keep_m, float* deltas, int64_t d_cap, void* stream);
+
 /* Archive kind of a stream for fc_decode_attention. */
 enum {
   FC_STORE_JPEG_I8 = 0,  /* rows: int8 coeffs x fp32 scale, s = k      */
   FC_STORE_JPEG_FP = 1,  /* rows: coeffs in the stream dtype, s = k    */
   FC_STORE_PNG = 2,      /* rows: anchor (stream dtype) + r-1 fp32 deltas, s = r */
-  FC_STORE_JPEG_I8G = 3  /* rows: int8 coeffs x one fp32 scale per 32 features
+  FC_STORE_JPEG_I8G = 3, /* rows: int8 coeffs x one fp32 scale per 32 features
                             (scales (B*H, cap, k, D/32)), s = k */
+  FC_STORE_PNG_PACKED = 4 /* rows: anchor (stream dtype) + the packed Top-M
+                            deltas of fc_png_encode_packed (vals (B*H, cap,
+                            keep_m, D) fp32 in `rows`, mask words (B*H, cap,
+                            D) in `masks`), s = keep_m */
 };
 
 /* One KV stream as seen by the decode attention. */
@@ -194,6 +245,7 @@ typedef struct fc_stream_view {
   int64_t cap;           /* capacity of the store in blocks */
   const void* raw;       /* raw tail (B, H, n_raw, D) in the stream dtype, or NULL */
   int64_t raw_sb, raw_sh, raw_st; /* element strides of the raw tail */
+  const uint32_t* masks; /* packed png: mask words (B*H, cap, D); else NULL */
 } fc_stream_view;
 
 /*
@@ -403,6 +455,7 @@ typedef struct fc_step_stream {
   void* tail;            /* (B, H, r, D) tail buffer */
   const void* token;     /* the new token */
   int64_t tok_sb, tok_sh;
+  uint32_t* masks;       /* packed png: mask words (B*H, cap, D); else NULL */
 } fc_step_stream;
 
 typedef struct fc_step_args {

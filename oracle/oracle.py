@@ -17,6 +17,11 @@ Parity status (each function's pinning is listed in tests/test_oracle.py):
   group; pinned by the one-group case equalling the row quantizer bit for
   bit, per-group absmax-to-127 and half-step error bounds, and the k = r
   round trip bound.
+  png_pack / png_unpack (the packed Top-M png archive, which the reference
+  leaves unbuilt): pinned by unpack(pack(d)) == d bit for bit on the golden
+  png_filter outputs and on planted +-0 / tie columns, by exhaustive small
+  columns, and by planted mistakes (a dropped sign word, a shifted rank)
+  that those checks catch.
   attention: fp64 by definition (synthesise every block, softmax over all
   tokens), pinned against brute-force dense attention on tiny inputs and the
   reference's torch-path outputs within tolerance.
@@ -254,6 +259,65 @@ def png_decode(deltas, anchors, dtype="f32"):
                          _p(_f32(anchors).reshape(items, D)), ctypes.c_long(items), r,
                          ctypes.c_long(D), DTYPES[dtype], _p(out))
     return out.reshape(lead + (n * r, D))
+
+
+# ---------------------------------------------------------------- packed png
+
+PACK_SIGN_SHIFT = 16   # mask word: bits 0..14 kept steps, bits 16..30 pruned-zero signs
+
+
+def png_pack(deltas, keep_m):
+    """Fixed-rate packing of png_filter's Top-M deltas (png.py:36-60: at most
+    keep_m of the r-1 steps of a (block, feature) column survive; the others
+    are +-0.0, the sign of the pruned delta kept).  This build's archive
+    format, which the reference leaves unbuilt (README.md:580-583):
+      vals (..., n, keep_m, D) fp32: the column's kept steps in step order;
+      mask (..., n, D) uint32: bit i = step i kept; bit 16 + i = sign bit
+        of step i when it is not kept (0 for kept steps).
+    Kept steps: every step whose bits are not +-0 (at most keep_m of them),
+    then the lowest-index +-0 steps until there are keep_m (a kept or a
+    pruned zero unpacks to the same bits).  r - 1 <= 15 steps.  Raises when
+    a column has more than keep_m non-zero steps (png_filter's pruned
+    non-finite deltas become NaN, which the format does not hold)."""
+    d = np.ascontiguousarray(deltas, np.float32)
+    *lead, n, rm1, D = d.shape
+    if not 1 <= keep_m <= rm1 or rm1 > 15:
+        raise ValueError(f"packing needs 1 <= keep_m <= r-1 <= 15 (keep_m={keep_m}, r-1={rm1})")
+    bits = d.view(np.uint32)
+    nz = (bits & 0x7FFFFFFF) != 0                                  # (..., n, rm1, D)
+    cnt = nz.sum(axis=-2)
+    if (cnt > keep_m).any():
+        raise ValueError("a column holds more than keep_m non-zero deltas")
+    # fill with the lowest-index zero steps: rank of each zero among zeros
+    zero_rank = np.cumsum(~nz, axis=-2) - 1
+    need = (keep_m - cnt)[..., None, :]
+    kept = nz | (~nz & (zero_rank < need))
+    steps = np.arange(rm1, dtype=np.uint32).reshape((rm1, 1))
+    kept_bits = (kept.astype(np.uint32) << steps).sum(axis=-2, dtype=np.uint32)
+    sign = ((bits >> 31) & 1).astype(np.uint32) * (~kept)
+    sign_bits = (sign << (steps + PACK_SIGN_SHIFT)).sum(axis=-2, dtype=np.uint32)
+    mask = (kept_bits | sign_bits).astype(np.uint32)
+    # slot j of a column = its j-th kept step
+    order = np.argsort(~kept, axis=-2, kind="stable")[..., :keep_m, :]
+    vals = np.take_along_axis(d, order, axis=-2)
+    return vals, mask
+
+
+def png_unpack(vals, mask, r):
+    """Dense deltas (..., n, r-1, D) fp32 of a packed archive: step i is the
+    column's next kept value when bit i of its mask word is set, else a zero
+    with the sign bit 16 + i (the inverse of png_pack, bit for bit)."""
+    v = np.ascontiguousarray(vals, np.float32)
+    m = np.ascontiguousarray(mask, np.uint32)
+    *lead, n, keep_m, D = v.shape
+    rm1 = r - 1
+    steps = np.arange(rm1, dtype=np.uint32).reshape((rm1, 1))
+    kept = ((m[..., None, :] >> steps) & 1).astype(bool)            # (..., n, rm1, D)
+    rank = np.cumsum(kept, axis=-2) - 1
+    picked = np.take_along_axis(v, np.clip(rank, 0, keep_m - 1), axis=-2)
+    sign = (m[..., None, :] >> (steps + PACK_SIGN_SHIFT)) & 1
+    zero = (sign << 31).astype(np.uint32).view(np.float32)
+    return np.where(kept, picked, zero).astype(np.float32)
 
 
 # ---------------------------------------------------------------- attention

@@ -58,8 +58,13 @@ def stream_rows(oracle, st):
             sc = st._scales[:, :, :n].cpu().numpy()
             return oracle.stored_rows_jpeg(c, sc if st.codec.quant_group else sc[..., 0])
         return oracle.stored_rows_jpeg(c)
-    return oracle.stored_rows_png(st._deltas[:, :, :n].cpu().numpy(),
-                                  st._anchors[:, :, :n].float().cpu().numpy())
+    if st.codec.packed:
+        d = oracle.png_unpack(st._packed[:, :, :n].cpu().numpy(),
+                              st._packed_mask[:, :, :n].cpu().numpy().view(np.uint32),
+                              st.block_size)
+    else:
+        d = st._deltas[:, :, :n].cpu().numpy()
+    return oracle.stored_rows_png(d, st._anchors[:, :, :n].float().cpu().numpy())
 
 
 def oracle_out(oracle, q, ks, vs, scale):
@@ -359,12 +364,14 @@ STEP_PAIRS = [
     (dict(I8, keep_freqs=1), "f16", 256, 8, True),
     (dict(I8, block_size=16, keep_freqs=4), "bf16", 128, 2, True),
     (dict(I8, quant_group=32), "bf16", 128, 2, False),
+    (dict(mode="png", block_size=8, keep_ratio=0.5, packed=True), "f32", 64, 4, False),
 ]
 
 
 @pytest.mark.parametrize("cfg,dt,D,G,single", STEP_PAIRS,
                          ids=[f"{c['mode']}-k{c.get('keep_freqs', 0)}-r{c['block_size']}"
-                              f"{'-g32' if c.get('quant_group') else ''}-{dt}-D{D}"
+                              f"{'-g32' if c.get('quant_group') else ''}"
+                              f"{'-packed' if c.get('packed') else ''}-{dt}-D{D}"
                               for c, dt, D, _, _ in STEP_PAIRS])
 def test_fused_decode_step_matches_append_then_attend(cfg, dt, D, G, single, oracle):
     """codec_decode_step (one library call per layer step) leaves the same

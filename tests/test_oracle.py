@@ -116,6 +116,39 @@ def test_jpeg_oracle_matches_reference(golden, oracle, name):
     assert np.array_equal(_bits(rec_q), _bits(c["rec_q"]))
 
 
+@pytest.mark.parametrize("name", _jpeg_cases())
+def test_torch_path_codec_matches_reference(golden, name):
+    """oracle/torch_path.py's jpeg operations (bench.py's C1 / C2 CPU
+    baselines) reproduce the reference's bits on this torch CPU build."""
+    from oracle import torch_path as T
+    G = golden("jpeg")
+    c, m = G.case(name), G.meta[name]
+    dt, r, k = m["dtype"], m["r"], m["k"]
+    basis = torch.from_numpy(np.ascontiguousarray(golden("basis").data[f"r{r}"][:k]))
+    x = _torch_of(c["x"], dt)
+    coef = T.dct_compress(x, r, basis)
+    assert np.array_equal(_bits(_np_of(coef, dt)), _bits(c["coef"]))
+    codes, scales = T.quantize(coef)
+    assert np.array_equal(codes.numpy(), c["codes"])
+    assert np.array_equal(_bits(scales[..., 0].numpy()), _bits(c["scales"]))
+    S = m["shape"][-2]
+    rec_q = T.dct_decompress(T.dequantize(codes, scales), r, basis)[..., :S, :]
+    assert np.array_equal(_bits(rec_q.numpy()), _bits(c["rec_q"]))
+
+
+def _torch_of(storage, dt):
+    a = np.ascontiguousarray(storage)
+    if dt == "bf16":
+        return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+    return torch.from_numpy(a.copy())
+
+
+def _np_of(t, dt):
+    if dt == "bf16":
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
 def test_jpeg_closed_form_properties(golden, oracle):
     rng = np.random.default_rng(3)
     r = 8
@@ -235,6 +268,86 @@ def test_png_oracle_matches_reference(golden, oracle, name):
     assert np.array_equal(_bits(a), _bits(oracle.values_of(c["anchors"], dt)))
     rec = oracle.png_decode(d, a, dt)
     assert np.array_equal(_bits(rec), _bits(oracle.values_of(c["rec"], dt)))
+
+
+@pytest.mark.parametrize("name", [n for n in _png_cases() if "_k1" not in n and "r32" not in n])
+def test_png_pack_round_trip_on_reference_outputs(golden, oracle, name):
+    """The packed Top-M archive holds png_filter's output exactly: unpacking
+    the packing of the reference's own deltas (golden, -0.0 signs and tie
+    columns included) gives them back bit for bit; every column keeps
+    exactly keep_m slots."""
+    G = golden("png")
+    c, m = G.case(name), G.meta[name]
+    keep_m = oracle.png_keep_m(m["r"], m["keep"])
+    d = np.asarray(c["deltas"], np.float32)
+    vals, mask = oracle.png_pack(d, keep_m)
+    assert vals.shape == d.shape[:-2] + (keep_m, d.shape[-1])
+    assert np.all(np.bitwise_count(mask & 0x7FFF) == keep_m)
+    assert np.all((mask & (mask >> 16) & 0x7FFF) == 0)          # no sign bit on a kept step
+    u = oracle.png_unpack(vals, mask, m["r"])
+    assert np.array_equal(_bits(u), _bits(d))
+
+
+def test_png_pack_exhaustive_small_columns(oracle):
+    """Every column of 4 steps over {+0, -0, 1, -2, 3, NaN-free ties} with at
+    most keep_m non-zero steps round-trips bit for bit, for keep_m 1..4;
+    the kept set is the non-zero steps plus the lowest-index zeros."""
+    import itertools
+    alphabet = np.array([0.0, -0.0, 1.0, -2.0, 3.0, 1.0], np.float32)
+    cols = np.array(list(itertools.product(range(len(alphabet)), repeat=4)))
+    vals_all = alphabet[cols]                                     # (N, 4)
+    nz = (vals_all.view(np.uint32) & 0x7FFFFFFF) != 0
+    for keep_m in range(1, 5):
+        ok = nz.sum(-1) <= keep_m
+        d = vals_all[ok].T[None, :, :].copy()                     # (1 block, 4 steps, N)
+        v, mask = oracle.png_pack(d, keep_m)
+        assert np.array_equal(_bits(oracle.png_unpack(v, mask, 5)), _bits(d))
+        kept = (mask[0][None, :] >> np.arange(4)[:, None]) & 1
+        nzc = nz[ok].T
+        assert np.all(kept[nzc] == 1)                             # non-zero steps kept
+        fill = np.cumsum(kept * ~nzc, 0)                          # zeros kept, lowest first
+        first_unkept = np.argmax((kept == 0) & ~nzc, axis=0)
+        assert np.all((fill[-1] == keep_m - nzc.sum(0)))
+        has = ((kept == 0) & ~nzc).any(0)
+        for col in np.nonzero(has)[0][:50]:
+            assert not np.any((kept[:, col] == 1) & ~nzc[:, col] & (np.arange(4) > first_unkept[col]))
+    with pytest.raises(ValueError):
+        oracle.png_pack(np.ones((1, 4, 2), np.float32), 2)       # 4 non-zero steps, keep_m 2
+
+
+def test_png_pack_planted_mistakes_are_caught(oracle):
+    """The round-trip check sees the mistakes a packer could make: sign
+    words dropped (pruned -0.0 come back as +0.0) and slot values shifted by
+    one rank."""
+    x = oracle.ar1((1, 2, 16 * 12, 32), 0.95, 3)
+    d, _ = oracle.png_encode(x, 16, 0.25)
+    vals, mask = oracle.png_pack(d, 4)
+    assert np.array_equal(_bits(oracle.png_unpack(vals, mask, 16)), _bits(d))
+    no_sign = mask & np.uint32(0xFFFF)
+    assert not np.array_equal(_bits(oracle.png_unpack(vals, no_sign, 16)), _bits(d))
+    shifted = np.roll(vals, 1, axis=-2)
+    assert not np.array_equal(_bits(oracle.png_unpack(shifted, mask, 16)), _bits(d))
+    # reconstruction through the dense decoder is the dense archive's own
+    a = oracle.png_encode(x, 16, 0.25)[1]
+    rec = oracle.png_decode(oracle.png_unpack(vals, mask, 16), a, "f32")
+    assert np.array_equal(_bits(rec), _bits(oracle.png_decode(d, a, "f32")))
+
+
+@pytest.mark.parametrize("name", _png_cases())
+def test_torch_path_png_matches_reference(golden, name):
+    """oracle/torch_path.py's png operations (bench.py's C4 CPU baseline)
+    reproduce the reference's bits on this torch CPU build (Top-M tie order
+    included)."""
+    from oracle import torch_path as T
+    G = golden("png")
+    c, m = G.case(name), G.meta[name]
+    dt = m["dtype"]
+    x = _torch_of(c["x"], dt)
+    d, a = T.png_filter(x, m["r"], m["keep"])
+    assert np.array_equal(_bits(d.numpy()), _bits(c["deltas"]))
+    assert np.array_equal(_bits(_np_of(a, dt)), _bits(c["anchors"]))
+    rec = T.png_reconstruct(d, a)
+    assert np.array_equal(_bits(_np_of(rec, dt)), _bits(c["rec"]))
 
 
 def test_png_closed_form_properties(oracle):
