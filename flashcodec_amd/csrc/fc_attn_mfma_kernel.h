@@ -835,8 +835,15 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   const int64_t rows_total = nb * SROWS;
   const int64_t npass = (rows_total + PR - 1) / PR;
   unsigned int* passq = p.passq + g * p.cstride;
-  const unsigned int wslot = (unsigned int)(split * kWaves + wave);
-  const unsigned int wstride = (unsigned int)(p.n_splits * kWaves);
+  // fused step: split 0's wavefronts run the step's prologue first and then
+  // take passes from the queue only; the other splits' wavefronts take the
+  // fixed first passes
+  const bool step_q = STEP && p.n_splits > 1 && !p.static_passes;
+  const bool step0 = step_q && split == 0;
+  const unsigned int wslot = step_q ? (unsigned int)(max(split - 1, 0) * kWaves + wave)
+                                    : (unsigned int)(split * kWaves + wave);
+  const unsigned int wstride =
+      step_q ? (unsigned int)((p.n_splits - 1) * kWaves) : (unsigned int)(p.n_splits * kWaves);
   // Pass k < nfix of a wavefront is fixed, wslot + k * wstride: three
   // quarters of the group's passes need no queue round trip (each queue
   // atomic costs HBM time: one per pass measured 2.2 us slower at C3; the
@@ -850,7 +857,7 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   auto grab = [&]() -> unsigned int {  // result in lane 0, read when needed
     const unsigned int f = next_fixed;
     next_fixed += wstride;
-    if (p.static_passes || f < qbase) return f;
+    if (!step0 && (p.static_passes || f < qbase)) return f;
     unsigned int v = 0;
     if (lane == 0)
       v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + qbase;
@@ -1063,8 +1070,15 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   // A fused step issues them after its step partial, whose registers they
   // would otherwise share.
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
-  int64_t cur = wslot;
-  if (!STEP && cur < npass) load_k(cur * PR, rows_of(cur));
+  int64_t cur = step0 ? npass : wslot;
+  bool v_first = false;  // the first pass's V codes are in flight already
+  if (!step0 && (!STEP || step_q) && cur < npass) {
+    load_k(cur * PR, rows_of(cur));
+    if constexpr (STEP) {
+      load_v(cur * PR, rows_of(cur));
+      v_first = true;
+    }
+  }
 
   // ---- the query as the B operand: per head a power of two scales it to
   // integers of at most 14 bits (QF: 30 bits)
@@ -1164,11 +1178,19 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   }
 
   __syncthreads();  // a_lds; the tail's scratch (w_lds) is free again
-  if (STEP && cur < npass) load_k(cur * PR, rows_of(cur));
+  if (step0) {
+    // split 0's first pass: the queue's next, after its step prologue
+    unsigned int v = 0;
+    if (lane == 0)
+      v = __hip_atomic_fetch_add(passq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + wstride;
+    cur = pass_of(v);
+  }
+  if (STEP && (step0 || !step_q) && cur < npass) load_k(cur * PR, rows_of(cur));
   while (cur < npass) {
     const int64_t pr0 = cur * PR;
     const int prow = rows_of(cur);  // multiple of SROWS
-    load_v(pr0, prow);
+    if (!v_first) load_v(pr0, prow);
+    v_first = false;
     // the next pass, taken now and read after the score products (a wavefront
     // holds at most one pass beyond the current one)
     const unsigned int nxt_v = grab();
