@@ -27,9 +27,9 @@ bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q
 bool split_i8_mfma_fusable(int n_splits) { return n_splits <= kFuseMaxSplits; }
 
 // Per-32 scales (FC_STORE_JPEG_I8G) on the matrix-core pass: fp16 / bf16
-// queries, head sizes 64 / 128 / 256 (whole 64-feature chunks of groups).
+// queries, head sizes 64 / 96 / 128 / 256 (whole groups of 32 features).
 bool mfma_group_shape_supported(int q_dtype, int64_t D, int s) {
-  return (q_dtype == FC_F16 || q_dtype == FC_BF16) && (D == 64 || D == 128 || D == 256) &&
+  return (q_dtype == FC_F16 || q_dtype == FC_BF16) && D % 32 == 0 &&
          mfma_shape_supported(q_dtype, D, s);
 }
 

@@ -254,11 +254,14 @@ __device__ __forceinline__ void raw_tail_partial(const MfmaArgs& p, int64_t b, i
 // archive kernels' arithmetic, bit for bit — stored when `write`; then x is
 // replaced by the block's tokens synthesised from the dequantised codes
 // through A (r x SROWS), so the block is attended exactly as an archived
-// one.  kk: SROWS x D, sc: SROWS floats of LDS scratch.
-template <int D, int SROWS, typename TT>
+// one.  NG scales per row: 1 (the row's absmax) or D / 32 (per 32 features,
+// scales[row * NG + group]).  kk: SROWS x D, sc: SROWS * NG floats of LDS
+// scratch.
+template <int D, int SROWS, typename TT, int NG = 1>
 __device__ __forceinline__ void step_archive(float* x, int r, const float* basis, const float* A,
                                              bool write, int8_t* codes, float* scales, float* kk,
                                              float* sc, int tid) {
+  static_assert(NG == 1 || NG * 32 == D, "one scale per row or per 32 features");
   const int lane = tid & 63, wave = tid >> 6;
   for (int e = tid; e < SROWS * D; e += kMThreads) {
     const int j = e / D, d = e - j * D;
@@ -268,20 +271,36 @@ __device__ __forceinline__ void step_archive(float* x, int r, const float* basis
   }
   __syncthreads();
   for (int j = wave; j < SROWS; j += kMThreads / 64) {  // one row per wavefront
-    float m = 0.f;
-    for (int d = lane; d < D; d += 64) m = fmaxf(m, fabsf(kk[j * D + d]));
+    if constexpr (NG == 1) {
+      float m = 0.f;
+      for (int d = lane; d < D; d += 64) m = fmaxf(m, fabsf(kk[j * D + d]));
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    float sj = to_f32(from_f32<TT>(m / 127.0f));
-    if (!(sj > 0.f)) sj = 1.0f;
-    if (lane == 0) {
-      sc[j] = sj;
-      if (write) scales[j] = sj;
+      for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      float sj = to_f32(from_f32<TT>(m / 127.0f));
+      if (!(sj > 0.f)) sj = 1.0f;
+      if (lane == 0) {
+        sc[j] = sj;
+        if (write) scales[j] = sj;
+      }
+    } else {
+      // features 64 i + lane: group 2 i + lane / 32, its max over 32 lanes
+      for (int i = 0; 64 * i < D; ++i) {
+        const int d = 64 * i + lane;
+        float m = d < D ? fabsf(kk[j * D + d]) : 0.f;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        float sj = to_f32(from_f32<TT>(m / 127.0f));
+        if (!(sj > 0.f)) sj = 1.0f;
+        if ((lane & 31) == 0 && d < D) {
+          sc[j * NG + d / 32] = sj;
+          if (write) scales[j * NG + d / 32] = sj;
+        }
+      }
     }
   }
   __syncthreads();
   for (int e = tid; e < SROWS * D; e += kMThreads) {
-    const float sj = sc[e / D];
+    const float sj = NG == 1 ? sc[e / D] : sc[(e / D) * NG + (e % D) / 32];
     const float q = quant_code(kk[e], sj, 1.0f / sj);
     if (write) codes[e] = (int8_t)(int)q;
     kk[e] = q * sj;
@@ -307,7 +326,7 @@ __device__ __forceinline__ void step_archive(float* x, int r, const float* basis
 // `write`: this workgroup stores the token / the block (one head group per
 // (batch, kv head) does; all compute the partial).  The query rows are
 // q + qb + (h0 + h) * q_sh for the G heads.
-template <int D, int SROWS, typename TT>
+template <int D, int SROWS, typename TT, int NG = 1>
 __device__ __forceinline__ void step_partial(
     int64_t t, int r, TT* ktail, TT* vtail, const TT* ktok, const TT* vtok, bool write,
     int8_t* kcodes, float* kscales, int8_t* vcodes, float* vscales, const float* basis,
@@ -329,8 +348,8 @@ __device__ __forceinline__ void step_partial(
     }
   __syncthreads();
   if (complete) {
-    step_archive<D, SROWS, TT>(xk, r, basis, A, write, kcodes, kscales, kk, sc, tid);
-    step_archive<D, SROWS, TT>(xv, r, basis, A, write, vcodes, vscales, kk, sc, tid);
+    step_archive<D, SROWS, TT, NG>(xk, r, basis, A, write, kcodes, kscales, kk, sc, tid);
+    step_archive<D, SROWS, TT, NG>(xv, r, basis, A, write, vcodes, vscales, kk, sc, tid);
   }
   // the partial over the n rows, at full precision
   {
@@ -752,8 +771,8 @@ template <int SROWS, int D, int GP, bool STEP, bool QF = false, bool QG = false>
 __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void attn_split_i8_mfma(
     MfmaArgs p) {
   static_assert(!(STEP && QF), "the fused step takes fp16 / bf16 queries");
-  static_assert(!QG || (!STEP && !QF && D % 32 == 0 && D == mfma_width<D>()),
-                "per-32 scales: plain calls, fp16 / bf16 queries, D = 64 / 128 / 256");
+  static_assert(!QG || (!QF && D % 32 == 0),
+                "per-32 scales: fp16 / bf16 queries, D = 64 / 96 / 128 / 256");
   constexpr int DC = mfma_width<D>();
   constexpr int DK = DC / 32;
   constexpr int DV = (DC + 127) / 128;  // 128-feature groups of the value product
@@ -924,28 +943,34 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   float ks_r, vs_r;
   float kgr[NGR], vgr[NGR];  // QG: the group scales of row lane % PRT
   const int sg_off = (lane % PRT) * NGR * 4;
+  // QG: the NGR group scales of row lane % PRT, in 16 / 8-byte pieces (NGR
+  // = 2, 4, 8) or dwords (NGR = 3: rows 12 bytes apart)
+  auto load_groups = [&](__amdgpu_buffer_rsrc_t rs, float* dst) {
+    if constexpr (NGR % 4 == 0) {
+#pragma unroll
+      for (int u = 0; u < NGR / 4; ++u) {
+        const u32x4_t a = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, sg_off + 16 * u, 0, 0));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[4 * u + i] = __uint_as_float(a[i]);
+      }
+    } else if constexpr (NGR == 2) {
+      const u32x2_t a = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs, sg_off, 0, 0));
+#pragma unroll
+      for (int i = 0; i < 2; ++i) dst[i] = __uint_as_float(a[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NGR; ++i)
+        dst[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, sg_off + 4 * i, 0, 0));
+    }
+  };
   // Code rows are read once per call: streaming (nontemporal) loads for K and
   // V, so the archive does not displace what the end phase needs from the
   // caches (C3 over rotating archive sets: 50.6 -> 49.9 us; the row scales
   // stay on the default policy, streaming them measured slower)
   auto load_k = [&](int64_t pr0, int prow) {
-    if constexpr (QG) {
-      // group scales ahead of the codes: the score stage needs them first
-      const __amdgpu_buffer_rsrc_t rks = buf_rsrc(ksc + pr0 * NGR, prow * NGR * 4);
-      if constexpr (NGR == 2) {
-        const u32x2_t a = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rks, sg_off, 0, 0));
-#pragma unroll
-        for (int i = 0; i < 2; ++i) kgr[i] = __uint_as_float(a[i]);
-      } else {
-#pragma unroll
-        for (int u = 0; u < NGR / 4; ++u) {
-          const u32x4_t a = __builtin_bit_cast(
-              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rks, sg_off + 16 * u, 0, 0));
-#pragma unroll
-          for (int i = 0; i < 4; ++i) kgr[4 * u + i] = __uint_as_float(a[i]);
-        }
-      }
-    }
+    // group scales ahead of the codes: the score stage needs them first
+    if constexpr (QG) load_groups(buf_rsrc(ksc + pr0 * NGR, prow * NGR * 4), kgr);
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kbase + pr0 * D, prow * D);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -966,24 +991,9 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   };
   uint32_t vr[NS][DV][16];
   auto load_v = [&](int64_t pr0, int prow) {
-    if constexpr (QG) {
-      // group scales ahead of the codes, with this pass's V (held one pass
-      // ahead with the K loads they cost registers that spilled)
-      const __amdgpu_buffer_rsrc_t rvs = buf_rsrc(vsc + pr0 * NGR, prow * NGR * 4);
-      if constexpr (NGR == 2) {
-        const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rvs, sg_off, 0, 0));
-#pragma unroll
-        for (int i = 0; i < 2; ++i) vgr[i] = __uint_as_float(v[i]);
-      } else {
-#pragma unroll
-        for (int u = 0; u < NGR / 4; ++u) {
-          const u32x4_t v = __builtin_bit_cast(
-              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rvs, sg_off + 16 * u, 0, 0));
-#pragma unroll
-          for (int i = 0; i < 4; ++i) vgr[4 * u + i] = __uint_as_float(v[i]);
-        }
-      }
-    }
+    // group scales ahead of the codes, with this pass's V (held one pass
+    // ahead with the K loads they cost registers that spilled)
+    if constexpr (QG) load_groups(buf_rsrc(vsc + pr0 * NGR, prow * NGR * 4), vgr);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vbase + pr0 * D, prow * D);
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl)
@@ -1150,19 +1160,20 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   const bool fold_tail = p.fused && split == 0 && (STEP || n_raw > 0);
   if constexpr (STEP) {
     if (split == 0) {
-      __shared__ float step_sc[SROWS];
+      __shared__ float step_sc[SROWS * NGR];
       float* xk = &s_lds[0][0][0];  // the pass loop has not started: its scratch is free
       float* etl = reinterpret_cast<float*>(&w_lds[0][0][0]);
       const int64_t bh_s = b * p.Hkv + hkv;
       const int64_t kblk = (bh_s * p.kcap + step_nb) * SROWS, vblk = (bh_s * p.vcap + step_nb) * SROWS;
       auto go = [&](auto tt) {
         using TT = decltype(tt);
-        step_partial<D, SROWS, TT>(
+        step_partial<D, SROWS, TT, NGR>(
             step_t, p.r, static_cast<TT*>(const_cast<void*>(p.kraw)) + bh_s * p.r * D,
             static_cast<TT*>(const_cast<void*>(p.vraw)) + bh_s * p.r * D,
             static_cast<const TT*>(p.ktok) + b * p.kt_sb + hkv * p.kt_sh,
             static_cast<const TT*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write,
-            p.kcodes_w + kblk * D, p.kscales_w + kblk, p.vcodes_w + vblk * D, p.vscales_w + vblk,
+            p.kcodes_w + kblk * D, p.kscales_w + kblk * NGR, p.vcodes_w + vblk * D,
+            p.vscales_w + vblk * NGR,
             p.basis, p.A, p.q, p.q_dtype, b * p.q_sb, p.q_sh, hkv * p.G + g0, G, p.scale_log2,
             tid, xk, xk + p.r * D, cbuf[0][0], step_sc, etl, part_lds, tail_ml[0], tail_ml[1]);
       };
@@ -1215,6 +1226,7 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
                              (int)kr[t][4 * c + 3]};
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf) {
+            if (2 * c + hf >= NGR) continue;  // D = 96: features 96.. are padding
             // the codes of the other group's lanes zeroed (the query stays
             // whole: a masked copy of it would be hoisted out of the loop)
             const bool mine = (lq >> 1) == hf;
@@ -1472,9 +1484,12 @@ int launch_mfma_rows(const MfmaArgs& a, int d, int gp, dim3 grid, hipStream_t st
     return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
       constexpr int GPv = decltype(gc)::value;
       if (a.qgroup) {
-        if constexpr (Dv == 64 || Dv == 128 || Dv == 256) {
-          if (a.step || a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
-          attn_split_i8_mfma<SR, Dv, GPv, false, false, true><<<grid, kMThreads, 0, st>>>(a);
+        if constexpr (Dv % 32 == 0) {
+          if (a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
+          if (a.step)
+            attn_split_i8_mfma<SR, Dv, GPv, true, false, true><<<grid, kMThreads, 0, st>>>(a);
+          else
+            attn_split_i8_mfma<SR, Dv, GPv, false, false, true><<<grid, kMThreads, 0, st>>>(a);
         } else {
           return FC_ERR_UNSUPPORTED;
         }

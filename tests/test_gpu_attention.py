@@ -143,6 +143,8 @@ CASES = [
     ("i8g-bf16-k1-d64-g1", dict(mode="jpeg", block_size=8, keep_freqs=1, quant_bits=8, quant_group=32), "bf16", 2, 2, 1, 8 * 100 + 7, 64),
     ("i8g-bf16-k3-r16-g4", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8, quant_group=32), "bf16", 1, 2, 4, 16 * 60 + 5, 128),
     ("i8g-bf16-k2-d256-g2", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8, quant_group=32), "bf16", 1, 2, 2, 8 * 100 + 3, 256),
+    ("i8g-f16-k4-d96-g4", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=32), "f16", 2, 2, 4, 8 * 150 + 6, 96),
+    ("i8g-bf16-k8-r16-d96-g2", dict(mode="jpeg", block_size=16, keep_freqs=8, quant_bits=8, quant_group=32), "bf16", 1, 2, 2, 16 * 70 + 1, 96),
 ]
 
 
@@ -363,7 +365,12 @@ STEP_PAIRS = [
     (dict(I8, keep_freqs=8), "f16", 96, 4, True),
     (dict(I8, keep_freqs=1), "f16", 256, 8, True),
     (dict(I8, block_size=16, keep_freqs=4), "bf16", 128, 2, True),
-    (dict(I8, quant_group=32), "bf16", 128, 2, False),
+    # per-32 scales: the one-launch step archives them in-kernel
+    (dict(I8, quant_group=32), "bf16", 128, 2, True),
+    (dict(I8, quant_group=32, keep_freqs=8), "f16", 96, 4, True),
+    (dict(I8, quant_group=32, keep_freqs=2), "bf16", 64, 1, True),
+    (dict(I8, quant_group=32, keep_freqs=1), "f16", 256, 8, True),
+    (dict(I8, quant_group=32, block_size=16, keep_freqs=3), "bf16", 128, 16, True),
     (dict(mode="png", block_size=8, keep_ratio=0.5, packed=True), "f32", 64, 4, False),
 ]
 

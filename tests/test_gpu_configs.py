@@ -227,26 +227,31 @@ def _archives_equal(a, b):
 C5 = dict(B=16, Hkv=8, G=2, D=128, dt="bf16")
 
 
-def test_fused_step_c5_scale_multi_split(oracle):
+C5_SCALES = [(I8_C3, N.STORE_JPEG_I8), (dict(I8_C3, quant_group=32), N.STORE_JPEG_I8G)]
+
+
+@pytest.mark.parametrize("cfg,kind", C5_SCALES, ids=["per-row", "per-32"])
+def test_fused_step_c5_scale_multi_split(cfg, kind, oracle):
     """The C5 model's per-layer decode step as it runs there: the one-launch
     step kernel (attn_split_i8_mfma<4, 128, 2, STEP>) at C5's geometry (batch
-    16, 16 q / 8 kv heads, D=128, bf16, k=4 int8) over 512 archived blocks +
-    a 5-token tail, so the split count is the model's (4 > 1: the cross-split
-    arrival and merge, the queued passes after the first and split 0's
-    in-kernel append / archive beside streaming splits all run).  12 steps
-    cross two block boundaries; after every step all 16 sequences are
-    checked against the fp64 oracle on the streams' rows, and the archives
-    the kernel wrote against the two-append path's, bit for bit."""
+    16, 16 q / 8 kv heads, D=128, bf16, k=4 int8; one scale per row or per 32
+    features) over 512 archived blocks + a 5-token tail, so the split count
+    is the model's (4 > 1: the cross-split arrival and merge, the queued
+    passes after the first and split 0's in-kernel append / archive beside
+    streaming splits all run).  12 steps cross two block boundaries; after
+    every step all 16 sequences are checked against the fp64 oracle on the
+    streams' rows, and the archives the kernel wrote against the two-append
+    path's, bit for bit."""
     B, Hkv, G, D, dt = C5["B"], C5["Hkv"], C5["G"], C5["D"], C5["dt"]
     r = 8
     S0 = 512 * r + 5
-    print("case fused step at C5 scale", flush=True)
-    ks, vs = build_streams(I8_C3, dt, B, Hkv, S0, D, 141, oracle)
-    ks_r, vs_r = build_streams(I8_C3, dt, B, Hkv, S0, D, 141, oracle)
+    print(f"case fused step at C5 scale {cfg}", flush=True)
+    ks, vs = build_streams(cfg, dt, B, Hkv, S0, D, 141, oracle)
+    ks_r, vs_r = build_streams(cfg, dt, B, Hkv, S0, D, 141, oracle)
     L = N.lib()
     g = torch.Generator(device=DEV).manual_seed(142)
     for step in range(r + 4):
-        ns = L.fc_attention_splits(N.STORE_JPEG_I8, N.BF16, N.BF16, 4, ks.n_blocks, B, Hkv, G, D,
+        ns = L.fc_attention_splits(kind, N.BF16, N.BF16, 4, ks.n_blocks, B, Hkv, G, D,
                                    N.num_cus(torch.device(DEV)))
         assert 1 < ns <= 64, ns
         q = _tokens(g, B, Hkv * G, D, dt)
@@ -301,14 +306,16 @@ def test_graph_replayed_steps_match_oracle(cfg, dt, G, oracle):
     _graph_steps(cfg, dt, 2, 2, G, 128, 4 * r + 5, 3 * r + 2, 222, oracle)
 
 
-def test_graph_replayed_steps_c5_scale(oracle):
+@pytest.mark.parametrize("cfg,kind", C5_SCALES, ids=["per-row", "per-32"])
+def test_graph_replayed_steps_c5_scale(cfg, kind, oracle):
     """Graph-replayed one-launch steps at C5's geometry (batch 16, 16 q / 8
-    kv heads, D=128, bf16, k=4 int8, 512 archived blocks + 5 tail tokens: 4
-    splits, the model's): 12 replays across two block boundaries, every
-    sequence of every replay against the fp64 oracle, and the archives the
-    replays wrote against the two-append path's, bit for bit."""
-    print("case graph step at C5 scale", flush=True)
-    _graph_steps(I8_C3, C5["dt"], C5["B"], C5["Hkv"], C5["G"], C5["D"], 512 * 8 + 5, 12, 151,
+    kv heads, D=128, bf16, k=4 int8 with one scale per row or per 32
+    features, 512 archived blocks + 5 tail tokens: 4 splits, the model's):
+    12 replays across two block boundaries, every sequence of every replay
+    against the fp64 oracle, and the archives the replays wrote against the
+    two-append path's, bit for bit."""
+    print(f"case graph step at C5 scale {cfg}", flush=True)
+    _graph_steps(cfg, C5["dt"], C5["B"], C5["Hkv"], C5["G"], C5["D"], 512 * 8 + 5, 12, 151,
                  oracle, check_archive=True, single_launch=True)
 
 
