@@ -26,11 +26,10 @@ bool split_i8_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q
 
 bool split_i8_mfma_fusable(int n_splits) { return n_splits <= kFuseMaxSplits; }
 
-// Per-32 scales (FC_STORE_JPEG_I8G) on the matrix-core pass: fp16 / bf16
-// queries, head sizes 64 / 96 / 128 / 256 (whole groups of 32 features).
+// Per-32 scales (FC_STORE_JPEG_I8G) on the matrix-core pass: head sizes 64
+// / 96 / 128 / 256 (whole groups of 32 features).
 bool mfma_group_shape_supported(int q_dtype, int64_t D, int s) {
-  return (q_dtype == FC_F16 || q_dtype == FC_BF16) && D % 32 == 0 &&
-         mfma_shape_supported(q_dtype, D, s);
+  return D % 32 == 0 && mfma_shape_supported(q_dtype, D, s);
 }
 
 // Whether the int8 matrix-core split pass takes this call's stores: int8
@@ -131,7 +130,9 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   a.cstride = stride;
   const dim3 grid((unsigned)(a.ngroups * n_splits));
   const int rc = mfma_with_int<FC_MFMA_ROWS_LIST>(s, [&](auto sc) {
-    return launch_mfma_rows<decltype(sc)::value>(a, (int)D, gp, grid, st);
+    constexpr int SR = decltype(sc)::value;
+    return grouped ? launch_mfma_rows_g<SR>(a, (int)D, gp, grid, st)
+                   : launch_mfma_rows<SR>(a, (int)D, gp, grid, st);
   });
   if (rc != FC_OK) return rc;
   return check_launch();

@@ -771,8 +771,7 @@ template <int SROWS, int D, int GP, bool STEP, bool QF = false, bool QG = false>
 __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void attn_split_i8_mfma(
     MfmaArgs p) {
   static_assert(!(STEP && QF), "the fused step takes fp16 / bf16 queries");
-  static_assert(!QG || (!QF && D % 32 == 0),
-                "per-32 scales: fp16 / bf16 queries, D = 64 / 96 / 128 / 256");
+  static_assert(!QG || D % 32 == 0, "per-32 scales: D = 64 / 96 / 128 / 256");
   constexpr int DC = mfma_width<D>();
   constexpr int DK = DC / 32;
   constexpr int DV = (DC + 127) / 128;  // 128-feature groups of the value product
@@ -797,10 +796,12 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
   auto& w_lds_f = w_buf.f;
   __shared__ float sc_lds[kWaves][2][PRT];  // K and V row scales of the pass
   // QG (one scale per 32 features): the pass's K group scales and the V
-  // group scales relative to their row's largest, by group then row
+  // group scales relative to their row's largest (QF: in fp32), by group
+  // then row
   constexpr int NGR = QG ? D / 32 : 1;
+  using vg_t = std::conditional_t<QF, float, _Float16>;
   __shared__ __attribute__((aligned(16))) float kg_lds[QG ? kWaves : 1][NGR][PRT];
-  __shared__ __attribute__((aligned(16))) _Float16 vg_lds[QG ? kWaves : 1][NGR][PRT];
+  __shared__ __attribute__((aligned(16))) vg_t vg_lds[QG ? kWaves : 1][NGR][PRT];
   __shared__ float a_lds[FC_MAX_BLOCK * SROWS];
   __shared__ float comb[kWaves][16][3];
   // the wavefronts' accumulators, for the combine (and the fused step's
@@ -1219,6 +1220,8 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
       if constexpr (QG) {
         // per 32-feature group: one score product (lanes q < 2 hold group 2c
         // of chunk c, q >= 2 group 2c + 1), scaled by the rows' group scales
+        // (QF: the group's exact digit sums joined in fp32, as the per-row
+        // pass joins them)
         float4_t accg = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -1238,11 +1241,25 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
             const float4_t kgv =
                 *reinterpret_cast<const float4_t*>(&kg_lds[wave][2 * c + hf][16 * t + 4 * lq]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              accg[i] = __builtin_fmaf(kgv[i], (float)(sd[1][i] * 256 + sd[0][i]), accg[i]);
+            for (int i = 0; i < 4; ++i) {
+              if constexpr (QF) {
+                float v = (float)sd[ND - 1][i];
+#pragma unroll
+                for (int k = ND - 2; k >= 0; --k) v = __builtin_fmaf(v, 256.f, (float)sd[k][i]);
+                accg[i] = __builtin_fmaf(kgv[i], v, accg[i]);
+              } else {
+                accg[i] = __builtin_fmaf(kgv[i], (float)(sd[1][i] * 256 + sd[0][i]), accg[i]);
+              }
+            }
           }
         }
-        if (lc < G) *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = accg * head_mul;
+        if constexpr (QF) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) accg[i] = ldexpf(accg[i], qe);  // the scale follows in fp64
+        } else {
+          accg *= head_mul;
+        }
+        if (lc < G) *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = accg;
         continue;
       }
       i32x4_t sd[ND];
@@ -1282,7 +1299,12 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
       const float rv = vmax > 0.f ? __builtin_amdgcn_rcpf(vmax) : 0.f;
       if (lane < PRT) {
 #pragma unroll
-        for (int i = 0; i < NGR; ++i) vg_lds[wave][i][lane] = (_Float16)(vgr[i] * rv);
+        for (int i = 0; i < NGR; ++i) {
+          if constexpr (QF)
+            vg_lds[wave][i][lane] = vmax > 0.f ? vgr[i] / vmax : 0.f;
+          else
+            vg_lds[wave][i][lane] = (_Float16)(vgr[i] * rv);
+        }
       }
       ks_r = 1.f;
       vs_r = vmax;
@@ -1347,6 +1369,38 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
     wave_lds_sync();
 
     // ------------------------------------------------------------ values
+    if constexpr (QF && QG) {
+      // fp32 weights by fp32 values (codes times their group scale relative
+      // to the row's largest, one rounding): v_mfma_f32_16x16x4_f32, row
+      // 32 sl + 8 q + m of the pass as k = q of instruction m; lane (q, c)
+      // holds column c (feature 128 dv + 8 c + e) of its rows 8q .. 8q+7
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) {
+        float4_t f0 = *reinterpret_cast<const float4_t*>(&w_lds_f[wave][lc][32 * sl + 8 * lq]);
+        float4_t f1 = *reinterpret_cast<const float4_t*>(&w_lds_f[wave][lc][32 * sl + 8 * lq + 4]);
+        if (lc >= G) f0 = f1 = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dv = 0; dv < DV; ++dv) {
+          const int gi = min(4 * dv + lc / 4, NGR - 1);
+          const float4_t r0 = *reinterpret_cast<const float4_t*>(&vg_lds[wave][gi][32 * sl + 8 * lq]);
+          const float4_t r1 = *reinterpret_cast<const float4_t*>(&vg_lds[wave][gi][32 * sl + 8 * lq + 4]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+              // code + 128 as an unsigned byte; (u - 128) * rat in one fma
+              const uint32_t u = (vr[sl][dv][2 * m + e / 4] ^ 0x80808080u) >> (8 * (e % 4));
+              const float rt = m < 4 ? r0[m] : r1[m - 4];
+              const float bv = __builtin_fmaf((float)(u & 0xffu), rt, -128.0f * rt);
+              acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(m < 4 ? f0[m] : f1[m - 4], bv,
+                                                                acc[dv][e], 0, 0, 0);
+            }
+        }
+      }
+      wave_lds_sync();
+      cur = nxt;
+      continue;
+    }
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl) {
       half8_t wop, wop_lo = {};
@@ -1475,25 +1529,17 @@ int mfma_with_int(int v, F&& f) {
 #define FC_MFMA_HEAD_DIMS 64, 80, 96, 128, 256
 
 // Launch of the split pass with SR stored rows per block, dispatched on the
-// head size and the head-group size.  Each SR is instantiated
-// in a translation unit of its own (fc_attn_mfma_s<SR>.hip).
+// head size and the head-group size: one scale per row (launch_mfma_rows)
+// or per 32 features (launch_mfma_rows_g).  Each SR and scale layout is
+// instantiated in a translation unit of its own (fc_attn_mfma_s<SR>.hip,
+// fc_attn_mfma_g<SR>.hip).
 template <int SR>
 int launch_mfma_rows(const MfmaArgs& a, int d, int gp, dim3 grid, hipStream_t st) {
   return mfma_with_int<FC_MFMA_HEAD_DIMS>(d, [&](auto dc) {
     constexpr int Dv = decltype(dc)::value;
     return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
       constexpr int GPv = decltype(gc)::value;
-      if (a.qgroup) {
-        if constexpr (Dv % 32 == 0) {
-          if (a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
-          if (a.step)
-            attn_split_i8_mfma<SR, Dv, GPv, true, false, true><<<grid, kMThreads, 0, st>>>(a);
-          else
-            attn_split_i8_mfma<SR, Dv, GPv, false, false, true><<<grid, kMThreads, 0, st>>>(a);
-        } else {
-          return FC_ERR_UNSUPPORTED;
-        }
-      } else if (a.step) {
+      if (a.step) {
         if (a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
         attn_split_i8_mfma<SR, Dv, GPv, true><<<grid, kMThreads, 0, st>>>(a);
       } else if (a.q_dtype == FC_F32) {
@@ -1506,10 +1552,33 @@ int launch_mfma_rows(const MfmaArgs& a, int d, int gp, dim3 grid, hipStream_t st
   });
 }
 
-extern template int launch_mfma_rows<1>(const MfmaArgs&, int, int, dim3, hipStream_t);
-extern template int launch_mfma_rows<2>(const MfmaArgs&, int, int, dim3, hipStream_t);
-extern template int launch_mfma_rows<3>(const MfmaArgs&, int, int, dim3, hipStream_t);
-extern template int launch_mfma_rows<4>(const MfmaArgs&, int, int, dim3, hipStream_t);
-extern template int launch_mfma_rows<8>(const MfmaArgs&, int, int, dim3, hipStream_t);
+template <int SR>
+int launch_mfma_rows_g(const MfmaArgs& a, int d, int gp, dim3 grid, hipStream_t st) {
+  return mfma_with_int<64, 96, 128, 256>(d, [&](auto dc) {
+    constexpr int Dv = decltype(dc)::value;
+    return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
+      constexpr int GPv = decltype(gc)::value;
+      if (a.step) {
+        if (a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
+        attn_split_i8_mfma<SR, Dv, GPv, true, false, true><<<grid, kMThreads, 0, st>>>(a);
+      } else if (a.q_dtype == FC_F32) {
+        attn_split_i8_mfma<SR, Dv, GPv, false, true, true><<<grid, kMThreads, 0, st>>>(a);
+      } else {
+        attn_split_i8_mfma<SR, Dv, GPv, false, false, true><<<grid, kMThreads, 0, st>>>(a);
+      }
+      return FC_OK;
+    });
+  });
+}
+
+#define FC_MFMA_EXTERN(SR)                                                                 \
+  extern template int launch_mfma_rows<SR>(const MfmaArgs&, int, int, dim3, hipStream_t); \
+  extern template int launch_mfma_rows_g<SR>(const MfmaArgs&, int, int, dim3, hipStream_t);
+FC_MFMA_EXTERN(1)
+FC_MFMA_EXTERN(2)
+FC_MFMA_EXTERN(3)
+FC_MFMA_EXTERN(4)
+FC_MFMA_EXTERN(8)
+#undef FC_MFMA_EXTERN
 
 }  // namespace fc

@@ -144,6 +144,12 @@ CASES = [
     ("i8g-bf16-k3-r16-g4", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8, quant_group=32), "bf16", 1, 2, 4, 16 * 60 + 5, 128),
     ("i8g-bf16-k2-d256-g2", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8, quant_group=32), "bf16", 1, 2, 2, 8 * 100 + 3, 256),
     ("i8g-f16-k4-d96-g4", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=32), "f16", 2, 2, 4, 8 * 150 + 6, 96),
+    # fp32 queries on per-32 archives: fp32 value products on the matrix cores
+    ("i8g-f32-k4-g4", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=32), "f32", 2, 2, 4, 8 * 300 + 5, 128),
+    ("i8g-f32-k8-d64-g16", dict(mode="jpeg", block_size=8, keep_freqs=8, quant_bits=8, quant_group=32), "f32", 1, 1, 16, 8 * 90 + 2, 64),
+    ("i8g-f32-k2-d256-g2", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8, quant_group=32), "f32", 1, 2, 2, 8 * 70 + 3, 256),
+    ("i8g-f32-k1-g1", dict(mode="jpeg", block_size=8, keep_freqs=1, quant_bits=8, quant_group=32), "f32", 2, 2, 1, 8 * 120, 128),
+    ("i8g-f32-k3-r16-d96-g8", dict(mode="jpeg", block_size=16, keep_freqs=3, quant_bits=8, quant_group=32), "f32", 1, 2, 8, 16 * 50 + 11, 96),
     ("i8g-bf16-k8-r16-d96-g2", dict(mode="jpeg", block_size=16, keep_freqs=8, quant_bits=8, quant_group=32), "bf16", 1, 2, 2, 16 * 70 + 1, 96),
 ]
 
@@ -229,6 +235,25 @@ def test_decode_attention_matches_oracle(case, variant, oracle, attention_pass):
     assert ks._rec is None and vs._rec is None
     ref = oracle_out(oracle, q, ks, vs, D ** -0.5)
     assert_close(to_values(out)[:, :, 0], ref, dt)
+
+
+@pytest.mark.parametrize("group", [0, 32], ids=["per-row", "per-32"])
+@pytest.mark.parametrize("variant", ["auto", "valu"])
+def test_fp32_queries_with_sharp_logits(group, variant, oracle, attention_pass):
+    """fp32 queries whose logits reach the tens (a nearly one-hot softmax,
+    where a logit's rounding moves the output most) on int8 archives with
+    one scale per row or per 32 features: within 1e-5 of the fp64 oracle
+    on both passes."""
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, quant_group=group)
+    attention_pass(variant)
+    B, Hk, G, S, D = 2, 2, 4, 8 * 200 + 3, 128
+    print(f"case fp32 sharp logits group={group} [{variant}]", flush=True)
+    ks, vs = build_streams(cfg, "f32", B, Hk, S, D, 77, oracle)
+    rng = np.random.default_rng(78)
+    q = torch.from_numpy((6 * rng.standard_normal((B, Hk * G, 1, D))).astype(np.float32)).to(DEV)
+    out = fc.codec_decode_attention(q, ks, vs)
+    ref = oracle_out(oracle, q, ks, vs, D ** -0.5)
+    assert_close(to_values(out)[:, :, 0], ref, "f32")
 
 
 @pytest.mark.parametrize("name", Golden("attention").names())
