@@ -119,6 +119,7 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
   const int64_t qpos_max = p.P0 + last_tok;
   const int myq = lane % GP;
   const int64_t qpos_lane = p.P0 + tok_of(myq);
+  const int64_t qpos_min = p.P0 + tq0;  // the wave's first query token
 
   // archived blocks this wavefront needs: up to its newest query's position
   const int64_t nbw = min<int64_t>(p.nb, qpos_max / r + 1);
@@ -254,45 +255,96 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
   // Output weights of the pass's (block, query) pairs (exponentials against
   // mref, times the V row scale * wm) into w_lds; causal: token t of block
   // `blk` takes part only when blk * r + t <= the query's position.
+  // 1 / A[t][0] when column 0 of A is one nonzero constant (jpeg: the DC
+  // row of the DCT basis, sqrt(1/r) at every tap), else 0; set once a_lds
+  // is filled
+  float dc_inv = 0.f;
   auto weights = [&](int64_t blk0, int prow, float mref, float wm, float& pmax, float& lsum) {
-    pmax = -INFINITY;
     lsum = 0.f;
     const int npair = (prow / SROWS) * GP;
-    for (int u = lane; u < npair; u += 64) {
-      const int row0 = (u / GP) * SROWS;
-      const int64_t tok0 = (blk0 + u / GP) * r;
-      const int tlim = (int)min<int64_t>(r, qpos_lane - tok0 + 1);  // causal taps (>= 1)
-      float sv[SROWS], w[SROWS];
+    // Logits are formed relative to mref by the fma chain (finite stand-in
+    // 0 in a lane whose mref is -inf: that lane's weights are formed again
+    // against its new maximum).
+    const float mo = mref == -INFINITY ? 0.f : mref;
+    float pm = -INFINITY;
+    // RC taps: compile-time for the common block sizes (no branches between
+    // taps), else a loop.  MASK: causal mask per (block, query) (the
+    // diagonal passes; a pass whose last token is at or before the wave's
+    // first query needs none).  MX: the wave's first pass (mref = -inf in
+    // every lane) yields only the maximum, its weights follow against it.
+    // DC (with RC): a constant column 0 of A (the DCT's DC row) gives the
+    // pair's exponential sum as w[0] / A[t][0], one product for r additions.
+    auto pairs = [&](auto rc, auto mask, auto mx) {
+      constexpr int RC = decltype(rc)::value;
+      constexpr bool MASK = decltype(mask)::value, MX = decltype(mx)::value;
+      constexpr bool DC = RC != 0;
+      for (int u = lane; u < npair; u += 64) {
+        const int row0 = (u / GP) * SROWS;
+        // causal taps of the pair (<= 0: the block starts after the query)
+        int tlim = r;
+        if constexpr (MASK) tlim = (int)min<int64_t>(r, qpos_lane - (blk0 + u / GP) * r + 1);
+        float sv[SROWS], w[SROWS];
 #pragma unroll
-      for (int j = 0; j < SROWS; ++j) {
-        sv[j] = s_lds[wave][myq][row0 + j] * sc_lds[wave][0][row0 + j];
-        w[j] = 0.f;
+        for (int j = 0; j < SROWS; ++j) {
+          sv[j] = s_lds[wave][myq][row0 + j] * sc_lds[wave][0][row0 + j];
+          w[j] = 0.f;
+        }
+        auto tap = [&](int t, bool on) {
+          float d = -mo;
+#pragma unroll
+          for (int j = 0; j < SROWS; ++j) d = __builtin_fmaf(a_lds[t * SROWS + j], sv[j], d);
+          if constexpr (MASK) d = on ? d : -INFINITY;
+          pm = fmaxf(pm, d);
+          if constexpr (!MX) {
+            const float e = __builtin_amdgcn_exp2f(d);
+            if constexpr (!DC) lsum += e;
+#pragma unroll
+            for (int j = 0; j < SROWS; ++j) w[j] = __builtin_fmaf(e, a_lds[t * SROWS + j], w[j]);
+          }
+        };
+        if constexpr (RC != 0) {
+#pragma unroll
+          for (int t = 0; t < RC; ++t) tap(t, t < tlim);
+        } else {
+          for (int t = 0; t < tlim; ++t) tap(t, true);
+        }
+        if constexpr (!MX) {
+          if constexpr (DC) lsum = __builtin_fmaf(w[0], dc_inv, lsum);
+#pragma unroll
+          for (int j = 0; j < SROWS; ++j)
+            w_lds[wave][myq][row0 + j] = (_Float16)(w[j] * (sc_lds[wave][1][row0 + j] * wm));
+        }
       }
-      auto tap = [&](int t) {
-        float lg = 0.f;
-#pragma unroll
-        for (int j = 0; j < SROWS; ++j) lg = __builtin_fmaf(a_lds[t * SROWS + j], sv[j], lg);
-        pmax = fmaxf(pmax, lg);
-        const float e = __builtin_amdgcn_exp2f(lg - mref);
-        lsum += e;
-#pragma unroll
-        for (int j = 0; j < SROWS; ++j) w[j] = __builtin_fmaf(e, a_lds[t * SROWS + j], w[j]);
-      };
-      if (r <= kTapsUnrolled) {
-#pragma unroll
-        for (int t = 0; t < kTapsUnrolled; ++t)
-          if (t < tlim) tap(t);
-      } else {
-        for (int t = 0; t < tlim; ++t) tap(t);
-      }
-#pragma unroll
-      for (int j = 0; j < SROWS; ++j)
-        w_lds[wave][myq][row0 + j] = (_Float16)(w[j] * (sc_lds[wave][1][row0 + j] * wm));
-    }
+    };
+    auto with_rc = [&](auto mask, auto mx) {
+      if (dc_inv != 0.f && r == 8)
+        pairs(std::integral_constant<int, 8>{}, mask, mx);
+      else if (dc_inv != 0.f && r == 4)
+        pairs(std::integral_constant<int, 4>{}, mask, mx);
+      else if (dc_inv != 0.f && r == 16)
+        pairs(std::integral_constant<int, 16>{}, mask, mx);
+      else
+        pairs(std::integral_constant<int, 0>{}, mask, mx);
+    };
+    const bool open = (blk0 + prow / SROWS) * r - 1 <= qpos_min;
+    const bool first = __builtin_amdgcn_ballot_w64(mref != -INFINITY) == 0;
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    if (first)
+      open ? with_rc(F_{}, T_{}) : with_rc(T_{}, T_{});
+    else
+      open ? with_rc(F_{}, F_{}) : with_rc(T_{}, F_{});
+    pmax = pm + mo;
   };
 
   __syncthreads();  // a_lds (the only workgroup barrier)
   if (tq0 >= p.Sq) return;  // a wavefront past the last query token
+  if (p.nb > 0) {
+    const float a0 = a_lds[0];
+    bool same = a0 != 0.f;
+    for (int t = 1; t < r; ++t) same = same && a_lds[t * SROWS] == a0;
+    dc_inv = same ? 1.0f / a0 : 0.f;
+  }
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
   if (npass > 0) load_k(0, rows_of(0));
   for (int64_t cur = 0; cur < npass; ++cur) {
