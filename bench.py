@@ -504,8 +504,8 @@ def shapes_mode(args):
            "unit": "GB/s", "shapes": []}
     prev = N.lib().fc_get_attention_pass()
     for D, k, grp, qdt in ((128, 3, 0, "f16"), (128, 8, 0, "f16"), (80, 4, 0, "f16"),
-                           (96, 4, 0, "f16"), (128, 4, 32, "f16"), (128, 4, 0, "f32"),
-                           (128, 4, 0, "f16")):
+                           (96, 4, 0, "f16"), (128, 4, 32, "f16"), (96, 4, 32, "f16"),
+                           (128, 4, 0, "f32"), (128, 4, 32, "f32"), (128, 4, 0, "f16")):
         cfg = dict(mode="jpeg", block_size=R, keep_freqs=k, quant_bits=8)
         if grp:
             cfg["quant_group"] = grp
@@ -556,6 +556,8 @@ def c5_mode(args):
     torch.manual_seed(0)
     model = Qwen3ForCausalLM(cfg).to(device=dev, dtype=torch.bfloat16).eval()
     model.generation_config.eos_token_id = None
+    # --c5-group 32: archives with one scale per 32 features
+    qgroup = {"quant_group": args.c5_group} if args.c5_group else {}
 
     def run(batch, prompt, steps):
         g = torch.Generator().manual_seed(1)
@@ -678,7 +680,7 @@ def c5_mode(args):
             except Exception as exc:         # a baseline that cannot be captured is reported
                 raw[tag] = {"error": f"{type(exc).__name__}: {exc}"[:300]}
             log(f"bench c5 graph: {tag} {raw[tag]}")
-        fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8,
+        fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, **qgroup,
                              materialization_free=True)
         run(2, 64, 4)
         res = {"metric": "end-to-end decode tokens/s (C5), codec, HIP-graph decode steps",
@@ -695,7 +697,7 @@ def c5_mode(args):
         # are the dispatch count of a run minus that of the same run with 0
         # steps, divided by the steps)
         if args.c5_kv != "raw":
-            fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8,
+            fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, **qgroup,
                                  materialization_free=True)
         if args.c5_kv == "codec-view-prefill":
             from flashcodec_amd import patch_attention as pa
@@ -709,12 +711,13 @@ def c5_mode(args):
     res = {"metric": "end-to-end decode tokens/s (C5)", "unit": "tokens/s", "n_gpus": 1,
            "config": {"workload": "C5 Qwen3-0.6B-shaped greedy decoding", "layers": 28,
                       "hidden": 1024, "q_heads": 16, "kv_heads": 8, "head_dim": 128,
-                      "dtype": "bf16", "codec": "jpeg r=8 k=4 int8, materialization-free"},
+                      "dtype": "bf16", "codec": "jpeg r=8 k=4 int8, materialization-free"
+                      + (f", one scale per {args.c5_group} features" if args.c5_group else "")},
            "data": "random-init weights, random prompt ids"}
     run(2, 64, 4)                                              # warm-up (kernels, allocator)
     res["raw_kv_b16"] = run(16, 4096, 256)
     res["raw_kv_b1"] = run(1, 4096, 32)
-    fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8,
+    fc.apply_flash_codec(model, mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8, **qgroup,
                          materialization_free=True)
     run(2, 64, 4)
     res["codec_b16"] = run(16, 4096, 256)
@@ -732,6 +735,152 @@ def c5_mode(args):
     res["reference_published_b1_tok_s"] = 40.3
     log(f"bench c5: {res}")
     print(json.dumps(res))
+
+
+C5_LAYERS, C5_B, C5_HQ, C5_HKV, C5_D = 28, 16, 16, 8, 128
+
+
+def _c5_codec_cfg(args):
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+    if args.c5_group:
+        cfg["quant_group"] = args.c5_group
+    return cfg
+
+
+def c5step_mode(args):
+    """The C5 model's decode-attention step kernel in isolation: 28 layers
+    of C5-shaped K/V streams (batch 16, 16 q / 8 kv heads, D=128, bf16, jpeg
+    r=8 k=4 int8, --c5-prompt tokens of AR(1) rho=0.95 archived), one decode
+    step of every layer (codec_decode_step with the counters on the device:
+    token append + in-kernel archive every 8th step + attention, one launch
+    per layer) captured as a HIP graph and replayed --steps times, so the
+    launches run back to back as in the graph-replayed model.  Algorithmic
+    bytes per layer-step: the K and V codes and fp32 scales of the archived
+    blocks, the tail rows, the new tokens, q and out."""
+    import types
+    import torch
+    import flashcodec_amd as fc
+    from flashcodec_amd import graph
+    from flashcodec_amd.cache import FlashCodecLayer
+    dev = torch.device("cuda:0")
+    cfg = _c5_codec_cfg(args)
+    L, B, Hq, Hkv, D = C5_LAYERS, C5_B, C5_HQ, C5_HKV, C5_D
+    S0 = args.c5_prompt + 5
+    layers = []
+    for li in range(L):
+        layer = FlashCodecLayer(**cfg)
+        for st, seed in ((layer._key_stream, 2 * li + 1), (layer._value_stream, 2 * li + 2)):
+            st.append(ar1_device((B, Hkv, S0, D), 0.95, seed, dev).to(torch.bfloat16))
+        layers.append(layer)
+    torch.cuda.empty_cache()
+    steps = args.steps
+    cache = types.SimpleNamespace(layers=layers)
+    graph.prepare(cache, steps + args.warmup + 2)
+    g = torch.Generator(device=dev).manual_seed(7)
+    tok = lambda H: torch.randn((B, 1, H, D), generator=g, device=dev).to(torch.bfloat16).transpose(1, 2)
+    q_in, k_in, v_in = tok(Hq) / math.sqrt(D), tok(Hkv), tok(Hkv)
+    outs = [None] * L
+
+    def one_step():
+        for li, layer in enumerate(layers):
+            outs[li] = fc.codec_decode_step(q_in, k_in, v_in, layer._key_stream,
+                                            layer._value_stream)
+
+    from flashcodec_amd import _native as N
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        one_step()                      # creates the workspace on the capture stream
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    single = N.lib().fc_last_step_single_launch()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=stream):
+        one_step()
+    done = 1
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            gr.replay()
+    torch.cuda.synchronize()
+    done += args.warmup
+    nb0 = layers[0]._key_stream.n_blocks + (layers[0]._key_stream._n_raw + done) // 8
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(steps):
+            gr.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    done += steps
+    graph.advance_host(cache, done)
+    graph.release(cache)
+    nb1 = layers[0]._key_stream.n_blocks
+    us = e0.elapsed_time(e1) / (steps * L) * 1e3
+    ngr = D // 32 if args.c5_group else 1
+    nb = (nb0 + nb1) / 2
+    # codes + scales of the archived blocks, the tail rows (3.5 on average)
+    # and the new tokens in bf16, q and out
+    alg = int(2 * B * Hkv * nb * 4 * (D + 4 * ngr) + 2 * B * Hkv * 3.5 * D * 2
+              + 2 * B * Hkv * D * 2 + 2 * B * Hq * D * 2)
+    res = {"metric": "C5 decode-attention step kernel, us per layer-step", "unit": "us",
+           "us_per_layer_step": round(us, 3), "launches_per_layer_step": 1 if single == 1 else None,
+           "single_launch": single == 1, "steps": steps, "layers": L,
+           "archived_blocks": [nb0, nb1],
+           "algorithmic_bytes_per_layer_step": alg, "GBs": round(alg / us / 1e3, 1),
+           "hbm_frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4),
+           "config": {"workload": "C5 step kernel", "B": B, "Hq": Hq, "Hkv": Hkv, "D": D,
+                      "codec": "jpeg r=8 k=4 int8" + (f", one scale per {args.c5_group} features"
+                                                      if args.c5_group else ""),
+                      "prompt": args.c5_prompt + 5, "dtype": "bf16"},
+           "data": "synthetic AR(1) rho=0.95 K/V, random tokens and queries"}
+    log(f"bench c5step: {res}")
+    print(json.dumps(res))
+
+
+def prefill_mode(args):
+    """The C5 prefill attention of one layer in isolation: batch 16, 16 q /
+    8 kv heads, D=128, bf16, a --c5-prompt-token prompt of AR(1) rho=0.95 K/V
+    archived as jpeg r=8 k=4 int8 (--c5-group); codec_prefill_attention (on
+    the archive) against the reference's semantics (the reconstructed view
+    and PyTorch SDPA, causal)."""
+    import torch
+    import torch.nn.functional as F
+    import flashcodec_amd as fc
+    from flashcodec_amd.attention import codec_prefill_attention
+    from flashcodec_amd.cache import _CodecStream
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, S = C5_B, C5_HQ, C5_HKV, C5_D, args.c5_prompt
+    cfg = _c5_codec_cfg(args)
+    ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
+    ks.append(ar1_device((B, Hkv, S, D), 0.95, 1, dev).to(torch.bfloat16))
+    vs.append(ar1_device((B, Hkv, S, D), 0.95, 2, dev).to(torch.bfloat16))
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = (torch.randn((B, Hq, S, D), generator=g, device=dev) / math.sqrt(D)).to(torch.bfloat16)
+
+    def view_sdpa():
+        k = ks.read().repeat_interleave(Hq // Hkv, 1)
+        v = vs.read().repeat_interleave(Hq // Hkv, 1)
+        ks.discard_view()
+        vs.discard_view()
+        return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+
+    t_arch = timed(lambda: codec_prefill_attention(q, ks, vs), args.steps, args.warmup)
+    t_view = timed(view_sdpa, args.steps, args.warmup)
+    a = codec_prefill_attention(q, ks, vs).float()
+    b = view_sdpa().float()
+    flops = 2 * 2 * B * Hq * D * S * (S + 1) / 2
+    res = {"metric": "C5 prefill attention of one layer", "unit": "us",
+           "archive_us": round(t_arch * 1e3, 1), "view_sdpa_us": round(t_view * 1e3, 1),
+           "dense_equivalent_TFLOPs_archive": round(flops / t_arch / 1e9, 1),
+           "max_abs_diff_vs_view_sdpa_rel_to_max": float((a - b).abs().max() / b.abs().max()),
+           "config": {"workload": "C5 prefill attention, one layer", "B": B, "Hq": Hq, "Hkv": Hkv,
+                      "D": D, "S": S, "codec": "jpeg r=8 k=4 int8" + (
+                          f", one scale per {args.c5_group} features" if args.c5_group else ""),
+                      "dtype": "bf16"},
+           "data": "synthetic AR(1) rho=0.95 K/V, q N(0,1)/sqrt(D)"}
+    log(f"bench prefill: {res}")
+    print(json.dumps(res))
+
 
 
 def read_pmc_traffic():
@@ -980,7 +1129,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--mode", choices=["c3", "c1", "c2", "c4", "c5", "refshapes", "shapes", "copy"],
+    ap.add_argument("--mode", choices=["c3", "c1", "c2", "c4", "c5", "c5step", "prefill", "refshapes",
+                                       "shapes", "copy"],
                     default="c3")
     ap.add_argument("--copy-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -992,6 +1142,8 @@ def main():
     ap.add_argument("--c5-batch", type=int, default=16)
     ap.add_argument("--c5-prompt", type=int, default=4096)
     ap.add_argument("--c5-kv", choices=["raw", "codec", "codec-view-prefill"], default="codec")
+    ap.add_argument("--c5-group", type=int, choices=[0, 32], default=0,
+                    help="C5 codec quantizer group (32: one scale per 32 features)")
     ap.add_argument("--c5-graph", action="store_true",
                     help="c5: codec decode steps replayed from a captured HIP graph")
     args = ap.parse_args()
@@ -1016,6 +1168,10 @@ def main():
         return shapes_mode(args)
     if args.mode == "c5":
         return c5_mode(args)
+    if args.mode == "c5step":
+        return c5step_mode(args)
+    if args.mode == "prefill":
+        return prefill_mode(args)
     if args.mode == "c4":
         return c4_mode(args)
 
