@@ -1165,7 +1165,9 @@ int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, in
   }
   const bool png_mfma =
       store_kind == FC_STORE_PNG && fc::png_mfma_shape_supported(q_dtype, stream_dtype, D, s);
-  const bool mfma = (png_mfma ||
+  const bool fpj_mfma =
+      store_kind == FC_STORE_JPEG_FP && fc::fpj_mfma_shape_supported(q_dtype, stream_dtype, D, s);
+  const bool mfma = (png_mfma || fpj_mfma ||
                      (store_kind == FC_STORE_JPEG_I8 && fc::mfma_shape_supported(q_dtype, D, s)) ||
                      (store_kind == FC_STORE_JPEG_I8G &&
                       fc::mfma_group_shape_supported(q_dtype, D, s))) &&
@@ -1182,7 +1184,8 @@ int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, in
     const int64_t cols = std::max<int64_t>(1, B * Hkv * groups);
     const int64_t per_cu = png_mfma ? fc::kPngWgPerCu : 2;
     int64_t want = (per_cu * (int64_t)n_cu + cols - 1) / cols;
-    const int64_t pr = png_mfma ? 16 : D == 256 ? 32 : 64;  // rows per pass
+    // rows per pass
+    const int64_t pr = png_mfma ? 16 : fpj_mfma ? (D == 64 ? 64 : 32) : D == 256 ? 32 : 64;
     const int64_t npass = (nb * s + pr - 1) / pr;
     want = std::min<int64_t>(want, std::max<int64_t>(1, npass / 4));
     want = std::min<int64_t>(want, std::max<int64_t>(16, npass / 10));
@@ -1431,6 +1434,24 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                                          kCounterWords, mstride,
                                          fuse ? &fz : nullptr, nullptr, st);
     if (rc != FC_OK || fuse) return rc;
+  } else if (nb > 0 && (parts & kPartSplit) && store_kind == FC_STORE_JPEG_FP &&
+             split_fpj_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, stream_dtype, key, value) &&
+             mstride > 0 && mfma_split_allowed()) {
+    if ((((nb + n_splits - 1) / n_splits) * (n_splits - 1)) >= nb) return FC_ERR_ARG;
+    const bool fuse = (parts & kPartMerge) && split_i8_mfma_fusable(n_splits);
+    MfmaFuse fz{};
+    if (fuse) {
+      fz.raw_dtype = stream_dtype;
+      fz.n_raw = n_raw;
+      fz.out = out;
+      fz.o_sb = o_sb;
+      fz.o_sh = o_sh;
+    }
+    const int rc = launch_split_fpj_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb, key,
+                                         value, A, scale_log2, pm, pl, pacc, n_splits, counters,
+                                         kCounterWords, mstride, fuse ? &fz : nullptr, nullptr,
+                                         st);
+    if (rc != FC_OK || fuse) return rc;
   } else if (nb > 0 && (parts & kPartSplit)) {
     // the merge runs inside the split pass when every group has a counter
     if (D % 8) return FC_ERR_UNSUPPORTED;
@@ -1555,6 +1576,20 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     return launch_split_png_mfma(q, q_sb, q_sh, B, Hq, Hkv, D, r, nb_hint, key, value,
                                  scale * kLog2e, pm, pl, pacc, n_splits, counters, kCounterWords,
                                  mstride, &fz, state, st);
+  }
+  if (store_kind == FC_STORE_JPEG_FP &&
+      split_fpj_mfma_supported(q, q_dtype, q_sb, q_sh, D, s, stream_dtype, key, value) &&
+      mfma_split_allowed() && mstride > 0) {
+    if (!split_i8_mfma_fusable(n_splits)) return FC_ERR_UNSUPPORTED;
+    MfmaFuse fz{};
+    fz.raw_dtype = stream_dtype;
+    fz.n_raw = 0;  // taken from the state
+    fz.out = out;
+    fz.o_sb = o_sb;
+    fz.o_sh = o_sh;
+    return launch_split_fpj_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, s, nb_hint, key, value,
+                                 A, scale * kLog2e, pm, pl, pacc, n_splits, counters,
+                                 kCounterWords, mstride, &fz, state, st);
   }
   if (!valu_fusable(B, Hkv, G)) return FC_ERR_UNSUPPORTED;
   return launch_split_valu(q, q_dtype, q_sb, q_sh, B, Hkv, G, D, store_kind, stream_dtype, r, s,

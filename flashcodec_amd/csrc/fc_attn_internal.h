@@ -113,6 +113,19 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
 // step's device counters (or NULL).
 bool png_mfma_shape_supported(int q_dtype, int stream_dtype, int64_t D, int r);
 constexpr int kPngWgPerCu = 2;  // workgroups per compute unit of the png pass
+// jpeg archives of fp16 / bf16 coefficients on the matrix cores
+// (fc_attn_fpj.hip): queries in the stream dtype, D = 64 / 128, s = 1 / 2 /
+// 3 / 4 / 8.
+bool fpj_mfma_shape_supported(int q_dtype, int stream_dtype, int64_t D, int s);
+bool split_fpj_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
+                              int s, int stream_dtype, const fc_stream_view* key,
+                              const fc_stream_view* value);
+int launch_split_fpj_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
+                          int64_t Hq, int64_t Hkv, int64_t D, int r, int s, int64_t nb,
+                          const fc_stream_view* key, const fc_stream_view* value, const float* A,
+                          float scale_log2, float* pm, float* pl, float* pacc, int n_splits,
+                          unsigned int* counters, int64_t counter_words, int64_t stride,
+                          const MfmaFuse* fuse, const int64_t* state, hipStream_t st);
 bool split_png_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
                               int r, int stream_dtype, const fc_stream_view* key,
                               const fc_stream_view* value);

@@ -125,6 +125,10 @@ struct MfmaArgs {
   const uint32_t* kmask;
   const uint32_t* vmask;
   int keep_m;
+  // jpeg archives of fp coefficients (fc_attn_fpj.hip): (B, H, cap, k, D)
+  // rows in the stream dtype
+  const void* kfp;
+  const void* vfp;
 };
 
 constexpr int kMThreads = 256;

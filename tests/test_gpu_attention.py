@@ -190,11 +190,26 @@ CASES += [
     ("fp-jpeg-f32-k2-g5", dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 1, 2, 5, 8 * 1000 + 3, 128),
 ]
 
+FPJ = dict(mode="jpeg", block_size=8, keep_freqs=4)
+CASES += [
+    # fp16 / bf16 coefficient rows on the matrix-core pass (queries in the
+    # stream dtype): rows per block, head groups, widths, tails
+    ("fpj-f16-k4-g4", FPJ, "f16", 2, 4, 4, 8 * 300 + 5, 128),
+    ("fpj-bf16-k4-g2", FPJ, "bf16", 2, 2, 2, 8 * 260 + 3, 128),
+    ("fpj-bf16-k2-d64-g8", dict(FPJ, keep_freqs=2), "bf16", 1, 2, 8, 8 * 200 + 7, 64),
+    ("fpj-f16-k8-r16-g16", dict(FPJ, block_size=16, keep_freqs=8), "f16", 1, 2, 16, 16 * 90 + 11, 128),
+    ("fpj-bf16-k1-g1", dict(FPJ, keep_freqs=1), "bf16", 2, 3, 1, 8 * 400 + 2, 128),
+    ("fpj-f16-k3-d64-g3", dict(FPJ, keep_freqs=3), "f16", 1, 2, 3, 8 * 150 + 1, 64),
+    ("fpj-bf16-k4-no-tail", FPJ, "bf16", 1, 2, 4, 8 * 100, 128),
+    ("fpj-f16-k2-r4-g5", dict(FPJ, block_size=4, keep_freqs=2), "f16", 1, 2, 5, 4 * 300 + 3, 64),
+]
+
 
 @pytest.fixture
 def attention_pass():
     """use(name) selects the split pass for this test ("auto": matrix cores
-    for int8 jpeg; "valu": the vector-ALU pass, the only one for fp stores);
+    for int8 jpeg, fp16 / bf16 jpeg and fp32 png; "valu": the vector-ALU
+    pass, the only one for the other stores);
     the previous selection is restored afterwards."""
     from flashcodec_amd import _native as N
     prev = []
@@ -216,7 +231,7 @@ def split_variant(request, attention_pass):
 
 # int8 cases on both split passes, fp-store cases on their one pass
 ORACLE_CASES = [(c, "auto") for c in CASES] + [(c, "valu") for c in CASES
-                                                if c[1].get("quant_bits")]
+                                                if c[1].get("quant_bits") or c[0].startswith("fpj")]
 
 
 @pytest.mark.parametrize("case,variant", ORACLE_CASES,
@@ -380,6 +395,7 @@ STEP_PAIRS = [
     (I8, "f16", 64, 4, True),
     (dict(I8, keep_freqs=2), "bf16", 64, 4, True),
     (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 64, 4, False),
+    (dict(mode="jpeg", block_size=8, keep_freqs=4), "bf16", 128, 2, False),
     (dict(mode="png", block_size=8, keep_ratio=0.5), "f32", 64, 4, False),
     (dict(mode="png", block_size=4, keep_ratio=1.0), "bf16", 64, 4, False),
     # the C5 instantiation (D=128, bf16, k=4, G=2), other row counts and widths
