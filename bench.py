@@ -489,9 +489,10 @@ def refshapes_mode(args):
 
 
 def shapes_mode(args):
-    """Decode attention on int8 archives at C3's geometry (B=8, 32 q / 8 kv
-    heads, 32768 archived + 5 raw tokens, fp16, r=8) for head sizes,
-    keep_freqs, per-32 scales and fp32 queries besides C3's: each on the
+    """Decode attention at C3's geometry (B=8, 32 q / 8 kv heads, 32768
+    archived + 5 raw tokens, r=8) on int8 archives (fp16 stream) for head
+    sizes, keep_freqs, per-32 scales and fp32 queries besides C3's, and on
+    fp16 / bf16 coefficient archives (quant_bits=0): each on the
     matrix-core pass (FC_PASS_AUTO) and on the vector-ALU pass
     (FC_PASS_VECTOR), one archive set, max error vs the fp64 oracle over all
     sequences."""
@@ -500,27 +501,32 @@ def shapes_mode(args):
     from flashcodec_amd import _native as N
     from flashcodec_amd.cache import _CodecStream
     dev = torch.device("cuda:0")
-    res = {"metric": "decode attention GB/s by head size and keep_freqs, int8 jpeg, C3 geometry",
+    res = {"metric": "decode attention GB/s by head size, keep_freqs and store, jpeg, C3 geometry",
            "unit": "GB/s", "shapes": []}
     prev = N.lib().fc_get_attention_pass()
-    for D, k, grp, qdt in ((128, 3, 0, "f16"), (128, 8, 0, "f16"), (80, 4, 0, "f16"),
-                           (96, 4, 0, "f16"), (128, 4, 32, "f16"), (96, 4, 32, "f16"),
-                           (128, 4, 0, "f32"), (128, 4, 32, "f32"), (128, 4, 0, "f16")):
-        cfg = dict(mode="jpeg", block_size=R, keep_freqs=k, quant_bits=8)
+    # (D, keep_freqs, quantizer group, query dtype, quant_bits): int8 rows
+    # (fp16 stream) and fp coefficient rows in the query's dtype
+    for D, k, grp, qdt, qb in ((128, 3, 0, "f16", 8), (128, 8, 0, "f16", 8), (80, 4, 0, "f16", 8),
+                               (96, 4, 0, "f16", 8), (128, 4, 32, "f16", 8), (96, 4, 32, "f16", 8),
+                               (128, 4, 0, "f32", 8), (128, 4, 32, "f32", 8),
+                               (128, 4, 0, "f16", 0), (128, 2, 0, "bf16", 0),
+                               (128, 4, 0, "f16", 8)):
+        cfg = dict(mode="jpeg", block_size=R, keep_freqs=k, quant_bits=qb)
         if grp:
             cfg["quant_group"] = grp
+        qt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[qdt]
+        st_dt = torch.float16 if qb else qt
         ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
         for st, seed in ((ks, 1), (vs, 2)):
-            x = ar1_device((B, HKV, S_ARCH + TAIL, D), 0.95, seed, dev).to(torch.float16)
+            x = ar1_device((B, HKV, S_ARCH + TAIL, D), 0.95, seed, dev).to(st_dt)
             st.append(x)
             del x
         g = torch.Generator(device=dev).manual_seed(3)
-        qt = torch.float32 if qdt == "f32" else torch.float16
         q = (torch.randn((B, HQ, 1, D), generator=g, device=dev) / math.sqrt(D)).to(qt)
-        scale_bytes = 4 * (D // grp if grp else 1)
+        row_bytes = D + 4 * (D // grp if grp else 1) if qb else 2 * D
         qo_bytes = 2 * B * HQ * D * q.element_size()
-        nbytes = 2 * (B * HKV * NB * k * (D + scale_bytes)) + 2 * B * HKV * TAIL * D * 2 + qo_bytes
-        row = {"D": D, "keep_freqs": k, "quant_group": grp, "q_dtype": qdt,
+        nbytes = 2 * (B * HKV * NB * k * row_bytes) + 2 * B * HKV * TAIL * D * 2 + qo_bytes
+        row = {"D": D, "keep_freqs": k, "quant_bits": qb, "quant_group": grp, "q_dtype": qdt,
                "algorithmic_bytes": nbytes}
         for name, code in (("matrix_core", N.PASS_AUTO), ("vector_alu", N.PASS_VECTOR)):
             N.lib().fc_set_attention_pass(code)
@@ -953,8 +959,11 @@ def check_against_oracle(q, ks, vs, out):
     # per-row scales (..., k) or, with quant_group, per-32 scales (..., k, D/32)
     sc = (lambda st: st._scales[:, :, :nb]) if ks.codec.quant_group else \
         (lambda st: st._scales[:, :, :nb, :, 0])
-    rows = [O.stored_rows_jpeg(st._coeffs[:, :, :nb].cpu().numpy(), sc(st).cpu().numpy())
-            for st in (ks, vs)]
+    if ks._scales is None:  # fp coefficients: the rows themselves
+        rows = [st._coeffs[:, :, :nb].float().cpu().numpy().astype(np.float64) for st in (ks, vs)]
+    else:
+        rows = [O.stored_rows_jpeg(st._coeffs[:, :, :nb].cpu().numpy(), sc(st).cpu().numpy())
+                for st in (ks, vs)]
     raws = [st.raw.float().cpu().numpy() for st in (ks, vs)]
     A = O.synthesis_matrix("jpeg", r, fc.dct_basis(r, k).numpy())
     ref = O.attention(q[:, :, 0].float().cpu().numpy(), rows[0], rows[1], raws[0], raws[1], A,
