@@ -25,6 +25,11 @@
 //      (no conversion).  fp16: the weights as f16 (2^-11 relative, as the
 //      int8 pass); bf16: the weights split w = hi + lo into two bf16
 //      operands (16 bits), two products.
+// STEP: the one-launch decode step, as the int8 pass's: split 0's
+// workgroups append the step's tokens to the tails (or archive the block
+// they complete: the coefficients rounded to the stream dtype, the fp
+// archive kernel's arithmetic, stored in place) and attend the step's rows
+// at full precision before their passes.
 #include "fc_attn_mfma_kernel.h"
 
 namespace fc {
@@ -33,7 +38,7 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
-template <int SROWS, int D, int GP, bool BF>
+template <int SROWS, int D, int GP, bool BF, bool STEP>
 __global__ __launch_bounds__(kMThreads, 2) void attn_split_fpj_mfma(MfmaArgs p) {
   static_assert(D == 64 || D == 128, "head size");
   using T = std::conditional_t<BF, bf16_t, f16_t>;
@@ -52,11 +57,15 @@ __global__ __launch_bounds__(kMThreads, 2) void attn_split_fpj_mfma(MfmaArgs p) 
   auto& w_lds_f = w_buf.f;
   __shared__ float a_lds[FC_MAX_BLOCK * SROWS];
   __shared__ float comb[kWaves][16][3];
-  __shared__ float cbuf[kWaves][GP][D];
+  // the wavefronts' accumulators, for the combine (and the step's SROWS x D
+  // coefficient scratch before the passes)
+  constexpr int CB = GP * kWaves >= SROWS ? GP : (SROWS + kWaves - 1) / kWaves;
+  __shared__ float cbuf[kWaves][CB][D];
   __shared__ __attribute__((aligned(16))) float part_lds[16 * D];
   __shared__ float tail_ml[2][16];
   __shared__ float wg_ml[2][16];
   __shared__ int s_last;
+  __shared__ int s_final;
 
   // 1-D grid, split-major, as the int8 pass
   const int64_t L = blockIdx.x;
@@ -74,7 +83,18 @@ __global__ __launch_bounds__(kMThreads, 2) void attn_split_fpj_mfma(MfmaArgs p) 
   for (int i = tid; i < r * SROWS; i += kMThreads) a_lds[i] = p.A[i];
 
   int64_t nb = p.nb, n_raw = p.n_raw;
-  if (p.state) {
+  int64_t step_t = 0, step_nb = 0;  // fused step: tail length and blocks before the token
+  bool step_write = false;
+  if constexpr (STEP) {
+    const int64_t cap = min(p.kcap, p.vcap);
+    step_t = p.state ? min<int64_t>(max<int64_t>(p.state[1], 0), p.r - 1) : p.step_t;
+    step_nb = p.state ? max<int64_t>(p.state[0], 0) : p.step_nb;
+    // one head group per (batch, kv head) stores the token / block; a block
+    // past the capacity is not stored (the state's overflow word says so)
+    step_write = split == 0 && g0 == 0 && (step_t + 1 < p.r || step_nb < cap);
+    nb = min(step_nb, cap);
+    n_raw = 0;
+  } else if (p.state) {
     // counts of a decode step's view on the device (graph replays)
     const int64_t t = min<int64_t>(max<int64_t>(p.state[1], 0), p.r - 1) + 1;
     nb = min<int64_t>(max<int64_t>(p.state[0], 0) + (t == p.r ? 1 : 0), min(p.kcap, p.vcap));
@@ -190,14 +210,34 @@ __global__ __launch_bounds__(kMThreads, 2) void attn_split_fpj_mfma(MfmaArgs p) 
 
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
   int64_t cur = wslot;
-  if (cur < npass) load_k(cur * PR, rows_of(cur));
+  if (!STEP && cur < npass) load_k(cur * PR, rows_of(cur));
 
-  // raw tail (fused calls): split 0 computes its partial before the passes
-  const bool fold_tail = p.fused && split == 0 && n_raw > 0;
-  if (fold_tail)
+  // raw tail (fused calls): split 0 computes its partial before the passes;
+  // in a fused step that partial covers the rows the step adds
+  const bool fold_tail = p.fused && split == 0 && (STEP || n_raw > 0);
+  if constexpr (STEP) {
+    if (split == 0) {
+      __shared__ float step_sc[1];  // no quantizer: unused
+      float* xk = &s_lds[0][0][0];  // the pass loop has not started: its scratch is free
+      float* etl = reinterpret_cast<float*>(&w_buf);
+      const int64_t kblk = (bh * p.kcap + step_nb) * SROWS, vblk = (bh * p.vcap + step_nb) * SROWS;
+      T* kw = static_cast<T*>(const_cast<void*>(p.kfp)) + kblk * D;
+      T* vw = static_cast<T*>(const_cast<void*>(p.vfp)) + vblk * D;
+      step_partial<D, SROWS, T, 0>(
+          step_t, p.r, static_cast<T*>(const_cast<void*>(p.kraw)) + bh * p.r * D,
+          static_cast<T*>(const_cast<void*>(p.vraw)) + bh * p.r * D,
+          static_cast<const T*>(p.ktok) + b * p.kt_sb + hkv * p.kt_sh,
+          static_cast<const T*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write, kw, nullptr, vw,
+          nullptr, p.basis, p.A, p.q, p.q_dtype, b * p.q_sb, p.q_sh, hkv * p.G + g0, G,
+          p.scale_log2, tid, xk, xk + p.r * D, cbuf[0][0], step_sc, etl, part_lds, tail_ml[0],
+          tail_ml[1]);
+    }
+  } else if (fold_tail) {
     raw_tail_partial<D>(p, b, hkv, g0, G, (int)n_raw, tid, &s_lds[0][0][0], part_lds, tail_ml[0],
                         tail_ml[1]);
-  __syncthreads();  // a_lds; the tail's scratch is free again
+  }
+  __syncthreads();  // a_lds; the prologue's scratch is free again
+  if (STEP && cur < npass) load_k(cur * PR, rows_of(cur));
 
   while (cur < npass) {
     const int64_t pr0 = cur * PR;
@@ -325,10 +365,27 @@ __global__ __launch_bounds__(kMThreads, 2) void attn_split_fpj_mfma(MfmaArgs p) 
 #pragma unroll
       for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][8 * lc + e] = acc[e][i];
   }
-  auto no_step = [] {};
-  split_epilogue<D, GP, false, true, decltype(no_step)&>(
-      p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf, part_lds, tail_ml, wg_ml,
-      &s_lds[0][0][0], s_last, passq, no_step);
+  // fused step with a device state: the launch's last workgroup to finish
+  // (all others have read the state by then) advances it
+  auto step_done = [&]() {
+    if constexpr (!STEP) return;
+    if (!p.state) return;
+    if (tid == 0) s_final = atomicAdd(p.done, 1u) + 1 == gridDim.x ? 1 : 0;
+    __syncthreads();
+    if (s_final && tid < 64) {  // lane-indexed vector stores
+      const int64_t cap = min(p.kcap, p.vcap);
+      const bool full = step_t + 1 == p.r;
+      const bool over = full && step_nb >= cap;
+      const int64_t word = tid == 0   ? (full ? step_nb + 1 : step_nb)
+                           : tid == 1 ? (full ? 0 : step_t + 1)
+                                      : ((p.state[2] != 0 || over) ? 1 : 0);
+      if (tid < 3) const_cast<int64_t*>(p.state)[tid] = word;
+      if (tid == 0) __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+  split_epilogue<D, CB, false, !STEP>(p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf,
+                                      part_lds, tail_ml, wg_ml, &s_lds[0][0][0], s_last, passq,
+                                      step_done);
 }
 
 }  // namespace
@@ -374,7 +431,7 @@ int launch_split_fpj_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh
   a.pm = pm;
   a.pl = pl;
   a.pacc = pacc;
-  a.state = state;
+  a.state = state ? state : (fuse ? fuse->state : nullptr);
   a.raw_dtype = q_dtype;
   if (fuse) {
     if (n_splits > kFuseMaxSplits) return FC_ERR_ARG;
@@ -392,6 +449,19 @@ int launch_split_fpj_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh
     a.out = fuse->out;
     a.o_sb = fuse->o_sb;
     a.o_sh = fuse->o_sh;
+    if (fuse->step) {
+      a.step = 1;
+      a.ktok = fuse->ktok;
+      a.vtok = fuse->vtok;
+      a.kt_sb = fuse->kt_sb;
+      a.kt_sh = fuse->kt_sh;
+      a.vt_sb = fuse->vt_sb;
+      a.vt_sh = fuse->vt_sh;
+      a.basis = fuse->basis;
+      a.step_t = fuse->step_t;
+      a.step_nb = fuse->step_nb;
+      a.done = fuse->done;
+    }
   }
   const int64_t G = Hq / Hkv;
   const int gg = (int)std::min<int64_t>(G, 16);
@@ -405,16 +475,21 @@ int launch_split_fpj_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh
   a.cstride = stride;
   const dim3 grid((unsigned)(a.ngroups * n_splits));
   const bool bf = q_dtype == FC_BF16;
+  const bool step = a.step != 0;
   const int rc = mfma_with_int<1, 2, 3, 4, 8>(s, [&](auto sc) {
     constexpr int Sv = decltype(sc)::value;
     return mfma_with_int<64, 128>((int)D, [&](auto dc) {
       constexpr int Dv = decltype(dc)::value;
       return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
         constexpr int GPv = decltype(gc)::value;
-        if (bf)
-          attn_split_fpj_mfma<Sv, Dv, GPv, true><<<grid, kMThreads, 0, st>>>(a);
+        if (bf && step)
+          attn_split_fpj_mfma<Sv, Dv, GPv, true, true><<<grid, kMThreads, 0, st>>>(a);
+        else if (bf)
+          attn_split_fpj_mfma<Sv, Dv, GPv, true, false><<<grid, kMThreads, 0, st>>>(a);
+        else if (step)
+          attn_split_fpj_mfma<Sv, Dv, GPv, false, true><<<grid, kMThreads, 0, st>>>(a);
         else
-          attn_split_fpj_mfma<Sv, Dv, GPv, false><<<grid, kMThreads, 0, st>>>(a);
+          attn_split_fpj_mfma<Sv, Dv, GPv, false, false><<<grid, kMThreads, 0, st>>>(a);
         return FC_OK;
       });
     });

@@ -259,22 +259,26 @@ __device__ __forceinline__ void raw_tail_partial(const MfmaArgs& p, int64_t b, i
 // replaced by the block's tokens synthesised from the dequantised codes
 // through A (r x SROWS), so the block is attended exactly as an archived
 // one.  NG scales per row: 1 (the row's absmax) or D / 32 (per 32 features,
-// scales[row * NG + group]).  kk: SROWS x D, sc: SROWS * NG floats of LDS
-// scratch.
+// scales[row * NG + group]); NG = 0: no quantizer, the coefficients rounded
+// to TT are the stored rows (`codes` then points at TT, `scales` is unused).
+// kk: SROWS x D, sc: SROWS * NG floats of LDS scratch.
 template <int D, int SROWS, typename TT, int NG = 1>
 __device__ __forceinline__ void step_archive(float* x, int r, const float* basis, const float* A,
-                                             bool write, int8_t* codes, float* scales, float* kk,
+                                             bool write, void* codes, float* scales, float* kk,
                                              float* sc, int tid) {
-  static_assert(NG == 1 || NG * 32 == D, "one scale per row or per 32 features");
+  static_assert(NG <= 1 || NG * 32 == D, "one scale per row or per 32 features");
   const int lane = tid & 63, wave = tid >> 6;
   for (int e = tid; e < SROWS * D; e += kMThreads) {
     const int j = e / D, d = e - j * D;
     float a = 0.f;
     for (int i = 0; i < r; ++i) a = __builtin_fmaf(x[i * D + d], basis[j * r + i], a);
     kk[e] = to_f32(from_f32<TT>(a));
+    if constexpr (NG == 0) {
+      if (write) static_cast<TT*>(codes)[e] = from_f32<TT>(a);
+    }
   }
   __syncthreads();
-  for (int j = wave; j < SROWS; j += kMThreads / 64) {  // one row per wavefront
+  for (int j = wave; j < SROWS && NG > 0; j += kMThreads / 64) {  // one row per wavefront
     if constexpr (NG == 1) {
       float m = 0.f;
       for (int d = lane; d < D; d += 64) m = fmaxf(m, fabsf(kk[j * D + d]));
@@ -302,12 +306,14 @@ __device__ __forceinline__ void step_archive(float* x, int r, const float* basis
       }
     }
   }
-  __syncthreads();
-  for (int e = tid; e < SROWS * D; e += kMThreads) {
-    const float sj = NG == 1 ? sc[e / D] : sc[(e / D) * NG + (e % D) / 32];
-    const float q = quant_code(kk[e], sj, 1.0f / sj);
-    if (write) codes[e] = (int8_t)(int)q;
-    kk[e] = q * sj;
+  if constexpr (NG > 0) {
+    __syncthreads();
+    for (int e = tid; e < SROWS * D; e += kMThreads) {
+      const float sj = NG == 1 ? sc[e / D] : sc[(e / D) * NG + (e % D) / 32];
+      const float q = quant_code(kk[e], sj, 1.0f / sj);
+      if (write) static_cast<int8_t*>(codes)[e] = (int8_t)(int)q;
+      kk[e] = q * sj;
+    }
   }
   __syncthreads();
   for (int e = tid; e < r * D; e += kMThreads) {
@@ -333,7 +339,7 @@ __device__ __forceinline__ void step_archive(float* x, int r, const float* basis
 template <int D, int SROWS, typename TT, int NG = 1>
 __device__ __forceinline__ void step_partial(
     int64_t t, int r, TT* ktail, TT* vtail, const TT* ktok, const TT* vtok, bool write,
-    int8_t* kcodes, float* kscales, int8_t* vcodes, float* vscales, const float* basis,
+    void* kcodes, float* kscales, void* vcodes, float* vscales, const float* basis,
     const float* A, const void* q, int q_dtype, int64_t qb, int64_t q_sh, int64_t h0, int G,
     float scale_log2, int tid, float* xk, float* xv, float* kk, float* sc, float* etl, float* acc,
     float* tm, float* tl) {

@@ -68,7 +68,8 @@ __global__ void state_advance_kernel(int64_t* state, int64_t r, int64_t cap) {
 // (then the step takes the multi-launch path).
 static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   const bool grouped = a->store_kind == FC_STORE_JPEG_I8G;
-  if ((a->store_kind != FC_STORE_JPEG_I8 && !grouped) || a->quant_bits != 8 ||
+  const bool fp = a->store_kind == FC_STORE_JPEG_FP;  // fp16 / bf16 coefficient rows
+  if ((a->store_kind != FC_STORE_JPEG_I8 && !grouped && !fp) || (!fp && a->quant_bits != 8) ||
       !mfma_split_allowed() || a->q_dtype == FC_F32)
     return FC_ERR_UNSUPPORTED;
   const int64_t B = a->B, Hq = a->Hq, Hkv = a->Hkv, D = a->D;
@@ -88,7 +89,10 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
     v[i].raw_sh = (int64_t)r * D;
     v[i].raw_st = D;
   }
-  if (!i8_mfma_takes(a->store_kind, a->q, a->q_dtype, a->q_sb, a->q_sh, D, a->s, &v[0], &v[1]))
+  if (fp ? !split_fpj_mfma_supported(a->q, a->q_dtype, a->q_sb, a->q_sh, D, a->s,
+                                     a->stream_dtype, &v[0], &v[1])
+         : !i8_mfma_takes(a->store_kind, a->q, a->q_dtype, a->q_sb, a->q_sh, D, a->s, &v[0],
+                          &v[1]))
     return FC_ERR_UNSUPPORTED;
   const int64_t mstride = counter_stride(2 * B * Hkv * ((G + 15) / 16));
   if (mstride == 0) return FC_ERR_UNSUPPORTED;
@@ -117,6 +121,11 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   fz.step_t = a->n_tail;
   fz.step_nb = a->n_blocks;
   fz.done = ws.done;
+  if (fp)
+    return launch_split_fpj_mfma(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, r, a->s, nb,
+                                 &v[0], &v[1], a->A, a->scale * 1.4426950408889634f, ws.pm,
+                                 ws.pl, ws.pacc, n_splits, ws.counters, kCounterWords, mstride,
+                                 &fz, state, (hipStream_t)a->stream);
   return launch_split_i8_mfma(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, r, a->s, nb,
                               &v[0], &v[1], a->A, a->scale * 1.4426950408889634f, ws.pm, ws.pl,
                               ws.pacc, n_splits, ws.counters, kCounterWords, mstride,

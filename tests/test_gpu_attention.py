@@ -395,7 +395,11 @@ STEP_PAIRS = [
     (I8, "f16", 64, 4, True),
     (dict(I8, keep_freqs=2), "bf16", 64, 4, True),
     (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 64, 4, False),
-    (dict(mode="jpeg", block_size=8, keep_freqs=4), "bf16", 128, 2, False),
+    # fp16 / bf16 coefficient rows: the one-launch step archives them in-kernel
+    (dict(mode="jpeg", block_size=8, keep_freqs=4), "bf16", 128, 2, True),
+    (dict(mode="jpeg", block_size=8, keep_freqs=2), "f16", 64, 4, True),
+    (dict(mode="jpeg", block_size=16, keep_freqs=8), "bf16", 128, 8, True),
+    (dict(mode="jpeg", block_size=4, keep_freqs=3), "f16", 128, 1, True),
     (dict(mode="png", block_size=8, keep_ratio=0.5), "f32", 64, 4, False),
     (dict(mode="png", block_size=4, keep_ratio=1.0), "bf16", 64, 4, False),
     # the C5 instantiation (D=128, bf16, k=4, G=2), other row counts and widths

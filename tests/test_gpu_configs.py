@@ -229,15 +229,18 @@ def _archives_equal(a, b):
 C5 = dict(B=16, Hkv=8, G=2, D=128, dt="bf16")
 
 
-C5_SCALES = [(I8_C3, N.STORE_JPEG_I8), (dict(I8_C3, quant_group=32), N.STORE_JPEG_I8G)]
+C5_SCALES = [(I8_C3, N.STORE_JPEG_I8), (dict(I8_C3, quant_group=32), N.STORE_JPEG_I8G),
+             (dict(mode="jpeg", block_size=8, keep_freqs=4), N.STORE_JPEG_FP)]
+C5_SCALE_IDS = ["per-row", "per-32", "fp-coefficients"]
 
 
-@pytest.mark.parametrize("cfg,kind", C5_SCALES, ids=["per-row", "per-32"])
+@pytest.mark.parametrize("cfg,kind", C5_SCALES, ids=C5_SCALE_IDS)
 def test_fused_step_c5_scale_multi_split(cfg, kind, oracle):
     """The C5 model's per-layer decode step as it runs there: the one-launch
     step kernel (attn_split_i8_mfma<4, 128, 2, STEP>) at C5's geometry (batch
-    16, 16 q / 8 kv heads, D=128, bf16, k=4 int8; one scale per row or per 32
-    features) over 512 archived blocks + a 5-token tail, so the split count
+    16, 16 q / 8 kv heads, D=128, bf16, k=4: int8 with one scale per row or
+    per 32 features, or the bf16 coefficients themselves) over 512 archived
+    blocks + a 5-token tail, so the split count
     is the model's (4 > 1: the cross-split arrival and merge, the queued
     passes after the first and split 0's in-kernel append / archive beside
     streaming splits all run).  12 steps cross two block boundaries; after
@@ -308,11 +311,11 @@ def test_graph_replayed_steps_match_oracle(cfg, dt, G, oracle):
     _graph_steps(cfg, dt, 2, 2, G, 128, 4 * r + 5, 3 * r + 2, 222, oracle)
 
 
-@pytest.mark.parametrize("cfg,kind", C5_SCALES, ids=["per-row", "per-32"])
+@pytest.mark.parametrize("cfg,kind", C5_SCALES, ids=C5_SCALE_IDS)
 def test_graph_replayed_steps_c5_scale(cfg, kind, oracle):
     """Graph-replayed one-launch steps at C5's geometry (batch 16, 16 q / 8
-    kv heads, D=128, bf16, k=4 int8 with one scale per row or per 32
-    features, 512 archived blocks + 5 tail tokens: 4 splits, the model's):
+    kv heads, D=128, bf16, k=4: int8 with one scale per row or per 32
+    features, or bf16 coefficients; 512 archived blocks + 5 tail tokens: 4 splits, the model's):
     12 replays across two block boundaries, every sequence of every replay
     against the fp64 oracle, and the archives the replays wrote against the
     two-append path's, bit for bit."""
