@@ -747,10 +747,17 @@ C5_LAYERS, C5_B, C5_HQ, C5_HKV, C5_D = 28, 16, 16, 8, 128
 
 
 def _c5_codec_cfg(args):
-    cfg = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
+    cfg = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=args.c5_quant_bits)
     if args.c5_group:
         cfg["quant_group"] = args.c5_group
     return cfg
+
+
+def _c5_codec_name(args):
+    if not args.c5_quant_bits:
+        return "jpeg r=8 k=4, bf16 coefficients"
+    return "jpeg r=8 k=4 int8" + (f", one scale per {args.c5_group} features"
+                                  if args.c5_group else "")
 
 
 def c5step_mode(args):
@@ -824,9 +831,10 @@ def c5step_mode(args):
     us = e0.elapsed_time(e1) / (steps * L) * 1e3
     ngr = D // 32 if args.c5_group else 1
     nb = (nb0 + nb1) / 2
-    # codes + scales of the archived blocks, the tail rows (3.5 on average)
-    # and the new tokens in bf16, q and out
-    alg = int(2 * B * Hkv * nb * 4 * (D + 4 * ngr) + 2 * B * Hkv * 3.5 * D * 2
+    # codes + scales (or bf16 coefficients) of the archived blocks, the tail
+    # rows (3.5 on average) and the new tokens in bf16, q and out
+    row_bytes = D + 4 * ngr if args.c5_quant_bits else 2 * D
+    alg = int(2 * B * Hkv * nb * 4 * row_bytes + 2 * B * Hkv * 3.5 * D * 2
               + 2 * B * Hkv * D * 2 + 2 * B * Hq * D * 2)
     res = {"metric": "C5 decode-attention step kernel, us per layer-step", "unit": "us",
            "us_per_layer_step": round(us, 3), "launches_per_layer_step": 1 if single == 1 else None,
@@ -835,9 +843,8 @@ def c5step_mode(args):
            "algorithmic_bytes_per_layer_step": alg, "GBs": round(alg / us / 1e3, 1),
            "hbm_frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4),
            "config": {"workload": "C5 step kernel", "B": B, "Hq": Hq, "Hkv": Hkv, "D": D,
-                      "codec": "jpeg r=8 k=4 int8" + (f", one scale per {args.c5_group} features"
-                                                      if args.c5_group else ""),
-                      "prompt": args.c5_prompt + 5, "dtype": "bf16"},
+                      "codec": _c5_codec_name(args), "prompt": args.c5_prompt + 5,
+                      "dtype": "bf16"},
            "data": "synthetic AR(1) rho=0.95 K/V, random tokens and queries"}
     log(f"bench c5step: {res}")
     print(json.dumps(res))
@@ -856,6 +863,9 @@ def prefill_mode(args):
     from flashcodec_amd.cache import _CodecStream
     dev = torch.device("cuda:0")
     B, Hq, Hkv, D, S = C5_B, C5_HQ, C5_HKV, C5_D, args.c5_prompt
+    if not args.c5_quant_bits:
+        print("prefill on the archive takes int8 archives (--c5-quant-bits 8)", file=sys.stderr)
+        sys.exit(2)
     cfg = _c5_codec_cfg(args)
     ks, vs = _CodecStream(fc.make_codec(**cfg)), _CodecStream(fc.make_codec(**cfg))
     ks.append(ar1_device((B, Hkv, S, D), 0.95, 1, dev).to(torch.bfloat16))
@@ -1153,6 +1163,8 @@ def main():
     ap.add_argument("--c5-kv", choices=["raw", "codec", "codec-view-prefill"], default="codec")
     ap.add_argument("--c5-group", type=int, choices=[0, 32], default=0,
                     help="C5 codec quantizer group (32: one scale per 32 features)")
+    ap.add_argument("--c5-quant-bits", type=int, choices=[0, 8], default=8,
+                    help="c5step: 0 stores the bf16 coefficients (the reference's default codec)")
     ap.add_argument("--c5-graph", action="store_true",
                     help="c5: codec decode steps replayed from a captured HIP graph")
     args = ap.parse_args()
