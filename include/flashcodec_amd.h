@@ -271,11 +271,13 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G,
  * Split count for a fc_decode_attention call over stores of `store_kind`
  * (stream dtype, query dtype, s stored rows per block, head size D): one
  * round of workgroups of the split pass that will run — the matrix-core
- * pass for int8 jpeg archives with fp16/bf16/fp32 queries and per-32 int8
- * archives with fp16/bf16 queries at D = 64/128/256 (two workgroups per
- * compute unit, but at least one 64-row pass per wavefront and at most
- * max(16, passes / 10) splits), otherwise the vector-ALU pass at the
- * occupancy it reaches on the current device.  0 when nb == 0.
+ * passes for int8 jpeg archives (one scale per row or per 32 features) with
+ * fp16/bf16/fp32 queries, for fp16/bf16 coefficient archives queried in
+ * their dtype at D = 64/128, and for fp32 png at r = 4/8/16 (two workgroups
+ * per compute unit, but at least one pass per wavefront and at most
+ * max(16, passes / 10) splits), the packed png pass, otherwise the
+ * vector-ALU pass at the occupancy it reaches on the current device.  0
+ * when nb == 0.
  * Replaces the split heuristic ns = max(1, min(32, ceil(n / 64))) of
  * flashcodec/triton_attention.py:191.
  */
@@ -393,7 +395,7 @@ int fc_decode_attention_noalloc(const void* q, int q_dtype, int64_t q_sb,
 
 /* Split pass selection for fc_decode_attention / fc_decode_step. */
 enum {
-  FC_PASS_AUTO = 0,   /* matrix-core pass for the int8 jpeg archives it supports,
+  FC_PASS_AUTO = 0,   /* matrix-core passes for the archives they support,
                          its passes handed out by a queue (outputs may differ in
                          the last bits between calls: fp32 summation order) */
   FC_PASS_VECTOR = 1, /* vector-ALU pass for every store (A/B measurements) */
@@ -516,7 +518,8 @@ int fc_decode_step(const fc_step_args* args);
 /*
  * How the calling thread's last successful fc_decode_step call ran: 1 when
  * the whole step was one kernel launch (int8 jpeg archives with one scale
- * per row, fp16 / bf16 queries and stream, the matrix-core pass), 0 when it
+ * per row or per 32 features, or jpeg archives of fp16 / bf16
+ * coefficients; fp16 / bf16 queries and stream; a matrix-core pass), 0 when it
  * took the multi-launch form (token append, archive, attention, state
  * advance), -1 before any such call.  No counterpart in the reference (its
  * step is always two appends and an attention call); for callers and tests
