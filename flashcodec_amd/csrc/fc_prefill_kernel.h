@@ -25,8 +25,8 @@
 //   scores: v_mfma_i32_16x16x64_i8 on the K codes with each query split as
 //      256 hi + lo int8 operands after scaling it by a power of two to at
 //      most 14-bit integers (exact integer scores);
-//   softmax: (block, query) pairs over the 64 lanes (query = lane % 16),
-//      r logits from the s scores through A, causal mask per token,
+//   softmax (RC == 0): (block, query) pairs over the 64 lanes (query =
+//      lane % 16), r logits from the s scores through A, causal mask per token,
 //      exponentials against a running reference maximum that moves only
 //      when a logit exceeds it by 2^8, output weights sum_t e_t A[t][j]
 //      times the V row scale stored as f16;
@@ -77,15 +77,9 @@ constexpr int kPWaves = kPThreads / 64;
 // relative to the row's largest as the value operand.
 //
 // RC != 0 (SROWS == 4, block size r == RC): the softmax runs on
-// v_mfma_f32_4x4x1_16b_f32, whose 16 independent 4x4 products are the 16
-// blocks of a pass.  Lane (mb, mj) = (lane / 4, lane % 4) holds block mb and
-// query 4 g + mj of query group g (0..3): the logits of the block's r taps
-// (r / 4 products of 4 k-steps: A operand A[4 th + i][k] x K row scale, B
-// operand the score of row 4 mb + k), the exponentials in place, and the
-// weights of the 4 stored rows (r k-steps: A operand A[t][i], B operand the
-// exponential of tap t in the same lane), so logits, exponentials and
-// weights never leave their lanes and the vector ALU keeps only the
-// exponentials, the maximum and the f16 stores.
+// v_mfma_f32_4x4x1_16b_f32 and the pass stays in registers (the loop of
+// that variant describes the lane layout); RC == 0: the softmax above on
+// the vector ALU, scores and weights through LDS.
 template <int SROWS, int DK, typename QT, typename RT, bool QG = false, int RC = 0>
 __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(PrefillArgs p) {
   static_assert(RC == 0 || (SROWS == 4 && RC % 4 == 0 && RC <= 16), "4x4 softmax: 4 rows");
@@ -212,7 +206,9 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
   const int k_off = lc * D + 16 * lq;
   int v_off[DV];
 #pragma unroll
-  for (int dv = 0; dv < DV; ++dv) v_off[dv] = 8 * lq * D + min(128 * dv + 8 * lc, D - 8);
+  // V rows of the lane's k-slice lq of a 32-row slice: 8 lq .. 8 lq + 7, or
+  // (RC != 0, the weights' register order) 4 lq .. + 3 and 16 + 4 lq .. + 3
+  for (int dv = 0; dv < DV; ++dv) v_off[dv] = (RC ? 4 : 8) * lq * D + min(128 * dv + 8 * lc, D - 8);
   const int sc_off = (lane % PR) * 4;
 
   uint32_t kr[NT][KDW];
@@ -266,8 +262,8 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const u32x2_t v = __builtin_bit_cast(
-              u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rv, v_off[dv] + (32 * sl + i) * D, 0,
-                                                            0));
+              u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                           rv, v_off[dv] + (32 * sl + (RC && i >= 4 ? 12 + i : i)) * D, 0, 0));
           vr[sl][dv][2 * i] = v[0];
           vr[sl][dv][2 * i + 1] = v[1];
         }
@@ -358,133 +354,38 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
     pmax = pm + mo;
   };
 
-  // ---- RC != 0: the matrix-core softmax (lane (mb, mj): block mb of the
-  // pass, query 4 g + mj of group g)
-  constexpr int NTH = RC ? RC / 4 : 1;
-  const int mb = lane >> 2, mj = lane & 3;
-  float m4[4];            // query 4 g + mj: reference maximum (-inf before the first pass)
-  float nmo4[4];          // minus the finite stand-in of m4 (0 while m4 is -inf)
-  float l4[4];            // block mb's share of the exponential sums
-  float a_log[NTH][4];    // A[4 th + mj][k]: A operand of the logits
-  float a_w[RC ? RC : 1]; // A[t][mj]: A operand of the weights
-  bool dc = false;        // column 0 of A is one constant (wave-uniform)
-  // the pass's 4 query groups; MASK: the causal mask and the pass's row
-  // count applied per tap (diagonal and partial passes)
-  auto ms_groups = [&](bool MASK, int64_t blk0, int prow, bool first, float4_t vs4,
-                       float4_t ks4) {
-    const int nblk = prow / 4;
+  // Value product of slice sl, column block dv: the lane's V codes (8 rows
+  // x 8 features, as loaded) to f16 operands by 8x8 byte transposes with
+  // v_perm: 1024 + (code + 128) (the weight sums take the 1152 off at the
+  // end), QG: the code times its group ratio
+  auto values_dv = [&](int sl, int dv, half8_t wop, half8_t rat) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      // scores of the block's 4 rows times their K scales (PR == 32:
-      // blocks 8.. read score columns no pass writes, zeroed)
-      float4_t s4 = *reinterpret_cast<const float4_t*>(&s_lds[wave][4 * g + mj][4 * mb]);
-      if constexpr (!QG) s4 *= ks4;
-      if constexpr (PR == 32) s4 = mb < PR / 4 ? s4 : (float4_t){0.f, 0.f, 0.f, 0.f};
-      float4_t L[NTH];
-      const float4_t c0 = {nmo4[g], nmo4[g], nmo4[g], nmo4[g]};
+    for (int hh = 0; hh < 2; ++hh) {
+      uint32_t t0[4], t1[4];
 #pragma unroll
-      for (int th = 0; th < NTH; ++th) {
-        L[th] = c0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          L[th] = __builtin_amdgcn_mfma_f32_4x4x1f32(a_log[th][k], s4[k], L[th], 0, 0, 0);
+      for (int pp = 0; pp < 4; ++pp) {
+        const uint32_t ra = vr[sl][dv][2 * (2 * pp) + hh] ^ 0x80808080u;
+        const uint32_t rb = vr[sl][dv][2 * (2 * pp + 1) + hh] ^ 0x80808080u;
+        t0[pp] = __builtin_amdgcn_perm(rb, ra, 0x05010400u);
+        t1[pp] = __builtin_amdgcn_perm(rb, ra, 0x07030602u);
       }
-      if (MASK) {
-        // taps after the query's position (and all taps of blocks past the
-        // pass's rows) get -2^100: four more k-steps, A = -2^100 on the
-        // diagonal (k == i), B = [tap 4 th + k masked] for the lane's query
-        const int rel = (int)(p.P0 + tok_of(4 * g + mj) - (blk0 + mb) * RC);
-        const float limf = (float)(mb < nblk ? rel : -1);
 #pragma unroll
-        for (int th = 0; th < NTH; ++th)
+      for (int ee = 0; ee < 4; ++ee) {
+        half8_t ov;
 #pragma unroll
-          for (int k = 0; k < 4; ++k)
-            L[th] = __builtin_amdgcn_mfma_f32_4x4x1f32(
-                mj == k ? -0x1p100f : 0.f,
-                __builtin_amdgcn_fmed3f((float)(4 * th + k) - limf, 0.f, 1.f), L[th], 0, 0, 0);
-      }
-      float pm = -INFINITY;
-#pragma unroll
-      for (int th = 0; th < NTH; ++th)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pm = fmaxf(pm, L[th][i]);
-      if (first || __builtin_amdgcn_ballot_w64(pm > kLazyMax) != 0) {
-        // the group's queries' maximum over the pass (the 16 lanes of one mj)
-#pragma unroll
-        for (int m = 4; m < 64; m <<= 1) pm = fmaxf(pm, __shfl_xor(pm, m, 64));
-        const float m_new = fmaxf(m4[g], pm - nmo4[g]);
-        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m4[g] - m_new);
-        const float nmo_new = m_new == -INFINITY ? 0.f : -m_new;
-        const float dm = nmo_new - nmo4[g];
-#pragma unroll
-        for (int th = 0; th < NTH; ++th) L[th] += dm;
-        l4[g] *= alpha;
-        // accumulator lane (q, c) register i holds query 4q + i: the group's
-        // alphas (lanes 0..3) to the lanes of q == g
-        float fac[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float ai = __shfl(alpha, i, 64);
-          fac[i] = lq == g ? ai : 1.f;
+        for (int pp = 0; pp < 4; ++pp) {
+          const uint32_t src = ee < 2 ? t0[pp] : t1[pp];
+          const uint32_t sel = (ee & 1) ? 0x04030402u : 0x04010400u;
+          half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, src, sel));
+          if constexpr (QG) h2 += (half2_t){(_Float16)-kVBias, (_Float16)-kVBias};
+          ov[2 * pp] = h2[0];
+          ov[2 * pp + 1] = h2[1];
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-          for (int dv = 0; dv < DV; ++dv)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[dv][e][i] *= fac[i];
-          accs[i] *= fac[i];
-        }
-        m4[g] = m_new;
-        nmo4[g] = nmo_new;
+        const int e = 4 * hh + ee;
+        if constexpr (QG) ov *= rat;
+        acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, ov, acc[dv][e], 0, 0, 0);
       }
-#pragma unroll
-      for (int th = 0; th < NTH; ++th)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) L[th][i] = __builtin_amdgcn_exp2f(L[th][i]);
-      float4_t W = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int t = 0; t < RC; ++t)
-        W = __builtin_amdgcn_mfma_f32_4x4x1f32(a_w[t], L[t / 4][t % 4], W, 0, 0, 0);
-      if (dc) {
-        l4[g] = __builtin_fmaf(W[0], dc_inv, l4[g]);
-      } else {
-#pragma unroll
-        for (int th = 0; th < NTH; ++th)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) l4[g] += L[th][i];
-      }
-      const float4_t wv = W * vs4;
-      const half2_t h01 = {(_Float16)wv[0], (_Float16)wv[1]};
-      const half2_t h23 = {(_Float16)wv[2], (_Float16)wv[3]};
-      *reinterpret_cast<u32x2_t*>(&w_lds[wave][4 * g + mj][4 * mb]) =
-          (u32x2_t){__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)};
     }
-  };
-  auto ms_pass = [&](int64_t blk0, int prow, bool first, bool open, bool sig_need, float vs_pass) {
-    // a V row scale at or above 2^(sig_run + 1): accumulators and weights to
-    // the new exponent first
-    if (__builtin_amdgcn_ballot_w64(sig_need) != 0) {
-      float smax = vs_pass;
-#pragma unroll
-      for (int m = 1; m < 64; m <<= 1) smax = fmaxf(smax, __shfl_xor(smax, m, 64));
-      const int sig_new = max(sig_run, pow2_exp_for(smax, 1));
-      const float sfix = ldexpf(1.0f, sig_run - sig_new);
-#pragma unroll
-      for (int dv = 0; dv < DV; ++dv)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[dv][e] *= sfix;
-      accs *= sfix;
-      sig_run = sig_new;
-      wmul_run = ldexpf(1.0f, -sig_new);
-    }
-    // V and K scales of the block's rows (PR == 32: blocks 8.. past the pass
-    // read block 7's and are masked)
-    const int mbr = min(mb, PR / 4 - 1);
-    const float4_t vs4 = *reinterpret_cast<const float4_t*>(&sc_lds[wave][1][4 * mbr]) * wmul_run;
-    float4_t ks4 = {1.f, 1.f, 1.f, 1.f};
-    if constexpr (!QG) ks4 = *reinterpret_cast<const float4_t*>(&sc_lds[wave][0][4 * mbr]);
-    ms_groups(!open, blk0, prow, first, vs4, ks4);
   };
 
   __syncthreads();  // a_lds (the only workgroup barrier)
@@ -495,109 +396,88 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
     for (int t = 1; t < r; ++t) same = same && a_lds[t * SROWS] == a0;
     dc_inv = same ? 1.0f / a0 : 0.f;
   }
-  if constexpr (RC != 0) {
-#pragma unroll
-    for (int th = 0; th < NTH; ++th)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) a_log[th][k] = a_lds[(4 * th + mj) * 4 + k];
-#pragma unroll
-    for (int t = 0; t < RC; ++t) a_w[t] = a_lds[4 * t + mj];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      m4[g] = -INFINITY;
-      nmo4[g] = 0.f;
-      l4[g] = 0.f;
-    }
-    dc = __builtin_amdgcn_readfirstlane(__float_as_uint(dc_inv)) != 0;
-  }
   auto rows_of = [&](int64_t pass) { return (int)min<int64_t>(PR, rows_total - pass * PR); };
-  if (npass > 0) load_k(0, rows_of(0));
-  // RC != 0: passes without the causal mask, a prefix of the wave's passes:
-  // 16 whole blocks (PR == 32: the lanes of blocks 8.. hold none, so never)
-  // whose last token is at or before the wave's first query
-  const int n_open = (int)(PR == 64 && RC != 0
-                               ? min<int64_t>(rows_total / PR, (qpos_min + 1) / (16 * max(RC, 1)))
-                               : 0);
-  for (int64_t cur = 0; cur < npass; ++cur) {
-    const int64_t pr0 = cur * PR;
-    const int prow = rows_of(cur);  // multiple of SROWS
-    load_v(pr0, prow);
+  if constexpr (RC == 0) {
+    if (npass > 0) load_k(0, rows_of(0));
+    for (int64_t cur = 0; cur < npass; ++cur) {
+      const int64_t pr0 = cur * PR;
+      const int prow = rows_of(cur);  // multiple of SROWS
+      load_v(pr0, prow);
 
-    // ------------------------------------------------------------ scores
-    if constexpr (QG) {
-      if (lane < PR) {
-#pragma unroll
-        for (int i = 0; i < NGR; ++i) kg_lds[wave][i][lane] = kgr[i];
-      }
-      wave_lds_sync();
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
+      // ------------------------------------------------------------ scores
       if constexpr (QG) {
-        // lanes q < 2 hold group 2c of chunk c, q >= 2 group 2c + 1
-        float4_t accg = {0.f, 0.f, 0.f, 0.f};
+        if (lane < PR) {
+#pragma unroll
+          for (int i = 0; i < NGR; ++i) kg_lds[wave][i][lane] = kgr[i];
+        }
+        wave_lds_sync();
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if constexpr (QG) {
+          // lanes q < 2 hold group 2c of chunk c, q >= 2 group 2c + 1
+          float4_t accg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
+                               (int)kr[t][4 * c + 3]};
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+              // the codes of the other group's lanes zeroed (the query stays
+              // whole: a masked copy of it would be hoisted out of the loop)
+              const bool mine = (lq >> 1) == hf;
+              const i32x4_t zero = {0, 0, 0, 0};
+              const i32x4_t am = mine ? a : zero;
+              const i32x4_t ghi = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qhi[c], zero, 0, 0, 0);
+              const i32x4_t glo = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qlo[c], zero, 0, 0, 0);
+              const float4_t kgv =
+                  *reinterpret_cast<const float4_t*>(&kg_lds[wave][2 * c + hf][16 * t + 4 * lq]);
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                accg[i] = __builtin_fmaf(kgv[i], (float)(ghi[i] * 256 + glo[i]), accg[i]);
+            }
+          }
+          *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = accg * head_mul;
+          continue;
+        }
+        i32x4_t shi = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
           const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
                              (int)kr[t][4 * c + 3]};
-#pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            // the codes of the other group's lanes zeroed (the query stays
-            // whole: a masked copy of it would be hoisted out of the loop)
-            const bool mine = (lq >> 1) == hf;
-            const i32x4_t zero = {0, 0, 0, 0};
-            const i32x4_t am = mine ? a : zero;
-            const i32x4_t ghi = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qhi[c], zero, 0, 0, 0);
-            const i32x4_t glo = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qlo[c], zero, 0, 0, 0);
-            const float4_t kgv =
-                *reinterpret_cast<const float4_t*>(&kg_lds[wave][2 * c + hf][16 * t + 4 * lq]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              accg[i] = __builtin_fmaf(kgv[i], (float)(ghi[i] * 256 + glo[i]), accg[i]);
-          }
+          shi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qhi[c], shi, 0, 0, 0);
+          slo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qlo[c], slo, 0, 0, 0);
         }
-        *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = accg * head_mul;
-        continue;
+        float4_t sv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = (float)(shi[i] * 256 + slo[i]) * head_mul;
+        *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = sv;
       }
-      i32x4_t shi = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
+      if constexpr (QG) {
+        // V group scales relative to the row's largest (that one joins the
+        // output weights as the row scale)
+        float vmax = 0.f;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
-                           (int)kr[t][4 * c + 3]};
-        shi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qhi[c], shi, 0, 0, 0);
-        slo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qlo[c], slo, 0, 0, 0);
+        for (int i = 0; i < NGR; ++i) vmax = fmaxf(vmax, vgr[i]);
+        const float rv = vmax > 0.f ? __builtin_amdgcn_rcpf(vmax) : 0.f;
+        if (lane < PR) {
+#pragma unroll
+          for (int i = 0; i < NGR; ++i) vg_lds[wave][i][lane] = (_Float16)(vgr[i] * rv);
+        }
+        ks_r = 1.f;
+        vs_r = vmax;
       }
-      float4_t sv;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sv[i] = (float)(shi[i] * 256 + slo[i]) * head_mul;
-      *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = sv;
-    }
-    if constexpr (QG) {
-      // V group scales relative to the row's largest (that one joins the
-      // output weights as the row scale)
-      float vmax = 0.f;
-#pragma unroll
-      for (int i = 0; i < NGR; ++i) vmax = fmaxf(vmax, vgr[i]);
-      const float rv = vmax > 0.f ? __builtin_amdgcn_rcpf(vmax) : 0.f;
       if (lane < PR) {
-#pragma unroll
-        for (int i = 0; i < NGR; ++i) vg_lds[wave][i][lane] = (_Float16)(vgr[i] * rv);
+        sc_lds[wave][0][lane] = ks_r;
+        sc_lds[wave][1][lane] = vs_r;
       }
-      ks_r = 1.f;
-      vs_r = vmax;
-    }
-    if (lane < PR) {
-      sc_lds[wave][0][lane] = ks_r;
-      sc_lds[wave][1][lane] = vs_r;
-    }
-    const bool sig_need = vs_r * wmul_run >= 2.0f;
-    const float vs_pass = vs_r;
-    if (cur + 1 < npass) load_k(pr0 + PR, rows_of(cur + 1));
-    wave_lds_sync();
+      const bool sig_need = vs_r * wmul_run >= 2.0f;
+      const float vs_pass = vs_r;
+      if (cur + 1 < npass) load_k(pr0 + PR, rows_of(cur + 1));
+      wave_lds_sync();
 
-    // ------------------------------------------------------------ softmax
-    const int64_t blk0 = pr0 / SROWS;
-    if constexpr (RC == 0) {
+      // ------------------------------------------------------------ softmax
+      const int64_t blk0 = pr0 / SROWS;
       float pmax, lsum;
       weights(blk0, prow, m_run, wmul_run, pmax, lsum);
       const bool m_need = pmax > m_run + kLazyMax;
@@ -636,76 +516,286 @@ __global__ __launch_bounds__(kPThreads, DK == 8 ? 1 : 2) void prefill_i8_mfma(Pr
       if (prow < PR)
         for (int i = prow + lane; i < PR; i += 64)
           for (int h = 0; h < 16; ++h) w_lds[wave][h][i] = (_Float16)0.f;
-    } else {
-      ms_pass(blk0, prow, cur == 0, (int)cur < n_open, sig_need, vs_pass);
-    }
-    wave_lds_sync();
+      wave_lds_sync();
 
-    // ------------------------------------------------------------ values
+      // ------------------------------------------------------------ values
 #pragma unroll
-    for (int sl = 0; sl < NS; ++sl) {
-      const u32x4_t wa = *reinterpret_cast<const u32x4_t*>(&w_lds[wave][lc][32 * sl + 8 * lq]);
-      const half8_t wop = __builtin_bit_cast(half8_t, wa);
-      if constexpr (!QG) {
-        const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
-        accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, ones, accs, 0, 0, 0);
+      for (int sl = 0; sl < NS; ++sl) {
+        const u32x4_t wa = *reinterpret_cast<const u32x4_t*>(&w_lds[wave][lc][32 * sl + 8 * lq]);
+        const half8_t wop = __builtin_bit_cast(half8_t, wa);
+        if constexpr (!QG) {
+          const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+          accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, ones, accs, 0, 0, 0);
+        }
+#pragma unroll
+        for (int dv = 0; dv < DV; ++dv) {
+          // QG: column c holds features 128 dv + 8 c + e, group 4 dv + c / 4
+          // (clamped: columns past D are dropped), rows 8q .. 8q+7
+          half8_t rat = {};
+          if constexpr (QG)
+            rat = *reinterpret_cast<const half8_t*>(
+                &vg_lds[wave][min(4 * dv + lc / 4, NGR - 1)][32 * sl + 8 * lq]);
+          values_dv(sl, dv, wop, rat);
+        }
+      }
+      wave_lds_sync();
+    }
+  } else {
+    // ---- RC != 0: the pass stays in registers.  Lane (lq, lc) holds query
+    // lc and, of each 16-row tile t of the pass, rows 16 t + 4 lq .. + 3 =
+    // block 4 t + lq: the score product's output layout, which is also an
+    // operand layout of v_mfma_f32_4x4x1_16b_f32 (its 16 independent 4x4
+    // products are the (lq, lc / 4) pairs, column lc % 4 the query).  Per
+    // tile: logits = A (r x 4) times the 4 scores (r / 4 products of 4
+    // k-steps, A operand A[4 th + i][k] for row i = lane % 4), causal mask
+    // as 4 more k-steps, exponentials in place, weights = A^T times them (r
+    // k-steps, A operand A[t][i]); the weights are the value product's A
+    // operand as they stand, with the value rows taken in the same order
+    // (k-slice q of a 32-row slice: rows 4q .. 4q+3 and 16+4q .. 16+4q+3).
+    constexpr int NTH = RC ? RC / 4 : 1;
+    const int ai = lane & 3;
+    float a_log[NTH][4], a_w[RC ? RC : 1];
+#pragma unroll
+    for (int th = 0; th < NTH; ++th)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a_log[th][k] = a_lds[(4 * th + ai) * 4 + k];
+#pragma unroll
+    for (int t = 0; t < RC; ++t) a_w[t] = a_lds[4 * t + ai];
+    const bool dc = __builtin_amdgcn_readfirstlane(__float_as_uint(dc_inv)) != 0;
+    float nmo = 0.f;  // minus the finite stand-in of m_run (0 while it is -inf)
+    // passes without the causal mask, a prefix of the wave's passes: whole
+    // and their last token at or before the wave's first query
+    const int n_open = (int)min<int64_t>(rows_total / PR, (qpos_min + 1) / ((PR / 4) * RC));
+    if (npass > 0) load_k(0, rows_of(0));
+    for (int64_t cur = 0; cur < npass; ++cur) {
+      const int64_t pr0 = cur * PR;
+      const int prow = rows_of(cur);  // multiple of SROWS
+      load_v(pr0, prow);
+      // K row scales (QG: the K group scales) of the pass's rows to LDS
+      if (lane < PR) {
+        if constexpr (QG) {
+#pragma unroll
+          for (int i = 0; i < NGR; ++i) kg_lds[wave][i][lane] = kgr[i];
+        } else {
+          sc_lds[wave][0][lane] = ks_r;
+        }
+      }
+      wave_lds_sync();
+
+      // ---------------------------------------------------------- scores
+      // sv[t][i]: base-2 logit contribution of row 16 t + 4 lq + i for
+      // query lc (the score times the head scale and the K row scale)
+      float4_t sv[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if constexpr (QG) {
+          float4_t accg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
+                               (int)kr[t][4 * c + 3]};
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+              const bool mine = (lq >> 1) == hf;
+              const i32x4_t zero = {0, 0, 0, 0};
+              const i32x4_t am = mine ? a : zero;
+              const i32x4_t ghi = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qhi[c], zero, 0, 0, 0);
+              const i32x4_t glo = __builtin_amdgcn_mfma_i32_16x16x64_i8(am, qlo[c], zero, 0, 0, 0);
+              const float4_t kgv =
+                  *reinterpret_cast<const float4_t*>(&kg_lds[wave][2 * c + hf][16 * t + 4 * lq]);
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                accg[i] = __builtin_fmaf(kgv[i], (float)(ghi[i] * 256 + glo[i]), accg[i]);
+            }
+          }
+          *reinterpret_cast<float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]) = accg * head_mul;
+        } else {
+          i32x4_t shi = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const i32x4_t a = {(int)kr[t][4 * c], (int)kr[t][4 * c + 1], (int)kr[t][4 * c + 2],
+                               (int)kr[t][4 * c + 3]};
+            shi = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qhi[c], shi, 0, 0, 0);
+            slo = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qlo[c], slo, 0, 0, 0);
+          }
+          const float4_t kh =
+              *reinterpret_cast<const float4_t*>(&sc_lds[wave][0][16 * t + 4 * lq]) * head_mul;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sv[t][i] = (float)(shi[i] * 256 + slo[i]) * kh[i];
+        }
+      }
+      if constexpr (QG) {
+        // V group scales relative to the row's largest (that one joins the
+        // weights as the row scale)
+        float vmax = 0.f;
+#pragma unroll
+        for (int i = 0; i < NGR; ++i) vmax = fmaxf(vmax, vgr[i]);
+        const float rv = vmax > 0.f ? __builtin_amdgcn_rcpf(vmax) : 0.f;
+        if (lane < PR) {
+#pragma unroll
+          for (int i = 0; i < NGR; ++i) vg_lds[wave][i][lane] = (_Float16)(vgr[i] * rv);
+        }
+        vs_r = vmax;
+      }
+      if (lane < PR) sc_lds[wave][1][lane] = vs_r;
+      const bool sig_need = vs_r * wmul_run >= 2.0f;
+      const float vs_pass = vs_r;
+      if (cur + 1 < npass) load_k(pr0 + PR, rows_of(cur + 1));
+      wave_lds_sync();
+
+      // ---------------------------------------------------------- softmax
+      // a V row scale at or above 2^(sig_run + 1): accumulators and weights
+      // to the new exponent first
+      if (__builtin_amdgcn_ballot_w64(sig_need) != 0) {
+        float smax = vs_pass;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) smax = fmaxf(smax, __shfl_xor(smax, m, 64));
+        const int sig_new = max(sig_run, pow2_exp_for(smax, 1));
+        const float sfix = ldexpf(1.0f, sig_run - sig_new);
+#pragma unroll
+        for (int dv = 0; dv < DV; ++dv)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[dv][e] *= sfix;
+        accs *= sfix;
+        sig_run = sig_new;
+        wmul_run = ldexpf(1.0f, -sig_new);
+      }
+      // QG: the scores went through LDS (the lane's own slots; kept in
+      // registers, the 32 group products of the score stage are all
+      // scheduled ahead and spill)
+      if constexpr (QG) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          sv[t] = *reinterpret_cast<const float4_t*>(&s_lds[wave][lc][16 * t + 4 * lq]);
+      }
+      const int64_t blk0 = pr0 / SROWS;
+      float4_t L[NT][NTH];
+      const float4_t c0 = {nmo, nmo, nmo, nmo};
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int th = 0; th < NTH; ++th) {
+          L[t][th] = c0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            L[t][th] = __builtin_amdgcn_mfma_f32_4x4x1f32(a_log[th][k], sv[t][k], L[t][th], 0, 0, 0);
+        }
+      if ((int)cur >= n_open) {
+        // taps after the query's position (and every tap of blocks past the
+        // pass's rows) get -2^100: A = -2^100 where k == i, B = [tap 4 th + k
+        // of the lane's block is masked for its query]
+        const int nblk = prow / 4;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int bl = 4 * t + lq;
+          const int64_t rel = min<int64_t>(qpos_lane - (blk0 + bl) * RC, RC);
+          const float limf = (float)(bl < nblk ? (int)rel : -1);
+#pragma unroll
+          for (int th = 0; th < NTH; ++th)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              L[t][th] = __builtin_amdgcn_mfma_f32_4x4x1f32(
+                  ai == k ? -0x1p100f : 0.f,
+                  __builtin_amdgcn_fmed3f((float)(4 * th + k) - limf, 0.f, 1.f), L[t][th], 0, 0,
+                  0);
+        }
+      }
+      float pm = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int th = 0; th < NTH; ++th)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pm = fmaxf(pm, L[t][th][i]);
+      if (cur == 0 || __builtin_amdgcn_ballot_w64(pm > kLazyMax) != 0) {
+        // query lc's maximum over the pass (its 4 lanes)
+#pragma unroll
+        for (int m = GP; m < 64; m <<= 1) pm = fmaxf(pm, __shfl_xor(pm, m, 64));
+        const float m_new = fmaxf(m_run, pm - nmo);
+        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const float nmo_new = m_new == -INFINITY ? 0.f : -m_new;
+        const float dm = nmo_new - nmo;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int th = 0; th < NTH; ++th) L[t][th] += dm;
+        l_lane *= alpha;
+        // accumulator lane (q, c) register i holds query 4q + i
+        float al[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lq + i, 64);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int dv = 0; dv < DV; ++dv)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[dv][e][i] *= al[i];
+          accs[i] *= al[i];
+        }
+        m_run = m_new;
+        nmo = nmo_new;
       }
 #pragma unroll
-      for (int dv = 0; dv < DV; ++dv) {
-        // QG: column c holds features 128 dv + 8 c + e, group 4 dv + c / 4
-        // (clamped: columns past D are dropped), rows 8q .. 8q+7
-        half8_t rat = {};
-        if constexpr (QG)
-          rat = *reinterpret_cast<const half8_t*>(
-              &vg_lds[wave][min(4 * dv + lc / 4, NGR - 1)][32 * sl + 8 * lq]);
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          uint32_t t0[4], t1[4];
+        for (int th = 0; th < NTH; ++th)
 #pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t ra = vr[sl][dv][2 * (2 * pp) + hh] ^ 0x80808080u;
-            const uint32_t rb = vr[sl][dv][2 * (2 * pp + 1) + hh] ^ 0x80808080u;
-            t0[pp] = __builtin_amdgcn_perm(rb, ra, 0x05010400u);
-            t1[pp] = __builtin_amdgcn_perm(rb, ra, 0x07030602u);
+          for (int i = 0; i < 4; ++i) L[t][th][i] = __builtin_amdgcn_exp2f(L[t][th][i]);
+      // weights of the block's 4 rows for the lane's query (the tiles'
+      // chains independent), then the exponential sums
+      float4_t W[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        W[t] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < RC; ++u)
+          W[t] = __builtin_amdgcn_mfma_f32_4x4x1f32(a_w[u], L[t][u / 4][u % 4], W[t], 0, 0, 0);
+      }
+      if (dc) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) l_lane = __builtin_fmaf(W[t][0], dc_inv, l_lane);
+      } else {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int th = 0; th < NTH; ++th)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) l_lane += L[t][th][i];
+      }
+      half8_t wop[NS];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const float4_t vw =
+            *reinterpret_cast<const float4_t*>(&sc_lds[wave][1][16 * t + 4 * lq]) * wmul_run;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wop[t / 2][4 * (t % 2) + i] = (_Float16)(W[t][i] * vw[i]);
+      }
+
+      // ---------------------------------------------------------- values
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) {
+        if constexpr (!QG) {
+          const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+          accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop[sl], ones, accs, 0, 0, 0);
+        }
+#pragma unroll
+        for (int dv = 0; dv < DV; ++dv) {
+          // QG: group 4 dv + c / 4 of column c, the slice's rows in k order
+          half8_t rat = {};
+          if constexpr (QG) {
+            const int grp = min(4 * dv + lc / 4, NGR - 1);
+            const u32x2_t r0 =
+                *reinterpret_cast<const u32x2_t*>(&vg_lds[wave][grp][32 * sl + 4 * lq]);
+            const u32x2_t r1 =
+                *reinterpret_cast<const u32x2_t*>(&vg_lds[wave][grp][32 * sl + 16 + 4 * lq]);
+            rat = __builtin_bit_cast(half8_t, (u32x4_t){r0[0], r0[1], r1[0], r1[1]});
           }
-#pragma unroll
-          for (int ee = 0; ee < 4; ++ee) {
-            half8_t ov;
-#pragma unroll
-            for (int pp = 0; pp < 4; ++pp) {
-              const uint32_t src = ee < 2 ? t0[pp] : t1[pp];
-              const uint32_t sel = (ee & 1) ? 0x04030402u : 0x04010400u;
-              // 1024 + (code + 128); QG: the code itself (scaled below)
-              half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, src, sel));
-              if constexpr (QG) h2 += (half2_t){(_Float16)-kVBias, (_Float16)-kVBias};
-              ov[2 * pp] = h2[0];
-              ov[2 * pp + 1] = h2[1];
-            }
-            const int e = 4 * hh + ee;
-            if constexpr (QG) ov *= rat;
-            acc[dv][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wop, ov, acc[dv][e], 0, 0, 0);
-          }
+          values_dv(sl, dv, wop[sl], rat);
         }
       }
     }
-    wave_lds_sync();
   }
 
-  if constexpr (RC != 0) {
-    // the matrix-core softmax's state to the layout below (lane c < 16:
-    // query c = 4 mb + mj): sums over the 16 blocks of each query
-    float lt[4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      float x = l4[g];
-#pragma unroll
-      for (int m = 4; m < 64; m <<= 1) x += __shfl_xor(x, m, 64);
-      lt[g] = x;
-    }
-    const float lsel = mb == 0 ? lt[0] : mb == 1 ? lt[1] : mb == 2 ? lt[2] : lt[3];
-    m_run = mb == 0 ? m4[0] : mb == 1 ? m4[1] : mb == 2 ? m4[2] : m4[3];
-    l_lane = lane < 16 ? lsel : 0.f;
-  }
   // ---- raw tail and output.  Sum of each query's exponentials over its 4
   // lanes; accumulators back to true scale.
 #pragma unroll
