@@ -108,6 +108,14 @@ CASES = [
     ("f16", 1, 2, 2, 128, 4, 20, 0, 0, 32),
     ("f16", 1, 1, 4, 128, 1, 50, 32 * 6 + 30, 0, 32),
     ("bf16", 2, 2, 2, 128, 2, 32 * 5 + 31, 0, 32, 32),
+    # the workgroup-shared pass (4 stored rows, one scale per row, D = 64 /
+    # 128, r = 4 / 8 / 16) at D = 64 and with 1 and 16 query heads per kv
+    # head (16 and 1 tokens per wavefront)
+    ("f16", 2, 2, 2, 64, 4, 8 * 25 + 5, 0),
+    ("bf16", 1, 2, 4, 64, 4, 4 * 41 + 2, 4 * 7 + 1, 0, 4),
+    ("f16", 1, 1, 2, 64, 4, 16 * 13 + 11, 0, 0, 16),
+    ("bf16", 1, 2, 1, 128, 4, 8 * 33 + 7, 0),
+    ("f16", 1, 1, 16, 128, 4, 8 * 11 + 3, 8 * 6),
 ]
 
 
