@@ -92,17 +92,15 @@ int fc_prefill_attention(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   const unsigned nblocks = (unsigned)blocks;
   int rc;
   // 4 stored rows per block of 4, 8 or 16 tokens: the softmax on the
-  // matrix cores (one 4x4 product per block); with one scale per row and D
-  // = 64 / 128 the workgroup shares each pass through LDS
-  // (its tail logits take up to 16 raw tokens: fewer than r)
-  const bool wg = s == 4 && !grouped && (D == 64 || D == 128) && (r == 4 || r == 8 || r == 16) &&
-                  n_raw < r;
+  // matrix cores (one 4x4 product per block); with one scale per row, D =
+  // 64 / 128 and blocks of 4 or 8 tokens the workgroup shares each pass
+  // through LDS (at 16 tokens its 3-wavefront register budget spills and
+  // the register-resident pass is faster: 1326 vs 1542 us at C5's shape)
+  const bool wg = s == 4 && !grouped && (D == 64 || D == 128) && (r == 4 || r == 8) && n_raw < r;
   if (wg && r == 8)
     rc = launch_prefill_wg<8>(a, dk, q_dtype, stream_dtype, nblocks, st);
   else if (wg && r == 4)
     rc = launch_prefill_wg<4>(a, dk, q_dtype, stream_dtype, nblocks, st);
-  else if (wg && r == 16)
-    rc = launch_prefill_wg<16>(a, dk, q_dtype, stream_dtype, nblocks, st);
   else if (s == 4 && r == 8)
     rc = launch_prefill<4, 8>(a, dk, q_dtype, stream_dtype, grouped, nblocks, st);
   else if (s == 4 && r == 4)

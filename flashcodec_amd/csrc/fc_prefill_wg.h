@@ -1,6 +1,6 @@
 // Causal prefill over an int8 jpeg archive with the passes shared by the
-// workgroup (4 stored rows per block of RC = 4 / 8 / 16 tokens, one fp32
-// scale per row, D = 64 / 128): the C5 prefill's kernel.
+// workgroup (4 stored rows per block of RC = 4 or 8 tokens, one fp32 scale
+// per row, D = 64 / 128): the C5 prefill's kernel.
 //
 // The 4 wavefronts of a workgroup own 16 queries each on consecutive token
 // runs of one (batch, kv head, head group), so they walk the same archived
@@ -27,7 +27,7 @@ __global__ __launch_bounds__(kPThreads, 3) void prefill_i8_wg(PrefillArgs p) {
   constexpr int SROWS = 4;
   constexpr int D = 32 * DK;
   static_assert(D == 64 || D == 128, "workgroup prefill: D = 64 or 128");
-  static_assert(RC == 4 || RC == 8 || RC == 16, "block of 4, 8 or 16 tokens");
+  static_assert(RC == 4 || RC == 8, "block of 4 or 8 tokens");
   constexpr int PR = 64;            // stored rows per pass
   constexpr int NT = PR / 16;       // 16-row tiles of a pass
   constexpr int NS = PR / 32;       // 32-row slices of the value product
@@ -514,6 +514,5 @@ int launch_prefill_wg(const PrefillArgs& a, int dk, int q_dtype, int stream_dtyp
 
 extern template int launch_prefill_wg<4>(const PrefillArgs&, int, int, int, unsigned, hipStream_t);
 extern template int launch_prefill_wg<8>(const PrefillArgs&, int, int, int, unsigned, hipStream_t);
-extern template int launch_prefill_wg<16>(const PrefillArgs&, int, int, int, unsigned, hipStream_t);
 
 }  // namespace fc

@@ -109,8 +109,8 @@ CASES = [
     ("f16", 1, 1, 4, 128, 1, 50, 32 * 6 + 30, 0, 32),
     ("bf16", 2, 2, 2, 128, 2, 32 * 5 + 31, 0, 32, 32),
     # the workgroup-shared pass (4 stored rows, one scale per row, D = 64 /
-    # 128, r = 4 / 8 / 16) at D = 64 and with 1 and 16 query heads per kv
-    # head (16 and 1 tokens per wavefront)
+    # 128, r = 4 / 8) at D = 64 and with 1 and 16 query heads per kv head
+    # (16 and 1 tokens per wavefront); r = 16 at D = 64 (register pass)
     ("f16", 2, 2, 2, 64, 4, 8 * 25 + 5, 0),
     ("bf16", 1, 2, 4, 64, 4, 4 * 41 + 2, 4 * 7 + 1, 0, 4),
     ("f16", 1, 1, 2, 64, 4, 16 * 13 + 11, 0, 0, 16),
