@@ -50,7 +50,8 @@ bool i8_mfma_takes(int store_kind, const void* q, int q_dtype, int64_t q_sb, int
 
 bool step_i8_mfma_supported(int stream_dtype, int r, int64_t D, int n_splits) {
   // the step's rows (2 r D floats) live in the score scratch before the passes
-  return (stream_dtype == FC_F16 || stream_dtype == FC_BF16) && split_i8_mfma_fusable(n_splits) &&
+  return (stream_dtype == FC_F16 || stream_dtype == FC_BF16 || stream_dtype == FC_F32) &&
+         split_i8_mfma_fusable(n_splits) &&
          2 * (int64_t)r * D <= (int64_t)kWaves * 16 * kSPad;
 }
 

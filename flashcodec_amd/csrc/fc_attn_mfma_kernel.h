@@ -780,7 +780,6 @@ constexpr int mfma_width() {
 template <int SROWS, int D, int GP, bool STEP, bool QF = false, bool QG = false>
 __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void attn_split_i8_mfma(
     MfmaArgs p) {
-  static_assert(!(STEP && QF), "the fused step takes fp16 / bf16 queries");
   static_assert(!QG || D % 32 == 0, "per-32 scales: D = 64 / 96 / 128 / 256");
   constexpr int DC = mfma_width<D>();
   constexpr int DK = DC / 32;
@@ -1190,8 +1189,10 @@ __global__ __launch_bounds__(kMThreads, mfma_width<D>() == 256 ? 1 : 2) void att
       };
       if (p.raw_dtype == FC_F16)
         go(f16_t{});
-      else
+      else if (p.raw_dtype == FC_BF16)
         go(bf16_t{});
+      else
+        go(float{});
     }
   } else if (fold_tail) {
     raw_tail_partial<D, QF>(p, b, hkv, g0, G, (int)n_raw, tid,
@@ -1549,8 +1550,9 @@ int launch_mfma_rows(const MfmaArgs& a, int d, int gp, dim3 grid, hipStream_t st
     constexpr int Dv = decltype(dc)::value;
     return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
       constexpr int GPv = decltype(gc)::value;
-      if (a.step) {
-        if (a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
+      if (a.step && a.q_dtype == FC_F32) {
+        attn_split_i8_mfma<SR, Dv, GPv, true, true><<<grid, kMThreads, 0, st>>>(a);
+      } else if (a.step) {
         attn_split_i8_mfma<SR, Dv, GPv, true><<<grid, kMThreads, 0, st>>>(a);
       } else if (a.q_dtype == FC_F32) {
         attn_split_i8_mfma<SR, Dv, GPv, false, true><<<grid, kMThreads, 0, st>>>(a);
@@ -1568,8 +1570,9 @@ int launch_mfma_rows_g(const MfmaArgs& a, int d, int gp, dim3 grid, hipStream_t 
     constexpr int Dv = decltype(dc)::value;
     return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
       constexpr int GPv = decltype(gc)::value;
-      if (a.step) {
-        if (a.q_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
+      if (a.step && a.q_dtype == FC_F32) {
+        attn_split_i8_mfma<SR, Dv, GPv, true, true, true><<<grid, kMThreads, 0, st>>>(a);
+      } else if (a.step) {
         attn_split_i8_mfma<SR, Dv, GPv, true, false, true><<<grid, kMThreads, 0, st>>>(a);
       } else if (a.q_dtype == FC_F32) {
         attn_split_i8_mfma<SR, Dv, GPv, false, true, true><<<grid, kMThreads, 0, st>>>(a);

@@ -69,8 +69,10 @@ __global__ void state_advance_kernel(int64_t* state, int64_t r, int64_t cap) {
 static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   const bool grouped = a->store_kind == FC_STORE_JPEG_I8G;
   const bool fp = a->store_kind == FC_STORE_JPEG_FP;  // fp16 / bf16 coefficient rows
+  // (fp32 queries: int8 archives; fp coefficient rows need queries in their
+  // own dtype, which split_fpj_mfma_supported checks)
   if ((a->store_kind != FC_STORE_JPEG_I8 && !grouped && !fp) || (!fp && a->quant_bits != 8) ||
-      !mfma_split_allowed() || a->q_dtype == FC_F32)
+      !mfma_split_allowed())
     return FC_ERR_UNSUPPORTED;
   const int64_t B = a->B, Hq = a->Hq, Hkv = a->Hkv, D = a->D;
   const int r = a->r;

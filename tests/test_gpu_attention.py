@@ -417,6 +417,12 @@ STEP_PAIRS = [
     (dict(I8, quant_group=32, keep_freqs=1), "f16", 256, 8, True),
     (dict(I8, quant_group=32, block_size=16, keep_freqs=3), "bf16", 128, 16, True),
     (dict(mode="png", block_size=8, keep_ratio=0.5, packed=True), "f32", 64, 4, False),
+    # fp32 queries and stream (an fp32 model): one launch, fp32 rows archived
+    # in-kernel
+    (I8, "f32", 128, 2, True),
+    (dict(I8, keep_freqs=3), "f32", 64, 4, True),
+    (dict(I8, quant_group=32), "f32", 128, 2, True),
+    (dict(I8, quant_group=32, block_size=16, keep_freqs=2), "f32", 96, 8, True),
 ]
 
 
