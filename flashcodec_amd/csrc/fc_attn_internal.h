@@ -83,6 +83,7 @@ struct MfmaFuse {
   const float* basis = nullptr;
   int64_t step_t = 0, step_nb = 0;
   unsigned int* done = nullptr;
+  int keep_m = 0;  // png: kept deltas per (block, feature)
 };
 
 // Whether fc_decode_step can run as one launch of the matrix-core pass for

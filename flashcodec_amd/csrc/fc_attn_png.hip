@@ -30,6 +30,7 @@
 // Products and sums are fp32 throughout (the query and the weights are not
 // rounded), so fp32 outputs meet the 1e-5 tolerance.
 #include "fc_attn_mfma_kernel.h"
+#include "fc_topm.h"
 
 namespace fc {
 
@@ -37,12 +38,125 @@ namespace {
 
 constexpr int kPngTile = 16;  // rows per pass
 
+// Fused decode step on a png archive, split 0 (fp32 stream): the rows this
+// step adds to the attention, in LDS as fp32 (xk, xv: n rows of D), and the
+// partial of the group's G heads over them (as raw_tail_partial_t: tm, tl,
+// acc).
+//   * t + 1 < R: the tail rows 0..t-1 and the new token; the token is
+//     written to tail row t.
+//   * t + 1 == R: the block of tail rows 0..R-2 and the new token is
+//     archived as png_encode_kernel does (anchor = token 0, fp32 deltas
+//     x_{i+1} - x_i, the keep_m largest |delta| kept by the same Top-M mask
+//     and the others multiplied by 0), stored when `write`, and attended as
+//     png_decode_kernel reconstructs it (anchor + the fp64 running sum of the
+//     deltas, rounded to fp32).
+// The query rows (fp32) are q + qb + (h0 + h) * q_sh for the G heads.
+template <int D, int R>
+__device__ __forceinline__ void png_step_partial(
+    int64_t t, float* ktail, float* vtail, const float* ktok, const float* vtok, bool write,
+    float* kanch, float* kdel, float* vanch, float* vdel, int keep_m, const float* q, int64_t qb,
+    int64_t q_sh, int64_t h0, int G, float scale_log2, int tid, float* xk, float* xv, float* etl,
+    float* acc, float* tm, float* tl) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const bool complete = t + 1 == R;
+  const int n = complete ? R : (int)t + 1;
+  for (int x = tid; x < n * D; x += kMThreads) {
+    const int i = x / D, d = x - i * D;
+    xk[x] = i < t ? ktail[i * D + d] : ktok[d];
+    xv[x] = i < t ? vtail[i * D + d] : vtok[d];
+  }
+  if (write && !complete)
+    for (int d = tid; d < D; d += kMThreads) {
+      ktail[t * D + d] = ktok[d];
+      vtail[t * D + d] = vtok[d];
+    }
+  __syncthreads();
+  if (complete) {
+    // one (stream, feature) per thread
+    for (int x = tid; x < 2 * D; x += kMThreads) {
+      const int sv = x / D, d = x - sv * D;
+      float* xs = sv ? xv : xk;
+      float* anch = sv ? vanch : kanch;
+      float* del = sv ? vdel : kdel;
+      float dl[R];
+#pragma unroll
+      for (int i = 0; i + 1 < R; ++i) dl[i] = xs[(i + 1) * D + d] - xs[i * D + d];
+      dl[R - 1] = 0.f;
+      constexpr int n1 = R - 1;
+      if (keep_m > 0 && keep_m < n1) {
+        uint32_t key[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) key[i] = i < n1 ? topm_key(__float_as_uint(dl[i])) : 0u;
+        const uint64_t mask = topm_mask<R>(key, n1, keep_m);
+#pragma unroll
+        for (int i = 0; i + 1 < R; ++i)
+          if (!((mask >> i) & 1)) dl[i] = dl[i] * 0.0f;
+      }
+      const float a = xs[d];
+      if (write) {
+        anch[d] = a;
+#pragma unroll
+        for (int i = 0; i + 1 < R; ++i) del[i * D + d] = dl[i];
+      }
+      double run = 0.0;
+#pragma unroll
+      for (int i = 0; i + 1 < R; ++i) {
+        run += (double)dl[i];
+        xs[(i + 1) * D + d] = a + (float)run;
+      }
+    }
+    __syncthreads();
+  }
+  // the partial over the n rows, at full precision
+  {
+    const int grp = tid >> 4, gl = tid & 15;
+    for (int u = grp; u < G * n; u += kMThreads / 16) {
+      const int h = u / n, i = u - h * n;
+      const float* qr = q + qb + (h0 + h) * q_sh + gl;
+      float a = 0.f;
+      for (int c = 0; c < D / 16; ++c) a = __builtin_fmaf(qr[16 * c], xk[i * D + gl + 16 * c], a);
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) a += __shfl_xor(a, m, 16);
+      if (gl == 0) etl[h * FC_MAX_BLOCK + i] = a * scale_log2;
+    }
+  }
+  __syncthreads();
+  for (int h = wave; h < G; h += kWaves) {
+    float mx = -INFINITY;
+    for (int i = lane; i < n; i += 64) mx = fmaxf(mx, etl[h * FC_MAX_BLOCK + i]);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    float l = 0.f;
+    for (int i = lane; i < n; i += 64) {
+      const float e = __builtin_amdgcn_exp2f(etl[h * FC_MAX_BLOCK + i] - mx);
+      etl[h * FC_MAX_BLOCK + i] = e;
+      l += e;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
+    if (lane == 0) {
+      tm[h] = mx;
+      tl[h] = l;
+    }
+  }
+  __syncthreads();
+  for (int x = tid; x < G * D; x += kMThreads) {
+    const int h = x / D, d = x - h * D;
+    float o = 0.f;
+    for (int i = 0; i < n; ++i) o = __builtin_fmaf(etl[h * FC_MAX_BLOCK + i], xv[i * D + d], o);
+    acc[h * D + d] = o;
+  }
+}
+
 
 // kPngWgPerCu (2) workgroups per compute unit: measured at C4, 2 per CU
 // (32 splits) take 59.2 us per call over rotating archive sets where 3 per
 // CU (48 splits, the query operands read from LDS to fit 168 VGPRs) take
-// 64.6 (more partials to merge, more contention on the pass queues)
-template <int R, int D, int GP>
+// 64.6 (more partials to merge, more contention on the pass queues).
+// STEP: the fused decode step (fc_decode_step; MfmaArgs.step): split 0
+// appends the token or archives the block it completes (png_step_partial)
+// and the passes cover the blocks before it.
+template <int R, int D, int GP, bool STEP = false>
 __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(MfmaArgs p) {
   constexpr int FPL = D / 4;   // score-operand features per lane
   constexpr int FPC = D / 16;  // value-product features per lane column
@@ -50,12 +164,18 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   __shared__ float s_lds[kWaves][16][kPngTile + 1];  // scaled scores [head][row]
   __shared__ float w_lds[kWaves][16][kPngTile + 4];  // weights [head][row]
   __shared__ float comb[kWaves][16][3];
-  __shared__ float cbuf[kWaves][GP][D];
+  // the end phase's per-wavefront accumulators; STEP: before the passes,
+  // the step's rows (2 R D floats)
+  constexpr int kCb = kWaves * GP * D;
+  constexpr int kCbN = STEP && 2 * R * D > kCb ? 2 * R * D : kCb;
+  __shared__ __attribute__((aligned(16))) float cbuf_raw[kCbN];
+  auto& cbuf = *reinterpret_cast<float (*)[kWaves][GP][D]>(cbuf_raw);
   __shared__ __attribute__((aligned(16))) float part_lds[16 * D];
   __shared__ float tail_ml[2][16];
   __shared__ float wg_ml[2][16];
   __shared__ float scratch[2 * 16 * kFuseMaxSplits];  // raw-tail logits, then merge statistics
   __shared__ int s_last;
+  __shared__ int s_final;
 
   // 1-D grid, split-major, as the int8 pass
   const int64_t L = blockIdx.x;
@@ -70,7 +190,18 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   const int G = (int)min<int64_t>(16, p.G - g0);
 
   int64_t nb = p.nb, n_raw = p.n_raw;
-  if (p.state) {
+  int64_t step_t = 0, step_nb = 0;  // fused step: tail length and blocks before the token
+  bool step_write = false;
+  if constexpr (STEP) {
+    const int64_t cap = min(p.kcap, p.vcap);
+    step_t = p.state ? min<int64_t>(max<int64_t>(p.state[1], 0), R - 1) : p.step_t;
+    step_nb = p.state ? max<int64_t>(p.state[0], 0) : p.step_nb;
+    // one head group per (batch, kv head) stores the token / block; a block
+    // past the capacity is not stored (the state's overflow word says so)
+    step_write = split == 0 && g0 == 0 && (step_t + 1 < R || step_nb < cap);
+    nb = min(step_nb, cap);
+    n_raw = 0;
+  } else if (p.state) {
     // counts of a decode step's view on the device (graph replays)
     const int64_t t = min<int64_t>(max<int64_t>(p.state[1], 0), R - 1) + 1;
     nb = min<int64_t>(max<int64_t>(p.state[0], 0) + (t == R ? 1 : 0), min(p.kcap, p.vcap));
@@ -188,11 +319,29 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   for (int j = 0; j < FPL / 4; ++j)
 #pragma unroll
     for (int i = 0; i < 4; ++i) qv[4 * j + i] = hq_ok ? qraw[j][i] : 0.f;
-  // raw tail (fused calls): split 0 computes its partial before the passes
-  const bool fold_tail = p.fused && split == 0 && n_raw > 0;
-  if (fold_tail)
+  // raw tail (fused calls): split 0 computes its partial before the passes;
+  // in a fused step that partial covers the rows the step adds
+  const bool fold_tail = p.fused && split == 0 && (STEP || n_raw > 0);
+  if constexpr (STEP) {
+    if (split == 0) {
+      const int64_t bh_s = b * p.Hkv + hkv;
+      float* xk = cbuf_raw;  // the passes have not started: the end-phase buffer is free
+      png_step_partial<D, R>(
+          step_t, static_cast<float*>(const_cast<void*>(p.kraw)) + bh_s * R * D,
+          static_cast<float*>(const_cast<void*>(p.vraw)) + bh_s * R * D,
+          static_cast<const float*>(p.ktok) + b * p.kt_sb + hkv * p.kt_sh,
+          static_cast<const float*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write,
+          static_cast<float*>(const_cast<void*>(p.kanch)) + (bh_s * p.kcap + step_nb) * D,
+          const_cast<float*>(p.kdel) + (bh_s * p.kcap + step_nb) * (R - 1) * D,
+          static_cast<float*>(const_cast<void*>(p.vanch)) + (bh_s * p.vcap + step_nb) * D,
+          const_cast<float*>(p.vdel) + (bh_s * p.vcap + step_nb) * (R - 1) * D, p.keep_m,
+          static_cast<const float*>(p.q), b * p.q_sb, p.q_sh, hkv * p.G + g0, G, p.scale_log2,
+          tid, xk, xk + R * D, scratch, part_lds, tail_ml[0], tail_ml[1]);
+    }
+  } else if (fold_tail) {
     raw_tail_partial<D, true>(p, b, hkv, g0, G, (int)n_raw, tid, scratch, part_lds, tail_ml[0],
                               tail_ml[1]);
+  }
   __syncthreads();
 
   while (cur < npass) {
@@ -273,10 +422,27 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   // the merge of up to 32 splits reads every partial in one batch, two
   // threads per output task (C4: 32 splits per group; 2.1 us shorter than
   // batches of 8 with the statistics staged in LDS)
-  auto no_step = [] {};
-  split_epilogue<D, GP, true, false, decltype(no_step)&, 32>(
+  // fused step with a device state: the launch's last workgroup to finish
+  // (all others have read the state by then) advances it
+  auto step_done = [&]() {
+    if constexpr (!STEP) return;
+    if (!p.state) return;
+    if (tid == 0) s_final = atomicAdd(p.done, 1u) + 1 == gridDim.x ? 1 : 0;
+    __syncthreads();
+    if (s_final && tid < 64) {  // lane-indexed vector stores
+      const int64_t cap = min(p.kcap, p.vcap);
+      const bool full = step_t + 1 == R;
+      const bool over = full && step_nb >= cap;
+      const int64_t word = tid == 0   ? (full ? step_nb + 1 : step_nb)
+                           : tid == 1 ? (full ? 0 : step_t + 1)
+                                      : ((p.state[2] != 0 || over) ? 1 : 0);
+      if (tid < 3) const_cast<int64_t*>(p.state)[tid] = word;
+      if (tid == 0) __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+  split_epilogue<D, GP, true, false, decltype(step_done)&, 32>(
       p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf, part_lds, tail_ml, wg_ml, scratch,
-      s_last, passq, no_step);
+      s_last, passq, step_done);
 }
 
 }  // namespace
@@ -341,6 +507,20 @@ int launch_split_png_mfma(const void* q, int64_t q_sb, int64_t q_sh, int64_t B, 
     a.out = fuse->out;
     a.o_sb = fuse->o_sb;
     a.o_sh = fuse->o_sh;
+    if (fuse->step) {
+      a.step = 1;
+      a.ktok = fuse->ktok;
+      a.vtok = fuse->vtok;
+      a.kt_sb = fuse->kt_sb;
+      a.kt_sh = fuse->kt_sh;
+      a.vt_sb = fuse->vt_sb;
+      a.vt_sh = fuse->vt_sh;
+      a.step_t = fuse->step_t;
+      a.step_nb = fuse->step_nb;
+      a.done = fuse->done;
+      a.keep_m = fuse->keep_m;
+      if (!fuse->done) return FC_ERR_ARG;
+    }
   }
   const int64_t G = Hq / Hkv;
   const int gg = (int)std::min<int64_t>(G, 16);
@@ -358,7 +538,10 @@ int launch_split_png_mfma(const void* q, int64_t q_sb, int64_t q_sh, int64_t B, 
     return mfma_with_int<64, 128>((int)D, [&](auto dc) {
       constexpr int Dv = decltype(dc)::value;
       return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
-        attn_split_png_mfma<Rv, Dv, decltype(gc)::value><<<grid, kMThreads, 0, st>>>(a);
+        if (a.step)
+          attn_split_png_mfma<Rv, Dv, decltype(gc)::value, true><<<grid, kMThreads, 0, st>>>(a);
+        else
+          attn_split_png_mfma<Rv, Dv, decltype(gc)::value><<<grid, kMThreads, 0, st>>>(a);
         return FC_OK;
       });
     });

@@ -527,57 +527,6 @@ __global__ __launch_bounds__(kThreads) void dequantize_rows_kernel(
 
 // ----------------------------------------------------------------- png encode
 
-// Descending bitonic sort of N (power of two) keys held in registers.
-template <int N>
-__device__ __forceinline__ void bitonic_sort_desc(uint32_t (&k)[N]) {
-#pragma unroll
-  for (int size = 2; size <= N; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const int j = i ^ stride;
-        if (j > i) {
-          const bool desc = (i & size) == 0;
-          const uint32_t a = k[i], c = k[j];
-          const uint32_t hi = a > c ? a : c, lo = a > c ? c : a;
-          k[i] = desc ? hi : lo;
-          k[j] = desc ? lo : hi;
-        }
-      }
-    }
-  }
-}
-
-// Keep mask of the `m` largest of `n` keys (n < RMAX).  The common case —
-// the m-th and (m+1)-th largest keys differ, or the cut falls on zero,
-// where keeping or zeroing a +-0 delta stores the same bits — is decided
-// from a sorting network; a nonzero tie across the cut takes the exact
-// introselect restatement.
-template <int RMAX>
-__device__ __forceinline__ uint64_t topm_mask(const uint32_t (&key)[RMAX], int n, int m) {
-  uint32_t s[RMAX];
-#pragma unroll
-  for (int i = 0; i < RMAX; ++i) s[i] = i < n ? key[i] : 0u;
-  bitonic_sort_desc<RMAX>(s);
-  uint32_t vm = 0, vm1 = 0;
-#pragma unroll
-  for (int i = 0; i < RMAX; ++i) {
-    if (i == m - 1) vm = s[i];
-    if (i == m) vm1 = s[i];
-  }
-  if (vm == 0u || vm != vm1) {
-    uint64_t mask = 0;
-#pragma unroll
-    for (int i = 0; i < RMAX; ++i)
-      if (i < n && key[i] >= vm) mask |= (uint64_t)1 << i;
-    return mask;
-  }
-  uint32_t kk[64];
-  for (int i = 0; i < n; ++i) kk[i] = key[i];
-  return topm_mask_exact(kk, n, m);
-}
-
 typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
 
 // PACK: the packed Top-M layout (fc_png_encode_packed) instead of dense

@@ -400,7 +400,11 @@ STEP_PAIRS = [
     (dict(mode="jpeg", block_size=8, keep_freqs=2), "f16", 64, 4, True),
     (dict(mode="jpeg", block_size=16, keep_freqs=8), "bf16", 128, 8, True),
     (dict(mode="jpeg", block_size=4, keep_freqs=3), "f16", 128, 1, True),
-    (dict(mode="png", block_size=8, keep_ratio=0.5), "f32", 64, 4, False),
+    # fp32 png: one launch that archives the block (anchor, Top-M deltas) in-kernel
+    (dict(mode="png", block_size=8, keep_ratio=0.5), "f32", 64, 4, True),
+    (dict(mode="png", block_size=4, keep_ratio=1.0), "f32", 128, 2, True),
+    (dict(mode="png", block_size=16, keep_ratio=0.25), "f32", 128, 8, True),
+    (dict(mode="png", block_size=8, keep_ratio=0.3), "f32", 64, 16, True),
     (dict(mode="png", block_size=4, keep_ratio=1.0), "bf16", 64, 4, False),
     # the C5 instantiation (D=128, bf16, k=4, G=2), other row counts and widths
     (I8, "bf16", 128, 2, True),

@@ -191,10 +191,12 @@ STEP_CFGS = [(I8_C3, "bf16", 2), (I8_C3, "f16", 4),
              (dict(mode="png", block_size=8, keep_ratio=0.5, packed=True), "bf16", 2),
              (dict(mode="jpeg", block_size=8, keep_freqs=4), "bf16", 2),
              (dict(mode="jpeg", block_size=8, keep_freqs=2), "f16", 4),
-             (I8_C3, "f32", 2), (dict(I8_C3, quant_group=32), "f32", 4)]
+             (I8_C3, "f32", 2), (dict(I8_C3, quant_group=32), "f32", 4),
+             (dict(mode="png", block_size=8, keep_ratio=0.5), "f32", 2),
+             (dict(mode="png", block_size=4, keep_ratio=0.67), "f32", 8)]
 STEP_IDS = ["i8-bf16", "i8-f16", "fp-f32", "png-f16", "i8g-bf16", "i8k8-f16", "i8k3-bf16",
             "png16-f32", "pngpk16-f32", "pngpk8-bf16", "fpj-bf16", "fpj-f16", "i8-f32",
-            "i8g-f32"]
+            "i8g-f32", "png8-f32", "png4-f32"]
 
 
 def _tokens(g, B, H, D, dt):
