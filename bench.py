@@ -365,6 +365,40 @@ def c4_mode(args):
                       "head) sequences (16384 tokens, 4 query heads); the reference's torch CPU "
                       "path (restated in oracle/torch_path.py), median of >= 5 calls",
             "archive": arch_gbs, "read": read_gbs, "attention": attn_gbs}
+        # decode steps on copies of the archives: codec_decode_step (token
+        # append, the block archived every r-th step, attention) against the
+        # reference's step (two appends, then the attention); room for every
+        # call reserved first, so no call regrows the archives
+        from flashcodec_amd import _native as N
+        kt = torch.randn((b_, h_, 1, d_), generator=g, device=dev)
+        vt = torch.randn((b_, h_, 1, d_), generator=g, device=dev)
+        n_pre = 1024
+        for name in ("step", "append_attend"):
+            sk, sv = archive_copy(ks), archive_copy(vs)
+            for st_ in (sk, sv):
+                st_._grow(st_.n_blocks + (n_pre + args.warmup + args.steps) // r + 2, kt)
+            if name == "step":
+                def fn():
+                    return fc.codec_decode_step(q, kt, vt, sk, sv)
+            else:
+                def fn():
+                    sk.append(kt)
+                    sv.append(vt)
+                    return fc.codec_decode_attention(q, sk, sv)
+            for _ in range(n_pre + args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            res[tag][f"{name}_us"] = round(e0.elapsed_time(e1) / args.steps * 1e3, 2)
+            if name == "step":
+                res[tag]["step_single_launch"] = N.lib().fc_last_step_single_launch() == 1
+            del sk, sv, fn
+        torch.cuda.empty_cache()
         log(f"bench c4 keep {keep}: {res[tag]}")
 
     # packed Top-M archives (this build's fixed-rate format; the reference
@@ -994,7 +1028,8 @@ def archive_copy(st):
             setattr(c, name, t.clone())
     c._capacity, c.n_blocks, c.n_archived = st._capacity, st.n_blocks, st.n_archived
     c.dtype, c.meta = st.dtype, st.meta
-    c._raw_buf, c._n_raw = st._raw_buf.clone(), st._n_raw
+    c._adopt_tail(st._raw_buf.clone())
+    c._n_raw = st._n_raw
     return c
 
 
