@@ -328,6 +328,19 @@ def test_graph_replayed_steps_c5_scale(cfg, kind, oracle):
                  oracle, check_archive=True, single_launch=True)
 
 
+@pytest.mark.parametrize("keep", [0.25, 1.0])
+def test_graph_replayed_steps_c4_scale(keep, oracle):
+    """Graph-replayed one-launch png steps at C4's geometry (fp32, batch 2,
+    32 q / 8 kv heads, D=128, r=16; 1024 archived blocks + 5 tail tokens: the
+    png pass's 32 splits): 14 replays across a block boundary, every sequence
+    of every replay against the fp64 oracle, and the anchors and deltas the
+    replays wrote against the two-append path's, bit for bit."""
+    cfg = dict(mode="png", block_size=16, keep_ratio=keep)
+    print(f"case graph step at C4 scale {cfg}", flush=True)
+    _graph_steps(cfg, "f32", 2, 8, 4, 128, 1024 * 16 + 5, 14, 161, oracle, check_archive=True,
+                 single_launch=True)
+
+
 def _graph_steps(cfg, dt, B, Hkv, G, D, S0, steps, seed, oracle, check_archive=False,
                  single_launch=False):
     pytest.importorskip("transformers")
