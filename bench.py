@@ -445,6 +445,35 @@ def c4_mode(args):
             "algorithmic_bytes_attention": alg_pk_attn,
             "cpu_baseline": "the reference stores these deltas dense: see keep0.25 (same rows)"}
         log(f"bench c4 packed keep {keep}: {res[f'packed_keep{keep}']}")
+
+    # the same shape as a bf16 / fp16 stream (16-bit anchors and queries, fp32
+    # deltas), keep 0.25: the png matrix-core pass against the vector-ALU pass,
+    # over 4 rotating archive sets
+    from flashcodec_amd import _native as N
+    for dname, dt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+        codec = fc.make_codec(mode="png", block_size=r, keep_ratio=0.25)
+        ks, vs = _CodecStream(codec), _CodecStream(codec)
+        ks.append(x["k"].to(dt))
+        vs.append(x["v"].to(dt))
+        q16 = q.to(dt)
+        alg16 = 2 * b_ * h_ * nb * (d_ * 2 + (r - 1) * d_ * 4) + 2 * b_ * hq * d_ * 2
+        sets = [(ks, vs)] + [(archive_copy(ks), archive_copy(vs)) for _ in range(3)]
+        t16 = {}
+        for pname in ("auto", "valu"):
+            prev = N.set_attention_pass(pname)
+            t16[pname] = timed_cycle(lambda i: fc.codec_decode_attention(q16, *sets[i % 4]),
+                                     args.steps, args.warmup)
+            N.set_attention_pass(prev)
+        del sets, ks, vs
+        torch.cuda.empty_cache()
+        res[f"{dname}_keep0.25"] = {
+            "algorithmic_bytes_attention": alg16,
+            "attention_rotating_us": round(t16["auto"] * 1e3, 2),
+            "attention_rotating_GBs": round(alg16 / (t16["auto"] * 1e-3) / 1e9, 1),
+            "attention_rotating_hbm_frac": round(alg16 / (t16["auto"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                                 4),
+            "vector_alu_pass_rotating_us": round(t16["valu"] * 1e3, 2)}
+        log(f"bench c4 {dname}: {res[f'{dname}_keep0.25']}")
     print(json.dumps(res))
 
 

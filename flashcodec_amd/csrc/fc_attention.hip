@@ -1429,7 +1429,7 @@ int decode_attention_parts(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
       fz.o_sb = o_sb;
       fz.o_sh = o_sh;
     }
-    const int rc = launch_split_png_mfma(q, q_sb, q_sh, B, Hq, Hkv, D, r, nb, key, value,
+    const int rc = launch_split_png_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, nb, key, value,
                                          scale_log2, pm, pl, pacc, n_splits, counters,
                                          kCounterWords, mstride,
                                          fuse ? &fz : nullptr, nullptr, st);
@@ -1573,7 +1573,7 @@ int decode_attention_state(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
     fz.out = out;
     fz.o_sb = o_sb;
     fz.o_sh = o_sh;
-    return launch_split_png_mfma(q, q_sb, q_sh, B, Hq, Hkv, D, r, nb_hint, key, value,
+    return launch_split_png_mfma(q, q_dtype, q_sb, q_sh, B, Hq, Hkv, D, r, nb_hint, key, value,
                                  scale * kLog2e, pm, pl, pacc, n_splits, counters, kCounterWords,
                                  mstride, &fz, state, st);
   }

@@ -109,9 +109,9 @@ int launch_split_i8_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          unsigned int* counters, int64_t counter_words, int64_t stride,
                          const MfmaFuse* fuse, hipStream_t st, bool grouped = false);
 
-// The png matrix-core split pass (fc_attn_png.hip): fp32 queries and
-// anchors, D in {64, 128}, r in {4, 8, 16}; `state` as the fused decode
-// step's device counters (or NULL).
+// The png matrix-core split pass (fc_attn_png.hip): queries in the stream's
+// dtype (fp32, fp16, bf16; anchors in it, deltas fp32), D in {64, 128}, r in
+// {4, 8, 16}; `state` as the fused decode step's device counters (or NULL).
 bool png_mfma_shape_supported(int q_dtype, int stream_dtype, int64_t D, int r);
 constexpr int kPngWgPerCu = 2;  // workgroups per compute unit of the png pass
 // jpeg archives of fp16 / bf16 coefficients on the matrix cores
@@ -130,8 +130,9 @@ int launch_split_fpj_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh
 bool split_png_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
                               int r, int stream_dtype, const fc_stream_view* key,
                               const fc_stream_view* value);
-int launch_split_png_mfma(const void* q, int64_t q_sb, int64_t q_sh, int64_t B, int64_t Hq,
-                          int64_t Hkv, int64_t D, int r, int64_t nb, const fc_stream_view* key,
+int launch_split_png_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t B,
+                          int64_t Hq, int64_t Hkv, int64_t D, int r, int64_t nb,
+                          const fc_stream_view* key,
                           const fc_stream_view* value, float scale_log2, float* pm, float* pl,
                           float* pacc, int n_splits, unsigned int* counters,
                           int64_t counter_words, int64_t stride, const MfmaFuse* fuse,

@@ -130,7 +130,8 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   fz.done = ws.done;
   fz.keep_m = a->keep_m;
   if (png)
-    return launch_split_png_mfma(a->q, a->q_sb, a->q_sh, B, Hq, Hkv, D, r, nb, &v[0], &v[1],
+    return launch_split_png_mfma(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, r, nb,
+                                 &v[0], &v[1],
                                  a->scale * 1.4426950408889634f, ws.pm, ws.pl, ws.pacc, n_splits,
                                  ws.counters, kCounterWords, mstride, &fz, state,
                                  (hipStream_t)a->stream);

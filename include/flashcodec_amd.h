@@ -273,7 +273,8 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G,
  * round of workgroups of the split pass that will run — the matrix-core
  * passes for int8 jpeg archives (one scale per row or per 32 features) with
  * fp16/bf16/fp32 queries, for fp16/bf16 coefficient archives queried in
- * their dtype at D = 64/128, and for fp32 png at r = 4/8/16 (two workgroups
+ * their dtype at D = 64/128, and for png (fp32 / fp16 / bf16 streams queried
+ * in their dtype) at r = 4/8/16 (two workgroups
  * per compute unit, but at least one pass per wavefront and at most
  * max(16, passes / 10) splits), the packed png pass, otherwise the
  * vector-ALU pass at the occupancy it reaches on the current device.  0
@@ -520,7 +521,7 @@ int fc_decode_step(const fc_step_args* args);
  * the whole step was one kernel launch (int8 jpeg archives with one scale
  * per row or per 32 features, fp16 / bf16 / fp32 queries and stream, or
  * jpeg archives of fp16 / bf16 coefficients with queries and stream of
- * their dtype, or fp32 png archives with fp32 queries and stream; a
+ * their dtype, or png archives with queries and stream of one dtype; a
  * matrix-core pass), 0 when it
  * took the multi-launch form (token append, archive, attention, state
  * advance), -1 before any such call.  No counterpart in the reference (its

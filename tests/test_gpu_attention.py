@@ -112,6 +112,8 @@ CASES = [
     ("png-f32-k1-g4", dict(mode="png", block_size=8, keep_ratio=1.0), "f32", 2, 2, 4, 8 * 30 + 6, 128),
     ("png-bf16-k05-g2", dict(mode="png", block_size=16, keep_ratio=0.5), "bf16", 1, 2, 2, 16 * 25 + 11, 64),
     ("png-f16-r4-g5", dict(mode="png", block_size=4, keep_ratio=1.0), "f16", 2, 1, 5, 4 * 40 + 2, 16),
+    ("png-bf16-r16-k025-g4", dict(mode="png", block_size=16, keep_ratio=0.25), "bf16", 2, 2, 4, 16 * 70 + 9, 128),
+    ("png-f16-r8-g3", dict(mode="png", block_size=8, keep_ratio=1.0), "f16", 1, 2, 3, 8 * 90 + 5, 128),
     ("jpeg-i8-f16-d256", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16", 1, 2, 4, 8 * 64 + 4, 256),
     ("jpeg-i8-bf16-d512", dict(mode="jpeg", block_size=8, keep_freqs=2, quant_bits=8), "bf16", 1, 1, 2, 8 * 16 + 2, 512),
     ("jpeg-i8-f16-tail-only", dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8), "f16", 2, 2, 4, 5, 128),
@@ -405,7 +407,11 @@ STEP_PAIRS = [
     (dict(mode="png", block_size=4, keep_ratio=1.0), "f32", 128, 2, True),
     (dict(mode="png", block_size=16, keep_ratio=0.25), "f32", 128, 8, True),
     (dict(mode="png", block_size=8, keep_ratio=0.3), "f32", 64, 16, True),
-    (dict(mode="png", block_size=4, keep_ratio=1.0), "bf16", 64, 4, False),
+    # fp16 / bf16 png (16-bit anchors and tails, fp32 deltas): the same launch
+    (dict(mode="png", block_size=16, keep_ratio=0.25), "bf16", 128, 4, True),
+    (dict(mode="png", block_size=8, keep_ratio=0.5), "f16", 128, 2, True),
+    (dict(mode="png", block_size=16, keep_ratio=1.0), "f16", 64, 8, True),
+    (dict(mode="png", block_size=4, keep_ratio=1.0), "bf16", 64, 4, True),
     # the C5 instantiation (D=128, bf16, k=4, G=2), other row counts and widths
     (I8, "bf16", 128, 2, True),
     (dict(I8, keep_freqs=3), "f16", 128, 4, True),

@@ -73,18 +73,19 @@ def test_c5_attention_instantiation(oracle):
     assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "bf16")
 
 
-@pytest.mark.parametrize("keep", [0.25, 1.0])
-def test_c4_png_full_shape(keep, oracle):
+@pytest.mark.parametrize("dt,keep", [("f32", 0.25), ("f32", 1.0), ("bf16", 0.25)])
+def test_c4_png_full_shape(dt, keep, oracle):
     """BASELINE C4: png fp32 (2, 8, 16384, 128), r=16, keep_ratio 0.25 and
-    1.0, decode attention with 32 q heads (fp32 queries: 1e-5 absolute)."""
+    1.0, decode attention with 32 q heads (fp32 queries: 1e-5 absolute); and
+    the same shape as a bf16 stream (bf16 anchors and queries, fp32 deltas)."""
     B, Hkv, G, D, S = 2, 8, 4, 128, 16384
-    print(f"case c4 png keep={keep}", flush=True)
+    print(f"case c4 png keep={keep} {dt}", flush=True)
     cfg = dict(mode="png", block_size=16, keep_ratio=keep)
-    ks, vs = build_streams(cfg, "f32", B, Hkv, S, D, 404, oracle)
+    ks, vs = build_streams(cfg, dt, B, Hkv, S, D, 404, oracle)
     assert ks.n_blocks == 1024 and ks.raw is None
-    q = queries(B, Hkv * G, D, 405, "f32")
+    q = queries(B, Hkv * G, D, 405, dt)
     out = fc.codec_decode_attention(q, ks, vs)
-    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), "f32")
+    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), dt)
 
 
 @pytest.mark.parametrize("dt,G,D", [("f16", 4, 128), ("bf16", 2, 128), ("f16", 8, 64),
@@ -328,16 +329,17 @@ def test_graph_replayed_steps_c5_scale(cfg, kind, oracle):
                  oracle, check_archive=True, single_launch=True)
 
 
-@pytest.mark.parametrize("keep", [0.25, 1.0])
-def test_graph_replayed_steps_c4_scale(keep, oracle):
-    """Graph-replayed one-launch png steps at C4's geometry (fp32, batch 2,
-    32 q / 8 kv heads, D=128, r=16; 1024 archived blocks + 5 tail tokens: the
-    png pass's 32 splits): 14 replays across a block boundary, every sequence
-    of every replay against the fp64 oracle, and the anchors and deltas the
-    replays wrote against the two-append path's, bit for bit."""
+@pytest.mark.parametrize("dt,keep", [("f32", 0.25), ("f32", 1.0), ("bf16", 0.25)])
+def test_graph_replayed_steps_c4_scale(dt, keep, oracle):
+    """Graph-replayed one-launch png steps at C4's geometry (fp32 as C4, and
+    bf16; batch 2, 32 q / 8 kv heads, D=128, r=16; 1024 archived blocks + 5
+    tail tokens: the png pass's 32 splits): 14 replays across a block
+    boundary, every sequence of every replay against the fp64 oracle, and
+    the anchors and deltas the replays wrote against the two-append path's,
+    bit for bit."""
     cfg = dict(mode="png", block_size=16, keep_ratio=keep)
-    print(f"case graph step at C4 scale {cfg}", flush=True)
-    _graph_steps(cfg, "f32", 2, 8, 4, 128, 1024 * 16 + 5, 14, 161, oracle, check_archive=True,
+    print(f"case graph step at C4 scale {cfg} {dt}", flush=True)
+    _graph_steps(cfg, dt, 2, 8, 4, 128, 1024 * 16 + 5, 14, 161, oracle, check_archive=True,
                  single_launch=True)
 
 
