@@ -276,6 +276,49 @@ def c2_mode(args):
         "data": "synthetic AR(1) rho=0.95, per-channel scale log-uniform [0.1, 10]"}))
 
 
+def step_timing(q, ks, vs, r, steps, warmup, g):
+    """Decode steps on copies of the streams ks / vs: codec_decode_step
+    (token append, the block archived every r-th step, attention; one launch
+    where the store kind allows) against the reference's step (two appends,
+    then the attention), each after 1024 untimed steps; room for every call
+    reserved first, so no call regrows the archives.  us per step, and
+    whether the step ran as one launch."""
+    import torch
+    import flashcodec_amd as fc
+    from flashcodec_amd import _native as N
+    B, H, D = ks._raw_buf.shape[0], ks._raw_buf.shape[1], q.shape[-1]
+    kt = torch.randn((B, H, 1, D), generator=g, device=q.device).to(q.dtype)
+    vt = torch.randn((B, H, 1, D), generator=g, device=q.device).to(q.dtype)
+    n_pre = 1024
+    out = {}
+    for name in ("step", "append_attend"):
+        sk, sv = archive_copy(ks), archive_copy(vs)
+        for st_ in (sk, sv):
+            st_._grow(st_.n_blocks + (n_pre + warmup + steps) // r + 2, kt)
+        if name == "step":
+            def fn():
+                return fc.codec_decode_step(q, kt, vt, sk, sv)
+        else:
+            def fn():
+                sk.append(kt)
+                sv.append(vt)
+                return fc.codec_decode_attention(q, sk, sv)
+        for _ in range(n_pre + warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[f"{name}_us"] = round(e0.elapsed_time(e1) / steps * 1e3, 2)
+        if name == "step":
+            out["step_single_launch"] = N.lib().fc_last_step_single_launch() == 1
+        del sk, sv, fn
+    return out
+
+
 def c4_mode(args):
     """png mode on fp32 KV (B=2, H=8, S=16384, D=128),
     AR(1) rho=0.98, r=16, keep_ratio 0.25 (4 of 15 deltas) and 1.0.  Bulk
@@ -365,39 +408,7 @@ def c4_mode(args):
                       "head) sequences (16384 tokens, 4 query heads); the reference's torch CPU "
                       "path (restated in oracle/torch_path.py), median of >= 5 calls",
             "archive": arch_gbs, "read": read_gbs, "attention": attn_gbs}
-        # decode steps on copies of the archives: codec_decode_step (token
-        # append, the block archived every r-th step, attention) against the
-        # reference's step (two appends, then the attention); room for every
-        # call reserved first, so no call regrows the archives
-        from flashcodec_amd import _native as N
-        kt = torch.randn((b_, h_, 1, d_), generator=g, device=dev)
-        vt = torch.randn((b_, h_, 1, d_), generator=g, device=dev)
-        n_pre = 1024
-        for name in ("step", "append_attend"):
-            sk, sv = archive_copy(ks), archive_copy(vs)
-            for st_ in (sk, sv):
-                st_._grow(st_.n_blocks + (n_pre + args.warmup + args.steps) // r + 2, kt)
-            if name == "step":
-                def fn():
-                    return fc.codec_decode_step(q, kt, vt, sk, sv)
-            else:
-                def fn():
-                    sk.append(kt)
-                    sv.append(vt)
-                    return fc.codec_decode_attention(q, sk, sv)
-            for _ in range(n_pre + args.warmup):
-                fn()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(args.steps):
-                fn()
-            e1.record()
-            torch.cuda.synchronize()
-            res[tag][f"{name}_us"] = round(e0.elapsed_time(e1) / args.steps * 1e3, 2)
-            if name == "step":
-                res[tag]["step_single_launch"] = N.lib().fc_last_step_single_launch() == 1
-            del sk, sv, fn
+        res[tag].update(step_timing(q, ks, vs, r, args.steps, args.warmup, g))
         torch.cuda.empty_cache()
         log(f"bench c4 keep {keep}: {res[tag]}")
 
@@ -431,6 +442,7 @@ def c4_mode(args):
                             args.warmup)
         del sets
         torch.cuda.empty_cache()
+        steps_pk = step_timing(q, ks, vs, r, args.steps, args.warmup, g)
         res[f"packed_keep{keep}"] = {
             "kept_deltas": m_keep, "store_bytes_per_stream": store,
             "dense_store_bytes_per_stream": b_ * h_ * nb * d_ * 4 * r,
@@ -443,7 +455,8 @@ def c4_mode(args):
             "archive_us": round(t_arch * 1e3, 2), "read_us": round(t_read * 1e3, 2),
             "attention_us": round(t_attn * 1e3, 2), "attention_rotating_us": round(t_rot * 1e3, 2),
             "algorithmic_bytes_attention": alg_pk_attn,
-            "cpu_baseline": "the reference stores these deltas dense: see keep0.25 (same rows)"}
+            "cpu_baseline": "the reference stores these deltas dense: see keep0.25 (same rows)",
+            **steps_pk}
         log(f"bench c4 packed keep {keep}: {res[f'packed_keep{keep}']}")
 
     # the same shape as a bf16 / fp16 stream (16-bit anchors and queries, fp32

@@ -38,7 +38,7 @@
 #pragma once
 
 #include "fc_attn_mfma_kernel.h"
-#include "fc_topm.h"
+#include "fc_png_step.h"
 
 namespace fc {
 
@@ -58,124 +58,12 @@ __device__ __forceinline__ float4_t half4_to_f32(u32x2_t w) {
 
 constexpr int kPngTile = 16;  // rows per pass
 
-// Fused decode step on a png archive, split 0 (stream dtype T, the queries'
-// too): the rows this step adds to the attention, in LDS as fp32 (xk, xv: n
-// rows of D), and the partial of the group's G heads over them (as
-// raw_tail_partial_t: tm, tl, acc).
-//   * t + 1 < R: the tail rows 0..t-1 and the new token; the token is
-//     written to tail row t.
-//   * t + 1 == R: the block of tail rows 0..R-2 and the new token is
-//     archived as png_encode_kernel does (anchor = token 0 in T, fp32
-//     deltas x_{i+1} - x_i, the keep_m largest |delta| kept by the same Top-M mask
-//     and the others multiplied by 0), stored when `write`, and attended as
-//     png_decode_kernel reconstructs it (anchor + the fp64 running sum of the
-//     deltas, rounded to fp32).
-// The query rows are q + qb + (h0 + h) * q_sh for the G heads.
-template <int D, int R, typename T>
-__device__ __forceinline__ void png_step_partial(
-    int64_t t, T* ktail, T* vtail, const T* ktok, const T* vtok, bool write,
-    T* kanch, float* kdel, T* vanch, float* vdel, int keep_m, const T* q, int64_t qb,
-    int64_t q_sh, int64_t h0, int G, float scale_log2, int tid, float* xk, float* xv, float* etl,
-    float* acc, float* tm, float* tl) {
-  const int lane = tid & 63, wave = tid >> 6;
-  const bool complete = t + 1 == R;
-  const int n = complete ? R : (int)t + 1;
-  for (int x = tid; x < n * D; x += kMThreads) {
-    const int i = x / D, d = x - i * D;
-    xk[x] = to_f32(i < t ? ktail[i * D + d] : ktok[d]);
-    xv[x] = to_f32(i < t ? vtail[i * D + d] : vtok[d]);
-  }
-  if (write && !complete)
-    for (int d = tid; d < D; d += kMThreads) {
-      ktail[t * D + d] = ktok[d];
-      vtail[t * D + d] = vtok[d];
-    }
-  __syncthreads();
-  if (complete) {
-    // one (stream, feature) per thread
-    for (int x = tid; x < 2 * D; x += kMThreads) {
-      const int sv = x / D, d = x - sv * D;
-      float* xs = sv ? xv : xk;
-      T* anch = sv ? vanch : kanch;
-      float* del = sv ? vdel : kdel;
-      float dl[R];
-#pragma unroll
-      for (int i = 0; i + 1 < R; ++i) dl[i] = xs[(i + 1) * D + d] - xs[i * D + d];
-      dl[R - 1] = 0.f;
-      constexpr int n1 = R - 1;
-      if (keep_m > 0 && keep_m < n1) {
-        uint32_t key[R];
-#pragma unroll
-        for (int i = 0; i < R; ++i) key[i] = i < n1 ? topm_key(__float_as_uint(dl[i])) : 0u;
-        const uint64_t mask = topm_mask<R>(key, n1, keep_m);
-#pragma unroll
-        for (int i = 0; i + 1 < R; ++i)
-          if (!((mask >> i) & 1)) dl[i] = dl[i] * 0.0f;
-      }
-      const float a = xs[d];
-      if (write) {
-        anch[d] = from_f32<T>(a);  // token 0 itself (a holds a value of T)
-#pragma unroll
-        for (int i = 0; i + 1 < R; ++i) del[i * D + d] = dl[i];
-      }
-      double run = 0.0;
-#pragma unroll
-      for (int i = 0; i + 1 < R; ++i) {
-        run += (double)dl[i];
-        xs[(i + 1) * D + d] = a + (float)run;
-      }
-    }
-    __syncthreads();
-  }
-  // the partial over the n rows, at full precision
-  {
-    const int grp = tid >> 4, gl = tid & 15;
-    for (int u = grp; u < G * n; u += kMThreads / 16) {
-      const int h = u / n, i = u - h * n;
-      const T* qr = q + qb + (h0 + h) * q_sh + gl;
-      float a = 0.f;
-      for (int c = 0; c < D / 16; ++c)
-        a = __builtin_fmaf(to_f32(qr[16 * c]), xk[i * D + gl + 16 * c], a);
-#pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) a += __shfl_xor(a, m, 16);
-      if (gl == 0) etl[h * FC_MAX_BLOCK + i] = a * scale_log2;
-    }
-  }
-  __syncthreads();
-  for (int h = wave; h < G; h += kWaves) {
-    float mx = -INFINITY;
-    for (int i = lane; i < n; i += 64) mx = fmaxf(mx, etl[h * FC_MAX_BLOCK + i]);
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-    float l = 0.f;
-    for (int i = lane; i < n; i += 64) {
-      const float e = __builtin_amdgcn_exp2f(etl[h * FC_MAX_BLOCK + i] - mx);
-      etl[h * FC_MAX_BLOCK + i] = e;
-      l += e;
-    }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) l += __shfl_xor(l, m, 64);
-    if (lane == 0) {
-      tm[h] = mx;
-      tl[h] = l;
-    }
-  }
-  __syncthreads();
-  for (int x = tid; x < G * D; x += kMThreads) {
-    const int h = x / D, d = x - h * D;
-    float o = 0.f;
-    for (int i = 0; i < n; ++i) o = __builtin_fmaf(etl[h * FC_MAX_BLOCK + i], xv[i * D + d], o);
-    acc[h * D + d] = o;
-  }
-}
-
-
 // kPngWgPerCu (2) workgroups per compute unit: measured at C4, 2 per CU
 // (32 splits) take 59.2 us per call over rotating archive sets where 3 per
 // CU (48 splits, the query operands read from LDS to fit 168 VGPRs) take
 // 64.6 (more partials to merge, more contention on the pass queues).
 // STEP: the fused decode step (fc_decode_step; MfmaArgs.step): split 0
-// appends the token or archives the block it completes (png_step_partial)
+// appends the token or archives the block it completes (png_step_rows)
 // and the passes cover the blocks before it.  T: the stream dtype (anchors,
 // tails, tokens) and the queries' (float, f16_t, bf16_t); deltas are fp32
 // and products fp32 for all.
@@ -409,17 +297,21 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     if (split == 0) {
       const int64_t bh_s = b * p.Hkv + hkv;
       float* xk = cbuf_raw;  // the passes have not started: the end-phase buffer is free
-      png_step_partial<D, R>(
-          step_t, static_cast<T*>(const_cast<void*>(p.kraw)) + bh_s * R * D,
+      const PngStepDst kd{static_cast<T*>(const_cast<void*>(p.kanch)) + (bh_s * p.kcap + step_nb) * D,
+                          const_cast<float*>(p.kdel) + (bh_s * p.kcap + step_nb) * (R - 1) * D,
+                          nullptr};
+      const PngStepDst vd{static_cast<T*>(const_cast<void*>(p.vanch)) + (bh_s * p.vcap + step_nb) * D,
+                          const_cast<float*>(p.vdel) + (bh_s * p.vcap + step_nb) * (R - 1) * D,
+                          nullptr};
+      const int n = png_step_rows<D, R, T, false>(
+          step_t, R, static_cast<T*>(const_cast<void*>(p.kraw)) + bh_s * R * D,
           static_cast<T*>(const_cast<void*>(p.vraw)) + bh_s * R * D,
           static_cast<const T*>(p.ktok) + b * p.kt_sb + hkv * p.kt_sh,
-          static_cast<const T*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write,
-          static_cast<T*>(const_cast<void*>(p.kanch)) + (bh_s * p.kcap + step_nb) * D,
-          const_cast<float*>(p.kdel) + (bh_s * p.kcap + step_nb) * (R - 1) * D,
-          static_cast<T*>(const_cast<void*>(p.vanch)) + (bh_s * p.vcap + step_nb) * D,
-          const_cast<float*>(p.vdel) + (bh_s * p.vcap + step_nb) * (R - 1) * D, p.keep_m,
-          static_cast<const T*>(p.q), b * p.q_sb, p.q_sh, hkv * p.G + g0, G, p.scale_log2,
-          tid, xk, xk + R * D, scratch, part_lds, tail_ml[0], tail_ml[1]);
+          static_cast<const T*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write, kd, vd,
+          p.keep_m, tid, xk, xk + R * D);
+      png_step_attend<D, T>(n, static_cast<const T*>(p.q), b * p.q_sb, p.q_sh, hkv * p.G + g0, G,
+                            p.scale_log2, tid, xk, xk + R * D, scratch, part_lds, tail_ml[0],
+                            tail_ml[1]);
     }
   } else if (fold_tail) {
     raw_tail_partial<D, F32>(p, b, hkv, g0, G, (int)n_raw, tid, scratch, part_lds, tail_ml[0],

@@ -35,6 +35,7 @@
 #pragma once
 
 #include "fc_attn_mfma_kernel.h"
+#include "fc_png_step.h"
 
 namespace fc {
 
@@ -178,8 +179,11 @@ struct PkData {
 
 // RB: block size bucket (r <= RB), D: head size, GP: heads per workgroup
 // (>= G), MB: value slots bucket (keep_m <= MB), QF32: fp32 queries (else
-// fp16 / bf16, outputs in the query dtype).
-template <int RB, int D, int GP, int MB, bool QF32>
+// fp16 / bf16, outputs in the query dtype).  STEP: the fused decode step
+// (fc_decode_step; MfmaArgs.step): split 0 appends the token or archives
+// the block it completes in the packed layout (png_step_rows) and attends
+// the step's rows, the iterations cover the blocks before it.
+template <int RB, int D, int GP, int MB, bool QF32, bool STEP = false>
 __global__ __launch_bounds__(kMThreads, GP <= 4 ? 2 : 1) void attn_split_pngpk(MfmaArgs p) {
   constexpr int F = kPkF;
   constexpr int LB = D / F;            // lanes per block
@@ -191,7 +195,8 @@ __global__ __launch_bounds__(kMThreads, GP <= 4 ? 2 : 1) void attn_split_pngpk(M
   constexpr int GL = RB / NB;          // lanes of one head's steps after the reduce-scatter
   constexpr int kW = kWaves * NB * RB * GP;  // weights [wave][blk][step][head]
   constexpr int kC = kWaves * GP * D;        // end phase: cbuf [wave][head][feature]
-  constexpr int kBig = kW > kC ? kW : kC;
+  constexpr int kBig0 = kW > kC ? kW : kC;
+  constexpr int kBig = STEP && 2 * RB * D > kBig0 ? 2 * RB * D : kBig0;  // STEP: the step's rows
   __shared__ __attribute__((aligned(16))) float big[kBig];
   __shared__ float comb[kWaves][16][3];
   __shared__ __attribute__((aligned(16))) float part_lds[16 * D];
@@ -199,6 +204,7 @@ __global__ __launch_bounds__(kMThreads, GP <= 4 ? 2 : 1) void attn_split_pngpk(M
   __shared__ float wg_ml[2][16];
   __shared__ float scratch[2 * 16 * kFuseMaxSplits];  // raw-tail logits, then merge statistics
   __shared__ int s_last;
+  __shared__ int s_final;
 
   // 1-D grid, split-major with a per-split rotation, as the other passes
   const int64_t L = blockIdx.x;
@@ -215,7 +221,18 @@ __global__ __launch_bounds__(kMThreads, GP <= 4 ? 2 : 1) void attn_split_pngpk(M
   const bool a32 = adt == FC_F32;
 
   int64_t nb = p.nb, n_raw = p.n_raw;
-  if (p.state) {
+  int64_t step_t = 0, step_nb = 0;  // fused step: tail length and blocks before the token
+  bool step_write = false;
+  if constexpr (STEP) {
+    const int64_t cap = min(p.kcap, p.vcap);
+    step_t = p.state ? min<int64_t>(max<int64_t>(p.state[1], 0), r - 1) : p.step_t;
+    step_nb = p.state ? max<int64_t>(p.state[0], 0) : p.step_nb;
+    // one head group per (batch, kv head) stores the token / block; a block
+    // past the capacity is not stored (the state's overflow word says so)
+    step_write = split == 0 && g0 == 0 && (step_t + 1 < r || step_nb < cap);
+    nb = min(step_nb, cap);
+    n_raw = 0;
+  } else if (p.state) {
     // counts of a decode step's view on the device (graph replays)
     const int64_t t = min<int64_t>(max<int64_t>(p.state[1], 0), r - 1) + 1;
     nb = min<int64_t>(max<int64_t>(p.state[0], 0) + (t == r ? 1 : 0), min(p.kcap, p.vcap));
@@ -295,11 +312,54 @@ __global__ __launch_bounds__(kMThreads, GP <= 4 ? 2 : 1) void attn_split_pngpk(M
     load_blk(p.vanch, p.vdel, vmask, vblk0, it, vd);
   }
 
-  // raw tail (fused calls): split 0 computes its partial before the passes
-  const bool fold_tail = p.fused && split == 0 && n_raw > 0;
-  if (fold_tail)
+  // raw tail (fused calls): split 0 computes its partial before the passes;
+  // in a fused step that partial covers the rows the step adds
+  const bool fold_tail = p.fused && split == 0 && (STEP || n_raw > 0);
+  if constexpr (STEP) {
+    if (split == 0) {
+      const int64_t bh_s = b * p.Hkv + hkv;
+      const int64_t kslot = bh_s * p.kcap + step_nb, vslot = bh_s * p.vcap + step_nb;
+      float* xk = big;  // the iterations have not started: their weight buffer is free
+      float* xv = big + RB * D;
+      const int64_t qb = b * p.q_sb, h0 = hkv * p.G + g0;
+      auto go = [&](auto tt) {
+        using T = decltype(tt);
+        const PngStepDst kdst{static_cast<T*>(const_cast<void*>(p.kanch)) + kslot * D,
+                            const_cast<float*>(p.kdel) + kslot * km * D,
+                            const_cast<uint32_t*>(kmask) + kslot * D};
+        const PngStepDst vdst{static_cast<T*>(const_cast<void*>(p.vanch)) + vslot * D,
+                            const_cast<float*>(p.vdel) + vslot * km * D,
+                            const_cast<uint32_t*>(vmask) + vslot * D};
+        const int n = png_step_rows<D, RB, T, true>(
+            step_t, r, static_cast<T*>(const_cast<void*>(p.kraw)) + bh_s * r * D,
+            static_cast<T*>(const_cast<void*>(p.vraw)) + bh_s * r * D,
+            static_cast<const T*>(p.ktok) + b * p.kt_sb + hkv * p.kt_sh,
+            static_cast<const T*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write, kdst, vdst, km,
+            tid, xk, xv);
+        if constexpr (QF32)
+          png_step_attend<D, float>(n, static_cast<const float*>(p.q), qb, p.q_sh, h0, G,
+                                    p.scale_log2, tid, xk, xv, scratch, part_lds, tail_ml[0],
+                                    tail_ml[1]);
+        else if (p.q_dtype == FC_F16)
+          png_step_attend<D, f16_t>(n, static_cast<const f16_t*>(p.q), qb, p.q_sh, h0, G,
+                                    p.scale_log2, tid, xk, xv, scratch, part_lds, tail_ml[0],
+                                    tail_ml[1]);
+        else
+          png_step_attend<D, bf16_t>(n, static_cast<const bf16_t*>(p.q), qb, p.q_sh, h0, G,
+                                     p.scale_log2, tid, xk, xv, scratch, part_lds, tail_ml[0],
+                                     tail_ml[1]);
+      };
+      if (adt == FC_F16)
+        go(f16_t{});
+      else if (adt == FC_BF16)
+        go(bf16_t{});
+      else
+        go(float{});
+    }
+  } else if (fold_tail) {
     raw_tail_partial<D, QF32>(p, b, hkv, g0, G, (int)n_raw, tid, scratch, part_lds, tail_ml[0],
                               tail_ml[1]);
+  }
   __syncthreads();
 
   const float sl2 = p.scale_log2;
@@ -501,10 +561,27 @@ __global__ __launch_bounds__(kMThreads, GP <= 4 ? 2 : 1) void attn_split_pngpk(M
       *reinterpret_cast<float4_t*>(&cbuf[wave][h][f0]) =
           (float4_t){acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
   }
-  auto no_step = [] {};
-  split_epilogue<D, GP, QF32, false, decltype(no_step)&, 32>(
+  // fused step with a device state: the launch's last workgroup to finish
+  // (all others have read the state by then) advances it
+  auto step_done = [&]() {
+    if constexpr (!STEP) return;
+    if (!p.state) return;
+    if (tid == 0) s_final = atomicAdd(p.done, 1u) + 1 == gridDim.x ? 1 : 0;
+    __syncthreads();
+    if (s_final && tid < 64) {  // lane-indexed vector stores
+      const int64_t cap = min(p.kcap, p.vcap);
+      const bool full = step_t + 1 == r;
+      const bool over = full && step_nb >= cap;
+      const int64_t word = tid == 0   ? (full ? step_nb + 1 : step_nb)
+                           : tid == 1 ? (full ? 0 : step_t + 1)
+                                      : ((p.state[2] != 0 || over) ? 1 : 0);
+      if (tid < 3) const_cast<int64_t*>(p.state)[tid] = word;
+      if (tid == 0) __hip_atomic_store(p.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+  split_epilogue<D, GP, QF32, false, decltype(step_done)&, 32>(
       p, g, b, hkv, g0, G, split, tid, fold_tail, comb, cbuf, part_lds, tail_ml, wg_ml, scratch,
-      s_last, passq, no_step);
+      s_last, passq, step_done);
 }
 
 }  // namespace pngpk
@@ -518,7 +595,11 @@ int launch_pngpk_rows(const MfmaArgs& a, int D, int gp, bool qf32, dim3 grid, hi
     constexpr int Dv = decltype(dc)::value;
     return mfma_with_int<4, 16>(gp, [&](auto gc) {
       constexpr int GPv = decltype(gc)::value;
-      if (qf32)
+      if (a.step && qf32)
+        pngpk::attn_split_pngpk<RB, Dv, GPv, MB, true, true><<<grid, kMThreads, 0, st>>>(a);
+      else if (a.step)
+        pngpk::attn_split_pngpk<RB, Dv, GPv, MB, false, true><<<grid, kMThreads, 0, st>>>(a);
+      else if (qf32)
         pngpk::attn_split_pngpk<RB, Dv, GPv, MB, true><<<grid, kMThreads, 0, st>>>(a);
       else
         pngpk::attn_split_pngpk<RB, Dv, GPv, MB, false><<<grid, kMThreads, 0, st>>>(a);

@@ -68,6 +68,19 @@ int launch_split_pngpk(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, i
     a.out = fuse->out;
     a.o_sb = fuse->o_sb;
     a.o_sh = fuse->o_sh;
+    if (fuse->step) {
+      a.step = 1;
+      a.ktok = fuse->ktok;
+      a.vtok = fuse->vtok;
+      a.kt_sb = fuse->kt_sb;
+      a.kt_sh = fuse->kt_sh;
+      a.vt_sb = fuse->vt_sb;
+      a.vt_sh = fuse->vt_sh;
+      a.step_t = fuse->step_t;
+      a.step_nb = fuse->step_nb;
+      a.done = fuse->done;
+      if (!fuse->done) return FC_ERR_ARG;
+    }
   }
   const int64_t G = Hq / Hkv;
   a.zg = (int)((G + 15) / 16);

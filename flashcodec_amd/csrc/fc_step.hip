@@ -69,11 +69,12 @@ __global__ void state_advance_kernel(int64_t* state, int64_t r, int64_t cap) {
 static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   const bool grouped = a->store_kind == FC_STORE_JPEG_I8G;
   const bool fp = a->store_kind == FC_STORE_JPEG_FP;  // fp16 / bf16 coefficient rows
-  const bool png = a->store_kind == FC_STORE_PNG;     // fp32 anchors and deltas
+  const bool png = a->store_kind == FC_STORE_PNG;     // anchors and fp32 deltas
+  const bool pk = a->store_kind == FC_STORE_PNG_PACKED;  // anchors, kept values, masks
   // (fp32 queries: int8 archives; fp coefficient rows need queries in their
   // own dtype, which split_fpj_mfma_supported checks)
-  if ((a->store_kind != FC_STORE_JPEG_I8 && !grouped && !fp && !png) ||
-      (!fp && !png && a->quant_bits != 8) || !mfma_split_allowed())
+  if ((a->store_kind != FC_STORE_JPEG_I8 && !grouped && !fp && !png && !pk) ||
+      (!fp && !png && !pk && a->quant_bits != 8) || !mfma_split_allowed())
     return FC_ERR_UNSUPPORTED;
   const int64_t B = a->B, Hq = a->Hq, Hkv = a->Hkv, D = a->D;
   const int r = a->r;
@@ -85,15 +86,18 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   for (int i = 0; i < 2; ++i) {
     v[i].rows = st[i]->rows;
     v[i].scales = st[i]->scales;
-    v[i].anchors = png ? st[i]->anchors : nullptr;
+    v[i].anchors = png || pk ? st[i]->anchors : nullptr;
+    v[i].masks = pk ? st[i]->masks : nullptr;
     v[i].cap = st[i]->cap;
     v[i].raw = st[i]->tail;
     v[i].raw_sb = Hkv * r * D;
     v[i].raw_sh = (int64_t)r * D;
     v[i].raw_st = D;
   }
-  if (png ? !split_png_mfma_supported(a->q, a->q_dtype, a->q_sb, a->q_sh, D, r,
-                                      a->stream_dtype, &v[0], &v[1])
+  if (pk ? !split_pngpk_supported(a->q, a->q_dtype, a->q_sb, a->q_sh, D, r, a->keep_m,
+                                  a->stream_dtype, &v[0], &v[1])
+      : png ? !split_png_mfma_supported(a->q, a->q_dtype, a->q_sb, a->q_sh, D, r,
+                                        a->stream_dtype, &v[0], &v[1])
       : fp ? !split_fpj_mfma_supported(a->q, a->q_dtype, a->q_sb, a->q_sh, D, a->s,
                                        a->stream_dtype, &v[0], &v[1])
            : !i8_mfma_takes(a->store_kind, a->q, a->q_dtype, a->q_sb, a->q_sh, D, a->s, &v[0],
@@ -103,9 +107,11 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   if (mstride == 0) return FC_ERR_UNSUPPORTED;
   const int n_splits = fc_attention_splits(a->store_kind, a->stream_dtype, a->q_dtype, a->s, nb,
                                            B, Hkv, G, D, a->n_cu);
-  // (the png pass holds the step's rows in its own LDS buffer)
-  if (n_splits < 1 || (png ? !split_i8_mfma_fusable(n_splits)
-                           : !step_i8_mfma_supported(a->stream_dtype, r, D, n_splits)))
+  // (the png passes hold the step's rows in LDS buffers of their own)
+  if (n_splits < 1 ||
+      (pk    ? n_splits > kFuseMaxSplitsPk
+       : png ? !split_i8_mfma_fusable(n_splits)
+             : !step_i8_mfma_supported(a->stream_dtype, r, D, n_splits)))
     return FC_ERR_UNSUPPORTED;
   if (!a->workspace || fc_attention_workspace_bytes(B, Hq, D, n_splits) > a->workspace_bytes)
     return FC_ERR_ARG;
@@ -129,6 +135,11 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   fz.step_nb = a->n_blocks;
   fz.done = ws.done;
   fz.keep_m = a->keep_m;
+  if (pk)
+    return launch_split_pngpk(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, r, a->keep_m,
+                              a->stream_dtype, nb, &v[0], &v[1], a->scale * 1.4426950408889634f,
+                              ws.pm, ws.pl, ws.pacc, n_splits, ws.counters, kCounterWords,
+                              mstride, &fz, state, (hipStream_t)a->stream);
   if (png)
     return launch_split_png_mfma(a->q, a->q_dtype, a->q_sb, a->q_sh, B, Hq, Hkv, D, r, nb,
                                  &v[0], &v[1],

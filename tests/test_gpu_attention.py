@@ -426,7 +426,11 @@ STEP_PAIRS = [
     (dict(I8, quant_group=32, keep_freqs=2), "bf16", 64, 1, True),
     (dict(I8, quant_group=32, keep_freqs=1), "f16", 256, 8, True),
     (dict(I8, quant_group=32, block_size=16, keep_freqs=3), "bf16", 128, 16, True),
-    (dict(mode="png", block_size=8, keep_ratio=0.5, packed=True), "f32", 64, 4, False),
+    # packed Top-M png: one launch that archives the packed block in-kernel
+    (dict(mode="png", block_size=8, keep_ratio=0.5, packed=True), "f32", 64, 4, True),
+    (dict(mode="png", block_size=16, keep_ratio=0.25, packed=True), "bf16", 128, 4, True),
+    (dict(mode="png", block_size=4, keep_ratio=0.67, packed=True), "f16", 256, 16, True),
+    (dict(mode="png", block_size=8, keep_ratio=0.75, packed=True), "f32", 128, 2, True),
     # fp32 queries and stream (an fp32 model): one launch, fp32 rows archived
     # in-kernel
     (I8, "f32", 128, 2, True),

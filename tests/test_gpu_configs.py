@@ -329,15 +329,16 @@ def test_graph_replayed_steps_c5_scale(cfg, kind, oracle):
                  oracle, check_archive=True, single_launch=True)
 
 
-@pytest.mark.parametrize("dt,keep", [("f32", 0.25), ("f32", 1.0), ("bf16", 0.25)])
-def test_graph_replayed_steps_c4_scale(dt, keep, oracle):
+@pytest.mark.parametrize("dt,keep,packed", [("f32", 0.25, False), ("f32", 1.0, False),
+                                            ("bf16", 0.25, False), ("f32", 0.25, True)])
+def test_graph_replayed_steps_c4_scale(dt, keep, packed, oracle):
     """Graph-replayed one-launch png steps at C4's geometry (fp32 as C4, and
     bf16; batch 2, 32 q / 8 kv heads, D=128, r=16; 1024 archived blocks + 5
     tail tokens: the png pass's 32 splits): 14 replays across a block
     boundary, every sequence of every replay against the fp64 oracle, and
     the anchors and deltas the replays wrote against the two-append path's,
-    bit for bit."""
-    cfg = dict(mode="png", block_size=16, keep_ratio=keep)
+    bit for bit; and the packed Top-M archive at keep 0.25."""
+    cfg = dict(mode="png", block_size=16, keep_ratio=keep, packed=packed)
     print(f"case graph step at C4 scale {cfg} {dt}", flush=True)
     _graph_steps(cfg, dt, 2, 8, 4, 128, 1024 * 16 + 5, 14, 161, oracle, check_archive=True,
                  single_launch=True)
