@@ -431,6 +431,10 @@ STEP_PAIRS = [
     (dict(mode="png", block_size=16, keep_ratio=0.25, packed=True), "bf16", 128, 4, True),
     (dict(mode="png", block_size=4, keep_ratio=0.67, packed=True), "f16", 256, 16, True),
     (dict(mode="png", block_size=8, keep_ratio=0.75, packed=True), "f32", 128, 2, True),
+    # more than 16 query heads per kv head: two head groups, one of them stores
+    (I8, "f16", 128, 20, True),
+    (dict(mode="png", block_size=8, keep_ratio=0.5), "f32", 64, 20, True),
+    (dict(mode="png", block_size=8, keep_ratio=0.5, packed=True), "bf16", 64, 24, True),
     # fp32 queries and stream (an fp32 model): one launch, fp32 rows archived
     # in-kernel
     (I8, "f32", 128, 2, True),

@@ -396,20 +396,29 @@ def _graph_steps(cfg, dt, B, Hkv, G, D, S0, steps, seed, oracle, check_archive=F
     graph.release(cache)                      # device counters == host counters, no overflow
 
 
-def test_graph_step_past_reserved_capacity_is_reported(oracle):
+@pytest.mark.parametrize("cfg,dt", [(I8_C3, "f16"),
+                                    (dict(mode="png", block_size=8, keep_ratio=0.5), "f32"),
+                                    (dict(mode="png", block_size=8, keep_ratio=1.0), "bf16"),
+                                    (dict(mode="png", block_size=8, keep_ratio=0.5, packed=True),
+                                     "bf16")],
+                         ids=["i8", "png-f32", "png-bf16", "pngpk-bf16"])
+def test_graph_step_past_reserved_capacity_is_reported(cfg, dt, oracle):
     """Device-state steps beyond the room prepare() reserved: the block that
-    does not fit is not archived, and release() reports it."""
+    does not fit is not archived (the one-launch steps gate their in-kernel
+    archive on the capacity), and release() reports it."""
     pytest.importorskip("transformers")
     from flashcodec_amd import graph
     B, Hkv, G, D, r = 1, 2, 2, 64, 8
-    ks, vs = build_streams(I8_C3, "f16", B, Hkv, 16 * r, D, 333, oracle)
+    print(f"case step past capacity {cfg} {dt}", flush=True)
+    ks, vs = build_streams(cfg, dt, B, Hkv, 16 * r, D, 333, oracle)
     assert ks.n_blocks == 16 and ks._capacity == 16
-    cache = _Cache([_codec_layer(I8_C3, ks, vs)])
+    cache = _Cache([_codec_layer(cfg, ks, vs)])
     graph.prepare(cache, 0)                   # room for one more block: 17 -> capacity 32
     g = torch.Generator(device=DEV).manual_seed(334)
     for _ in range(16 * r + 2 * r):           # 18 more blocks: two past the 32
-        fc.codec_decode_step(_tokens(g, B, Hkv * G, D, "f16"), _tokens(g, B, Hkv, D, "f16"),
-                             _tokens(g, B, Hkv, D, "f16"), ks, vs)
+        fc.codec_decode_step(_tokens(g, B, Hkv * G, D, dt), _tokens(g, B, Hkv, D, dt),
+                             _tokens(g, B, Hkv, D, dt), ks, vs)
+        assert N.lib().fc_last_step_single_launch() == 1
         graph.advance_host(cache)
     with pytest.raises(RuntimeError, match="capacity"):
         graph.release(cache)
