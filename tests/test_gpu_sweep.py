@@ -1,7 +1,9 @@
-"""GPU: seeded random sweeps over the png paths' shape space (dense and
-packed archives; fp32 / fp16 / bf16 streams; block sizes, keep ratios, head
-sizes, query heads per kv head, batch, tails), each case against the fp64
-oracle on the streams' rows, and decode steps against two appends.
+"""GPU: seeded random sweeps over the shape space of the png paths (dense
+and packed archives) and the jpeg paths (int8 with one scale per row or per
+32 features, unquantised coefficients): fp32 / fp16 / bf16 streams, block
+sizes, keep ratios / kept frequencies, head sizes, query heads per kv head,
+batch, tails; each case against the fp64 oracle on the streams' rows, and
+decode steps against two appends.
 
 The cases are drawn once from a fixed seed (the same list on every run), so
 a failure names a reproducible configuration.
@@ -14,7 +16,6 @@ import pytest
 import torch
 
 import flashcodec_amd as fc
-from flashcodec_amd import _native as N
 from tests.conftest import to_values, torch_dtype
 from tests.test_gpu_attention import (_archive_of, assert_close, assert_close_pair, build_streams,
                                       oracle_out)
@@ -60,14 +61,13 @@ def test_png_attention_sweep(case, oracle):
 STEPS = _draw(2026, 10, False) + _draw(2027, 8, True)
 
 
-@pytest.mark.parametrize("case", STEPS, ids=[f"s{i}" for i in range(len(STEPS))])
-def test_png_step_sweep(case, oracle):
+def _step_sweep(case, oracle):
     """r + 2 fused steps from a random archive state: archives, tails and
     counters equal two appends' bit for bit, outputs within the contract of
     the oracle and of codec_decode_attention after the appends."""
     cfg, dt, B, Hkv, G, S, D = case
     r = cfg["block_size"]
-    print(f"case png step sweep {case}", flush=True)
+    print(f"case step sweep {case}", flush=True)
     ks_f, vs_f = build_streams(cfg, dt, B, Hkv, S, D, 700 + S, oracle)
     ks_r, vs_r = build_streams(cfg, dt, B, Hkv, S, D, 700 + S, oracle)
     g = torch.Generator(device=DEV).manual_seed(S)
@@ -88,4 +88,54 @@ def test_png_step_sweep(case, oracle):
                 assert torch.equal(a.raw, b.raw)
         assert_close(to_values(out_f)[:, :, 0], oracle_out(oracle, q, ks_f, vs_f, D ** -0.5), dt)
         assert_close_pair(to_values(out_f), to_values(out_r), dt)
-    assert N.lib().fc_last_step_single_launch() in (0, 1)
+
+
+@pytest.mark.parametrize("case", STEPS, ids=[f"s{i}" for i in range(len(STEPS))])
+def test_png_step_sweep(case, oracle):
+    _step_sweep(case, oracle)
+
+
+def _draw_jpeg(seed, n):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        r = int(rng.choice([4, 8, 16]))
+        k = int(rng.integers(1, min(r, 8) + 1))
+        quant = int(rng.choice([8, 8, 0]))
+        dt = str(rng.choice(["f32", "f16", "bf16"]))
+        D = int(rng.choice([64, 80, 96, 128, 256]))
+        group = quant == 8 and D % 32 == 0 and bool(rng.integers(0, 2))
+        G = int(rng.choice([1, 2, 3, 4, 8, 16, 20]))
+        B = int(rng.integers(1, 4))
+        Hkv = int(rng.choice([1, 2, 4]))
+        S = int(rng.integers(1, 80)) * r + int(rng.integers(0, r))
+        cfg = dict(mode="jpeg", block_size=r, keep_freqs=k, quant_bits=quant)
+        if group:
+            cfg["quant_group"] = 32
+        out.append((cfg, dt, B, Hkv, G, S, D))
+    return out
+
+
+JPEG_ATTN = _draw_jpeg(2028, 40)
+
+
+@pytest.mark.parametrize("case", JPEG_ATTN, ids=[f"j{i}" for i in range(len(JPEG_ATTN))])
+def test_jpeg_attention_sweep(case, oracle):
+    cfg, dt, B, Hkv, G, S, D = case
+    print(f"case jpeg sweep {case}", flush=True)
+    ks, vs = build_streams(cfg, dt, B, Hkv, S, D, 500 + S, oracle)
+    rng = np.random.default_rng(S + 3 * D)
+    q = torch.from_numpy((rng.standard_normal((B, Hkv * G, 1, D)) / math.sqrt(D))
+                         .astype(np.float32)).to(torch_dtype(dt)).to(DEV)
+    out = fc.codec_decode_attention(q, ks, vs)
+    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), dt)
+
+
+JPEG_STEPS = _draw_jpeg(2029, 16)
+
+
+@pytest.mark.parametrize("case", JPEG_STEPS, ids=[f"t{i}" for i in range(len(JPEG_STEPS))])
+def test_jpeg_step_sweep(case, oracle):
+    """As test_png_step_sweep, on jpeg archives (int8 with one scale per row
+    or per 32 features, or unquantised coefficients)."""
+    _step_sweep(case, oracle)
