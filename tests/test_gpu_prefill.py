@@ -127,6 +127,37 @@ def _case_id(c):
 
 @pytest.mark.parametrize("case", CASES, ids=[_case_id(c) for c in CASES])
 def test_prefill_matches_causal_attention_on_the_view(case, oracle):
+    _prefill_case(case, oracle)
+
+
+def _draw_prefill(seed, n):
+    """Seeded random prefill cases (same list on every run): dtype, batch,
+    kv heads, query heads per kv head, head size, kept frequencies, prompt
+    and cached lengths (chunked prefills, tails, prompts shorter than a
+    block), scale layout and block size."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        r = int(rng.choice([4, 8, 16, 32]))
+        k = int(rng.choice([kk for kk in (1, 2, 4) if kk <= r]))
+        D = int(rng.choice([64, 128, 256]))
+        G = int(rng.choice([1, 2, 3, 4, 8, 16]))
+        S = int(rng.integers(1, 320))
+        S0 = int(rng.choice([0, 0, int(rng.integers(1, 200))]))
+        out.append((str(rng.choice(["f16", "bf16"])), int(rng.integers(1, 3)),
+                    int(rng.choice([1, 2])), G, D, k, S, S0, int(rng.choice([0, 32])), r))
+    return out
+
+
+SWEEP = _draw_prefill(2030, 24)
+
+
+@pytest.mark.parametrize("case", SWEEP, ids=[f"p{i}" for i in range(len(SWEEP))])
+def test_prefill_sweep(case, oracle):
+    _prefill_case(case, oracle)
+
+
+def _prefill_case(case, oracle):
     dt, B, Hkv, G, D, k, S, S0 = case[:8]
     group = case[8] if len(case) > 8 else 0
     r = case[9] if len(case) > 9 else 8
