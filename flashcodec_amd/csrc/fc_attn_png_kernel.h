@@ -297,12 +297,11 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     if (split == 0) {
       const int64_t bh_s = b * p.Hkv + hkv;
       float* xk = cbuf_raw;  // the passes have not started: the end-phase buffer is free
-      const PngStepDst kd{static_cast<T*>(const_cast<void*>(p.kanch)) + (bh_s * p.kcap + step_nb) * D,
-                          const_cast<float*>(p.kdel) + (bh_s * p.kcap + step_nb) * (R - 1) * D,
-                          nullptr};
-      const PngStepDst vd{static_cast<T*>(const_cast<void*>(p.vanch)) + (bh_s * p.vcap + step_nb) * D,
-                          const_cast<float*>(p.vdel) + (bh_s * p.vcap + step_nb) * (R - 1) * D,
-                          nullptr};
+      const int64_t kslot = bh_s * p.kcap + step_nb, vslot = bh_s * p.vcap + step_nb;
+      const PngStepDst kd{static_cast<T*>(const_cast<void*>(p.kanch)) + kslot * D,
+                          const_cast<float*>(p.kdel) + kslot * (R - 1) * D, nullptr};
+      const PngStepDst vd{static_cast<T*>(const_cast<void*>(p.vanch)) + vslot * D,
+                          const_cast<float*>(p.vdel) + vslot * (R - 1) * D, nullptr};
       const int n = png_step_rows<D, R, T, false>(
           step_t, R, static_cast<T*>(const_cast<void*>(p.kraw)) + bh_s * R * D,
           static_cast<T*>(const_cast<void*>(p.vraw)) + bh_s * R * D,

@@ -334,8 +334,8 @@ __global__ __launch_bounds__(kMThreads, GP <= 4 ? 2 : 1) void attn_split_pngpk(M
             step_t, r, static_cast<T*>(const_cast<void*>(p.kraw)) + bh_s * r * D,
             static_cast<T*>(const_cast<void*>(p.vraw)) + bh_s * r * D,
             static_cast<const T*>(p.ktok) + b * p.kt_sb + hkv * p.kt_sh,
-            static_cast<const T*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write, kdst, vdst, km,
-            tid, xk, xv);
+            static_cast<const T*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write, kdst, vdst,
+            km, tid, xk, xv);
         if constexpr (QF32)
           png_step_attend<D, float>(n, static_cast<const float*>(p.q), qb, p.q_sh, h0, G,
                                     p.scale_log2, tid, xk, xv, scratch, part_lds, tail_ml[0],
