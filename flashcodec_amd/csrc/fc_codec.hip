@@ -665,6 +665,16 @@ __global__ __launch_bounds__(kThreads) void png_encode_kernel(
 
 // ----------------------------------------------------------------- png decode
 
+// The delta rows of a block are requested kPngDecodeBatch at a time before
+// any is used (a thread has that many loads in flight instead of one).  The
+// C4 read's rate depends on where the anchors sit relative to the deltas:
+// with one row per load-use step 43.3 us when both start 128 MB apart in
+// one allocation, 52.7-56.9 us at the other offsets tried (so 4.7 to 6.2
+// TB/s between runs and boxes, with the allocator's placement); 4 rows per
+// batch: 43.2 us and 50.4-52.3 us; 8 rows: 46.6 us and 49.7-51.1 us (the
+// registers of 8 rows lower the occupancy).
+constexpr int kPngDecodeBatch = 4;
+
 template <typename T, int VEC>
 __global__ __launch_bounds__(kThreads) void png_decode_kernel(
     const float* __restrict__ deltas, const T* __restrict__ anchors, int64_t H, int64_t cap,
@@ -679,24 +689,32 @@ __global__ __launch_bounds__(kThreads) void png_decode_kernel(
   const int64_t slot = bh * cap + blk;
   T* dst = out + b * osb + h * osh + d0;
   const int64_t tok0 = blk * r;
+  // rows 1 .. n-1 of the block are written (the output may end inside it)
+  const int n = (int)min<int64_t>(r, max<int64_t>(out_len - tok0, 0));
+  const float* src = deltas + slot * (int64_t)(r - 1) * D + d0;
   float base[VEC];
   load_f32<T, VEC>(anchors + slot * D + d0, base);
-  if (tok0 < out_len) store_from_f32<T, VEC>(dst + tok0 * oss, base);
   double run[VEC];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) run[v] = 0.0;
-  const float* src = deltas + slot * (int64_t)(r - 1) * D + d0;
-  for (int i = 1; i < r; ++i) {
-    if (tok0 + i >= out_len) break;
-    float dv[VEC], o[VEC];
-    load_f32<float, VEC>(src + (int64_t)(i - 1) * D, dv);
+  for (int i0 = 1; i0 < n; i0 += kPngDecodeBatch) {
+    float dv[kPngDecodeBatch][VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      run[v] += (double)dv[v];
-      o[v] = base[v] + (float)run[v];
+    for (int c = 0; c < kPngDecodeBatch; ++c)
+      if (i0 + c < n) load_f32<float, VEC>(src + (int64_t)(i0 + c - 1) * D, dv[c]);
+#pragma unroll
+    for (int c = 0; c < kPngDecodeBatch; ++c) {
+      if (i0 + c >= n) break;
+      float o[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        run[v] += (double)dv[c][v];
+        o[v] = base[v] + (float)run[v];
+      }
+      store_from_f32<T, VEC>(dst + (tok0 + i0 + c) * oss, o);
     }
-    store_from_f32<T, VEC>(dst + (tok0 + i) * oss, o);
   }
+  if (n > 0) store_from_f32<T, VEC>(dst + tok0 * oss, base);
 }
 
 constexpr int kPackMaxKept = 8;  // kept deltas the packed read holds in registers
