@@ -139,3 +139,46 @@ def test_jpeg_step_sweep(case, oracle):
     """As test_png_step_sweep, on jpeg archives (int8 with one scale per row
     or per 32 features, or unquantised coefficients)."""
     _step_sweep(case, oracle)
+
+
+def _draw_mixed(seed, n):
+    """Cases whose queries have another dtype than the stream (png dense /
+    packed, int8 jpeg, coefficient jpeg): the dispatch falls back to the
+    pass that takes them."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        kind = i % 4
+        r = int(rng.choice([4, 8, 16]))
+        if kind == 0:
+            cfg = dict(mode="png", block_size=r, keep_ratio=float(rng.choice([0.25, 1.0])))
+        elif kind == 1:
+            cfg = dict(mode="png", block_size=r, keep_ratio=0.5, packed=True)
+        elif kind == 2:
+            cfg = dict(mode="jpeg", block_size=r, keep_freqs=min(r, 4), quant_bits=8)
+        else:
+            cfg = dict(mode="jpeg", block_size=r, keep_freqs=min(r, 2))
+        dts = ["f32", "f16", "bf16"]
+        st_dt = str(rng.choice(dts))
+        q_dt = str(rng.choice([d for d in dts if d != st_dt]))
+        D = int(rng.choice([64, 128]))
+        S = int(rng.integers(2, 60)) * r + int(rng.integers(0, r))
+        out.append((cfg, st_dt, q_dt, int(rng.integers(1, 3)), int(rng.choice([1, 2])),
+                    int(rng.choice([1, 2, 4, 8])), S, D))
+    return out
+
+
+MIXED = _draw_mixed(2031, 16)
+
+
+@pytest.mark.parametrize("case", MIXED, ids=[f"m{i}" for i in range(len(MIXED))])
+def test_mixed_dtype_attention_sweep(case, oracle):
+    cfg, st_dt, q_dt, B, Hkv, G, S, D = case
+    print(f"case mixed dtype sweep {case}", flush=True)
+    ks, vs = build_streams(cfg, st_dt, B, Hkv, S, D, 300 + S, oracle)
+    rng = np.random.default_rng(S + 7 * D)
+    q = torch.from_numpy((rng.standard_normal((B, Hkv * G, 1, D)) / math.sqrt(D))
+                         .astype(np.float32)).to(torch_dtype(q_dt)).to(DEV)
+    out = fc.codec_decode_attention(q, ks, vs)
+    assert out.dtype == q.dtype
+    assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), q_dt)
