@@ -568,7 +568,7 @@ def shapes_mode(args):
     """Decode attention at C3's geometry (B=8, 32 q / 8 kv heads, 32768
     archived + 5 raw tokens, r=8) on int8 archives (fp16 stream) for head
     sizes, keep_freqs, per-32 scales and fp32 queries besides C3's, and on
-    fp16 / bf16 coefficient archives (quant_bits=0): each on the
+    fp16 / bf16 / fp32 coefficient archives (quant_bits=0): each on the
     matrix-core pass (FC_PASS_AUTO) and on the vector-ALU pass
     (FC_PASS_VECTOR), one archive set, max error vs the fp64 oracle over all
     sequences."""
@@ -586,6 +586,7 @@ def shapes_mode(args):
                                (96, 4, 0, "f16", 8), (128, 4, 32, "f16", 8), (96, 4, 32, "f16", 8),
                                (128, 4, 0, "f32", 8), (128, 4, 32, "f32", 8),
                                (128, 4, 0, "f16", 0), (128, 2, 0, "bf16", 0),
+                               (128, 4, 0, "f32", 0), (128, 2, 0, "f32", 0),
                                (128, 4, 0, "f16", 8)):
         cfg = dict(mode="jpeg", block_size=R, keep_freqs=k, quant_bits=qb)
         if grp:
@@ -599,9 +600,10 @@ def shapes_mode(args):
             del x
         g = torch.Generator(device=dev).manual_seed(3)
         q = (torch.randn((B, HQ, 1, D), generator=g, device=dev) / math.sqrt(D)).to(qt)
-        row_bytes = D + 4 * (D // grp if grp else 1) if qb else 2 * D
+        st_es = torch.empty((), dtype=st_dt).element_size()
+        row_bytes = D + 4 * (D // grp if grp else 1) if qb else st_es * D
         qo_bytes = 2 * B * HQ * D * q.element_size()
-        nbytes = 2 * (B * HKV * NB * k * row_bytes) + 2 * B * HKV * TAIL * D * 2 + qo_bytes
+        nbytes = 2 * (B * HKV * NB * k * row_bytes) + 2 * B * HKV * TAIL * D * st_es + qo_bytes
         row = {"D": D, "keep_freqs": k, "quant_bits": qb, "quant_group": grp, "q_dtype": qdt,
                "algorithmic_bytes": nbytes}
         for name, code in (("matrix_core", N.PASS_AUTO), ("vector_alu", N.PASS_VECTOR)):

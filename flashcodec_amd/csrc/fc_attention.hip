@@ -1182,10 +1182,12 @@ int fc_attention_splits(int store_kind, int stream_dtype, int q_dtype, int s, in
     // S=64K where 64 take 28.6
     const int64_t groups = (G + 15) / 16;
     const int64_t cols = std::max<int64_t>(1, B * Hkv * groups);
-    const int64_t per_cu = png_mfma ? fc::kPngWgPerCu : 2;
+    // fp32 coefficient archives run on the png pass (16-row passes)
+    const bool fpj32 = fpj_mfma && stream_dtype == FC_F32;
+    const int64_t per_cu = png_mfma || fpj32 ? fc::kPngWgPerCu : 2;
     int64_t want = (per_cu * (int64_t)n_cu + cols - 1) / cols;
     // rows per pass
-    const int64_t pr = png_mfma ? 16 : fpj_mfma ? (D == 64 ? 64 : 32) : D == 256 ? 32 : 64;
+    const int64_t pr = png_mfma || fpj32 ? 16 : fpj_mfma ? (D == 64 ? 64 : 32) : D == 256 ? 32 : 64;
     const int64_t npass = (nb * s + pr - 1) / pr;
     want = std::min<int64_t>(want, std::max<int64_t>(1, npass / 4));
     want = std::min<int64_t>(want, std::max<int64_t>(16, npass / 10));

@@ -34,6 +34,10 @@
 
 namespace fc {
 
+// fp32 coefficient rows take the png pass's fp32 products (JPG variant of
+// attn_split_png_mfma, launched from fc_attn_png.hip)
+int launch_fpj32_t(const MfmaArgs& a, int s, int D, int gp, dim3 grid, hipStream_t st);
+
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -392,6 +396,9 @@ __global__ __launch_bounds__(kMThreads, 2) void attn_split_fpj_mfma(MfmaArgs p) 
 
 // Query / stream dtypes, head sizes and stored rows per block of the pass.
 bool fpj_mfma_shape_supported(int q_dtype, int stream_dtype, int64_t D, int s) {
+  if (q_dtype == FC_F32)  // fp32 coefficient rows: the png pass's fp32 products (JPG)
+    return stream_dtype == FC_F32 && (D == 64 || D == 128) &&
+           (s == 1 || s == 2 || s == 4 || s == 8 || s == 16);
   return (q_dtype == FC_F16 || q_dtype == FC_BF16) && stream_dtype == q_dtype &&
          (D == 64 || D == 128) && (s == 1 || s == 2 || s == 3 || s == 4 || s == 8);
 }
@@ -474,6 +481,12 @@ int launch_split_fpj_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh
   a.static_passes = static_pass_order() ? 1 : 0;
   a.cstride = stride;
   const dim3 grid((unsigned)(a.ngroups * n_splits));
+  if (q_dtype == FC_F32) {  // fp32 coefficient rows (fc_attn_png_kernel.h, JPG)
+    if (a.step) return FC_ERR_UNSUPPORTED;
+    const int rc = launch_fpj32_t(a, s, (int)D, gp, grid, st);
+    if (rc != FC_OK) return rc;
+    return check_launch();
+  }
   const bool bf = q_dtype == FC_BF16;
   const bool step = a.step != 0;
   const int rc = mfma_with_int<1, 2, 3, 4, 8>(s, [&](auto sc) {

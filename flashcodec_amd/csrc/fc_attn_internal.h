@@ -116,7 +116,8 @@ bool png_mfma_shape_supported(int q_dtype, int stream_dtype, int64_t D, int r);
 constexpr int kPngWgPerCu = 2;  // workgroups per compute unit of the png pass
 // jpeg archives of fp16 / bf16 coefficients on the matrix cores
 // (fc_attn_fpj.hip): queries in the stream dtype, D = 64 / 128, s = 1 / 2 /
-// 3 / 4 / 8.
+// 3 / 4 / 8; fp32 coefficients with fp32 queries (the png pass's fp32
+// products), s = 1 / 2 / 4 / 8 / 16.
 bool fpj_mfma_shape_supported(int q_dtype, int stream_dtype, int64_t D, int s);
 bool split_fpj_mfma_supported(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t D,
                               int s, int stream_dtype, const fc_stream_view* key,

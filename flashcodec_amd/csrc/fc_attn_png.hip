@@ -6,6 +6,20 @@ namespace fc {
 
 template int launch_png_t<float>(const MfmaArgs&, int, int, int, dim3, hipStream_t);
 
+int launch_fpj32_t(const MfmaArgs& a, int s, int D, int gp, dim3 grid, hipStream_t st) {
+  return mfma_with_int<1, 2, 4, 8, 16>(s, [&](auto sc) {
+    constexpr int Sv = decltype(sc)::value;
+    return mfma_with_int<64, 128>(D, [&](auto dc) {
+      constexpr int Dv = decltype(dc)::value;
+      return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
+        pngk::attn_split_png_mfma<Sv, Dv, decltype(gc)::value, false, float, true>
+            <<<grid, kMThreads, 0, st>>>(a);
+        return FC_OK;
+      });
+    });
+  });
+}
+
 // Query / stream dtypes, head size and block size of the png matrix-core
 // pass: queries in the stream's dtype (fp32, fp16 or bf16).
 bool png_mfma_shape_supported(int q_dtype, int stream_dtype, int64_t D, int r) {

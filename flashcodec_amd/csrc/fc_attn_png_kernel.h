@@ -67,9 +67,16 @@ constexpr int kPngTile = 16;  // rows per pass
 // and the passes cover the blocks before it.  T: the stream dtype (anchors,
 // tails, tokens) and the queries' (float, f16_t, bf16_t); deltas are fp32
 // and products fp32 for all.
-template <int R, int D, int GP, bool STEP, typename T>
+// JPG: the same pass over jpeg archives of fp32 coefficients (the reference's
+// default codec, quant_bits=0, in an fp32 model): R stored coefficient rows
+// per block (MfmaArgs.kfp / vfp), the p.r token logits of a (block, query)
+// pair taps of A over its R scaled scores and the row weights
+// w_j = sum_t p_t A[t][j] (flashcodec/attention.py:101-140), both in fp64 as
+// the int8 pass forms them for fp32 queries.
+template <int R, int D, int GP, bool STEP, typename T, bool JPG = false>
 __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(MfmaArgs p) {
   constexpr bool F32 = std::is_same_v<T, float>;
+  static_assert(!JPG || (F32 && !STEP), "fp32 coefficient archives: no fused step");
   constexpr int FPL = D / 4;   // score-operand features per lane
   constexpr int FPC = D / 16;  // value-product features per lane column
   static_assert(kPngTile % R == 0 && FPC % 4 == 0, "block size / head size");
@@ -88,6 +95,7 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   __shared__ float scratch[2 * 16 * kFuseMaxSplits];  // raw-tail logits, then merge statistics
   __shared__ int s_last;
   __shared__ int s_final;
+  __shared__ float a_lds[JPG ? FC_MAX_BLOCK * R : 1];  // JPG: A (p.r x R)
 
   // 1-D grid, split-major, as the int8 pass
   const int64_t L = blockIdx.x;
@@ -100,6 +108,9 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane >> 4, lc = lane & 15;
   const int G = (int)min<int64_t>(16, p.G - g0);
+  const int rblk = JPG ? p.r : R;  // tokens per block
+  if constexpr (JPG)
+    for (int i = tid; i < p.r * R; i += kMThreads) a_lds[i] = p.A[i];
 
   int64_t nb = p.nb, n_raw = p.n_raw;
   int64_t step_t = 0, step_nb = 0;  // fused step: tail length and blocks before the token
@@ -115,9 +126,9 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     n_raw = 0;
   } else if (p.state) {
     // counts of a decode step's view on the device (graph replays)
-    const int64_t t = min<int64_t>(max<int64_t>(p.state[1], 0), R - 1) + 1;
-    nb = min<int64_t>(max<int64_t>(p.state[0], 0) + (t == R ? 1 : 0), min(p.kcap, p.vcap));
-    n_raw = t == R ? 0 : t;
+    const int64_t t = min<int64_t>(max<int64_t>(p.state[1], 0), rblk - 1) + 1;
+    nb = min<int64_t>(max<int64_t>(p.state[0], 0) + (t == rblk ? 1 : 0), min(p.kcap, p.vcap));
+    n_raw = t == rblk ? 0 : t;
   }
   const int64_t rows_total = nb * R;
   const int64_t npass = (rows_total + kPngTile - 1) / kPngTile;
@@ -140,10 +151,13 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   };
   auto pass_of = [](unsigned int v) { return (int64_t)__builtin_amdgcn_readfirstlane((int)v); };
 
-  const T* kanch = static_cast<const T*>(p.kanch) + bh * p.kcap * D;
-  const T* vanch = static_cast<const T*>(p.vanch) + bh * p.vcap * D;
-  const float* kdel = p.kdel + bh * p.kcap * (R - 1) * D;
-  const float* vdel = p.vdel + bh * p.vcap * (R - 1) * D;
+  const T* kanch = JPG ? nullptr : static_cast<const T*>(p.kanch) + bh * p.kcap * D;
+  const T* vanch = JPG ? nullptr : static_cast<const T*>(p.vanch) + bh * p.vcap * D;
+  const float* kdel = JPG ? nullptr : p.kdel + bh * p.kcap * (R - 1) * D;
+  const float* vdel = JPG ? nullptr : p.vdel + bh * p.vcap * (R - 1) * D;
+  // JPG: coefficient row gr of the (batch, kv head) at + gr * D
+  const float* kcoef = JPG ? static_cast<const float*>(p.kfp) + bh * p.kcap * R * D : nullptr;
+  const float* vcoef = JPG ? static_cast<const float*>(p.vfp) + bh * p.vcap * R * D : nullptr;
   // row gr of a stream: the anchor of its block or one of its deltas; rows
   // past the archive read row 0 and are zeroed by the caller (fp32 anchors)
   auto row_ptr = [&](const float* anch, const float* del, int64_t gr) {
@@ -208,7 +222,9 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     const bool ok = gr < rows_total;
     const float* src = nullptr;
     RowRef rr{};
-    if constexpr (F32)
+    if constexpr (JPG)
+      src = kcoef + (ok ? gr : 0) * D + 4 * lq;
+    else if constexpr (F32)
       src = row_ptr(kanch, kdel, ok ? gr : 0) + 4 * lq;
     else
       rr = row_ref(kanch, kdel, ok ? gr : 0);
@@ -231,7 +247,9 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
       const bool ok = gr < rows_total;
       const float* src = nullptr;
       RowRef rr{};
-      if constexpr (F32)
+      if constexpr (JPG)
+        src = vcoef + (ok ? gr : 0) * D + 4 * lc;
+      else if constexpr (F32)
         src = row_ptr(vanch, vdel, ok ? gr : 0) + 4 * lc;
       else
         rr = row_ref(vanch, vdel, ok ? gr : 0);
@@ -256,6 +274,33 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     lsum = 0.f;
     if (myh >= G) return;
     const int npair = (prow / R) * GP;
+    if constexpr (JPG) {
+      // the block's p.r logits as taps of A over its R scaled scores
+      const int r = p.r;
+      for (int u = lane; u < npair; u += 64) {
+        const int row0 = (u / GP) * R;
+        double sv[R];
+        float w[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+          sv[j] = (double)s_lds[wave][myh][row0 + j];
+          w[j] = 0.f;
+        }
+        for (int t = 0; t < r; ++t) {
+          double lg = 0.0;
+#pragma unroll
+          for (int j = 0; j < R; ++j) lg = __builtin_fma((double)a_lds[t * R + j], sv[j], lg);
+          pmax = fmaxf(pmax, (float)lg);
+          const float e = __builtin_amdgcn_exp2f((float)(lg - (double)mref));
+          lsum += e;
+#pragma unroll
+          for (int j = 0; j < R; ++j) w[j] = __builtin_fmaf(e, a_lds[t * R + j], w[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < R; ++j) w_lds[wave][myh][row0 + j] = w[j];
+      }
+      return;
+    }
     for (int u = lane; u < npair; u += 64) {
       const int row0 = (u / GP) * R;
       float e[R];
@@ -442,6 +487,10 @@ int launch_png_t(const MfmaArgs& a, int r, int D, int gp, dim3 grid, hipStream_t
     });
   });
 }
+
+// Launch of the pass over jpeg archives of fp32 coefficients (JPG): s
+// stored rows per block (1, 2, 4, 8, 16), head size D (64, 128).
+int launch_fpj32_t(const MfmaArgs& a, int s, int D, int gp, dim3 grid, hipStream_t st);
 
 extern template int launch_png_t<float>(const MfmaArgs&, int, int, int, dim3, hipStream_t);
 extern template int launch_png_t<f16_t>(const MfmaArgs&, int, int, int, dim3, hipStream_t);

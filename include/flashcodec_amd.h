@@ -272,8 +272,8 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G,
  * (stream dtype, query dtype, s stored rows per block, head size D): one
  * round of workgroups of the split pass that will run — the matrix-core
  * passes for int8 jpeg archives (one scale per row or per 32 features) with
- * fp16/bf16/fp32 queries, for fp16/bf16 coefficient archives queried in
- * their dtype at D = 64/128, and for png (fp32 / fp16 / bf16 streams queried
+ * fp16/bf16/fp32 queries, for fp16/bf16/fp32 coefficient archives queried
+ * in their dtype at D = 64/128, and for png (fp32 / fp16 / bf16 streams queried
  * in their dtype) at r = 4/8/16 (two workgroups
  * per compute unit, but at least one pass per wavefront and at most
  * max(16, passes / 10) splits), the packed png pass, otherwise the

@@ -88,6 +88,30 @@ def test_c4_png_full_shape(dt, keep, oracle):
     assert_close(to_values(out)[:, :, 0], oracle_out(oracle, q, ks, vs, D ** -0.5), dt)
 
 
+@pytest.mark.parametrize("r,k,G,D", [(8, 2, 4, 128), (8, 4, 4, 128), (16, 16, 2, 64),
+                                     (4, 1, 16, 128), (8, 8, 3, 64)])
+def test_fp32_coefficient_archive_on_matrix_cores(r, k, G, D, oracle, attention_pass):
+    """fp32 coefficient archives (quant_bits=0 in an fp32 model: the
+    reference's default codec) on the png pass's fp32 products, many splits
+    (B=2, 8 kv heads, 3000+ blocks and a raw tail): every sequence against
+    the fp64 oracle (1e-5 absolute), and against the vector-ALU pass."""
+    B, Hkv = 2, 8
+    S = r * (24000 // r) + 5
+    print(f"case fp32 coefficients r={r} k={k} G={G} D={D}", flush=True)
+    cfg = dict(mode="jpeg", block_size=r, keep_freqs=k)
+    ks, vs = build_streams(cfg, "f32", B, Hkv, S, D, 909 + k, oracle)
+    q = queries(B, Hkv * G, D, 910 + k, "f32")
+    n_splits = N.lib().fc_attention_splits(N.STORE_JPEG_FP, N.F32, N.F32, k, ks.n_blocks, B, Hkv,
+                                           G, D, N.num_cus(q.device))
+    assert n_splits > 1
+    out = fc.codec_decode_attention(q, ks, vs)
+    ref = oracle_out(oracle, q, ks, vs, D ** -0.5)
+    assert_close(to_values(out)[:, :, 0], ref, "f32")
+    attention_pass("valu")
+    out_v = fc.codec_decode_attention(q, ks, vs)
+    assert_close(to_values(out_v)[:, :, 0], ref, "f32")
+
+
 @pytest.mark.parametrize("dt,G,D", [("f16", 4, 128), ("bf16", 2, 128), ("f16", 8, 64),
                                     ("bf16", 4, 256), ("f32", 4, 128), ("f32", 2, 256)])
 def test_outlier_queries_on_matrix_cores(dt, G, D, oracle):
