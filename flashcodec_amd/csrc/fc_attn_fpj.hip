@@ -482,7 +482,7 @@ int launch_split_fpj_mfma(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh
   a.cstride = stride;
   const dim3 grid((unsigned)(a.ngroups * n_splits));
   if (q_dtype == FC_F32) {  // fp32 coefficient rows (fc_attn_png_kernel.h, JPG)
-    if (a.step) return FC_ERR_UNSUPPORTED;
+    if (a.step && r > 16) return FC_ERR_UNSUPPORTED;  // the step's rows in LDS: r <= 16
     const int rc = launch_fpj32_t(a, s, (int)D, gp, grid, st);
     if (rc != FC_OK) return rc;
     return check_launch();

@@ -12,8 +12,11 @@ int launch_fpj32_t(const MfmaArgs& a, int s, int D, int gp, dim3 grid, hipStream
     return mfma_with_int<64, 128>(D, [&](auto dc) {
       constexpr int Dv = decltype(dc)::value;
       return mfma_with_int<1, 2, 4, 8, 16>(gp, [&](auto gc) {
-        pngk::attn_split_png_mfma<Sv, Dv, decltype(gc)::value, false, float, true>
-            <<<grid, kMThreads, 0, st>>>(a);
+        constexpr int GPv = decltype(gc)::value;
+        if (a.step)
+          pngk::attn_split_png_mfma<Sv, Dv, GPv, true, float, true><<<grid, kMThreads, 0, st>>>(a);
+        else
+          pngk::attn_split_png_mfma<Sv, Dv, GPv, false, float, true><<<grid, kMThreads, 0, st>>>(a);
         return FC_OK;
       });
     });

@@ -76,7 +76,9 @@ constexpr int kPngTile = 16;  // rows per pass
 template <int R, int D, int GP, bool STEP, typename T, bool JPG = false>
 __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(MfmaArgs p) {
   constexpr bool F32 = std::is_same_v<T, float>;
-  static_assert(!JPG || (F32 && !STEP), "fp32 coefficient archives: no fused step");
+  static_assert(!JPG || F32, "coefficient archives here: fp32");
+  // JPG STEP: blocks of at most kJpgStepMaxR tokens (the host checks)
+  constexpr int kJpgStepMaxR = 16;
   constexpr int FPL = D / 4;   // score-operand features per lane
   constexpr int FPC = D / 16;  // value-product features per lane column
   static_assert(kPngTile % R == 0 && FPC % 4 == 0, "block size / head size");
@@ -86,7 +88,9 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   // the end phase's per-wavefront accumulators; STEP: before the passes,
   // the step's rows (2 R D floats)
   constexpr int kCb = kWaves * GP * D;
-  constexpr int kCbN = STEP && 2 * R * D > kCb ? 2 * R * D : kCb;
+  // (JPG: the block's 2 r rows and its R coefficient rows)
+  constexpr int kStepN = JPG ? (2 * kJpgStepMaxR + R) * D : 2 * R * D;
+  constexpr int kCbN = STEP && kStepN > kCb ? kStepN : kCb;
   __shared__ __attribute__((aligned(16))) float cbuf_raw[kCbN];
   auto& cbuf = *reinterpret_cast<float (*)[kWaves][GP][D]>(cbuf_raw);
   __shared__ __attribute__((aligned(16))) float part_lds[16 * D];
@@ -117,11 +121,11 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   bool step_write = false;
   if constexpr (STEP) {
     const int64_t cap = min(p.kcap, p.vcap);
-    step_t = p.state ? min<int64_t>(max<int64_t>(p.state[1], 0), R - 1) : p.step_t;
+    step_t = p.state ? min<int64_t>(max<int64_t>(p.state[1], 0), rblk - 1) : p.step_t;
     step_nb = p.state ? max<int64_t>(p.state[0], 0) : p.step_nb;
     // one head group per (batch, kv head) stores the token / block; a block
     // past the capacity is not stored (the state's overflow word says so)
-    step_write = split == 0 && g0 == 0 && (step_t + 1 < R || step_nb < cap);
+    step_write = split == 0 && g0 == 0 && (step_t + 1 < rblk || step_nb < cap);
     nb = min(step_nb, cap);
     n_raw = 0;
   } else if (p.state) {
@@ -338,7 +342,25 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   // raw tail (fused calls): split 0 computes its partial before the passes;
   // in a fused step that partial covers the rows the step adds
   const bool fold_tail = p.fused && split == 0 && (STEP || n_raw > 0);
-  if constexpr (STEP) {
+  if constexpr (STEP && JPG) {
+    if (split == 0) {
+      // the fp archive kernel's arithmetic on a completed block (the
+      // coefficients stored as fp32 rows), the step's rows at full precision
+      const int64_t bh_s = b * p.Hkv + hkv;
+      float* xk = cbuf_raw;  // the passes have not started: the end-phase buffer is free
+      const int64_t kblk = (bh_s * p.kcap + step_nb) * R, vblk = (bh_s * p.vcap + step_nb) * R;
+      float* kw = static_cast<float*>(const_cast<void*>(p.kfp)) + kblk * D;
+      float* vw = static_cast<float*>(const_cast<void*>(p.vfp)) + vblk * D;
+      step_partial<D, R, float, 0>(
+          step_t, rblk, static_cast<float*>(const_cast<void*>(p.kraw)) + bh_s * rblk * D,
+          static_cast<float*>(const_cast<void*>(p.vraw)) + bh_s * rblk * D,
+          static_cast<const float*>(p.ktok) + b * p.kt_sb + hkv * p.kt_sh,
+          static_cast<const float*>(p.vtok) + b * p.vt_sb + hkv * p.vt_sh, step_write, kw,
+          nullptr, vw, nullptr, p.basis, p.A, p.q, FC_F32, b * p.q_sb, p.q_sh, hkv * p.G + g0, G,
+          p.scale_log2, tid, xk, xk + rblk * D, xk + 2 * rblk * D, nullptr, scratch, part_lds,
+          tail_ml[0], tail_ml[1]);
+    }
+  } else if constexpr (STEP) {
     if (split == 0) {
       const int64_t bh_s = b * p.Hkv + hkv;
       float* xk = cbuf_raw;  // the passes have not started: the end-phase buffer is free
@@ -450,7 +472,7 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     __syncthreads();
     if (s_final && tid < 64) {  // lane-indexed vector stores
       const int64_t cap = min(p.kcap, p.vcap);
-      const bool full = step_t + 1 == R;
+      const bool full = step_t + 1 == rblk;
       const bool over = full && step_nb >= cap;
       const int64_t word = tid == 0   ? (full ? step_nb + 1 : step_nb)
                            : tid == 1 ? (full ? 0 : step_t + 1)

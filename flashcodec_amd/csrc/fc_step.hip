@@ -76,9 +76,9 @@ static int step_single_launch(const fc_step_args* a, const int64_t* state) {
   if ((a->store_kind != FC_STORE_JPEG_I8 && !grouped && !fp && !png && !pk) ||
       (!fp && !png && !pk && a->quant_bits != 8) || !mfma_split_allowed())
     return FC_ERR_UNSUPPORTED;
-  // (fp32 coefficient archives: the attention runs on the png pass, which
-  // has no in-kernel jpeg archive)
-  if (fp && a->stream_dtype == FC_F32) return FC_ERR_UNSUPPORTED;
+  // (fp32 coefficient archives run on the png pass: its step holds blocks of
+  // up to 16 tokens in LDS)
+  if (fp && a->stream_dtype == FC_F32 && a->r > 16) return FC_ERR_UNSUPPORTED;
   const int64_t B = a->B, Hq = a->Hq, Hkv = a->Hkv, D = a->D;
   const int r = a->r;
   const int64_t G = Hq / Hkv;

@@ -520,8 +520,8 @@ int fc_decode_step(const fc_step_args* args);
  * How the calling thread's last successful fc_decode_step call ran: 1 when
  * the whole step was one kernel launch (int8 jpeg archives with one scale
  * per row or per 32 features, fp16 / bf16 / fp32 queries and stream, or
- * jpeg archives of fp16 / bf16 coefficients with queries and stream of
- * their dtype, png archives with queries and stream of one dtype, or packed
+ * jpeg archives of fp16 / bf16 / fp32 coefficients with queries and stream
+ * of their dtype (fp32: blocks of up to 16 tokens), png archives with queries and stream of one dtype, or packed
  * Top-M png archives; a
  * matrix-core pass), 0 when it
  * took the multi-launch form (token append, archive, attention, state

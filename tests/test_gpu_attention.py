@@ -396,7 +396,11 @@ I8 = dict(mode="jpeg", block_size=8, keep_freqs=4, quant_bits=8)
 STEP_PAIRS = [
     (I8, "f16", 64, 4, True),
     (dict(I8, keep_freqs=2), "bf16", 64, 4, True),
-    (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 64, 4, False),
+    # fp32 coefficient rows (fp32 model, default codec): one launch on the png pass
+    (dict(mode="jpeg", block_size=8, keep_freqs=2), "f32", 64, 4, True),
+    (dict(mode="jpeg", block_size=16, keep_freqs=4), "f32", 128, 2, True),
+    (dict(mode="jpeg", block_size=4, keep_freqs=1), "f32", 128, 8, True),
+    (dict(mode="jpeg", block_size=16, keep_freqs=16), "f32", 64, 20, True),
     # fp16 / bf16 coefficient rows: the one-launch step archives them in-kernel
     (dict(mode="jpeg", block_size=8, keep_freqs=4), "bf16", 128, 2, True),
     (dict(mode="jpeg", block_size=8, keep_freqs=2), "f16", 64, 4, True),
