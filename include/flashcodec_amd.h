@@ -273,12 +273,11 @@ int fc_attention_default_splits(int64_t nb, int64_t B, int64_t Hkv, int64_t G,
  * round of workgroups of the split pass that will run — the matrix-core
  * passes for int8 jpeg archives (one scale per row or per 32 features) with
  * fp16/bf16/fp32 queries, for fp16/bf16/fp32 coefficient archives queried
- * in their dtype at D = 64/128, and for png (fp32 / fp16 / bf16 streams queried
- * in their dtype) at r = 4/8/16 (two workgroups
- * per compute unit, but at least one pass per wavefront and at most
- * max(16, passes / 10) splits), the packed png pass, otherwise the
- * vector-ALU pass at the occupancy it reaches on the current device.  0
- * when nb == 0.
+ * in their dtype at D = 64/128, and for png (fp32/fp16/bf16 streams
+ * queried in their dtype) at r = 4/8/16 (two workgroups per compute unit,
+ * but at least one pass per wavefront and at most max(16, passes / 10)
+ * splits), the packed png pass, otherwise the vector-ALU pass at the
+ * occupancy it reaches on the current device.  0 when nb == 0.
  * Replaces the split heuristic ns = max(1, min(32, ceil(n / 64))) of
  * flashcodec/triton_attention.py:191.
  */
@@ -519,13 +518,12 @@ int fc_decode_step(const fc_step_args* args);
 /*
  * How the calling thread's last successful fc_decode_step call ran: 1 when
  * the whole step was one kernel launch (int8 jpeg archives with one scale
- * per row or per 32 features, fp16 / bf16 / fp32 queries and stream, or
- * jpeg archives of fp16 / bf16 / fp32 coefficients with queries and stream
- * of their dtype (fp32: blocks of up to 16 tokens), png archives with queries and stream of one dtype, or packed
- * Top-M png archives; a
- * matrix-core pass), 0 when it
- * took the multi-launch form (token append, archive, attention, state
- * advance), -1 before any such call.  No counterpart in the reference (its
+ * per row or per 32 features, fp16 / bf16 / fp32 queries and stream; jpeg
+ * archives of fp16 / bf16 / fp32 coefficients with queries and stream of
+ * their dtype, fp32 with blocks of up to 16 tokens; png archives with
+ * queries and stream of one dtype; packed Top-M png archives; a matrix-core
+ * pass's shapes), 0 when it took the multi-launch form (token append,
+ * archive, attention, state advance), -1 before any such call.  No counterpart in the reference (its
  * step is always two appends and an attention call); for callers and tests
  * that report or check launches per decode step.
  */
