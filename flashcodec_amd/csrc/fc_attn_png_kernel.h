@@ -169,39 +169,39 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     const int j = (int)(gr - blk * R);
     return j == 0 ? anch + blk * D : del + (blk * (R - 1) + (j - 1)) * D;
   };
-  // 16-bit anchors: a lane's row is its block's anchor (16-bit elements) or
-  // a delta (fp32); every lane loads two 8-byte pieces (an anchor lane's
-  // second piece repeats its first), so no branch holds a load and the
-  // widening waits for the data only where it is used
+  // 16-bit anchors: a lane's row is its block's anchor (2-byte elements) or
+  // a delta (fp32).  Every lane loads a 16-byte piece of a delta row (an
+  // anchor lane: its block's first delta row, which a neighbour lane loads
+  // too) and an 8-byte piece of its block's anchor row (the lanes of a
+  // block share those lines), then keeps the one its row is: no branch
+  // holds a load, and the delta rows keep full-width loads
   struct RowRef {
-    const char* base;
+    const float* del;
+    const T* anch;
     bool anc;
   };
   auto row_ref = [&](const T* anch, const float* del, int64_t gr) {
     const int64_t blk = gr / R;
     const int j = (int)(gr - blk * R);
     const bool anc = j == 0;
-    const char* base = anc ? reinterpret_cast<const char*>(anch + blk * D)
-                           : reinterpret_cast<const char*>(del + (blk * (R - 1) + (j - 1)) * D);
-    return RowRef{base, anc};
+    return RowRef{del + (blk * (R - 1) + (anc ? 0 : j - 1)) * D, anch + blk * D, anc};
   };
   // features e .. e+3 of row rr; NT: nontemporal
   auto row4_16 = [&](const RowRef& rr, int e, auto nt) -> float4_t {
     constexpr bool NT = decltype(nt)::value;
-    const u32x2_t* lo_p = reinterpret_cast<const u32x2_t*>(rr.base + e * (rr.anc ? 2 : 4));
-    const u32x2_t* hi_p = rr.anc ? lo_p : lo_p + 1;
-    u32x2_t lo, hi;
+    const float4_t* dp = reinterpret_cast<const float4_t*>(rr.del + e);
+    const u32x2_t* ap = reinterpret_cast<const u32x2_t*>(rr.anch + e);
+    float4_t dv;
+    u32x2_t av;
     if constexpr (NT) {
-      lo = __builtin_nontemporal_load(lo_p);
-      hi = __builtin_nontemporal_load(hi_p);
+      dv = __builtin_nontemporal_load(dp);
+      av = __builtin_nontemporal_load(ap);
     } else {
-      lo = *lo_p;
-      hi = *hi_p;
+      dv = *dp;
+      av = *ap;
     }
-    const float4_t wide = half4_to_f32<T>(lo);
-    const float4_t full = {__uint_as_float(lo[0]), __uint_as_float(lo[1]), __uint_as_float(hi[0]),
-                           __uint_as_float(hi[1])};
-    return rr.anc ? wide : full;
+    const float4_t wide = half4_to_f32<T>(av);
+    return rr.anc ? wide : dv;
   };
 
   // ---- queries: lane (q, c) holds head c's features 16 j + 4 q + i
