@@ -76,7 +76,7 @@ def test_noalloc_matches_workspace_entry(first, second, oracle, static_order):
 
 @pytest.mark.parametrize("cfg,first,second", [
     # other store kinds through the same entry: png (16-bit anchors), packed
-    # Top-M png, fp16 / bf16 coefficient jpeg, per-32 int8 jpeg
+    # Top-M png, fp16 / bf16 / fp32 coefficient jpeg, per-32 int8 jpeg
     (dict(mode="png", block_size=16, keep_ratio=0.25), ("bf16", 2, 8, 4, 128, 16 * 900 + 5),
      ("bf16", 1, 2, 2, 64, 16 * 40 + 3)),
     (dict(mode="png", block_size=8, keep_ratio=0.5, packed=True), ("f32", 2, 4, 4, 128, 8 * 1500),
@@ -84,7 +84,9 @@ def test_noalloc_matches_workspace_entry(first, second, oracle, static_order):
     (dict(mode="jpeg", block_size=8, keep_freqs=2), ("bf16", 4, 8, 2, 128, 8 * 2000 + 3),
      ("bf16", 2, 2, 4, 64, 8 * 100 + 1)),
     (dict(I8, quant_group=32), ("f16", 4, 8, 4, 128, 8 * 2000 + 5), ("f16", 1, 2, 2, 96, 8 * 70)),
-], ids=["png-bf16", "pngpk-f32", "fpj-bf16", "i8g-f16"])
+    (dict(mode="jpeg", block_size=8, keep_freqs=4), ("f32", 2, 8, 4, 128, 8 * 2000 + 3),
+     ("f32", 1, 2, 2, 64, 8 * 90 + 1)),
+], ids=["png-bf16", "pngpk-f32", "fpj-bf16", "i8g-f16", "fpj-f32"])
 def test_noalloc_other_store_kinds(cfg, first, second, oracle, static_order):
     L = N.lib()
     for i, (dt, B, Hkv, G, D, S) in enumerate((first, second)):
