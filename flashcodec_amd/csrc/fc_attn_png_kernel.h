@@ -203,15 +203,34 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     const float4_t wide = half4_to_f32<T>(av);
     return rr.anc ? wide : dv;
   };
+  // features e .. e+7 of row rr as two float4: two 16-byte delta pieces and
+  // one 16-byte anchor piece (the score operand's 16-bit layout, which
+  // gives each lane runs of 8 features so one anchor load serves both)
+  auto row8_16 = [&](const RowRef& rr, int e, auto& lo, auto& hi) {
+    const float4_t* dp = reinterpret_cast<const float4_t*>(rr.del + e);
+    const float4_t d0 = dp[0], d1 = dp[1];
+    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(rr.anch + e);
+    const float4_t w0 = half4_to_f32<T>((u32x2_t){a[0], a[1]});
+    const float4_t w1 = half4_to_f32<T>((u32x2_t){a[2], a[3]});
+    lo = rr.anc ? w0 : d0;
+    hi = rr.anc ? w1 : d1;
+  };
+  // score-operand feature of lane quarter lq's piece j (4 features): fp32
+  // rows 16 j + 4 lq; 16-bit rows 32 (j / 2) + 8 lq + 4 (j % 2), runs of 8
+  // per lane (the product sums over features, so K and Q only have to agree)
+  auto sfeat = [&](int j) { return F32 ? 16 * j + 4 * lq : 32 * (j >> 1) + 8 * lq + 4 * (j & 1); };
+  // value-product feature of lane column lc's register f (runs of 8 per
+  // lane here, as the score operand's, measured 1 us slower at C4's shape)
+  auto vfeat = [&](int f) { return 64 * (f / 4) + 4 * lc + (f % 4); };
 
-  // ---- queries: lane (q, c) holds head c's features 16 j + 4 q + i
+  // ---- queries: lane (q, c) holds head c's features sfeat(j) + i (q = lq)
   const bool hq_ok = lc < G;
   const int64_t hq = hkv * p.G + g0 + (hq_ok ? lc : 0);
-  const T* qrow = static_cast<const T*>(p.q) + b * p.q_sb + hq * p.q_sh + 4 * lq;
+  const T* qrow = static_cast<const T*>(p.q) + b * p.q_sb + hq * p.q_sh;
   using qraw_t = std::conditional_t<F32, float4_t, u32x2_t>;  // converted when read
   qraw_t qraw[FPL / 4];
 #pragma unroll
-  for (int j = 0; j < FPL / 4; ++j) qraw[j] = *reinterpret_cast<const qraw_t*>(qrow + 16 * j);
+  for (int j = 0; j < FPL / 4; ++j) qraw[j] = *reinterpret_cast<const qraw_t*>(qrow + sfeat(j));
 
   float4_t acc[FPC];
 #pragma unroll
@@ -227,20 +246,29 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
     const float* src = nullptr;
     RowRef rr{};
     if constexpr (JPG)
-      src = kcoef + (ok ? gr : 0) * D + 4 * lq;
+      src = kcoef + (ok ? gr : 0) * D;
     else if constexpr (F32)
-      src = row_ptr(kanch, kdel, ok ? gr : 0) + 4 * lq;
+      src = row_ptr(kanch, kdel, ok ? gr : 0);
     else
       rr = row_ref(kanch, kdel, ok ? gr : 0);
+    if constexpr (F32) {
 #pragma unroll
-    for (int j = 0; j < FPL / 4; ++j) {
-      float4_t v;
-      if constexpr (F32)
-        v = *reinterpret_cast<const float4_t*>(src + 16 * j);
-      else
-        v = row4_16(rr, 4 * lq + 16 * j, std::false_type{});
+      for (int j = 0; j < FPL / 4; ++j) {
+        const float4_t v = *reinterpret_cast<const float4_t*>(src + sfeat(j));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kr[4 * j + i] = ok ? v[i] : 0.f;
+        for (int i = 0; i < 4; ++i) kr[4 * j + i] = ok ? v[i] : 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < FPL / 4; j += 2) {
+        float4_t lo, hi;
+        row8_16(rr, sfeat(j), lo, hi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kr[4 * j + i] = ok ? lo[i] : 0.f;
+          kr[4 * j + 4 + i] = ok ? hi[i] : 0.f;
+        }
+      }
     }
   };
   float vr[4][FPC];
@@ -252,18 +280,18 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
       const float* src = nullptr;
       RowRef rr{};
       if constexpr (JPG)
-        src = vcoef + (ok ? gr : 0) * D + 4 * lc;
+        src = vcoef + (ok ? gr : 0) * D;
       else if constexpr (F32)
-        src = row_ptr(vanch, vdel, ok ? gr : 0) + 4 * lc;
+        src = row_ptr(vanch, vdel, ok ? gr : 0);
       else
         rr = row_ref(vanch, vdel, ok ? gr : 0);
 #pragma unroll
       for (int k = 0; k < FPC / 4; ++k) {
         float4_t v;
         if constexpr (F32)
-          v = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(src + 64 * k));
+          v = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(src + vfeat(4 * k)));
         else
-          v = row4_16(rr, 4 * lc + 64 * k, std::true_type{});
+          v = row4_16(rr, vfeat(4 * k), std::true_type{});
 #pragma unroll
         for (int i = 0; i < 4; ++i) vr[rg][4 * k + i] = ok ? v[i] : 0.f;
       }
@@ -445,7 +473,7 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
   }
 
   // ---- combine the wavefronts: (max, sum, 1) per head and the accumulators
-  // (lane (q, c) register i of acc[f]: head 4q + i, feature D/16 * c + f)
+  // (lane (q, c) register i of acc[f]: head 4q + i, feature vfeat(f))
 #pragma unroll
   for (int m = GP; m < 64; m <<= 1) l_lane += __shfl_xor(l_lane, m, 64);
   if (lane < GP) {
@@ -458,7 +486,7 @@ __global__ __launch_bounds__(kMThreads, kPngWgPerCu) void attn_split_png_mfma(Mf
 #pragma unroll
     for (int f = 0; f < FPC; ++f)
 #pragma unroll
-      for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][64 * (f / 4) + 4 * lc + (f % 4)] = acc[f][i];
+      for (int i = 0; i < NI; ++i) cbuf[wave][4 * lq + i][vfeat(f)] = acc[f][i];
   }
   // the merge of up to 32 splits reads every partial in one batch, two
   // threads per output task (C4: 32 splits per group; 2.1 us shorter than
